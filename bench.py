@@ -1,0 +1,380 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X DPA4/SeZM operator slice (one GPU).
+
+Headline: segment_softmax forward with the null
+logit, N = 16,384 nodes (1 % hubs of degree 512, rest Poisson(48)),
+E ~ 862k edges, C = 8 heads, fp32.  A *step* is one forward pass over one
+batch of that shape.  The job cycles through enough distinct input batches
+(same graph, fresh logits / envelopes / null logits) that their total size
+exceeds the 256 MB Infinity Cache several times over, so every step streams
+its inputs from HBM.  The K timed steps are captured once into a HIP graph
+and replayed between two HIP events on the capturing stream; warmup steps run
+eagerly first.  `value` is edges per second over the K steps.
+
+The `roofline` object prices the same timed region: algorithmic bytes of one
+launch (every input read once, every output written once) over the average
+duration per launch.  `cpu_baseline` times the CPU oracle (the reference's
+ATen chain restated in torch) on the host cores on a bounded sample.  `ops`
+repeats the measurement for the other operators at their configuration sizes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 * 2**20
+ROTATION_BYTES = 1 << 30  # distinct input bytes cycled through per op
+
+
+def parse_args():
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--headline-only", action="store_true", help="skip the per-operator lines")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    parser.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
+    parser.add_argument("--roofline-shapes", action="store_true",
+                        help="also run the >=10M-edge shapes (1R, 2R, 4R)")
+    parser.add_argument("--calibrate-copy", action="store_true",
+                        help="launch one plain 256 MiB copy (counter calibration for rocprofv3 --pmc)")
+    return parser.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# timing harness
+# ---------------------------------------------------------------------------
+
+def time_steps(step, n_sets: int, steps: int, warmup: int, *, graph: bool = True) -> float:
+    """Average milliseconds per step over `steps` steps (step(i) uses input set i % n_sets)."""
+    import torch
+
+    for i in range(warmup):
+        step(i % n_sets)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    if graph:
+        hip_graph = torch.cuda.CUDAGraph()
+        keep = []
+        with torch.cuda.graph(hip_graph):
+            for i in range(steps):
+                keep.append(step(i % n_sets))
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        hip_graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        elapsed = start.elapsed_time(stop)
+        del keep, hip_graph
+    else:
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            step(i % n_sets)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        elapsed = start.elapsed_time(stop)
+    return elapsed / steps
+
+
+def n_sets_for(bytes_per_set: int) -> int:
+    return max(1, min(64, -(-ROTATION_BYTES // max(1, bytes_per_set))))
+
+
+def roofline(bytes_per_launch: int, ms_per_launch: float) -> dict:
+    achieved = bytes_per_launch / (ms_per_launch * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "algorithmic_bytes": int(bytes_per_launch)}
+
+
+def cpu_time(function, seconds: float) -> tuple[float, int]:
+    """Median seconds per call of `function` over about `seconds` of work (after 2 warmups)."""
+    for _ in range(2):
+        function()
+    samples = []
+    begin = time.perf_counter()
+    while len(samples) < 5 or (time.perf_counter() - begin < seconds and len(samples) < 1000):
+        t0 = time.perf_counter()
+        function()
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    return samples[len(samples) // 2], len(samples)
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+    import torch
+
+    from bysj_amd import kernels, workloads
+
+    base = workloads.segment_softmax_config(n_nodes=n_nodes, seed=0, device="cuda")
+    edges, channels = base["logit"].shape
+    offsets = base["offsets"]
+    bytes_per_step = 2 * edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + 2 * n_nodes * channels * 4
+    n_sets = n_sets_for(bytes_per_step)
+    sets = [base] + [workloads.segment_softmax_config(n_nodes=n_nodes, seed=s, device="cuda")
+                     for s in range(1, n_sets)]
+
+    def step(i):
+        case = sets[i]
+        return kernels.segment_softmax(case["logit"], case["env"], offsets, case["null_logit"])
+
+    with torch.no_grad():
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets,
+            "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
+
+
+def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+    import torch
+
+    from bysj_amd import kernels, workloads
+
+    base = workloads.segment_sum_config(n_nodes=n_nodes, seed=0, device="cuda")
+    edges, channels = base["src"].shape
+    bytes_per_step = edges * channels * 4 + (n_nodes + 1) * 8 + n_nodes * channels * 4
+    n_sets = n_sets_for(bytes_per_step)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(1)
+    sets = [base["src"]] + [torch.randn(base["src"].shape, generator=generator, device="cuda")
+                            for _ in range(1, n_sets)]
+
+    def step(i):
+        return kernels.segment_sum(sets[i], base["dst"], base["offsets"])
+
+    with torch.no_grad():
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets,
+            "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
+
+
+def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool):
+    import torch
+
+    from bysj_amd import workloads
+    from bysj_amd.kernels import _C
+
+    water = workloads.water_graph(n_atoms, seed=0)
+    case = workloads.gie_config(water, seed=0, device="cuda", primary=True)
+    edges = water.n_edges
+    offsets, order, _ = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, 16)
+
+    def gie_step(_):
+        return _C.gie_zonal_scatter_forward_csr(case["zonal"], case["radial"], offsets, order,
+                                                case["radial_slot"], case["inv_sqrt_deg"])
+
+    gie_bytes = edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 + n_atoms * 4 \
+        + n_atoms * 16 * 64 * 4
+    with torch.no_grad():
+        gie_ms = time_steps(gie_step, 1, max(4, steps // 10), min(warmup, 3), graph=graph)
+        rows = gie_step(0).reshape(n_atoms, 1024)
+    rms_bytes = 2 * n_atoms * 1024 * 4 + 1024 * 4 + n_atoms * 4
+    n_sets = n_sets_for(rms_bytes)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(3)
+    row_sets = [rows] + [torch.randn(rows.shape, generator=generator, device="cuda") for _ in range(1, n_sets)]
+
+    def rms_step(i):
+        return _C.rmsnorm_forward(row_sets[i], case["rms_scale"], 1e-6)
+
+    with torch.no_grad():
+        rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
+    gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_bytes, "sets": 1}
+    rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
+    return gie, rms, water, case
+
+
+def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: str, water=None):
+    import torch
+
+    from bysj_amd import kernels, workloads
+
+    dtype = torch.float32 if dtype_name == "f32" else torch.float64
+    water = water or workloads.water_graph(n_atoms, seed=0)
+    base = workloads.force_config(water, seed=0, device="cuda", dtype=dtype)
+    edges = water.n_edges
+    size = 4 if dtype == torch.float32 else 8
+    bytes_per_step = 2 * edges * 3 * size + edges * 8 + 2 * (n_atoms + 1) * 8 + n_atoms * 12 * size
+    n_sets = n_sets_for(bytes_per_step)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(5)
+    grads = [base["grad_edge"]] + [torch.randn(base["grad_edge"].shape, generator=generator, device="cuda",
+                                               dtype=dtype) for _ in range(1, n_sets)]
+
+    def step(i):
+        return kernels.force_assembly(grads[i], base["edge_vec"], base["src"], base["dst"], base["dst_offsets"],
+                                      base["src_offsets"], base["src_order"])
+
+    with torch.no_grad():
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    return {"edges": edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": bytes_per_step, "sets": n_sets,
+            "dtype": dtype_name}, water, base
+
+
+def op_line(name: str, job: dict, unit_count: int, unit: str = "edges/s") -> dict:
+    line = {"op": name, "value": round(unit_count / (job["ms_per_step"] * 1e-3), 1), "unit": unit,
+            "ms_per_step": round(job["ms_per_step"], 5), "input_sets": job.get("sets", 1),
+            "roofline": roofline(job["bytes"], job["ms_per_step"])}
+    for key in ("edges", "nodes", "channels", "rows", "width", "dtype"):
+        if key in job:
+            line[key] = job[key]
+    return line
+
+
+# ---------------------------------------------------------------------------
+# CPU baselines (the oracle on the host cores)
+# ---------------------------------------------------------------------------
+
+def cpu_baselines(softmax_case, seconds: float, extra_ops: dict | None) -> tuple[dict, dict]:
+    import torch
+
+    from oracle import segment as ref
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in softmax_case.items()}
+    per_call, samples = cpu_time(
+        lambda: ref.segment_softmax_reference(c["logit"], c["env"], c["dst"], c["offsets"], c["null_logit"]),
+        seconds,
+    )
+    edges = int(c["logit"].shape[0])
+    headline = {"value": round(edges / per_call, 1), "unit": "edges/s", "cores": threads, "kind": "port",
+                "sample": f"config 2 full input (E={edges}, C=8, null logit); median of {samples} calls of the "
+                          f"oracle ATen chain (torch CPU, {threads} threads)",
+                "ms_per_call": round(per_call * 1e3, 3)}
+    extras = {}
+    if extra_ops:
+        for name, (function, count, description) in extra_ops.items():
+            per, n = cpu_time(function, min(seconds, 5.0))
+            extras[name] = {"value": round(count / per, 1), "unit": "edges/s", "sample": description,
+                            "cores": threads, "ms_per_call": round(per * 1e3, 3), "calls": n}
+    return headline, extras
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(the operators shard by destination-node ranges; see DESIGN.md)", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a gfx950 GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    from bysj_amd import kernels
+
+    if not kernels.segment_available():
+        print("libdpa4k.so is not usable on this device (build it with __graft_entry__.build())", file=sys.stderr)
+        return 1
+    graph = not args.eager
+    print(f"[bench] headline: segment_softmax config 2, {args.steps} steps, {args.warmup} warmup", file=sys.stderr,
+          flush=True)
+    head = softmax_job(16384, args.steps, args.warmup, graph)
+    value = head["edges"] / (head["ms_per_step"] * 1e-3)
+    line = {
+        "metric": "segment-op edges/s + % HBM roofline (segment_softmax forward, config 2)",
+        "value": round(value, 1),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded; BASELINE.json config 2 generator)",
+        "config": {"workload": "segment_softmax_fwd_config2", "nodes": head["nodes"], "edges": head["edges"],
+                   "channels": head["channels"], "hub_fraction": 0.01, "hub_degree": 512, "null_logit": True,
+                   "input_sets": head["sets"], "timing": "hip-graph replay" if graph else "eager",
+                   "parallelism": "single-gpu"},
+        "roofline": roofline(head["bytes"], head["ms_per_step"]),
+    }
+    print(f"[bench] headline done: {head['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+
+    ops = {}
+    extra_cpu = {}
+    if not args.headline_only:
+        from oracle import gie as gie_ref
+        from oracle import segment as ref
+
+        steps = max(10, args.steps // 4)
+        warm = max(2, args.warmup // 4)
+        job = segment_sum_job(1024, steps, warm, graph)
+        ops["segment_sum_config1"] = op_line("segment_sum_fwd", job, job["edges"])
+        b = {k: (v.cpu() if v is not None else None) for k, v in job["base"].items()}
+        extra_cpu["segment_sum_config1"] = (
+            lambda b=b: ref.segment_sum_reference(b["src"], b["dst"], b["offsets"]), job["edges"],
+            "config 1 full input, oracle zeros->index_add_ chain")
+        print("[bench] segment_sum config 1 done", file=sys.stderr, flush=True)
+        gie, rms, water3, case3 = gie_rmsnorm_jobs(24576, steps, warm, graph)
+        ops["gie_config3"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
+        ops["rmsnorm_config3"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
+        sample_nodes = 2048
+        cut = int(water3.offsets()[sample_nodes])
+        sample = tuple(t.cpu() for t in (case3["zonal"][:cut], case3["radial"][:cut], case3["dst"][:cut],
+                                         case3["radial_slot"], case3["inv_sqrt_deg"][:sample_nodes]))
+        extra_cpu["gie_config3"] = (lambda s=sample: gie_ref.zonal_scatter_reference(*s), cut,
+                                    f"first {sample_nodes} atoms of config 3 ({cut} edges), oracle chain")
+        del case3
+        print("[bench] gie + rmsnorm config 3 done", file=sys.stderr, flush=True)
+        from bysj_amd import workloads
+
+        water4 = workloads.water_graph(65536, seed=0)
+        for dtype_name in ("f32", "f64"):
+            job, _, base = force_job(65536, steps, warm, graph, dtype_name, water=water4)
+            ops[f"force_assembly_config4_{dtype_name}"] = op_line("force_assembly", job, job["edges"])
+            bb = {k: v.cpu() for k, v in base.items()}
+            extra_cpu[f"force_assembly_config4_{dtype_name}"] = (
+                lambda bb=bb: ref.force_assembly_reference(bb["grad_edge"], bb["edge_vec"], bb["src"], bb["dst"],
+                                                           bb["dst_offsets"], bb["src_offsets"]),
+                job["edges"], f"config 4 full input ({dtype_name}), oracle two index_add_ + outer product")
+            print(f"[bench] force config 4 {dtype_name} done", file=sys.stderr, flush=True)
+        if args.roofline_shapes:
+            job = segment_sum_job(262144, steps, warm, graph)
+            ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])
+            job = softmax_job(210000, steps, warm, graph)
+            ops["segment_softmax_config2R"] = op_line("segment_softmax_fwd", job, job["edges"])
+            job, _, _ = force_job(131072, steps, warm, graph, "f32")
+            ops["force_assembly_config4R_f32"] = op_line("force_assembly", job, job["edges"])
+            print("[bench] roofline shapes done", file=sys.stderr, flush=True)
+        line["ops"] = ops
+
+    if args.calibrate_copy:
+        source = torch.ones(64 * 2**20, dtype=torch.float32, device="cuda")
+        target = torch.empty_like(source)
+        target.copy_(source)
+        torch.cuda.synchronize()
+        line["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4}
+
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        headline_cpu, extras = cpu_baselines(head["base"], args.cpu_seconds, extra_cpu)
+        line["cpu_baseline"] = headline_cpu
+        for name, result in extras.items():
+            if name in ops:
+                ops[name]["cpu_baseline"] = result
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,231 @@
+// Shared host/device helpers of libdpa4k (gfx950 / CDNA4, wave64).
+//
+// Host side: error plumbing for the C ABI (status codes + a thread-local
+// message) and workspace carving.  Device side: clamped CSR bounds and
+// cross-lane butterflies built from DPP (xor 1, 2), ds_swizzle bit mode
+// (xor 4, 8, 16) and ds_bpermute (xor 32).  The butterflies must be executed
+// with every lane of the group active; all callers keep them in code that is
+// uniform over the lane group.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/dpa4k.h"
+
+namespace dpa4k {
+
+// ---------------------------------------------------------------------------
+// Host: status plumbing
+// ---------------------------------------------------------------------------
+
+// Stores a printf-style message as the thread's last error and returns `code`.
+int fail(int code, const char* format, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks hipGetLastError() after a launch; DPA4K_EHIP with the kernel name on
+// failure, DPA4K_OK otherwise.
+int launched(const char* kernel);
+
+// Wraps a HIP runtime call result.
+int hip_status(hipError_t status, const char* what);
+
+// Clears the thread's last error (called on entry by every ABI function).
+void clear_error();
+
+inline hipStream_t as_stream(dpa4k_stream_t stream) {
+  return reinterpret_cast<hipStream_t>(stream);
+}
+
+inline bool aligned16(const void* pointer) {
+  return (reinterpret_cast<uintptr_t>(pointer) & 15u) == 0;
+}
+
+// Rounds a byte count up to the 256-byte granularity used for every carve.
+constexpr size_t round_up_256(size_t bytes) { return (bytes + 255u) & ~size_t(255u); }
+
+// Sequential bump allocator over a caller-provided workspace.
+struct Carver {
+  char* base;
+  size_t size;
+  size_t used = 0;
+  template <typename T>
+  T* take(size_t count) {
+    const size_t bytes = round_up_256(count * sizeof(T));
+    if (used + bytes > size) return nullptr;
+    T* out = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return out;
+  }
+};
+
+inline unsigned int blocks_for(int64_t items, int64_t per_block) {
+  return static_cast<unsigned int>((items + per_block - 1) / per_block);
+}
+
+// Grid-dimension ceiling of a 1-D launch on gfx950.
+constexpr int64_t kMaxGrid = 2147483647;
+
+// ---------------------------------------------------------------------------
+// Device: CSR bounds
+// ---------------------------------------------------------------------------
+
+// Segment [begin, end) of `segment`, clamped to [0, n_edges] so that a
+// malformed offsets array cannot send a kernel out of bounds.
+__device__ __forceinline__ void segment_bounds(const int64_t* __restrict__ offsets,
+                                               int64_t segment, int64_t n_edges,
+                                               int64_t& begin, int64_t& end) {
+  int64_t b = offsets[segment];
+  int64_t e = offsets[segment + 1];
+  b = b < 0 ? 0 : (b > n_edges ? n_edges : b);
+  e = e < b ? b : (e > n_edges ? n_edges : e);
+  begin = b;
+  end = e;
+}
+
+// Edge addressed by CSR slot `slot`; -1 when `order` holds an out-of-range
+// entry (the caller skips it).
+template <bool kOrdered>
+__device__ __forceinline__ int64_t edge_of(const int64_t* __restrict__ order,
+                                           int64_t slot, int64_t n_edges) {
+  if constexpr (!kOrdered) {
+    return slot;
+  } else {
+    const int64_t edge = order[slot];
+    return static_cast<uint64_t>(edge) < static_cast<uint64_t>(n_edges) ? edge : -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Device: cross-lane butterflies (lane ^ MASK within the wave)
+// ---------------------------------------------------------------------------
+
+template <int MASK>
+__device__ __forceinline__ int xor_lane(int value) {
+  static_assert(MASK >= 1 && MASK <= 32 && (MASK & (MASK - 1)) == 0, "power-of-two mask");
+  if constexpr (MASK == 1) {
+    // DPP quad_perm [1,0,3,2]
+    return __builtin_amdgcn_update_dpp(0, value, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (MASK == 2) {
+    // DPP quad_perm [2,3,0,1]
+    return __builtin_amdgcn_update_dpp(0, value, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (MASK < 32) {
+    // ds_swizzle bit mode inside each 32-lane half: and 0x1F, or 0, xor MASK
+    return __builtin_amdgcn_ds_swizzle(value, 0x1F | (MASK << 10));
+  } else {
+    // crosses the 32-lane halves: ds_bpermute
+    const int lane = __lane_id();
+    return __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, value);
+  }
+}
+
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float value) {
+  return __int_as_float(xor_lane<MASK>(__float_as_int(value)));
+}
+
+template <int MASK>
+__device__ __forceinline__ double xor_lane(double value) {
+  const int64_t bits = __double_as_longlong(value);
+  const int lo = xor_lane<MASK>(static_cast<int>(bits & 0xffffffffll));
+  const int hi = xor_lane<MASK>(static_cast<int>(bits >> 32));
+  return __longlong_as_double((static_cast<int64_t>(hi) << 32) |
+                              (static_cast<int64_t>(lo) & 0xffffffffll));
+}
+
+// Sum over the aligned group of GROUP lanes containing this lane (GROUP a
+// power of two <= 64); every lane of the group receives the total.  The
+// butterfly order is fixed, so the result is reproducible.
+template <int GROUP, typename T>
+__device__ __forceinline__ T group_sum(T value) {
+  if constexpr (GROUP >= 2) value += xor_lane<1>(value);
+  if constexpr (GROUP >= 4) value += xor_lane<2>(value);
+  if constexpr (GROUP >= 8) value += xor_lane<4>(value);
+  if constexpr (GROUP >= 16) value += xor_lane<8>(value);
+  if constexpr (GROUP >= 32) value += xor_lane<16>(value);
+  if constexpr (GROUP >= 64) value += xor_lane<32>(value);
+  return value;
+}
+
+template <int GROUP>
+__device__ __forceinline__ float group_max(float value) {
+  if constexpr (GROUP >= 2) value = fmaxf(value, xor_lane<1>(value));
+  if constexpr (GROUP >= 4) value = fmaxf(value, xor_lane<2>(value));
+  if constexpr (GROUP >= 8) value = fmaxf(value, xor_lane<4>(value));
+  if constexpr (GROUP >= 16) value = fmaxf(value, xor_lane<8>(value));
+  if constexpr (GROUP >= 32) value = fmaxf(value, xor_lane<16>(value));
+  if constexpr (GROUP >= 64) value = fmaxf(value, xor_lane<32>(value));
+  return value;
+}
+
+// Sum across lanes that differ only in the bits [FROM, 64) of the lane id
+// (i.e. across the 64/FROM sub-groups of FROM lanes); lanes keep their
+// position inside the sub-group.
+template <int FROM, typename T>
+__device__ __forceinline__ T across_sum(T value) {
+  if constexpr (FROM <= 1) value += xor_lane<1>(value);
+  if constexpr (FROM <= 2) value += xor_lane<2>(value);
+  if constexpr (FROM <= 4) value += xor_lane<4>(value);
+  if constexpr (FROM <= 8) value += xor_lane<8>(value);
+  if constexpr (FROM <= 16) value += xor_lane<16>(value);
+  if constexpr (FROM <= 32) value += xor_lane<32>(value);
+  return value;
+}
+
+template <int FROM>
+__device__ __forceinline__ float across_max(float value) {
+  if constexpr (FROM <= 1) value = fmaxf(value, xor_lane<1>(value));
+  if constexpr (FROM <= 2) value = fmaxf(value, xor_lane<2>(value));
+  if constexpr (FROM <= 4) value = fmaxf(value, xor_lane<4>(value));
+  if constexpr (FROM <= 8) value = fmaxf(value, xor_lane<8>(value));
+  if constexpr (FROM <= 16) value = fmaxf(value, xor_lane<16>(value));
+  if constexpr (FROM <= 32) value = fmaxf(value, xor_lane<32>(value));
+  return value;
+}
+
+// Plain vector of N floats with 16-byte (N == 4) or natural alignment.
+template <int N>
+struct alignas(N == 4 ? 16 : 4) fvec {
+  float v[N];
+};
+
+template <int N>
+__device__ __forceinline__ fvec<N> load_vec(const float* __restrict__ p) {
+  if constexpr (N == 4) {
+    const float4 raw = *reinterpret_cast<const float4*>(p);
+    return fvec<4>{{raw.x, raw.y, raw.z, raw.w}};
+  } else {
+    fvec<N> out;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out.v[i] = p[i];
+    return out;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_vec(float* __restrict__ p, const fvec<N>& value) {
+  if constexpr (N == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(value.v[0], value.v[1], value.v[2], value.v[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = value.v[i];
+  }
+}
+
+// Non-temporal variants for streams that are written once and not re-read by
+// the same kernel (outputs of [E, C] size).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+__device__ __forceinline__ void store_vec_stream(float* __restrict__ p, const fvec<N>& value) {
+  if constexpr (N == 4) {
+    f32x4 raw = {value.v[0], value.v[1], value.v[2], value.v[3]};
+    __builtin_nontemporal_store(raw, reinterpret_cast<f32x4*>(p));
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) __builtin_nontemporal_store(value.v[i], p + i);
+  }
+}
+
+}  // namespace dpa4k

@@ -1,0 +1,655 @@
+// GIE zonal scatter, forward and backward (python/kernels/gie.py:50-93,
+// csrc/gie.cpp:148-228 of the reference; arithmetic of the oracle
+// python/reference/gie.py:42-65):
+//   out[n, 0, :]   = 0 * inv[n]
+//   out[n, r+1, c] = inv[n] * sum_{dst(e)=n} zonal[e, r] * radial[e, slot[r], c]
+//
+// The reference scatters every (edge, row, channel) product with a float
+// atomic into a zero-filled output and rescales it in a second pass.  Here
+// the edges are grouped by destination first (csr.hip) and one wave owns one
+// node: lane l owns the output chunks q = l, l + 64, ... of rows 1..R
+// (chunk = 4 channels), walks the node's edges in CSR order and accumulates
+// each element sequentially (product rounded, then added), normalising once
+// after the sum.  The node's [R, C] accumulator never leaves registers, the
+// output is written once, and the result equals the sequential fp32 chain
+// `gather -> mul -> index_add_ -> mul` bit for bit.
+//
+// Backward is node-parallel as well.  It recomputes the unnormalised sum for
+// the inverse-degree gradient in the same pass that reads radial/zonal for
+// the zonal/radial gradients, so each edge row is read once.  With distinct
+// radial slots (each slot feeds at most one row) lanes own (slot, chunk)
+// pairs and everything stays in registers; shared slots (several rows
+// reading one slot, e.g. one radial channel per degree l) go through a
+// one-wave kernel that stages the per-row products in LDS and sums them per
+// slot in ascending row order.
+#include "common.h"
+
+namespace dpa4k {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+
+template <int V, int CPL, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_forward_kernel(
+    const float* __restrict__ zonal, const float* __restrict__ radial,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ order,
+    const int64_t* __restrict__ radial_slot, const float* __restrict__ inv,
+    float* __restrict__ out, int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+    int64_t channels, int64_t chunk_base) {
+  constexpr int U = CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
+  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (node >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t row_chunks = channels / V;
+  const int64_t chunks = n_rows * row_chunks;
+  const int64_t edge_stride = n_radial * channels;
+
+  int64_t zonal_col[CPL], radial_col[CPL], out_col[CPL];
+  bool live[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t q = chunk_base + lane + 64 * j;
+    const int64_t r = q / row_chunks;
+    const int64_t c = q - r * row_chunks;
+    int64_t slot = q < chunks ? radial_slot[r] : -1;
+    live[j] = static_cast<uint64_t>(slot) < static_cast<uint64_t>(n_radial);
+    zonal_col[j] = live[j] ? r : 0;
+    radial_col[j] = live[j] ? slot * channels + c * V : 0;
+    out_col[j] = (r + 1) * channels + c * V;
+    if (q >= chunks) out_col[j] = -1;
+  }
+
+  fvec<V> acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[j].v[i] = 0.0f;
+
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  int64_t slot = begin;
+  for (; slot + U <= end; slot += U) {
+    int64_t edge[U];
+    float z[U][CPL];
+    fvec<V> x[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) edge[u] = edge_of<kOrdered>(order, slot + u, n_edges);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (live[j] && (!kOrdered || edge[u] >= 0)) {
+          z[u][j] = zonal[edge[u] * n_rows + zonal_col[j]];
+          x[u][j] = load_vec<V>(radial + edge[u] * edge_stride + radial_col[j]);
+        } else {
+          z[u][j] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[u][j].v[i] = 0.0f;
+        }
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kOrdered && edge[u] < 0) continue;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + z[u][j] * x[u][j].v[i];
+    }
+  }
+  for (; slot < end; ++slot) {
+    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+    if (kOrdered && e < 0) continue;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (!live[j]) continue;
+      const float zv = zonal[e * n_rows + zonal_col[j]];
+      const fvec<V> xv = load_vec<V>(radial + e * edge_stride + radial_col[j]);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + zv * xv.v[i];
+    }
+  }
+
+  const float scale = inv[node];
+  float* node_out = out + node * (n_rows + 1) * channels;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    if (out_col[j] < 0) continue;
+    fvec<V> result;
+#pragma unroll
+    for (int i = 0; i < V; ++i) result.v[i] = acc[j].v[i] * scale;
+    store_vec<V>(node_out + out_col[j], result);
+  }
+  if (chunk_base == 0) {
+    fvec<V> zero;
+#pragma unroll
+    for (int i = 0; i < V; ++i) zero.v[i] = 0.0f * scale;
+    for (int64_t c = lane; c < row_chunks; c += 64) store_vec<V>(node_out + c * V, zero);
+  }
+}
+
+// Distinct slots: lane owns (slot s, chunk c) pairs q = s * row_chunks + c of
+// one edge's radial block; RC = row_chunks lanes share a slot (power of two).
+template <int V, int CPL, int RC, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
+    const float* __restrict__ grad_output, const float* __restrict__ zonal,
+    const float* __restrict__ radial, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ order, const int64_t* __restrict__ radial_slot,
+    const float* __restrict__ inv, float* __restrict__ grad_zonal, float* __restrict__ grad_radial,
+    float* __restrict__ grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+    int64_t n_radial, int64_t channels) {
+  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (node >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t chunks = n_radial * RC;
+  const int64_t edge_stride = n_radial * channels;
+  const float scale = inv[node];
+
+  int64_t row[CPL], radial_col[CPL];
+  bool in_range[CPL];
+  fvec<V> g[CPL], h[CPL], pre[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t q = lane + 64 * j;
+    const int64_t s = q / RC;
+    const int64_t c = q % RC;
+    in_range[j] = q < chunks;
+    int64_t r = -1;
+    if (in_range[j])
+      for (int64_t k = 0; k < n_rows; ++k)
+        if (radial_slot[k] == s) r = k;
+    row[j] = r;
+    radial_col[j] = s * channels + c * V;
+    if (r >= 0) {
+      g[j] = load_vec<V>(grad_output + (node * (n_rows + 1) + r + 1) * channels + c * V);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) g[j].v[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      h[j].v[i] = g[j].v[i] * scale;
+      pre[j].v[i] = 0.0f;
+    }
+  }
+
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  for (int64_t slot = begin; slot < end; ++slot) {
+    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+    if (kOrdered && e < 0) continue;
+    fvec<V> x[CPL];
+    float z[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (row[j] >= 0) {
+        x[j] = load_vec<V>(radial + e * edge_stride + radial_col[j]);
+        z[j] = zonal[e * n_rows + row[j]];
+      } else {
+        z[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) x[j].v[i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float dot = 0.0f;
+      fvec<V> out;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        pre[j].v[i] = pre[j].v[i] + z[j] * x[j].v[i];
+        dot = dot + h[j].v[i] * x[j].v[i];
+        out.v[i] = h[j].v[i] * z[j];
+      }
+      dot = group_sum<RC>(dot);
+      if (in_range[j]) {
+        if (grad_radial != nullptr) store_vec_stream<V>(grad_radial + e * edge_stride + radial_col[j], out);
+        if (grad_zonal != nullptr && row[j] >= 0 && (lane % RC) == 0)
+          grad_zonal[e * n_rows + row[j]] = dot;
+      }
+    }
+  }
+  if (grad_inv != nullptr) {
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < V; ++i) total = total + g[j].v[i] * pre[j].v[i];
+    total = group_sum<64>(total);
+    if (lane == 0) grad_inv[node] = total;
+  }
+}
+
+// General slot map: one wave per block.  Read chunks q = r * wc + c over
+// rows x window chunks, write chunks t = s * wc + c over slots x window
+// chunks.  LDS holds, per edge, the dot partials and the products
+// h[r, c] * zonal[e, r]; the per-slot row lists are built once per block.
+template <int V, int CPL>
+__global__ __launch_bounds__(64) void gie_backward_general_kernel(
+    const float* __restrict__ grad_output, const float* __restrict__ zonal,
+    const float* __restrict__ radial, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ order, const int64_t* __restrict__ radial_slot,
+    const float* __restrict__ inv, float* __restrict__ grad_zonal, float* __restrict__ grad_radial,
+    float* __restrict__ grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+    int64_t n_radial, int64_t channels, int64_t window_base, int64_t window_chunks) {
+  extern __shared__ float lds[];
+  // Layout: dot[64*CPL] | product[64*CPL*V] | slot_begin[n_radial+1] | slot_rows[n_rows]
+  float* dot_part = lds;
+  float* product = lds + 64 * CPL;
+  int* slot_begin = reinterpret_cast<int*>(product + 64 * CPL * V);
+  int* slot_rows = slot_begin + n_radial + 1;
+
+  const int64_t node = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t wc = window_chunks;
+  const bool ordered = order != nullptr;
+  const int64_t edge_stride = n_radial * channels;
+  const bool first_window = window_base == 0;
+
+  if (lane == 0) {
+    int cursor = 0;
+    for (int64_t s = 0; s < n_radial; ++s) {
+      slot_begin[s] = cursor;
+      for (int64_t r = 0; r < n_rows; ++r)
+        if (radial_slot[r] == s) slot_rows[cursor++] = static_cast<int>(r);
+    }
+    slot_begin[n_radial] = cursor;
+  }
+  __syncthreads();
+
+  const float scale = inv[node];
+  const int64_t read_chunks = n_rows * wc;
+  const int64_t write_chunks = n_radial * wc;
+  int64_t rrow[CPL], rcol[CPL], slotcol[CPL];
+  bool rlive[CPL];
+  fvec<V> g[CPL], h[CPL], pre[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t q = lane + 64 * j;
+    const int64_t r = q / wc;
+    const int64_t c = q - r * wc;
+    rlive[j] = q < read_chunks;
+    const int64_t s = rlive[j] ? radial_slot[r] : 0;
+    rlive[j] = rlive[j] && static_cast<uint64_t>(s) < static_cast<uint64_t>(n_radial);
+    rrow[j] = r;
+    rcol[j] = window_base + c * V;
+    slotcol[j] = s * channels + window_base + c * V;
+    if (rlive[j]) {
+      g[j] = load_vec<V>(grad_output + (node * (n_rows + 1) + r + 1) * channels + rcol[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) g[j].v[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      h[j].v[i] = g[j].v[i] * scale;
+      pre[j].v[i] = 0.0f;
+    }
+  }
+
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  for (int64_t slot = begin; slot < end; ++slot) {
+    const int64_t e = ordered ? edge_of<true>(order, slot, n_edges) : slot;
+    if (e < 0) continue;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float dot = 0.0f;
+      fvec<V> u;
+      if (rlive[j]) {
+        const fvec<V> x = load_vec<V>(radial + e * edge_stride + slotcol[j]);
+        const float z = zonal[e * n_rows + rrow[j]];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          pre[j].v[i] = pre[j].v[i] + z * x.v[i];
+          dot = dot + h[j].v[i] * x.v[i];
+          u.v[i] = h[j].v[i] * z;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) u.v[i] = 0.0f;
+      }
+      dot_part[lane + 64 * j] = dot;
+#pragma unroll
+      for (int i = 0; i < V; ++i) product[(lane + 64 * j) * V + i] = u.v[i];
+    }
+    __syncthreads();
+    if (grad_zonal != nullptr)
+      for (int64_t r = lane; r < n_rows; r += 64) {
+        float sum = first_window ? 0.0f : grad_zonal[e * n_rows + r];
+        for (int64_t c = 0; c < wc; ++c) sum = sum + dot_part[r * wc + c];
+        grad_zonal[e * n_rows + r] = sum;
+      }
+    if (grad_radial != nullptr)
+      for (int64_t t = lane; t < write_chunks; t += 64) {
+        const int64_t s = t / wc;
+        const int64_t c = t - s * wc;
+        fvec<V> sum;
+#pragma unroll
+        for (int i = 0; i < V; ++i) sum.v[i] = 0.0f;
+        for (int k = slot_begin[s]; k < slot_begin[s + 1]; ++k) {
+          const int64_t q = static_cast<int64_t>(slot_rows[k]) * wc + c;
+#pragma unroll
+          for (int i = 0; i < V; ++i) sum.v[i] = sum.v[i] + product[q * V + i];
+        }
+        store_vec<V>(grad_radial + e * edge_stride + s * channels + window_base + c * V, sum);
+      }
+    __syncthreads();
+  }
+  if (grad_inv != nullptr) {
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < V; ++i) total = total + g[j].v[i] * pre[j].v[i];
+    total = group_sum<64>(total);
+    if (lane == 0) grad_inv[node] = first_window ? total : grad_inv[node] + total;
+  }
+}
+
+int per_lane_for(int64_t chunks) {
+  int cpl = 1;
+  while (cpl < 8 && 64 * cpl < chunks) cpl <<= 1;
+  return cpl;
+}
+
+template <int V, bool kOrdered>
+int launch_forward(int cpl, const float* zonal, const float* radial, const int64_t* offsets,
+                   const int64_t* order, const int64_t* radial_slot, const float* inv, float* out,
+                   int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+                   int64_t channels, int64_t base, hipStream_t stream) {
+  const unsigned int grid = blocks_for(n_nodes, kWaves);
+#define DPA4K_GIE_FWD(C)                                                                      \
+  gie_forward_kernel<V, C, kOrdered><<<grid, kBlock, 0, stream>>>(                           \
+      zonal, radial, offsets, order, radial_slot, inv, out, n_edges, n_nodes, n_rows, n_radial, \
+      channels, base)
+  switch (cpl) {
+    case 1: DPA4K_GIE_FWD(1); break;
+    case 2: DPA4K_GIE_FWD(2); break;
+    case 4: DPA4K_GIE_FWD(4); break;
+    default: DPA4K_GIE_FWD(8); break;
+  }
+#undef DPA4K_GIE_FWD
+  return launched("gie_forward_kernel");
+}
+
+template <int V, int RC, bool kOrdered>
+int launch_distinct(int cpl, const float* grad_output, const float* zonal, const float* radial,
+                    const int64_t* offsets, const int64_t* order, const int64_t* radial_slot,
+                    const float* inv, float* grad_zonal, float* grad_radial, float* grad_inv,
+                    int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+                    int64_t channels, hipStream_t stream) {
+  const unsigned int grid = blocks_for(n_nodes, kWaves);
+#define DPA4K_GIE_DIST(C)                                                                     \
+  gie_backward_distinct_kernel<V, C, RC, kOrdered><<<grid, kBlock, 0, stream>>>(             \
+      grad_output, zonal, radial, offsets, order, radial_slot, inv, grad_zonal, grad_radial,  \
+      grad_inv, n_edges, n_nodes, n_rows, n_radial, channels)
+  switch (cpl) {
+    case 1: DPA4K_GIE_DIST(1); break;
+    case 2: DPA4K_GIE_DIST(2); break;
+    case 4: DPA4K_GIE_DIST(4); break;
+    default: DPA4K_GIE_DIST(8); break;
+  }
+#undef DPA4K_GIE_DIST
+  return launched("gie_backward_distinct_kernel");
+}
+
+template <int V, bool kOrdered>
+int dispatch_distinct(int64_t row_chunks, int cpl, const float* grad_output, const float* zonal,
+                      const float* radial, const int64_t* offsets, const int64_t* order,
+                      const int64_t* radial_slot, const float* inv, float* grad_zonal,
+                      float* grad_radial, float* grad_inv, int64_t n_edges, int64_t n_nodes,
+                      int64_t n_rows, int64_t n_radial, int64_t channels, hipStream_t stream) {
+#define DPA4K_GIE_RC(RCV)                                                                    \
+  return launch_distinct<V, RCV, kOrdered>(cpl, grad_output, zonal, radial, offsets, order,  \
+                                           radial_slot, inv, grad_zonal, grad_radial,        \
+                                           grad_inv, n_edges, n_nodes, n_rows, n_radial,     \
+                                           channels, stream)
+  switch (row_chunks) {
+    case 1: DPA4K_GIE_RC(1);
+    case 2: DPA4K_GIE_RC(2);
+    case 4: DPA4K_GIE_RC(4);
+    case 8: DPA4K_GIE_RC(8);
+    case 16: DPA4K_GIE_RC(16);
+    case 32: DPA4K_GIE_RC(32);
+    default: DPA4K_GIE_RC(64);
+  }
+#undef DPA4K_GIE_RC
+}
+
+template <int V>
+int launch_general(int cpl, size_t lds_bytes, const float* grad_output, const float* zonal,
+                   const float* radial, const int64_t* offsets, const int64_t* order,
+                   const int64_t* radial_slot, const float* inv, float* grad_zonal,
+                   float* grad_radial, float* grad_inv, int64_t n_edges, int64_t n_nodes,
+                   int64_t n_rows, int64_t n_radial, int64_t channels, int64_t base, int64_t wc,
+                   hipStream_t stream) {
+#define DPA4K_GIE_GEN(C)                                                                      \
+  gie_backward_general_kernel<V, C><<<static_cast<unsigned int>(n_nodes), 64, lds_bytes,      \
+                                      stream>>>(grad_output, zonal, radial, offsets, order,   \
+                                                radial_slot, inv, grad_zonal, grad_radial,    \
+                                                grad_inv, n_edges, n_nodes, n_rows, n_radial, \
+                                                channels, base, wc)
+  switch (cpl) {
+    case 1: DPA4K_GIE_GEN(1); break;
+    case 2: DPA4K_GIE_GEN(2); break;
+    case 4: DPA4K_GIE_GEN(4); break;
+    default: DPA4K_GIE_GEN(8); break;
+  }
+#undef DPA4K_GIE_GEN
+  return launched("gie_backward_general_kernel");
+}
+
+int check_shapes(int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+                 int64_t channels, const char* what) {
+  if (n_edges < 0 || n_nodes < 0 || n_rows < 0 || n_radial < 0 || channels < 0)
+    return fail(DPA4K_EINVAL, "%s: negative sizes", what);
+  if (n_rows > 0 && n_radial == 0)
+    return fail(DPA4K_EINVAL, "GIE radial slots are required for non-scalar rows");
+  if (n_edges > 0 && n_nodes == 0) return fail(DPA4K_EINVAL, "GIE edges require destination nodes");
+  if (n_nodes > kMaxGrid) return fail(DPA4K_EINVAL, "GIE node count exceeds the HIP grid limit");
+  return DPA4K_OK;
+}
+
+}  // namespace
+}  // namespace dpa4k
+
+using namespace dpa4k;
+
+extern "C" int dpa4k_gie_zonal_scatter_forward_csr(
+    const float* zonal, const float* radial, const int64_t* offsets, const int64_t* order,
+    const int64_t* radial_slot, const float* inv_sqrt_deg, float* out, int64_t n_edges,
+    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels,
+    dpa4k_stream_t stream_handle) {
+  clear_error();
+  if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE forward")) return s;
+  if (n_nodes == 0 || channels == 0) return DPA4K_OK;
+  if (offsets == nullptr || inv_sqrt_deg == nullptr || out == nullptr ||
+      (n_rows > 0 && radial_slot == nullptr) ||
+      (n_edges > 0 && n_rows > 0 && (zonal == nullptr || radial == nullptr)))
+    return fail(DPA4K_EINVAL, "GIE forward: null pointer");
+  hipStream_t stream = as_stream(stream_handle);
+  const bool vec4 = channels % 4 == 0 && aligned16(radial) && aligned16(out);
+  const int64_t row_chunks = vec4 ? channels / 4 : channels;
+  const int64_t chunks = n_rows * row_chunks;
+  const int cpl = per_lane_for(chunks);
+  const int64_t window = 64 * static_cast<int64_t>(cpl);
+  int64_t base = 0;
+  do {
+    int status;
+    if (vec4)
+      status = order != nullptr
+                   ? launch_forward<4, true>(cpl, zonal, radial, offsets, order, radial_slot,
+                                             inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial,
+                                             channels, base, stream)
+                   : launch_forward<4, false>(cpl, zonal, radial, offsets, order, radial_slot,
+                                              inv_sqrt_deg, out, n_edges, n_nodes, n_rows,
+                                              n_radial, channels, base, stream);
+    else
+      status = order != nullptr
+                   ? launch_forward<1, true>(cpl, zonal, radial, offsets, order, radial_slot,
+                                             inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial,
+                                             channels, base, stream)
+                   : launch_forward<1, false>(cpl, zonal, radial, offsets, order, radial_slot,
+                                              inv_sqrt_deg, out, n_edges, n_nodes, n_rows,
+                                              n_radial, channels, base, stream);
+    if (status) return status;
+    base += window;
+  } while (base < chunks);
+  return DPA4K_OK;
+}
+
+extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
+    const float* grad_output, const float* zonal, const float* radial, const int64_t* offsets,
+    const int64_t* order, const int64_t* radial_slot, const float* inv_sqrt_deg,
+    float* grad_zonal, float* grad_radial, float* grad_inv_sqrt_deg, int64_t n_edges,
+    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels, int slots_distinct,
+    dpa4k_stream_t stream_handle) {
+  clear_error();
+  if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE backward")) return s;
+  if (n_nodes == 0) return DPA4K_OK;
+  if (offsets == nullptr || inv_sqrt_deg == nullptr || grad_output == nullptr ||
+      (n_rows > 0 && radial_slot == nullptr) ||
+      (n_edges > 0 && (zonal == nullptr || radial == nullptr)))
+    return fail(DPA4K_EINVAL, "GIE backward: null pointer");
+  hipStream_t stream = as_stream(stream_handle);
+  if (n_rows == 0 || channels == 0 || n_radial == 0) {
+    // Nothing flows back: zero every requested output.
+    if (grad_zonal != nullptr && n_edges * n_rows > 0)
+      if (int s = hip_status(hipMemsetAsync(grad_zonal, 0, n_edges * n_rows * 4, stream), "hipMemsetAsync"))
+        return s;
+    if (grad_radial != nullptr && n_edges * n_radial * channels > 0)
+      if (int s = hip_status(hipMemsetAsync(grad_radial, 0, n_edges * n_radial * channels * 4, stream),
+                             "hipMemsetAsync"))
+        return s;
+    if (grad_inv_sqrt_deg != nullptr)
+      if (int s = hip_status(hipMemsetAsync(grad_inv_sqrt_deg, 0, n_nodes * 4, stream), "hipMemsetAsync"))
+        return s;
+    return DPA4K_OK;
+  }
+  const bool vec4 = channels % 4 == 0 && aligned16(radial) && aligned16(grad_output) &&
+                    (grad_radial == nullptr || aligned16(grad_radial));
+  const int64_t row_chunks = vec4 ? channels / 4 : channels;
+  // Register-only path: distinct slots, a power-of-two chunk count per row
+  // and the whole radial block of an edge within 8 chunks per lane.
+  const bool pow2 = row_chunks <= 64 && (row_chunks & (row_chunks - 1)) == 0;
+  if (slots_distinct && pow2 && n_radial * row_chunks <= 512) {
+    const int cpl = per_lane_for(n_radial * row_chunks);
+    if (vec4)
+      return order != nullptr
+                 ? dispatch_distinct<4, true>(row_chunks, cpl, grad_output, zonal, radial, offsets,
+                                              order, radial_slot, inv_sqrt_deg, grad_zonal,
+                                              grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes,
+                                              n_rows, n_radial, channels, stream)
+                 : dispatch_distinct<4, false>(row_chunks, cpl, grad_output, zonal, radial,
+                                               offsets, order, radial_slot, inv_sqrt_deg,
+                                               grad_zonal, grad_radial, grad_inv_sqrt_deg, n_edges,
+                                               n_nodes, n_rows, n_radial, channels, stream);
+    return order != nullptr
+               ? dispatch_distinct<1, true>(row_chunks, cpl, grad_output, zonal, radial, offsets,
+                                            order, radial_slot, inv_sqrt_deg, grad_zonal,
+                                            grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes,
+                                            n_rows, n_radial, channels, stream)
+               : dispatch_distinct<1, false>(row_chunks, cpl, grad_output, zonal, radial, offsets,
+                                             order, radial_slot, inv_sqrt_deg, grad_zonal,
+                                             grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes,
+                                             n_rows, n_radial, channels, stream);
+  }
+  // General path: split the channels into windows of wc chunks so that both
+  // rows x wc and slots x wc fit in 8 chunks per lane.
+  const int64_t widest = n_rows > n_radial ? n_rows : n_radial;
+  if (widest > 512)
+    return fail(DPA4K_EINVAL, "GIE backward supports at most 512 rows and radial slots");
+  int64_t wc = 512 / widest;
+  if (wc > row_chunks) wc = row_chunks;
+  const int cpl = per_lane_for((n_rows > n_radial ? n_rows : n_radial) * wc);
+  const int vw = vec4 ? 4 : 1;
+  const size_t lds_bytes = sizeof(float) * (64 * cpl + 64 * cpl * vw) +
+                           sizeof(int) * static_cast<size_t>(n_radial + 1 + n_rows);
+  if (lds_bytes > 64 * 1024) return fail(DPA4K_EINVAL, "GIE backward: slot map too large");
+  for (int64_t c0 = 0; c0 < row_chunks; c0 += wc) {
+    const int64_t this_wc = row_chunks - c0 < wc ? row_chunks - c0 : wc;
+    const int status =
+        vec4 ? launch_general<4>(cpl, lds_bytes, grad_output, zonal, radial, offsets, order,
+                                 radial_slot, inv_sqrt_deg, grad_zonal, grad_radial,
+                                 grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
+                                 c0 * 4, this_wc, stream)
+             : launch_general<1>(cpl, lds_bytes, grad_output, zonal, radial, offsets, order,
+                                 radial_slot, inv_sqrt_deg, grad_zonal, grad_radial,
+                                 grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
+                                 c0, this_wc, stream);
+    if (status) return status;
+  }
+  return DPA4K_OK;
+}
+
+extern "C" size_t dpa4k_gie_workspace_size(int64_t n_edges, int64_t n_nodes) {
+  if (n_nodes <= 0) return 0;
+  return round_up_256(static_cast<size_t>(n_nodes + 1) * 8) +
+         round_up_256(static_cast<size_t>(n_edges > 0 ? n_edges : 1) * 8) +
+         dpa4k_gie_group_workspace_size(n_edges, n_nodes);
+}
+
+namespace {
+struct GroupedCsr {
+  int64_t* offsets;
+  int64_t* order;  // NULL when dst is already grouped
+  int info;
+};
+
+int group_into(const int64_t* dst, const int64_t* radial_slot, int64_t n_edges, int64_t n_nodes,
+               int64_t n_rows, int64_t n_radial, void* workspace, size_t workspace_bytes,
+               dpa4k_stream_t stream, GroupedCsr& out) {
+  const size_t needed = dpa4k_gie_workspace_size(n_edges, n_nodes);
+  if (workspace == nullptr || workspace_bytes < needed)
+    return fail(DPA4K_EWORKSPACE, "GIE: workspace of %zu bytes is smaller than %zu", workspace_bytes,
+                needed);
+  Carver carver{static_cast<char*>(workspace), workspace_bytes};
+  out.offsets = carver.take<int64_t>(static_cast<size_t>(n_nodes + 1));
+  int64_t* order = carver.take<int64_t>(static_cast<size_t>(n_edges > 0 ? n_edges : 1));
+  void* rest = static_cast<char*>(workspace) + carver.used;
+  int32_t info = 0;
+  if (int s = dpa4k_gie_group(dst, radial_slot, n_edges, n_nodes, n_rows, n_radial, out.offsets,
+                              order, &info, rest, workspace_bytes - carver.used, stream))
+    return s;
+  out.order = (info & 1) ? nullptr : order;
+  out.info = info;
+  return DPA4K_OK;
+}
+}  // namespace
+
+extern "C" int dpa4k_gie_zonal_scatter_forward(const float* zonal, const float* radial,
+                                               const int64_t* dst, const int64_t* radial_slot,
+                                               const float* inv_sqrt_deg, float* out,
+                                               int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+                                               int64_t n_radial, int64_t channels, void* workspace,
+                                               size_t workspace_bytes, dpa4k_stream_t stream) {
+  clear_error();
+  if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE forward")) return s;
+  if (n_nodes == 0) return DPA4K_OK;
+  GroupedCsr csr{};
+  if (int s = group_into(dst, radial_slot, n_edges, n_nodes, n_rows, n_radial, workspace,
+                         workspace_bytes, stream, csr))
+    return s;
+  return dpa4k_gie_zonal_scatter_forward_csr(zonal, radial, csr.offsets, csr.order, radial_slot,
+                                             inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial,
+                                             channels, stream);
+}
+
+extern "C" int dpa4k_gie_zonal_scatter_backward(
+    const float* grad_output, const float* zonal, const float* radial, const int64_t* dst,
+    const int64_t* radial_slot, const float* inv_sqrt_deg, float* grad_zonal, float* grad_radial,
+    float* grad_inv_sqrt_deg, int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+    int64_t channels, void* workspace, size_t workspace_bytes, dpa4k_stream_t stream) {
+  clear_error();
+  if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE backward")) return s;
+  if (n_nodes == 0) return DPA4K_OK;
+  GroupedCsr csr{};
+  if (int s = group_into(dst, radial_slot, n_edges, n_nodes, n_rows, n_radial, workspace,
+                         workspace_bytes, stream, csr))
+    return s;
+  return dpa4k_gie_zonal_scatter_backward_csr(
+      grad_output, zonal, radial, csr.offsets, csr.order, radial_slot, inv_sqrt_deg, grad_zonal,
+      grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
+      (csr.info & 2) ? 1 : 0, stream);
+}

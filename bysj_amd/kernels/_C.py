@@ -1,0 +1,472 @@
+"""Native entry points of the operator slice over the libdpa4k C ABI.
+
+This module takes the place of the reference's pybind module ``kernels._C``
+(csrc/bindings.cpp:6-29): the same nine symbols with the same positional and
+keyword arguments, returning the same tuples.  Each entry point re-checks its
+tensors the way the reference's ``TORCH_CHECK`` host launchers do (raising
+``RuntimeError``), allocates the outputs and any workspace with torch on the
+tensors' device, and enqueues the HIP kernels on the current torch stream
+through ctypes.  There is no CPU path: importing this module fails when
+libdpa4k.so has not been built.
+
+Extensions over the reference, all keyword-only or additional symbols:
+``segment_sum_backward(..., want_edge_scale_grad=True)`` returns a third
+tensor, the ``edge_scale`` gradient; ``force_assembly`` also takes float64
+inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
+``*_csr`` GIE entry points expose the device-side CSR construction.
+"""
+from __future__ import annotations
+
+import contextlib
+
+import torch
+
+from .. import _lib
+
+_LIB = _lib.load()
+
+
+# ---------------------------------------------------------------------------
+# checks (restating csrc/checks.h:6-20 and the per-op TORCH_CHECKs)
+# ---------------------------------------------------------------------------
+
+def _check(condition: bool, message: str) -> None:
+    if not condition:
+        raise RuntimeError(message)
+
+
+def _f32(tensor, what: str) -> None:
+    _check(
+        isinstance(tensor, torch.Tensor)
+        and tensor.is_cuda
+        and tensor.dtype == torch.float32
+        and tensor.is_contiguous(),
+        f"{what}: expected a contiguous gfx950 float32 tensor",
+    )
+
+
+def _i64(tensor, what: str) -> None:
+    _check(
+        isinstance(tensor, torch.Tensor)
+        and tensor.is_cuda
+        and tensor.dtype == torch.int64
+        and tensor.is_contiguous(),
+        f"{what} must be a contiguous gfx950 int64 tensor",
+    )
+
+
+def _offsets(tensor, what: str) -> int:
+    _i64(tensor, what)
+    _check(tensor.dim() == 1 and tensor.numel() >= 1, f"{what} must be a one-dimensional exclusive prefix sum")
+    return int(tensor.numel()) - 1
+
+
+def _order(order, edges: int, what: str) -> None:
+    if order is None:
+        return
+    _i64(order, f"{what} order")
+    _check(order.dim() == 1 and order.numel() == edges, f"{what} order must have shape (n_edges,)")
+
+
+def _same_device(reference: torch.Tensor, *others) -> None:
+    for other in others:
+        if other is not None:
+            _check(other.device == reference.device, "all tensors must share a device")
+
+
+def _ptr(tensor):
+    return None if tensor is None or tensor.numel() == 0 else tensor.data_ptr()
+
+
+@contextlib.contextmanager
+def _on(device: torch.device):
+    """Make `device` current for the launch (the reference's CUDAGuard)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        yield torch.cuda.current_stream(device).cuda_stream
+        return
+    with torch.cuda.device(device):
+        yield torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# CSR construction (python/kernels/segment.py:46-71)
+# ---------------------------------------------------------------------------
+
+def segment_offsets(keys: torch.Tensor, n_nodes: int) -> torch.Tensor:
+    """``[0] ++ cumsum(bincount(keys, minlength=n_nodes))``; ValueError on out-of-range keys."""
+    _i64(keys, "segment offsets keys")
+    _check(keys.dim() == 1, "segment offsets keys must be one-dimensional")
+    n_nodes = int(n_nodes)
+    offsets = torch.empty(n_nodes + 1, dtype=torch.int64, device=keys.device)
+    nbytes = _LIB.dpa4k_segment_offsets_workspace_size(keys.numel(), n_nodes)
+    workspace = _workspace(nbytes, keys.device)
+    with _on(keys.device) as stream:
+        status = _LIB.dpa4k_segment_offsets(
+            _ptr(keys), keys.numel(), n_nodes, offsets.data_ptr(), workspace.data_ptr(), nbytes, stream
+        )
+    _lib.check(status, index_error=True)
+    return offsets
+
+
+def group_by_key(keys: torch.Tensor, n_nodes: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(stable argsort(keys), segment_offsets(keys))``; ValueError on out-of-range keys."""
+    _i64(keys, "group_by_source keys")
+    _check(keys.dim() == 1, "group_by_source keys must be one-dimensional")
+    n_nodes = int(n_nodes)
+    edges = keys.numel()
+    order = torch.empty(edges, dtype=torch.int64, device=keys.device)
+    offsets = torch.empty(n_nodes + 1, dtype=torch.int64, device=keys.device)
+    nbytes = _LIB.dpa4k_group_by_key_workspace_size(edges, n_nodes)
+    workspace = _workspace(nbytes, keys.device)
+    with _on(keys.device) as stream:
+        status = _LIB.dpa4k_group_by_key(
+            _ptr(keys), edges, n_nodes, _ptr(order), offsets.data_ptr(), workspace.data_ptr(), nbytes, stream
+        )
+    _lib.check(status, index_error=True)
+    return order, offsets
+
+
+# ---------------------------------------------------------------------------
+# segment_sum (csrc/segment_sum.cpp:214, :271)
+# ---------------------------------------------------------------------------
+
+def _segment_sum_checks(src, offsets, edge_scale, node_scale, order):
+    _f32(src, "segment sum src")
+    _check(src.dim() == 2, "segment sum src must have shape (n_edges, channels)")
+    edges, channels = int(src.shape[0]), int(src.shape[1])
+    _check(channels > 0, "segment sum requires at least one channel")
+    nodes = _offsets(offsets, "segment sum offsets")
+    if edge_scale is not None:
+        _f32(edge_scale, "segment sum edge_scale")
+        _check(edge_scale.dim() == 1 and edge_scale.numel() == edges,
+               "segment sum edge_scale must have shape (n_edges,)")
+    if node_scale is not None:
+        _f32(node_scale, "segment sum node_scale")
+        _check(node_scale.numel() == nodes, "segment sum node_scale must have one value per segment")
+    _order(order, edges, "segment sum")
+    _same_device(src, offsets, edge_scale, node_scale, order)
+    return edges, nodes, channels
+
+
+def segment_sum_forward(src, offsets, edge_scale=None, node_scale=None, order=None):
+    edges, nodes, channels = _segment_sum_checks(src, offsets, edge_scale, node_scale, order)
+    out = torch.empty((nodes, channels), dtype=torch.float32, device=src.device)
+    if nodes == 0:
+        return out
+    with _on(src.device) as stream:
+        status = _LIB.dpa4k_segment_sum_forward(
+            _ptr(src), offsets.data_ptr(), _ptr(edge_scale), _ptr(node_scale), _ptr(order),
+            out.data_ptr(), edges, nodes, channels, stream,
+        )
+    _lib.check(status)
+    return out
+
+
+def segment_sum_backward(grad_out, src, dst, offsets, edge_scale=None, node_scale=None,
+                         want_node_scale_grad=False, order=None, *, want_edge_scale_grad=False):
+    edges, nodes, channels = _segment_sum_checks(src, offsets, edge_scale, node_scale, order)
+    _f32(grad_out, "segment sum grad_out")
+    _check(grad_out.dim() == 2 and tuple(grad_out.shape) == (nodes, channels),
+           "segment sum grad_out must have shape (n_nodes, channels)")
+    _i64(dst, "segment sum dst")
+    _check(dst.dim() == 1 and dst.numel() == edges, f"segment sum dst must have shape ({edges},)")
+    _same_device(src, grad_out, dst)
+    grad_src = torch.empty_like(src)
+    node_grad = want_node_scale_grad and node_scale is not None
+    edge_grad = want_edge_scale_grad and edge_scale is not None
+    grad_node_scale = torch.empty_like(node_scale) if node_grad else None
+    grad_edge_scale = torch.empty_like(edge_scale) if edge_grad else None
+    if nodes > 0 and (edges > 0 or node_grad):
+        with _on(src.device) as stream:
+            status = _LIB.dpa4k_segment_sum_backward(
+                grad_out.data_ptr(), _ptr(src), offsets.data_ptr(), _ptr(edge_scale),
+                _ptr(node_scale), _ptr(order), _ptr(grad_src), _ptr(grad_edge_scale),
+                None if grad_node_scale is None else grad_node_scale.data_ptr(),
+                edges, nodes, channels, stream,
+            )
+        _lib.check(status)
+    if want_edge_scale_grad:
+        return grad_src, grad_node_scale, grad_edge_scale
+    return grad_src, grad_node_scale
+
+
+# ---------------------------------------------------------------------------
+# segment_softmax (csrc/segment_softmax.cpp:235, :279)
+# ---------------------------------------------------------------------------
+
+def _softmax_checks(logit, env, offsets, order):
+    _f32(logit, "segment softmax logit")
+    _f32(env, "segment softmax env")
+    _check(logit.dim() == 2, "segment softmax logit must have shape (n_edges, channels)")
+    edges, channels = int(logit.shape[0]), int(logit.shape[1])
+    _check(channels > 0, "segment softmax requires at least one channel")
+    _check(env.dim() == 1 and env.numel() == edges, "segment softmax env must have shape (n_edges,)")
+    nodes = _offsets(offsets, "segment softmax offsets")
+    _order(order, edges, "segment softmax")
+    _same_device(logit, env, offsets, order)
+    return edges, nodes, channels
+
+
+def _null_checks(tensor, nodes, channels, what):
+    if tensor is None:
+        return
+    _f32(tensor, what)
+    _check(tensor.numel() == nodes * channels, f"{what} must have shape (n_nodes, channels)")
+
+
+def segment_softmax_forward(logit, env, offsets, null_logit=None, order=None):
+    edges, nodes, channels = _softmax_checks(logit, env, offsets, order)
+    _null_checks(null_logit, nodes, channels, "segment softmax null_logit")
+    _same_device(logit, null_logit)
+    alpha = torch.empty((edges, channels), dtype=torch.float32, device=logit.device)
+    null_alpha = None
+    if null_logit is not None:
+        null_alpha = torch.empty((nodes, channels), dtype=torch.float32, device=logit.device)
+    if nodes == 0:
+        return alpha, null_alpha
+    with _on(logit.device) as stream:
+        status = _LIB.dpa4k_segment_softmax_forward(
+            _ptr(logit), _ptr(env), offsets.data_ptr(), _ptr(null_logit), _ptr(order), _ptr(alpha),
+            _ptr(null_alpha), edges, nodes, channels, stream,
+        )
+    _lib.check(status)
+    return alpha, null_alpha
+
+
+def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
+                             grad_null_alpha=None, order=None):
+    edges, nodes, channels = _softmax_checks(alpha, env, offsets, order)
+    _f32(grad_alpha, "segment softmax grad_alpha")
+    _check(tuple(grad_alpha.shape) == tuple(alpha.shape), "segment softmax grad_alpha must match alpha")
+    _same_device(alpha, grad_alpha)
+    has_null = null_alpha is not None
+    _check(has_null == (grad_null_alpha is not None),
+           "segment softmax requires null_alpha and grad_null_alpha together")
+    _null_checks(null_alpha, nodes, channels, "segment softmax null_alpha")
+    _null_checks(grad_null_alpha, nodes, channels, "segment softmax grad_null_alpha")
+    _same_device(alpha, null_alpha, grad_null_alpha)
+    grad_logit = torch.empty_like(alpha)
+    grad_null = torch.empty((nodes, channels), dtype=torch.float32, device=alpha.device) if has_null else None
+    grad_env = torch.empty((edges,), dtype=torch.float32, device=alpha.device)
+    if nodes == 0:
+        return grad_logit, grad_null, grad_env
+    with _on(alpha.device) as stream:
+        status = _LIB.dpa4k_segment_softmax_backward(
+            _ptr(alpha), _ptr(grad_alpha), _ptr(env), offsets.data_ptr(), _ptr(null_alpha),
+            _ptr(grad_null_alpha), _ptr(order), _ptr(grad_logit), _ptr(grad_null), _ptr(grad_env),
+            edges, nodes, channels, stream,
+        )
+    _lib.check(status)
+    return grad_logit, grad_null, grad_env
+
+
+# ---------------------------------------------------------------------------
+# force_assembly (csrc/force_assembly.cpp:106)
+# ---------------------------------------------------------------------------
+
+def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order):
+    for name, tensor in (("grad_edge", grad_edge), ("edge_vec", edge_vec)):
+        _check(isinstance(tensor, torch.Tensor) and tensor.is_cuda and tensor.is_contiguous()
+               and tensor.dtype in (torch.float32, torch.float64),
+               f"force assembly {name}: expected a contiguous gfx950 float32 or float64 tensor")
+    _check(grad_edge.dtype == edge_vec.dtype, "force assembly grad_edge and edge_vec must share a dtype")
+    _check(grad_edge.dim() == 2 and grad_edge.shape[1] == 3, "force assembly grad_edge must have shape (n_edges, 3)")
+    _check(tuple(edge_vec.shape) == tuple(grad_edge.shape), "force assembly edge_vec must match grad_edge")
+    edges = int(grad_edge.shape[0])
+    nodes = _offsets(dst_offsets, "force assembly dst_offsets")
+    _check(_offsets(src_offsets, "force assembly src_offsets") == nodes,
+           "force assembly offsets must describe the same atom count")
+    _i64(src_order, "force assembly src_order")
+    _check(src_order.dim() == 1 and src_order.numel() == edges, "force assembly src_order must have shape (n_edges,)")
+    _check(nodes > 0, "force assembly requires at least one atom")
+    _same_device(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
+    force = torch.empty((nodes, 3), dtype=grad_edge.dtype, device=grad_edge.device)
+    virial = torch.empty((nodes, 9), dtype=grad_edge.dtype, device=grad_edge.device)
+    entry = (_LIB.dpa4k_force_assembly_f32 if grad_edge.dtype == torch.float32
+             else _LIB.dpa4k_force_assembly_f64)
+    with _on(grad_edge.device) as stream:
+        status = entry(_ptr(grad_edge), _ptr(edge_vec), dst_offsets.data_ptr(), src_offsets.data_ptr(),
+                       _ptr(src_order), force.data_ptr(), virial.data_ptr(), edges, nodes, stream)
+    _lib.check(status)
+    return force, virial
+
+
+# ---------------------------------------------------------------------------
+# GIE zonal scatter (csrc/gie.cpp:148, :178)
+# ---------------------------------------------------------------------------
+
+def _gie_checks(zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    _f32(zonal, "GIE zonal")
+    _f32(radial, "GIE radial")
+    _f32(inv_sqrt_deg, "GIE inv_sqrt_deg")
+    _check(zonal.dim() == 2, "GIE zonal must have shape (n_edges, n_rows)")
+    _check(radial.dim() == 3, "GIE radial must have shape (n_edges, n_radial, channels)")
+    edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
+    _check(radial.shape[0] == edges, "GIE radial edge dimension must match zonal")
+    _i64(dst, "GIE dst")
+    _check(dst.dim() == 1 and dst.numel() == edges, f"GIE dst must have shape ({edges},)")
+    _i64(radial_slot, "GIE radial_slot")
+    _check(radial_slot.dim() == 1 and radial_slot.numel() == rows, f"GIE radial_slot must have shape ({rows},)")
+    _check(inv_sqrt_deg.dim() in (1, 3), "GIE inv_sqrt_deg must have shape (n_nodes,) or (n_nodes, 1, 1)")
+    _check(inv_sqrt_deg.dim() != 3 or tuple(inv_sqrt_deg.shape[1:]) == (1, 1),
+           "GIE inv_sqrt_deg must have shape (n_nodes, 1, 1)")
+    _check(rows == 0 or radial.shape[1] > 0, "GIE radial slots are required for non-scalar rows")
+    _check(edges == 0 or inv_sqrt_deg.shape[0] > 0, "GIE edges require destination nodes")
+    _same_device(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    return edges, rows, int(radial.shape[1]), int(radial.shape[2]), int(inv_sqrt_deg.shape[0])
+
+
+def gie_group(dst, radial_slot, n_nodes: int, n_radial: int):
+    """Destination CSR of an unsorted ``dst``: ``(offsets, order or None, info)``.
+
+    ``order`` is None when ``dst`` is already non-decreasing; ``info`` bit 2
+    says every radial slot feeds at most one row.  ValueError on out-of-range
+    ``dst`` or ``radial_slot`` values.
+    """
+    edges, rows = int(dst.numel()), int(radial_slot.numel())
+    offsets = torch.empty(n_nodes + 1, dtype=torch.int64, device=dst.device)
+    order = torch.empty(max(edges, 1), dtype=torch.int64, device=dst.device)
+    nbytes = _LIB.dpa4k_gie_group_workspace_size(edges, n_nodes)
+    workspace = _workspace(nbytes, dst.device)
+    info = _lib.ctypes.c_int32(0)
+    with _on(dst.device) as stream:
+        status = _LIB.dpa4k_gie_group(
+            _ptr(dst), _ptr(radial_slot), edges, n_nodes, rows, n_radial, offsets.data_ptr(),
+            order.data_ptr(), _lib.ctypes.byref(info), workspace.data_ptr(), nbytes, stream,
+        )
+    _lib.check(status, index_error=True)
+    grouped = bool(info.value & 1)
+    return offsets, (None if grouped else order[:edges]), int(info.value)
+
+
+def gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg):
+    edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
+    n_radial, channels = int(radial.shape[1]), int(radial.shape[2])
+    nodes = int(inv_sqrt_deg.shape[0])
+    out = torch.empty((nodes, rows + 1, channels), dtype=torch.float32, device=zonal.device)
+    if nodes == 0 or channels == 0:
+        return out.zero_()
+    with _on(zonal.device) as stream:
+        status = _LIB.dpa4k_gie_zonal_scatter_forward_csr(
+            _ptr(zonal), _ptr(radial), offsets.data_ptr(), _ptr(order), _ptr(radial_slot),
+            inv_sqrt_deg.data_ptr(), out.data_ptr(), edges, nodes, rows, n_radial, channels, stream,
+        )
+    _lib.check(status)
+    return out
+
+
+def gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, radial_slot,
+                                   inv_sqrt_deg, slots_distinct, *, need=(True, True, True)):
+    edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
+    n_radial, channels = int(radial.shape[1]), int(radial.shape[2])
+    nodes = int(inv_sqrt_deg.shape[0])
+    grad_zonal = torch.empty_like(zonal) if need[0] else None
+    grad_radial = torch.empty_like(radial) if need[1] else None
+    grad_inv = torch.empty_like(inv_sqrt_deg) if need[2] else None
+    if edges == 0 or rows == 0 or channels == 0 or nodes == 0:
+        for tensor in (grad_zonal, grad_radial, grad_inv):
+            if tensor is not None:
+                tensor.zero_()
+        return grad_zonal, grad_radial, grad_inv
+    with _on(zonal.device) as stream:
+        status = _LIB.dpa4k_gie_zonal_scatter_backward_csr(
+            grad_output.data_ptr(), _ptr(zonal), _ptr(radial), offsets.data_ptr(), _ptr(order),
+            _ptr(radial_slot), inv_sqrt_deg.data_ptr(), _ptr(grad_zonal), _ptr(grad_radial),
+            _ptr(grad_inv), edges, nodes, rows, n_radial, channels, int(bool(slots_distinct)), stream,
+        )
+    _lib.check(status)
+    return grad_zonal, grad_radial, grad_inv
+
+
+def gie_zonal_scatter_forward(zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    edges, rows, n_radial, channels, nodes = _gie_checks(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    if nodes == 0 or edges * rows * channels == 0:
+        return torch.zeros((nodes, rows + 1, channels), dtype=torch.float32, device=zonal.device)
+    offsets, order, _ = gie_group(dst, radial_slot, nodes, n_radial)
+    return gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg)
+
+
+def gie_zonal_scatter_backward(grad_output, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    edges, rows, n_radial, channels, nodes = _gie_checks(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    _f32(grad_output, "GIE grad_output")
+    _same_device(zonal, grad_output)
+    _check(grad_output.dim() == 3 and tuple(grad_output.shape) == (nodes, rows + 1, channels),
+           "GIE grad_output must have shape (n_nodes, n_rows + 1, channels)")
+    if nodes == 0 or edges * rows * channels == 0:
+        return torch.zeros_like(zonal), torch.zeros_like(radial), torch.zeros_like(inv_sqrt_deg)
+    offsets, order, info = gie_group(dst, radial_slot, nodes, n_radial)
+    return gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, radial_slot,
+                                          inv_sqrt_deg, info & 2)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm (csrc/rmsnorm.cpp:99, :123)
+# ---------------------------------------------------------------------------
+
+def _rmsnorm_checks(x, scale):
+    _f32(x, "RMSNorm input")
+    _f32(scale, "RMSNorm scale")
+    _same_device(x, scale)
+    _check(x.dim() >= 1, "RMSNorm input must have at least one dimension")
+    _check(x.shape[-1] > 0, "RMSNorm feature dimension must be positive")
+    _check(scale.dim() == 1 and scale.numel() in (0, x.shape[-1]),
+           "RMSNorm scale must be an empty vector or have shape (feature_dim,)")
+    width = int(x.shape[-1])
+    return x.numel() // width, width
+
+
+def rmsnorm_forward(x, scale, eps):
+    rows, width = _rmsnorm_checks(x, scale)
+    eps = float(eps)
+    _check(eps > 0.0 and eps != float("inf"), "RMSNorm eps must be a finite positive number")
+    out = torch.empty_like(x)
+    inverse_rms = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    if rows == 0:
+        return out, inverse_rms
+    with _on(x.device) as stream:
+        status = _LIB.dpa4k_rmsnorm_forward(
+            x.data_ptr(), _ptr(scale), out.data_ptr(), inverse_rms.data_ptr(), rows, width, eps, stream
+        )
+    _lib.check(status)
+    return out, inverse_rms
+
+
+def rmsnorm_backward(grad_output, x, scale, inverse_rms, compute_scale_grad):
+    rows, width = _rmsnorm_checks(x, scale)
+    _f32(grad_output, "RMSNorm grad_output")
+    _f32(inverse_rms, "RMSNorm inverse_rms")
+    _same_device(x, grad_output, inverse_rms)
+    _check(tuple(grad_output.shape) == tuple(x.shape), "RMSNorm grad_output must have the input shape")
+    _check(inverse_rms.dim() == 1 and inverse_rms.numel() == rows, "RMSNorm saved inverse_rms has an invalid shape")
+    has_scale = scale.numel() != 0
+    _check(not compute_scale_grad or has_scale, "cannot compute a scale gradient when scale is omitted")
+    grad_x = torch.empty_like(x)
+    grad_scale = (torch.empty((width,), dtype=torch.float32, device=x.device) if compute_scale_grad
+                  else torch.empty((0,), dtype=torch.float32, device=x.device))
+    nbytes = _LIB.dpa4k_rmsnorm_backward_workspace_size(rows, width) if compute_scale_grad else 0
+    workspace = _workspace(nbytes, x.device) if compute_scale_grad else None
+    with _on(x.device) as stream:
+        status = _LIB.dpa4k_rmsnorm_backward(
+            _ptr(grad_output), _ptr(x), _ptr(scale), _ptr(inverse_rms), _ptr(grad_x),
+            grad_scale.data_ptr() if compute_scale_grad else None, rows, width,
+            None if workspace is None else workspace.data_ptr(), nbytes, stream,
+        )
+    _lib.check(status)
+    return grad_x, grad_scale
+
+
+__all__ = [
+    "force_assembly",
+    "gie_zonal_scatter_backward",
+    "gie_zonal_scatter_forward",
+    "rmsnorm_backward",
+    "rmsnorm_forward",
+    "segment_softmax_backward",
+    "segment_softmax_forward",
+    "segment_sum_backward",
+    "segment_sum_forward",
+]

@@ -1,0 +1,64 @@
+"""Device gate and native-module loader (python/kernels/native.py:9-62 of the reference).
+
+The reference admits Hygon DCU architectures; this build admits the MI355X
+(``gfx950``) only.  The gate keeps the reference's name, ``require_dcu``, so
+code and tests that patch ``kernels.<op>.require_dcu`` keep working.
+"""
+from __future__ import annotations
+
+import importlib
+
+import torch
+
+SUPPORTED_ARCHITECTURES = frozenset({"gfx950"})
+_NATIVE_MODULE = __name__.rsplit(".", 1)[0] + "._C"
+
+
+def _require_hip_runtime() -> None:
+    if not torch.version.hip:
+        raise RuntimeError("gfx950 operators require a ROCm (HIP) build of PyTorch")
+    if not torch.cuda.is_available():
+        raise RuntimeError("gfx950 operators require a visible MI355X (gfx950) device")
+
+
+def require_dcu(*tensors) -> torch.device:
+    """Check the HIP runtime, that every tensor lives on one gfx950 device, and return it.
+
+    ``None`` and non-tensor arguments are skipped.  Raises ``RuntimeError``.
+    """
+    _require_hip_runtime()
+    device = None
+    for tensor in tensors:
+        if not isinstance(tensor, torch.Tensor):
+            continue
+        if tensor.device.type != "cuda":
+            raise RuntimeError(f"gfx950 operator inputs must be on the GPU, got {tensor.device}")
+        if device is not None and tensor.device != device:
+            raise RuntimeError("gfx950 operator inputs must share one device")
+        device = tensor.device
+    index = torch.cuda.current_device() if device is None or device.index is None else device.index
+    try:
+        properties = torch.cuda.get_device_properties(index)
+    except (AssertionError, RuntimeError) as error:
+        raise RuntimeError(f"cannot inspect GPU device {index}") from error
+    architecture = str(getattr(properties, "gcnArchName", "")).split(":", 1)[0]
+    if architecture not in SUPPORTED_ARCHITECTURES:
+        raise RuntimeError(
+            f"unsupported GPU architecture {architecture!r}; these operators are built for gfx950 (MI355X)"
+        )
+    return torch.device("cuda", index)
+
+
+def _extension(required_symbol: str):
+    """Import the native module and require one of its entry points."""
+    _require_hip_runtime()
+    try:
+        extension = importlib.import_module(_NATIVE_MODULE)
+    except (ImportError, OSError) as error:
+        raise RuntimeError(
+            "the gfx950 operator library is not built: run __graft_entry__.build() "
+            "(segment, GIE and RMSNorm operators)"
+        ) from error
+    if not hasattr(extension, required_symbol):
+        raise RuntimeError(f"the loaded {_NATIVE_MODULE} has no {required_symbol!r} entry point")
+    return extension

@@ -1,0 +1,280 @@
+/*
+ * dpa4k.h -- C ABI of the MI355X (gfx950) DPA4/SeZM operator library
+ * (libdpa4k.so, built from bysj_amd/csrc/).
+ *
+ * Conventions shared by every entry point
+ * ---------------------------------------
+ *  - Plain pointers and sizes only.  Every pointer is a device pointer into
+ *    HBM of the current HIP device, except where a parameter says "host".
+ *  - Tensors are dense, row-major and contiguous; shapes are given in the
+ *    comment of each function ([E, C] means E rows of C elements).
+ *  - Index tensors (offsets, orders, dst, src, radial_slot) are int64.
+ *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.  All
+ *    work is enqueued on it.  Only the functions marked "synchronises" wait
+ *    for the stream; every other function returns as soon as its kernels are
+ *    enqueued.
+ *  - The library never allocates device memory.  Functions that need scratch
+ *    memory take a caller-provided workspace and have a *_workspace_size
+ *    query.
+ *  - Return value: DPA4K_OK (0) on success, otherwise an error code; the
+ *    message of the last error raised on the calling thread is returned by
+ *    dpa4k_last_error().  No C++ exception crosses this boundary.
+ *  - CSR contract (segment operators): `offsets[N+1]` is the exclusive prefix
+ *    sum of the per-segment edge counts (offsets[0] == 0, offsets[N] == E,
+ *    non-decreasing).  Segment n owns the slots [offsets[n], offsets[n+1]);
+ *    slot s addresses edge `order[s]` when `order` is given and edge `s`
+ *    otherwise.  Outputs indexed by edge are written in the natural edge
+ *    order.  Offsets are clamped to [0, E] and order entries outside [0, E)
+ *    are skipped on the device, so a malformed CSR yields wrong values but
+ *    never an out-of-bounds access.
+ *  - Every reduction runs in a fixed order that depends only on the shapes
+ *    and the CSR, never on timing: results are bitwise reproducible from
+ *    run to run.  No floating-point atomics are used anywhere.
+ *
+ * Each declaration names the reference interface it replaces
+ * (lipengfei1409/bysj, file:line).
+ */
+#ifndef DPA4K_H
+#define DPA4K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dpa4k_stream_t;
+
+enum {
+  DPA4K_OK = 0,
+  DPA4K_EINVAL = 1,    /* bad argument (shape, size, pointer, index range) */
+  DPA4K_EHIP = 2,      /* a HIP runtime call or kernel launch failed        */
+  DPA4K_EWORKSPACE = 3 /* workspace missing or smaller than required        */
+};
+
+/* Message of the last error on this thread ("" if none).  No reference
+ * counterpart: replaces TORCH_CHECK's exception text (csrc/checks.h:6-20). */
+const char* dpa4k_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int dpa4k_abi_version(void);
+#define DPA4K_ABI_VERSION 1
+
+/* ------------------------------------------------------------------------
+ * CSR construction
+ * ---------------------------------------------------------------------- */
+
+/* Replaces kernels.segment.segment_offsets (python/kernels/segment.py:46-57).
+ * offsets[N+1] = [0, cumsum(bincount(keys, minlength=N))].  Bit-exact.
+ * Synchronises: returns DPA4K_EINVAL ("... values must be within the node
+ * range") when a key lies outside [0, N), matching the reference's
+ * dst.min()/dst.max() check (:54).  N >= 1, E >= 0.
+ * workspace >= dpa4k_segment_offsets_workspace_size(E, N) bytes. */
+size_t dpa4k_segment_offsets_workspace_size(int64_t n_edges, int64_t n_nodes);
+int dpa4k_segment_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
+                          int64_t* offsets, void* workspace,
+                          size_t workspace_bytes, dpa4k_stream_t stream);
+
+/* Replaces kernels.segment.group_by_source (python/kernels/segment.py:60-71):
+ * order[E] = stable argsort(keys), offsets[N+1] as above.  Bit-exact (a
+ * stable order is unique).  Synchronises (same range check as above). */
+size_t dpa4k_group_by_key_workspace_size(int64_t n_edges, int64_t n_nodes);
+int dpa4k_group_by_key(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
+                       int64_t* order, int64_t* offsets, void* workspace,
+                       size_t workspace_bytes, dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * segment_sum
+ * ---------------------------------------------------------------------- */
+
+/* Replaces segment_sum_forward_hip (csrc/segment_sum.cpp:214).
+ * out[n, c] = node_scale[n] * sum_{slots of n} edge_scale[e] * src[e, c]
+ * src[E, C], edge_scale[E] or NULL, node_scale[N] or NULL, order[E] or NULL,
+ * out[N, C].  C >= 1.  Each output element is accumulated sequentially in
+ * slot order (product rounded, then added), so the result equals the
+ * sequential fp32 chain `zeros -> index_add_ -> mul` bit for bit. */
+int dpa4k_segment_sum_forward(const float* src, const int64_t* offsets,
+                              const float* edge_scale, const float* node_scale,
+                              const int64_t* order, float* out,
+                              int64_t n_edges, int64_t n_nodes, int64_t channels,
+                              dpa4k_stream_t stream);
+
+/* Replaces segment_sum_backward_hip (csrc/segment_sum.cpp:271), adding the
+ * edge_scale gradient the reference leaves out (python/kernels/segment.py:221-230):
+ *   grad_src[e, c]      = (grad_out[n, c] * node_scale[n]) * edge_scale[e]
+ *   grad_edge_scale[e]  = sum_c (grad_out[n, c] * node_scale[n]) * src[e, c]
+ *   grad_node_scale[n]  = sum_c grad_out[n, c] * (sum_{slots} edge_scale * src)[n, c]
+ * with n the segment owning edge e.  grad_edge_scale / grad_node_scale may be
+ * NULL (not computed); grad_src must cover [E, C].  The reference's `dst`
+ * argument is not needed: the CSR (offsets, order) identifies each edge's
+ * segment, which the grouping contract makes equal to dst[e]. */
+int dpa4k_segment_sum_backward(const float* grad_out, const float* src,
+                               const int64_t* offsets, const float* edge_scale,
+                               const float* node_scale, const int64_t* order,
+                               float* grad_src, float* grad_edge_scale,
+                               float* grad_node_scale, int64_t n_edges,
+                               int64_t n_nodes, int64_t channels,
+                               dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * segment_softmax
+ * ---------------------------------------------------------------------- */
+
+/* Replaces segment_softmax_forward_hip (csrc/segment_softmax.cpp:235).
+ * Per segment and channel: l_e = logit[e, c] + 2 ln(max(env[e], 1e-30)) for
+ * env[e] > 0 (other edges carry no mass), m = max(null_logit[n, c], max_e l_e),
+ * w_e = exp(l_e - m), D = exp(null - m) + sum_e w_e, alpha = w_e / D,
+ * null_alpha = exp(null - m) / D; a segment with no mass gives zeros.
+ * logit[E, C], env[E], null_logit[N, C] or NULL, order[E] or NULL,
+ * alpha[E, C], null_alpha[N, C] (required iff null_logit is given). */
+int dpa4k_segment_softmax_forward(const float* logit, const float* env,
+                                  const int64_t* offsets, const float* null_logit,
+                                  const int64_t* order, float* alpha,
+                                  float* null_alpha, int64_t n_edges,
+                                  int64_t n_nodes, int64_t channels,
+                                  dpa4k_stream_t stream);
+
+/* Replaces segment_softmax_backward_hip (csrc/segment_softmax.cpp:279).
+ *   S = sum_e alpha * grad_alpha + null_alpha * grad_null_alpha
+ *   grad_logit = alpha (grad_alpha - S); grad_null_logit = null_alpha (grad_null_alpha - S)
+ *   grad_env[e] = (sum_c grad_logit[e, c]) * 2 / env[e]  (0 where !(env > 0))
+ * null_alpha, grad_null_alpha and grad_null_logit are all given or all NULL. */
+int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha,
+                                   const float* env, const int64_t* offsets,
+                                   const float* null_alpha,
+                                   const float* grad_null_alpha,
+                                   const int64_t* order, float* grad_logit,
+                                   float* grad_null_logit, float* grad_env,
+                                   int64_t n_edges, int64_t n_nodes,
+                                   int64_t channels, dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * force_assembly
+ * ---------------------------------------------------------------------- */
+
+/* Replaces force_assembly_hip (csrc/force_assembly.cpp:106).
+ *   force[k]         = sum_{dst slots of k} g_e - sum_{src slots of k} g_e
+ *   virial[k, 3r+c]  = - sum_{src slots of k} g_e[r] * v_e[c]
+ * grad_edge[E, 3], edge_vec[E, 3], dst_offsets[N+1] addressing the natural
+ * (dst-grouped) edge order, src_offsets[N+1] + src_order[E] grouping the
+ * edges by source; force[N, 3], virial[N, 9].  N >= 1.  Accumulates in
+ * double in a fixed order; the f32 variant rounds once on output. */
+int dpa4k_force_assembly_f32(const float* grad_edge, const float* edge_vec,
+                             const int64_t* dst_offsets,
+                             const int64_t* src_offsets,
+                             const int64_t* src_order, float* force,
+                             float* virial, int64_t n_edges, int64_t n_nodes,
+                             dpa4k_stream_t stream);
+
+/* fp64 extension of the above (the reference is fp32-only,
+ * csrc/force_assembly.cpp:110-111): double inputs, double outputs. */
+int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
+                             const int64_t* dst_offsets,
+                             const int64_t* src_offsets,
+                             const int64_t* src_order, double* force,
+                             double* virial, int64_t n_edges, int64_t n_nodes,
+                             dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * GIE zonal scatter
+ * ---------------------------------------------------------------------- */
+
+/* Grouping step of the GIE operator (no reference counterpart: the
+ * reference scatters with atomics on the unsorted dst, csrc/gie.cpp:68-87).
+ * Builds the destination CSR of an unsorted dst: offsets[N+1] always,
+ * order[E] only when dst is not already non-decreasing.  Also checks
+ * 0 <= dst < N and 0 <= radial_slot < S.  Synchronises.
+ * host_info (host pointer, may be NULL) receives a bit set:
+ *   1 = dst was non-decreasing (order left untouched: use NULL order),
+ *   2 = every radial slot is referenced by at most one row.
+ * Out-of-range indices return DPA4K_EINVAL. */
+size_t dpa4k_gie_group_workspace_size(int64_t n_edges, int64_t n_nodes);
+int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot,
+                    int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+                    int64_t n_radial, int64_t* offsets, int64_t* order,
+                    int32_t* host_info, void* workspace, size_t workspace_bytes,
+                    dpa4k_stream_t stream);
+
+/* Replaces gie_zonal_scatter_forward_hip (csrc/gie.cpp:148), given the CSR
+ * from dpa4k_gie_group:
+ *   out[n, 0, :]   = 0 * inv[n]
+ *   out[n, r+1, c] = inv[n] * sum_{slots of n} zonal[e, r] * radial[e, slot[r], c]
+ * (normalise after the sum).  zonal[E, R], radial[E, S, C], radial_slot[R],
+ * inv_sqrt_deg[N], out[N, R+1, C].  Sequential per-element accumulation:
+ * equals the fp32 chain `gather -> mul -> index_add_ -> mul` bit for bit. */
+int dpa4k_gie_zonal_scatter_forward_csr(const float* zonal, const float* radial,
+                                        const int64_t* offsets,
+                                        const int64_t* order,
+                                        const int64_t* radial_slot,
+                                        const float* inv_sqrt_deg, float* out,
+                                        int64_t n_edges, int64_t n_nodes,
+                                        int64_t n_rows, int64_t n_radial,
+                                        int64_t channels, dpa4k_stream_t stream);
+
+/* Replaces gie_zonal_scatter_backward_hip (csrc/gie.cpp:178), given the CSR:
+ *   grad_zonal[e, r]     = sum_c inv[n] grad[n, r+1, c] radial[e, slot[r], c]
+ *   grad_radial[e, s, c] = sum_{r: slot[r]=s} inv[n] grad[n, r+1, c] zonal[e, r]
+ *   grad_inv[n]          = sum_{r, c} grad[n, r+1, c] pre[n, r+1, c]
+ * with pre the unnormalised destination sum (recomputed, not saved).  Any
+ * of the three outputs may be NULL.  grad_radial is written in full (zeros
+ * for unreferenced slots).  `slots_distinct` is bit 2 of dpa4k_gie_group's
+ * host_info and selects the register-only kernel. */
+int dpa4k_gie_zonal_scatter_backward_csr(
+    const float* grad_output, const float* zonal, const float* radial,
+    const int64_t* offsets, const int64_t* order, const int64_t* radial_slot,
+    const float* inv_sqrt_deg, float* grad_zonal, float* grad_radial,
+    float* grad_inv_sqrt_deg, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+    int64_t n_radial, int64_t channels, int slots_distinct,
+    dpa4k_stream_t stream);
+
+/* One-call forms with the reference's signature (csrc/gie.cpp:148,178):
+ * group + forward/backward.  Synchronise (grouping step). */
+int dpa4k_gie_zonal_scatter_forward(const float* zonal, const float* radial,
+                                    const int64_t* dst,
+                                    const int64_t* radial_slot,
+                                    const float* inv_sqrt_deg, float* out,
+                                    int64_t n_edges, int64_t n_nodes,
+                                    int64_t n_rows, int64_t n_radial,
+                                    int64_t channels, void* workspace,
+                                    size_t workspace_bytes,
+                                    dpa4k_stream_t stream);
+int dpa4k_gie_zonal_scatter_backward(
+    const float* grad_output, const float* zonal, const float* radial,
+    const int64_t* dst, const int64_t* radial_slot, const float* inv_sqrt_deg,
+    float* grad_zonal, float* grad_radial, float* grad_inv_sqrt_deg,
+    int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+    int64_t channels, void* workspace, size_t workspace_bytes,
+    dpa4k_stream_t stream);
+/* Workspace of the one-call forms (CSR arrays + grouping scratch). */
+size_t dpa4k_gie_workspace_size(int64_t n_edges, int64_t n_nodes);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm
+ * ---------------------------------------------------------------------- */
+
+/* Replaces rmsnorm_forward_hip (csrc/rmsnorm.cpp:99).
+ * y = x * (1 / sqrt(mean(x^2) + eps)) * scale over rows of width W.
+ * x[rows, W], scale[W] or NULL, y[rows, W], inverse_rms[rows].  W >= 1,
+ * eps finite and > 0. */
+int dpa4k_rmsnorm_forward(const float* x, const float* scale, float* y,
+                          float* inverse_rms, int64_t rows, int64_t width,
+                          float eps, dpa4k_stream_t stream);
+
+/* Replaces rmsnorm_backward_hip (csrc/rmsnorm.cpp:123).
+ *   u = grad * scale;  grad_x = inv u - x inv^3 mean(x u)
+ *   grad_scale[w] = sum_rows grad * x * inv      (if grad_scale != NULL)
+ * grad_scale is reduced over rows in a fixed two-stage order (no atomics);
+ * it needs workspace >= dpa4k_rmsnorm_backward_workspace_size(rows, W). */
+size_t dpa4k_rmsnorm_backward_workspace_size(int64_t rows, int64_t width);
+int dpa4k_rmsnorm_backward(const float* grad, const float* x,
+                           const float* scale, const float* inverse_rms,
+                           float* grad_x, float* grad_scale, int64_t rows,
+                           int64_t width, void* workspace,
+                           size_t workspace_bytes, dpa4k_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DPA4K_H */

@@ -1,0 +1,191 @@
+"""GPU parity of the GIE zonal scatter and RMSNorm (forward and backward).
+
+Cases follow the reference's device tests (tests/csrc/accuracy/test_gie_accuracy.py,
+test_rmsnorm_accuracy.py) plus the water-box configuration at a reduced size.
+The GIE forward accumulates sequentially in edge order, so it is compared
+with the oracle bit for bit.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from bysj_amd import kernels, workloads
+from oracle import gie as gie_ref
+from oracle import loops
+from oracle.rmsnorm import rmsnorm as reference_rmsnorm
+from oracle.rmsnorm import rmsnorm_backward_reference
+from parity import announce, assert_bitwise, assert_close_scaled
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _fixture(degree_shape=(2,)):
+    zonal = torch.tensor([[0.2, -0.1, 0.3], [0.4, 0.5, -0.2], [-0.3, 0.6, 0.1], [0.7, -0.2, 0.4]])
+    radial = torch.arange(24, dtype=torch.float32).reshape(4, 2, 3) / 10
+    dst = torch.tensor([1, 0, 1, 1], dtype=torch.int64)
+    radial_slot = torch.tensor([0, 0, 1], dtype=torch.int64)
+    inverse = torch.tensor([0.7, 0.5]).reshape(degree_shape)
+    return zonal, radial, dst, radial_slot, inverse
+
+
+def _to(values):
+    return [value.to(DEV) for value in values]
+
+
+@pytest.mark.parametrize("degree_shape", [(2,), (2, 1, 1)])
+def test_gie_reference_fixture_forward_and_backward(degree_shape):
+    announce("gie fixture", degree_shape)
+    inputs = _fixture(degree_shape)
+    zonal, radial, dst, slots, inverse = [t.to(DEV) for t in inputs]
+    z = zonal.requires_grad_(True)
+    r = radial.requires_grad_(True)
+    inv = inverse.requires_grad_(True)
+    out = kernels.zonal_scatter(z, r, dst, slots, inv)
+    expected = gie_ref.zonal_scatter_reference(*inputs)
+    assert_bitwise(out, expected, "forward")
+    assert out[:, 0, :].count_nonzero().item() == 0
+    up = torch.randn(2, 4, 3, generator=torch.Generator().manual_seed(0))
+    grads = torch.autograd.grad(out, (z, r, inv), up.to(DEV))
+    expected_grads = gie_ref.zonal_scatter_backward_reference(up, *inputs)
+    for label, actual, wanted in zip(("zonal", "radial", "inverse"), grads, expected_grads):
+        assert actual.shape == wanted.shape
+        assert_close_scaled(actual, wanted, rtol=2e-5, what=f"grad {label}")
+
+
+def test_gie_normalise_after_sum_known_answer_and_inverse_gradient():
+    announce("gie known answer")
+    zonal = torch.tensor([[1e8], [-1e8 + 8], [1.0]])
+    radial = torch.ones(3, 1, 1)
+    dst = torch.zeros(3, dtype=torch.int64)
+    slots = torch.zeros(1, dtype=torch.int64)
+    inverse = torch.tensor([0.3])
+    out = kernels.zonal_scatter(*_to((zonal, radial, dst, slots, inverse)))
+    expected = zonal.sum(0) * inverse
+    assert_bitwise(out[0, 1], expected, "normalise after the sum")
+    inv = torch.ones(1, device=DEV, requires_grad=True)
+    out = kernels.zonal_scatter(zonal.to(DEV), radial.to(DEV), dst.to(DEV), slots.to(DEV), inv)
+    (grad,) = torch.autograd.grad(out, (inv,), torch.tensor([[[0.0], [0.3]]], device=DEV))
+    assert 2.39 <= grad.item() <= 2.71
+
+
+def test_gie_empty_edges_and_range_errors():
+    announce("gie empty")
+    zonal = torch.empty((0, 3), device=DEV)
+    radial = torch.empty((0, 2, 4), device=DEV)
+    dst = torch.empty((0,), dtype=torch.int64, device=DEV)
+    slots = torch.tensor([0, 0, 1], dtype=torch.int64, device=DEV)
+    inverse = torch.ones((2,), device=DEV)
+    out = kernels.zonal_scatter(zonal, radial, dst, slots, inverse)
+    assert tuple(out.shape) == (2, 4, 4) and out.count_nonzero().item() == 0
+    zonal, radial, dst, slots, inverse = _to(_fixture())
+    with pytest.raises(ValueError):
+        kernels.zonal_scatter(zonal, radial, torch.tensor([2, 0, 1, 1], device=DEV), slots, inverse)
+    with pytest.raises(ValueError):
+        kernels.zonal_scatter(zonal, radial, dst, torch.tensor([0, 2, 1], device=DEV), inverse)
+
+
+@pytest.mark.parametrize("primary", [True, False])
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_gie_water_box(primary, shuffle):
+    announce("gie water", primary, shuffle)
+    graph = workloads.water_graph(768, seed=2, rcut=3.0)
+    case = workloads.gie_config(graph, seed=2, primary=primary, channels=64)
+    dst = case["dst"]
+    zonal, radial = case["zonal"], case["radial"]
+    if shuffle:
+        perm = torch.randperm(dst.numel(), generator=torch.Generator().manual_seed(4))
+        dst, zonal, radial = dst[perm].contiguous(), zonal[perm].contiguous(), radial[perm].contiguous()
+    inputs = (zonal, radial, dst, case["radial_slot"], case["inv_sqrt_deg"])
+    z, r = zonal.to(DEV).requires_grad_(True), radial.to(DEV).requires_grad_(True)
+    inv = case["inv_sqrt_deg"].to(DEV).requires_grad_(True)
+    out = kernels.zonal_scatter(z, r, dst.to(DEV), case["radial_slot"].to(DEV), inv)
+    assert_bitwise(out, gie_ref.zonal_scatter_reference(*inputs), "forward")
+    up = torch.randn(out.shape, generator=torch.Generator().manual_seed(1))
+    grads = torch.autograd.grad(out, (z, r, inv), up.to(DEV))
+    expected = gie_ref.zonal_scatter_backward_reference(up, *inputs)
+    for label, actual, wanted in zip(("zonal", "radial", "inverse"), grads, expected):
+        assert_close_scaled(actual, wanted, rtol=2e-5, what=f"grad {label}")
+
+
+def test_gie_forward_against_fp64_truth():
+    announce("gie fp64 truth")
+    graph = workloads.water_graph(600, seed=5, rcut=3.0)
+    case = workloads.gie_config(graph, seed=5, primary=False, channels=8)
+    inputs = (case["zonal"], case["radial"], case["dst"], case["radial_slot"], case["inv_sqrt_deg"])
+    out = kernels.zonal_scatter(*_to(inputs))
+    assert_close_scaled(out, loops.zonal_scatter_loop(*inputs), what="vs fp64 truth")
+
+
+def test_gie_current_stream():
+    announce("gie stream")
+    stream = torch.cuda.Stream()
+    inputs = _fixture()
+    with torch.cuda.stream(stream):
+        out = kernels.zonal_scatter(*_to(inputs))
+    torch.cuda.current_stream().wait_stream(stream)
+    assert_bitwise(out, gie_ref.zonal_scatter_reference(*inputs), "side stream")
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 127), (2, 3, 257), (0, 65), (5, 1024), (3, 4096), (2, 5000)])
+def test_rmsnorm_forward_tail_widths(shape):
+    announce("rmsnorm fwd", shape)
+    gen = torch.Generator().manual_seed(len(shape) + shape[-1])
+    x = torch.randn(*shape, generator=gen)
+    scale = torch.randn(shape[-1], generator=gen)
+    out = kernels.rmsnorm(x.to(DEV), scale.to(DEV), eps=1e-5)
+    assert tuple(out.shape) == shape
+    assert_close_scaled(out, reference_rmsnorm(x, scale, eps=1e-5), what="vs oracle")
+    if x.numel():
+        assert_close_scaled(out, loops.rmsnorm_loop(x, scale, 1e-5), what="vs fp64 truth")
+
+
+@pytest.mark.parametrize("shape", [(5, 3, 127), (64, 1024), (9, 5000)])
+def test_rmsnorm_gradients(shape):
+    announce("rmsnorm bwd", shape)
+    gen = torch.Generator().manual_seed(shape[-1])
+    x = torch.randn(*shape, generator=gen)
+    scale = torch.randn(shape[-1], generator=gen)
+    up = torch.randn(*shape, generator=gen)
+    xd = x.to(DEV).requires_grad_(True)
+    sd = scale.to(DEV).requires_grad_(True)
+    out = kernels.rmsnorm(xd, sd, eps=1e-5)
+    grads = torch.autograd.grad(out, (xd, sd), up.to(DEV))
+    e_x, e_s = rmsnorm_backward_reference(up, x, scale, eps=1e-5)
+    assert_close_scaled(grads[0], e_x, rtol=3e-5, what="grad_x")
+    assert_close_scaled(grads[1], e_s, rtol=3e-5, what="grad_scale")
+    again = torch.autograd.grad(kernels.rmsnorm(xd, sd, eps=1e-5), (xd, sd), up.to(DEV))
+    assert_bitwise(again[1], grads[1], "grad_scale run-to-run")
+
+
+def test_rmsnorm_zero_input_no_scale_and_stream():
+    announce("rmsnorm zero/stream")
+    x = torch.zeros(2, 7, device=DEV)
+    out = kernels.rmsnorm(x, eps=1e-6)
+    assert torch.equal(out, x)
+    stream = torch.cuda.Stream()
+    gen = torch.Generator().manual_seed(3)
+    xs, ss = torch.randn(9, 131, generator=gen), torch.randn(131, generator=gen)
+    with torch.cuda.stream(stream):
+        out = kernels.rmsnorm(xs.to(DEV), ss.to(DEV))
+    torch.cuda.current_stream().wait_stream(stream)
+    assert_close_scaled(out, reference_rmsnorm(xs, ss), what="side stream")
+
+
+def test_gie_then_rmsnorm_config3_reduced():
+    announce("gie+rmsnorm config3 reduced")
+    graph = workloads.water_graph(1200, seed=0)
+    case = workloads.gie_config(graph, seed=0, primary=True, channels=64)
+    inputs = (case["zonal"], case["radial"], case["dst"], case["radial_slot"], case["inv_sqrt_deg"])
+    out = kernels.zonal_scatter(*_to(inputs))
+    expected = gie_ref.zonal_scatter_reference(*inputs)
+    assert_bitwise(out, expected, "gie")
+    rows = out.reshape(out.shape[0], -1)
+    y = kernels.rmsnorm(rows, case["rms_scale"].to(DEV), eps=1e-6)
+    assert_close_scaled(y, reference_rmsnorm(expected.reshape(expected.shape[0], -1), case["rms_scale"], 1e-6),
+                        what="rmsnorm")

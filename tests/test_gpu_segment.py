@@ -1,0 +1,362 @@
+"""GPU parity of the CSR helpers, segment_sum, segment_softmax and force_assembly.
+
+Every case compares the gfx950 path (through kernels.* -> kernels._C ->
+libdpa4k.so) with the CPU oracle on the same seeded inputs: bit for bit for
+indices and for the sequential segment_sum forward, the fp32 rule against the
+oracle and an fp64 ground truth otherwise.  Shapes follow the reference's
+device tests (tests/csrc/accuracy/test_segment_ops_accuracy.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from bysj_amd import kernels, workloads
+from oracle import loops
+from oracle import segment as ref
+from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _graph(sizes):
+    sizes = torch.tensor(sizes, dtype=torch.int64)
+    dst = torch.repeat_interleave(torch.arange(sizes.numel(), dtype=torch.int64), sizes)
+    return dst, torch.cat([torch.zeros(1, dtype=torch.int64), sizes.cumsum(0)])
+
+
+def _shuffled(dst_sorted: torch.Tensor, seed: int):
+    """Natural order = a seeded permutation of a grouped list; CSR via stable argsort."""
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(dst_sorted.numel(), generator=gen)
+    dst = dst_sorted[perm]
+    n = int(dst_sorted.max()) + 1 if dst_sorted.numel() else 1
+    order, offsets = ref.group_by_source(dst, n)
+    return dst, order, offsets
+
+
+# ---------------------------------------------------------------------------
+# CSR construction (bit-exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("edges,nodes,seed", [(0, 5, 0), (1, 1, 1), (1000, 37, 2), (200000, 5000, 3),
+                                              (300000, 300001, 4)])
+def test_segment_offsets_and_grouping_bit_exact(edges, nodes, seed):
+    announce("csr", edges, nodes, seed)
+    gen = torch.Generator().manual_seed(seed)
+    keys = torch.randint(0, nodes, (edges,), generator=gen, dtype=torch.int64)
+    offsets = kernels.segment_offsets(keys.to(DEV), nodes)
+    assert_bitwise(offsets, ref.segment_offsets(keys, nodes), "segment_offsets")
+    order, src_offsets = kernels.group_by_source(keys.to(DEV), nodes)
+    e_order, e_offsets = ref.group_by_source(keys, nodes)
+    assert_bitwise(order, e_order, "group_by_source order")
+    assert_bitwise(src_offsets, e_offsets, "group_by_source offsets")
+
+
+def test_grouping_known_answer_and_range_errors():
+    announce("csr known answer")
+    src = torch.tensor([2, 0, 2, 1, 0], dtype=torch.int64, device=DEV)
+    order, offsets = kernels.group_by_source(src, 3)
+    assert offsets.cpu().tolist() == [0, 2, 3, 5]
+    assert order.cpu().tolist() == [1, 4, 3, 0, 2]
+    dst, expected = _graph([2, 0, 3])
+    assert kernels.segment_offsets(dst.to(DEV), 3).cpu().tolist() == expected.tolist()
+    with pytest.raises(ValueError):
+        kernels.segment_offsets(torch.tensor([0, 3], dtype=torch.int64, device=DEV), 3)
+    with pytest.raises(ValueError):
+        kernels.group_by_source(torch.tensor([-1, 0], dtype=torch.int64, device=DEV), 3)
+
+
+# ---------------------------------------------------------------------------
+# segment_sum
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("channels", [1, 3, 8, 64, 128, 640, 1024, 2052, 4100])
+@pytest.mark.parametrize("scales", [False, True])
+def test_segment_sum_forward_bit_exact(channels, scales):
+    announce("segment_sum fwd", channels, scales)
+    case = workloads.segment_sum_config(n_nodes=97, channels=channels, seed=channels, scales=scales)
+    d = {k: (v.to(DEV) if v is not None else None) for k, v in case.items()}
+    out = kernels.segment_sum(d["src"], d["dst"], d["offsets"], d["edge_scale"], d["node_scale"])
+    expected = ref.segment_sum_reference(case["src"], case["dst"], case["offsets"], case["edge_scale"],
+                                         case["node_scale"])
+    assert_bitwise(out, expected, "segment_sum vs sequential oracle")
+
+
+def test_segment_sum_reference_cases_and_empty_segments():
+    announce("segment_sum reference cases")
+    for channels in (1, 3, 64, 640):
+        dst, offsets = _graph([2, 0, 3])
+        gen = torch.Generator().manual_seed(channels)
+        src = torch.randn(5, channels, generator=gen)
+        edge_scale = torch.rand(5, generator=gen) + 0.5
+        node_scale = torch.rand(3, generator=gen) + 0.5
+        out = kernels.segment_sum(src.to(DEV), dst.to(DEV), offsets.to(DEV), edge_scale.to(DEV), node_scale.to(DEV))
+        assert_bitwise(out, ref.segment_sum_reference(src, dst, offsets, edge_scale, node_scale), "reference case")
+        assert out[1].count_nonzero().item() == 0
+    # no edges at all: zeros (times the node scale)
+    src = torch.empty(0, 4)
+    dst = torch.empty(0, dtype=torch.int64)
+    offsets = torch.zeros(4, dtype=torch.int64)
+    out = kernels.segment_sum(src.to(DEV), dst.to(DEV), offsets.to(DEV))
+    assert out.shape == (3, 4) and out.count_nonzero().item() == 0
+
+
+@pytest.mark.parametrize("channels", [5, 128])
+def test_segment_sum_with_order_is_bit_exact(channels):
+    announce("segment_sum order", channels)
+    degrees = workloads.poisson_degrees(211, 12.0, seed=5)
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    dst, order, offsets = _shuffled(dst_sorted, seed=7)
+    gen = torch.Generator().manual_seed(9)
+    src = torch.randn(dst.numel(), channels, generator=gen)
+    w = torch.rand(dst.numel(), generator=gen) + 0.5
+    s = torch.rand(211, generator=gen) + 0.5
+    out = kernels.segment_sum(src.to(DEV), dst.to(DEV), offsets.to(DEV), w.to(DEV), s.to(DEV), order=order.to(DEV))
+    assert_bitwise(out, ref.segment_sum_reference(src, dst, offsets, w, s), "segment_sum with order")
+
+
+def test_segment_sum_large_graph_against_fp64_truth():
+    announce("segment_sum fp64 truth")
+    gen = torch.Generator().manual_seed(11)
+    atoms, edges, channels = 64, 4096, 32
+    dst = torch.sort(torch.randint(0, atoms, (edges,), generator=gen)).values
+    offsets = ref.segment_offsets(dst, atoms)
+    src = torch.randn(edges, channels, generator=gen)
+    node_scale = torch.rand(atoms, generator=gen) + 0.5
+    out = kernels.segment_sum(src.to(DEV), dst.to(DEV), offsets.to(DEV), None, node_scale.to(DEV))
+    truth = loops.segment_sum_loop(src, dst, atoms, None, node_scale)
+    assert_close_scaled(out, truth, what="vs fp64 truth")
+
+
+def test_segment_sum_config1_full_size_and_determinism():
+    announce("segment_sum config 1")
+    case = workloads.segment_sum_config(seed=0)
+    d = {k: (v.to(DEV) if v is not None else None) for k, v in case.items()}
+    first = kernels.segment_sum(d["src"], d["dst"], d["offsets"])
+    second = kernels.segment_sum(d["src"], d["dst"], d["offsets"])
+    assert_bitwise(first, second, "run-to-run")
+    assert_bitwise(first, ref.segment_sum_reference(case["src"], case["dst"], case["offsets"]), "config 1")
+
+
+@pytest.mark.parametrize("channels", [3, 8, 128, 640])
+@pytest.mark.parametrize("use_order", [False, True])
+def test_segment_sum_backward_matches_autograd(channels, use_order):
+    announce("segment_sum bwd", channels, use_order)
+    degrees = workloads.poisson_degrees(53, 9.0, seed=channels)
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    if use_order:
+        dst, order, offsets = _shuffled(dst_sorted, seed=3)
+    else:
+        dst, order, offsets = dst_sorted, None, ref.segment_offsets(dst_sorted, 53)
+    gen = torch.Generator().manual_seed(channels + 1)
+    src = torch.randn(dst.numel(), channels, generator=gen)
+    w = torch.rand(dst.numel(), generator=gen) + 0.5
+    s = torch.rand(53, generator=gen) + 0.5
+    g = torch.randn(53, channels, generator=gen)
+    x = src.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    sd = s.to(DEV).requires_grad_(True)
+    out = kernels.segment_sum(x, dst.to(DEV), offsets.to(DEV), wd, sd, order=None if order is None else order.to(DEV))
+    grads = torch.autograd.grad(out, (x, wd, sd), g.to(DEV))
+    e_src, e_w, e_s = ref.segment_sum_backward_reference(g, src, dst, offsets, w, s)
+    assert_bitwise(grads[0], e_src, "grad_src")
+    assert_close_scaled(grads[1], e_w, what="grad_edge_scale")
+    assert_close_scaled(grads[2], e_s, what="grad_node_scale")
+
+
+def test_segment_sum_node_scale_shape_and_empty_edges_backward():
+    announce("segment_sum bwd shapes")
+    dst, offsets = _graph([2, 1, 3])
+    src = torch.arange(12, dtype=torch.float32).reshape(6, 2) / 7
+    node_scale = torch.tensor([[1.0], [2.0], [3.0]])
+    x = src.to(DEV).requires_grad_(True)
+    s = node_scale.to(DEV).requires_grad_(True)
+    out = kernels.segment_sum(x, dst.to(DEV), offsets.to(DEV), None, s)
+    g = torch.randn(3, 2)
+    grad_x, grad_s = torch.autograd.grad(out, (x, s), g.to(DEV))
+    assert grad_s.shape == (3, 1)
+    e_src, _, e_s = ref.segment_sum_backward_reference(g, src, dst, offsets, None, node_scale.reshape(-1))
+    assert_bitwise(grad_x, e_src, "grad_src")
+    assert_close_scaled(grad_s.reshape(-1), e_s, what="grad_node_scale")
+
+
+# ---------------------------------------------------------------------------
+# segment_softmax
+# ---------------------------------------------------------------------------
+
+def test_segment_softmax_reference_case_forward_and_backward():
+    announce("softmax reference case")
+    dst, offsets = _graph([2, 0, 3, 1])
+    gen = torch.Generator().manual_seed(0)
+    logit = torch.randn(6, 16, generator=gen)
+    env = torch.tensor([0.9, -0.2, 0.7, 0.0, 1.1, 0.3])
+    null_logit = torch.randn(4, 16, generator=gen)
+    up = torch.randn(6, 16, generator=gen)
+    up_null = torch.randn(4, 16, generator=gen)
+    x = logit.to(DEV).requires_grad_(True)
+    e = env.to(DEV).requires_grad_(True)
+    n = null_logit.to(DEV).requires_grad_(True)
+    alpha, null_alpha = kernels.segment_softmax(x, e, offsets.to(DEV), n)
+    grads = torch.autograd.grad((alpha, null_alpha), (x, e, n), (up.to(DEV), up_null.to(DEV)))
+    e_alpha, e_null = ref.segment_softmax_reference(logit, env, dst, offsets, null_logit)
+    assert_close_scaled(alpha, e_alpha, what="alpha")
+    assert_close_scaled(null_alpha, e_null, what="null_alpha")
+    e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
+    assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
+    assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
+    assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+    per_segment = torch.zeros(4, 16).index_add_(0, dst, alpha.detach().cpu())
+    assert_close_scaled(per_segment + null_alpha.detach().cpu(), torch.ones(4, 16), what="sum to one")
+    assert alpha[1].count_nonzero().item() == 0 and alpha[3].count_nonzero().item() == 0
+
+
+@pytest.mark.parametrize("channels", [1, 3, 8, 16, 64, 256, 260, 640])
+@pytest.mark.parametrize("null", [False, True])
+@pytest.mark.parametrize("use_order", [False, True])
+def test_segment_softmax_with_hubs(channels, null, use_order):
+    announce("softmax", channels, null, use_order)
+    # Poisson(6) segments plus hubs long enough for the block-cooperative path.
+    degrees = workloads.poisson_degrees(67, 6.0, seed=channels, minimum=0, hub_fraction=0.06, hub_degree=700)
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    if use_order:
+        dst, order, offsets = _shuffled(dst_sorted, seed=channels)
+    else:
+        dst, order, offsets = dst_sorted, None, ref.segment_offsets(dst_sorted, 67)
+    gen = torch.Generator().manual_seed(channels + 5)
+    logit = torch.randn(dst.numel(), channels, generator=gen) * 2.0
+    logit.view(-1)[::97] = 40.0
+    logit.view(-1)[5::89] = -40.0
+    env = torch.rand(dst.numel(), generator=gen) + 0.1
+    env[::13] = 0.0
+    env[7::29] = -1.0
+    null_logit = torch.randn(67, channels, generator=gen) if null else None
+    up = torch.randn(dst.numel(), channels, generator=gen)
+    up_null = torch.randn(67, channels, generator=gen) if null else None
+
+    x = logit.to(DEV).requires_grad_(True)
+    e = env.to(DEV).requires_grad_(True)
+    nd = null_logit.to(DEV).requires_grad_(True) if null else None
+    o = None if order is None else order.to(DEV)
+    result = kernels.segment_softmax(x, e, offsets.to(DEV), nd, order=o)
+    alpha = result[0] if null else result
+    e_alpha, e_null = ref.segment_softmax_reference(logit, env, dst, offsets, null_logit)
+    assert_close_scaled(alpha, e_alpha, what="alpha vs oracle")
+    truth_alpha, truth_null = (loops.segment_softmax_loop(logit, env, dst, 67, null_logit)
+                               if channels <= 16 else (None, None))
+    if truth_alpha is not None:
+        assert_close_scaled(alpha, truth_alpha, what="alpha vs fp64 truth")
+    if null:
+        assert_close_scaled(result[1], e_null, what="null_alpha")
+        if truth_null is not None:
+            assert_close_scaled(result[1], truth_null, what="null_alpha vs fp64 truth")
+        outputs, cotangents, inputs = (result[0], result[1]), (up.to(DEV), up_null.to(DEV)), (x, e, nd)
+    else:
+        outputs, cotangents, inputs = (alpha,), (up.to(DEV),), (x, e)
+    grads = torch.autograd.grad(outputs, inputs, cotangents)
+    e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
+    assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
+    assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
+    if null:
+        assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+
+
+def test_segment_softmax_empty_and_masked_segments():
+    announce("softmax empty/masked")
+    dst, offsets = _graph([0, 2, 3])
+    logit = torch.randn(5, 4)
+    env = torch.tensor([-1.0, 0.0, 0.5, 0.5, 0.5])  # segment 1 fully masked
+    alpha = kernels.segment_softmax(logit.to(DEV), env.to(DEV), offsets.to(DEV))
+    e_alpha, _ = ref.segment_softmax_reference(logit, env, dst, offsets)
+    assert_close_scaled(alpha, e_alpha, what="alpha")
+    assert alpha[:2].count_nonzero().item() == 0
+    null_logit = torch.randn(3, 4)
+    alpha, null_alpha = kernels.segment_softmax(logit.to(DEV), env.to(DEV), offsets.to(DEV), null_logit.to(DEV))
+    torch.testing.assert_close(null_alpha[0].cpu(), torch.ones(4))  # null only: all mass on the null
+    torch.testing.assert_close(null_alpha[1].cpu(), torch.ones(4))
+
+
+def test_segment_softmax_config2_full_size_and_determinism():
+    announce("softmax config 2")
+    case = workloads.segment_softmax_config(seed=0)
+    d = {k: (v.to(DEV) if v is not None else None) for k, v in case.items()}
+    alpha, null_alpha = kernels.segment_softmax(d["logit"], d["env"], d["offsets"], d["null_logit"])
+    again, again_null = kernels.segment_softmax(d["logit"], d["env"], d["offsets"], d["null_logit"])
+    assert_bitwise(alpha, again, "run-to-run alpha")
+    assert_bitwise(null_alpha, again_null, "run-to-run null")
+    e_alpha, e_null = ref.segment_softmax_reference(case["logit"], case["env"], case["dst"], case["offsets"],
+                                                    case["null_logit"])
+    assert_close_scaled(alpha, e_alpha, what="config 2 alpha")
+    assert_close_scaled(null_alpha, e_null, what="config 2 null_alpha")
+    total = torch.zeros_like(null_alpha).index_add_(0, d["dst"], alpha) + null_alpha
+    assert_close_scaled(total, torch.ones_like(total), what="sum to one")
+
+
+# ---------------------------------------------------------------------------
+# force_assembly
+# ---------------------------------------------------------------------------
+
+def test_force_assembly_reference_case():
+    announce("force reference case")
+    dst, dst_offsets = _graph([2, 1, 3, 0])
+    src = torch.tensor([2, 0, 2, 1, 0, 2], dtype=torch.int64)
+    gen = torch.Generator().manual_seed(0)
+    g = torch.randn(6, 3, generator=gen)
+    v = torch.randn(6, 3, generator=gen)
+    force, virial = kernels.force_assembly(g.to(DEV), v.to(DEV), src.to(DEV), dst.to(DEV), dst_offsets.to(DEV))
+    order, src_offsets = ref.group_by_source(src, 4)
+    e_force, e_virial = ref.force_assembly_reference(g, v, src, dst, dst_offsets, src_offsets)
+    truth_force, truth_virial = loops.force_assembly_loop(g, v, src, dst, 4)
+    assert_close_scaled(force, e_force, what="force vs oracle")
+    assert_close_scaled(virial, e_virial, what="virial vs oracle")
+    assert_close_scaled(force, truth_force, what="force vs fp64 truth")
+    assert_close_scaled(virial, truth_virial, what="virial vs fp64 truth")
+    assert force[3].count_nonzero().item() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_force_assembly_grouped_graph(dtype):
+    announce("force grouped", dtype)
+    gen = torch.Generator().manual_seed(7)
+    atoms, edges = 64, 4096
+    dst = torch.sort(torch.randint(0, atoms, (edges,), generator=gen)).values
+    offsets = ref.segment_offsets(dst, atoms)
+    src = torch.randint(0, atoms, (edges,), generator=gen)
+    order, src_offsets = ref.group_by_source(src, atoms)
+    g = torch.randn(edges, 3, generator=gen, dtype=torch.float64).to(dtype)
+    v = torch.randn(edges, 3, generator=gen, dtype=torch.float64).to(dtype)
+    force, virial = kernels.force_assembly(g.to(DEV), v.to(DEV), src.to(DEV), dst.to(DEV), offsets.to(DEV),
+                                           src_offsets.to(DEV), order.to(DEV))
+    assert force.dtype == dtype and virial.dtype == dtype
+    truth_force, truth_virial = loops.force_assembly_loop(g, v, src, dst, atoms)
+    if dtype == torch.float64:
+        assert_fp64(force, truth_force, "fp64 force")
+        assert_fp64(virial, truth_virial, "fp64 virial")
+        assert abs(float(force.sum(0).abs().max())) <= 1e-12 * float(g.abs().sum())
+    else:
+        e_force, e_virial = ref.force_assembly_reference(g, v, src, dst, offsets, src_offsets)
+        assert_close_scaled(force, e_force, what="force vs oracle")
+        assert_close_scaled(virial, e_virial, what="virial vs oracle")
+        assert_close_scaled(force, truth_force, what="force vs truth")
+        assert_close_scaled(virial, truth_virial, what="virial vs truth")
+
+
+def test_force_assembly_water_graph_newton_and_determinism():
+    announce("force water graph")
+    graph = workloads.water_graph(2048, seed=3)
+    case = workloads.force_config(graph, seed=3, device="cpu", dtype=torch.float64)
+    d = {k: v.to(DEV) for k, v in case.items()}
+    force, virial = kernels.force_assembly(d["grad_edge"], d["edge_vec"], d["src"], d["dst"], d["dst_offsets"],
+                                           d["src_offsets"], d["src_order"])
+    again, again_virial = kernels.force_assembly(d["grad_edge"], d["edge_vec"], d["src"], d["dst"],
+                                                 d["dst_offsets"], d["src_offsets"], d["src_order"])
+    assert_bitwise(force, again, "run-to-run force")
+    assert_bitwise(virial, again_virial, "run-to-run virial")
+    e_force, e_virial = ref.force_assembly_reference(case["grad_edge"], case["edge_vec"], case["src"], case["dst"],
+                                                     case["dst_offsets"], case["src_offsets"])
+    assert_fp64(force, e_force, "fp64 force vs oracle")
+    assert_fp64(virial, e_virial, "fp64 virial vs oracle")
+    net = force.sum(0).abs().max().item()
+    assert net <= 1e-12 * case["grad_edge"].abs().sum().item()
