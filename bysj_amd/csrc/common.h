@@ -34,6 +34,11 @@ int hip_status(hipError_t status, const char* what);
 // Clears the thread's last error (called on entry by every ABI function).
 void clear_error();
 
+// Enqueues a kernel that writes `bytes` zero bytes at `pointer` (4-byte
+// aligned, `bytes` a multiple of 4).  Used instead of hipMemsetAsync so that
+// callers may capture the library's launches into a HIP graph.
+int zero_fill(void* pointer, size_t bytes, hipStream_t stream);
+
 inline hipStream_t as_stream(dpa4k_stream_t stream) {
   return reinterpret_cast<hipStream_t>(stream);
 }

@@ -516,15 +516,11 @@ extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
   if (n_rows == 0 || channels == 0 || n_radial == 0) {
     // Nothing flows back: zero every requested output.
     if (grad_zonal != nullptr && n_edges * n_rows > 0)
-      if (int s = hip_status(hipMemsetAsync(grad_zonal, 0, n_edges * n_rows * 4, stream), "hipMemsetAsync"))
-        return s;
+      if (int s = zero_fill(grad_zonal, n_edges * n_rows * 4, stream)) return s;
     if (grad_radial != nullptr && n_edges * n_radial * channels > 0)
-      if (int s = hip_status(hipMemsetAsync(grad_radial, 0, n_edges * n_radial * channels * 4, stream),
-                             "hipMemsetAsync"))
-        return s;
+      if (int s = zero_fill(grad_radial, n_edges * n_radial * channels * 4, stream)) return s;
     if (grad_inv_sqrt_deg != nullptr)
-      if (int s = hip_status(hipMemsetAsync(grad_inv_sqrt_deg, 0, n_nodes * 4, stream), "hipMemsetAsync"))
-        return s;
+      if (int s = zero_fill(grad_inv_sqrt_deg, n_nodes * 4, stream)) return s;
     return DPA4K_OK;
   }
   const bool vec4 = channels % 4 == 0 && aligned16(radial) && aligned16(grad_output) &&

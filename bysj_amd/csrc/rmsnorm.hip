@@ -327,9 +327,7 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
     return fail(DPA4K_EINVAL, "cannot compute a scale gradient when scale is omitted");
   hipStream_t stream = as_stream(stream_handle);
   if (rows == 0) {
-    if (grad_scale != nullptr)
-      return hip_status(hipMemsetAsync(grad_scale, 0, width * sizeof(float), stream),
-                        "hipMemsetAsync");
+    if (grad_scale != nullptr) return zero_fill(grad_scale, width * sizeof(float), stream);
     return DPA4K_OK;
   }
   if (grad == nullptr || x == nullptr || inverse_rms == nullptr || grad_x == nullptr)

@@ -21,7 +21,7 @@ import contextlib
 
 import torch
 
-from .. import _lib
+from . import _lib
 
 _LIB = _lib.load()
 

@@ -10,7 +10,9 @@ import ctypes
 import threading
 from pathlib import Path
 
-LIBRARY_PATH = Path(__file__).resolve().parent / "libdpa4k.so"
+# bysj_amd/libdpa4k.so, one directory above this package (also when the package
+# is imported under its reference name, `kernels`, with bysj_amd/ on sys.path).
+LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
 ABI_VERSION = 1

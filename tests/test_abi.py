@@ -1,0 +1,112 @@
+"""The C ABI of libdpa4k.so on the CPU: it loads, and it exports what include/dpa4k.h declares.
+
+No compute call is made (there is no GPU here).  Only entry points whose
+argument checks return before any HIP call are exercised: the version and
+error queries, the workspace-size queries, and the EINVAL paths for sizes a
+caller must never pass.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dpa4k.h"
+LIBRARY = ROOT / "bysj_amd" / "libdpa4k.so"
+
+pytestmark = pytest.mark.skipif(not LIBRARY.exists(), reason="libdpa4k.so is not built (run __graft_entry__.build())")
+
+
+def _declarations() -> dict[str, int]:
+    """name -> parameter count of every function declared in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    found = {}
+    for match in re.finditer(r"\b(dpa4k_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = match.group(2).strip()
+        found[match.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return found
+
+
+def _lib():
+    from bysj_amd.kernels import _lib
+
+    return _lib
+
+
+def test_header_and_binding_declare_the_same_entry_points():
+    declared = _declarations()
+    prototypes = _lib().PROTOTYPES
+    assert set(declared) == set(prototypes), set(declared) ^ set(prototypes)
+    for name, count in declared.items():
+        assert len(prototypes[name][1]) == count, f"{name}: header has {count} parameters"
+
+
+def test_library_exports_every_declared_symbol():
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(LIBRARY)], capture_output=True, text=True,
+                              check=True).stdout
+    names = {line.split()[-1] for line in exported.splitlines() if line.strip()}
+    missing = sorted(set(_declarations()) - names)
+    assert not missing, f"not exported: {missing}"
+    dpa4k_exports = sorted(n for n in names if n.startswith("dpa4k_"))
+    assert set(dpa4k_exports) == set(_declarations()), "exports beyond the header"
+
+
+def test_library_loads_and_reports_its_abi_version():
+    lib = _lib().load()
+    version = int(re.search(r"#define DPA4K_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.dpa4k_abi_version() == version == _lib().ABI_VERSION
+    assert lib.dpa4k_last_error() == b""
+
+
+def test_workspace_queries_are_host_only_and_grow_with_the_input():
+    lib = _lib().load()
+    for query in ("dpa4k_segment_offsets_workspace_size", "dpa4k_group_by_key_workspace_size",
+                  "dpa4k_gie_group_workspace_size", "dpa4k_gie_workspace_size",
+                  "dpa4k_rmsnorm_backward_workspace_size"):
+        function = getattr(lib, query)
+        small, large = function(1000, 100), function(10_000_000, 100_000)
+        assert large >= small, query
+        assert large % 256 == 0 or large == 0, f"{query}: carve granularity"
+
+
+def test_invalid_sizes_fail_before_any_device_call():
+    binding = _lib()
+    lib = binding.load()
+    null = None
+    cases = [
+        (lib.dpa4k_segment_sum_forward, (null,) * 6 + (-1, 1, 1, null), "negative sizes"),
+        (lib.dpa4k_segment_sum_forward, (null,) * 6 + (1, 1, 0, null), "at least one channel"),
+        (lib.dpa4k_segment_softmax_forward, (null,) * 7 + (-1, 1, 1, null), ""),
+        (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (1, 0, ctypes.c_float(1e-6), null), "feature dimension"),
+        (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (1, 4, ctypes.c_float(0.0), null), "eps"),
+        (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 0, null), ""),
+        (lib.dpa4k_force_assembly_f64, (null,) * 7 + (-1, 1, null), ""),
+    ]
+    for function, args, fragment in cases:
+        status = function(*args)
+        assert status == binding.EINVAL, (function.__name__, status)
+        message = lib.dpa4k_last_error().decode()
+        assert message and fragment in message, (function.__name__, message)
+
+
+def test_package_imports_under_the_reference_names():
+    """With bysj_amd/ on sys.path the operators import as the reference's `kernels` package."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import kernels, kernels._C as native\n"
+        "print(','.join(kernels.__all__)); print(native.segment_sum_forward.__module__)\n"
+    ) % str(ROOT / "bysj_amd")
+    result = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert result.returncode == 0, result.stderr
+    names, module = result.stdout.strip().splitlines()
+    assert names.split(",") == [
+        "force_assembly", "gie_available", "gie_zonal_scatter", "group_by_source", "rmsnorm",
+        "rmsnorm_available", "segment_available", "segment_offsets", "segment_softmax", "segment_sum",
+        "zonal_scatter",
+    ]
+    assert module == "kernels._C"
