@@ -128,7 +128,8 @@ def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
     offsets = base["offsets"]
     bytes_per_step = 2 * edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + 2 * n_nodes * channels * 4
     n_sets = n_sets_for(bytes_per_step)
-    sets = [base] + [workloads.segment_softmax_config(n_nodes=n_nodes, seed=s, device="cuda")
+    # one graph; every input set draws fresh logits, envelopes and null logits
+    sets = [base] + [workloads.segment_softmax_features(edges, n_nodes, channels, seed=s, device="cuda")
                      for s in range(1, n_sets)]
 
     def step(i):

@@ -2,20 +2,35 @@
 // csrc/segment_softmax.cpp:235-343 of the reference; the arithmetic follows
 // the oracle chain python/reference/segment.py:63-118).
 //
-// Edge-major layout for rows of up to 64 vector chunks (C <= 256): LC lanes
-// cover one edge row (a power of two >= C/4), so one wave reads P = 64/LC
-// edges per load instruction (C = 8: 2 lanes per 32-byte row, 32 edges per
-// wave-load).  A 256-thread block owns four consecutive segments:
-//   * degree-binned schedule: a segment of at most RMAX*P edges is handled by
-//     one wave, its effective logits held in registers between the max, sum
-//     and write passes (one HBM read of logit/env, one write of alpha);
-//   * a longer segment (hub) is handled afterwards by all four waves of the
-//     block: each wave takes every fourth tile of P slots, per-wave partial
-//     maxima and sums are combined in LDS in a fixed order.
-// Reductions across the P edge slots of a wave are DPP / ds_swizzle /
-// ds_bpermute butterflies, so every result is reproducible bit for bit.
-// Rows wider than 64 chunks use a channel-major kernel (one lane per chunk,
-// sequential passes over the segment).
+// Per segment and channel, in the base-2 domain:
+//   y_e = logit_e * log2(e) + 2 log2(max(env_e, 1e-30))   (env_e > 0; else no mass)
+//   m = max(null * log2(e), max_e y_e),  w_e = 2^(y_e - m),  D = 2^(null log2 e - m) + sum_e w_e
+//   alpha_e = w_e * (1 / D),  null_alpha = 2^(null log2 e - m) * (1 / D)
+// which is the natural-base softmax of the reference with the exponent
+// rescaled once; v_exp_f32 / v_log_f32 / v_rcp_f32 evaluate it (relative error
+// a few 1e-7, inside the 1e-5 parity bar).
+//
+// Work decomposition (rows of up to 64 vector chunks, C <= 256):
+//   * LC lanes cover one edge row (LC = next power of two >= C / V).
+//   * Short segments (degree <= CAP) belong to G-lane groups (G = 32, or 64
+//     when LC = 64): the group issues all of its segment's loads at once into
+//     RMAX register tiles of PG = G / LC rows, so one memory round trip
+//     brings the whole segment in; max, sum and normalisation run on the
+//     registers and alpha is written once.
+//   * Long segments (degree > CAP) belong to a whole 256-thread workgroup:
+//     up to RMAXB tiles of PB = 256 / LC rows are staged in registers (one
+//     read); longer segments stream twice (an online max/sum pass, then the
+//     write pass).  Partial results of the four waves meet in LDS in a fixed
+//     order.
+//   * With a plan (dpa4k_segment_softmax_plan: the list of long segments of
+//     the CSR, built once per graph), workgroups [0, n_long) take one long
+//     segment each and the remaining workgroups take SPB consecutive
+//     segments and skip the long ones, so no workgroup runs a long segment
+//     after its short ones.  This is the degree-binned schedule.  Without a
+//     plan, a workgroup handles its own long segments after its short ones.
+// All reductions are DPP / ds_swizzle / ds_bpermute butterflies or fixed LDS
+// orders: results are reproducible bit for bit from run to run.
+// Rows wider than 64 chunks use a channel-major kernel (one lane per chunk).
 #include "common.h"
 
 namespace dpa4k {
@@ -23,476 +38,762 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
+constexpr float kLog2e = 1.4426950408889634f;
+// Plan layout (int64 words): [0] short-path capacity the plan was built for,
+// [1] n_long, [2, 2 + n_long) ascending ids of the long segments, then
+// scratch (one count per tile of segments).
+constexpr int64_t kPlanHeader = 2;
 
-// l_e = logit + 2 ln(max(env, 1e-30)) for env > 0, else -inf (no mass).
-__device__ __forceinline__ float effective_logit(float logit, float env) {
-  return env > 0.0f ? logit + 2.0f * logf(fmaxf(env, 1e-30f)) : -INFINITY;
+// ---------------------------------------------------------------------------
+// arithmetic
+// ---------------------------------------------------------------------------
+
+// y = logit * log2(e) + 2 log2(max(env, 1e-30)) for env > 0, else -inf.
+__device__ __forceinline__ float log2_weight(float logit, float env) {
+  return env > 0.0f ? logit * kLog2e + 2.0f * __builtin_amdgcn_logf(fmaxf(env, 1e-30f)) : -INFINITY;
 }
 
-// d l_e / d env = 2 / env where the clamp is inactive, 0 elsewhere.
+__device__ __forceinline__ float exp2_of(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 2^(y - peak), zero when the segment has no mass (peak = -inf).
+__device__ __forceinline__ float weight_of(float y, float peak) {
+  return peak > -INFINITY ? exp2_of(y - peak) : 0.0f;
+}
+
+// 1 / D, with D = 1 for a segment without mass.
+__device__ __forceinline__ float inverse_total(float total) {
+  return __builtin_amdgcn_rcpf(total > 0.0f ? total : 1.0f);
+}
+
+// d l_e / d env = 2 / env where the clamp of the oracle is inactive, 0 elsewhere.
 __device__ __forceinline__ float env_gradient(float row_sum, float env) {
   return env >= 1e-30f ? row_sum * 2.0f / env : 0.0f;
 }
 
-template <int LOG_LC>
-struct Shape {
-  static constexpr int LC = 1 << LOG_LC;   // lanes per edge row
-  static constexpr int P = 64 / LC;        // edges per wave-load
-  static constexpr int RMAX = LOG_LC <= 2 ? 4 : (LOG_LC == 3 ? 8 : 16);  // register tiles
+// Online (max, sum) state of a base-2 softmax: sum = sum_i 2^(y_i - max).
+__device__ __forceinline__ void online_add(float& peak, float& sum, float y) {
+  if (y == -INFINITY) return;
+  if (y > peak) {
+    sum = (peak == -INFINITY ? 0.0f : sum * exp2_of(peak - y)) + 1.0f;
+    peak = y;
+  } else {
+    sum += exp2_of(y - peak);
+  }
+}
+
+// Merges (peak_b, sum_b) into (peak, sum); symmetric in its operands.
+__device__ __forceinline__ void online_merge(float& peak, float& sum, float peak_b, float sum_b) {
+  const float top = fmaxf(peak, peak_b);
+  const float a = peak == -INFINITY ? 0.0f : sum * exp2_of(peak - top);
+  const float b = peak_b == -INFINITY ? 0.0f : sum_b * exp2_of(peak_b - top);
+  peak = top;
+  sum = a + b;
+}
+
+// Butterflies over the lane bits [FROM, TO) of the wave.
+template <int FROM, int TO>
+__device__ __forceinline__ float span_max(float v) {
+  if constexpr (FROM <= 1 && TO > 1) v = fmaxf(v, xor_lane<1>(v));
+  if constexpr (FROM <= 2 && TO > 2) v = fmaxf(v, xor_lane<2>(v));
+  if constexpr (FROM <= 4 && TO > 4) v = fmaxf(v, xor_lane<4>(v));
+  if constexpr (FROM <= 8 && TO > 8) v = fmaxf(v, xor_lane<8>(v));
+  if constexpr (FROM <= 16 && TO > 16) v = fmaxf(v, xor_lane<16>(v));
+  if constexpr (FROM <= 32 && TO > 32) v = fmaxf(v, xor_lane<32>(v));
+  return v;
+}
+
+template <int FROM, int TO>
+__device__ __forceinline__ float span_sum(float v) {
+  if constexpr (FROM <= 1 && TO > 1) v += xor_lane<1>(v);
+  if constexpr (FROM <= 2 && TO > 2) v += xor_lane<2>(v);
+  if constexpr (FROM <= 4 && TO > 4) v += xor_lane<4>(v);
+  if constexpr (FROM <= 8 && TO > 8) v += xor_lane<8>(v);
+  if constexpr (FROM <= 16 && TO > 16) v += xor_lane<16>(v);
+  if constexpr (FROM <= 32 && TO > 32) v += xor_lane<32>(v);
+  return v;
+}
+
+template <int MASK>
+__device__ __forceinline__ void merge_lane(float& peak, float& sum) {
+  const float peak_b = xor_lane<MASK>(peak);
+  const float sum_b = xor_lane<MASK>(sum);
+  online_merge(peak, sum, peak_b, sum_b);
+}
+
+template <int FROM, int TO>
+__device__ __forceinline__ void span_merge(float& peak, float& sum) {
+  if constexpr (FROM <= 1 && TO > 1) merge_lane<1>(peak, sum);
+  if constexpr (FROM <= 2 && TO > 2) merge_lane<2>(peak, sum);
+  if constexpr (FROM <= 4 && TO > 4) merge_lane<4>(peak, sum);
+  if constexpr (FROM <= 8 && TO > 8) merge_lane<8>(peak, sum);
+  if constexpr (FROM <= 16 && TO > 16) merge_lane<16>(peak, sum);
+  if constexpr (FROM <= 32 && TO > 32) merge_lane<32>(peak, sum);
+}
+
+// ---------------------------------------------------------------------------
+// geometry
+// ---------------------------------------------------------------------------
+
+template <int V, int LOG_LC>
+struct Geo {
+  static constexpr int LC = 1 << LOG_LC;               // lanes per edge row
+  static constexpr int LOG_G = LOG_LC > 5 ? LOG_LC : 5;
+  static constexpr int G = 1 << LOG_G;                 // lanes per short segment
+  static constexpr int PG = G / LC;                    // rows per group load
+  static constexpr int SPB = kBlock / G;               // segments per short workgroup
+  static constexpr int PB = kBlock / LC;               // rows per workgroup load
+  static constexpr int RMAX = 24 / V;                  // register tiles, short path
+  static constexpr int RMAXB = 16 / V;                 // register tiles, staged long path
+  static constexpr int CAP = RMAX * PG;                // longest short segment
+  static constexpr int UNROLL = 4;                     // loads in flight, streaming path
 };
 
-template <int V, int LOG_LC, bool kNull, bool kOrdered>
-__global__ __launch_bounds__(kBlock) void softmax_forward_kernel(
-    const float* __restrict__ logit, const float* __restrict__ env,
-    const int64_t* __restrict__ offsets, const float* __restrict__ null_logit,
-    const int64_t* __restrict__ order, float* __restrict__ alpha, float* __restrict__ null_alpha,
-    int64_t n_edges, int64_t n_nodes, int64_t channels) {
-  using S = Shape<LOG_LC>;
-  constexpr int LC = S::LC, P = S::P, RMAX = S::RMAX;
-  __shared__ float partial[kWaves][LC * V];
+// Lane roles inside a workgroup for rows of LC lanes.
+template <int V, int LOG_LC>
+struct Lanes {
+  using S = Geo<V, LOG_LC>;
+  int lane, wave, k, p, pb, gidx;
+  bool live;
+  int64_t column;
+  __device__ Lanes(int64_t chunks) {
+    lane = threadIdx.x & 63;
+    wave = threadIdx.x >> 6;
+    k = lane & (S::LC - 1);
+    p = (threadIdx.x & (S::G - 1)) >> LOG_LC;
+    pb = threadIdx.x >> LOG_LC;
+    gidx = threadIdx.x >> S::LOG_G;
+    live = k < chunks;
+    column = static_cast<int64_t>(k) * V;
+  }
+};
 
+// Segment bounds of the SPB segments [first, first + SPB) held by lanes
+// 0..SPB of every wave (one vector load); lane i gets segment first + i.
+struct BlockBounds {
+  int64_t lo, hi;
+};
+
+template <int SPB>
+__device__ __forceinline__ BlockBounds block_bounds(const int64_t* __restrict__ offsets, int64_t first,
+                                                    int64_t n_nodes, int64_t n_edges) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int k = lane & (LC - 1);
-  const int p = lane >> LOG_LC;
-  const bool live = k < channels / V;
-  const int64_t column = static_cast<int64_t>(k) * V;
-  const int64_t first = static_cast<int64_t>(blockIdx.x) * kWaves;
+  const int64_t last = first + SPB < n_nodes ? first + SPB : n_nodes;
+  const int64_t index = first + lane < last ? first + lane : last;
+  int64_t lo = offsets[index];
+  lo = lo < 0 ? 0 : (lo > n_edges ? n_edges : lo);
+  int64_t hi = __shfl_down(lo, 1);
+  if (hi < lo || first + lane >= last) hi = lo;
+  return {lo, hi};
+}
 
-  // ---- short segments: one wave each, logits staged in registers --------
-  {
-    const int64_t segment = first + wave;
-    int64_t begin = 0, end = 0;
-    if (segment < n_nodes) segment_bounds(offsets, segment, n_edges, begin, end);
-    if (segment < n_nodes && end - begin <= RMAX * P) {
-      const int64_t degree = end - begin;
-      float value[RMAX][V];
-      int64_t edge[RMAX];
-      float peak[V];
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+
+struct ForwardArgs {
+  const float* logit;
+  const float* env;
+  const int64_t* offsets;
+  const float* null_logit;
+  const int64_t* order;
+  float* alpha;
+  float* null_alpha;
+  int64_t n_edges, n_nodes, channels;
+};
+
+// One long segment [begin, end) of `segment`, processed by the whole workgroup.
+template <int V, int LOG_LC, bool kNull, bool kOrdered>
+__device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end,
+                             float (*partial)[2][Geo<V, LOG_LC>::LC * V]) {
+  using S = Geo<V, LOG_LC>;
+  constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
+  const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t degree = end - begin;
+  float nv[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
+  for (int v = 0; v < V; ++v) nv[v] = -INFINITY;
+  if (kNull && L.live) {
+    const fvec<V> n0 = load_vec<V>(a.null_logit + segment * a.channels + L.column);
 #pragma unroll
-      for (int i = 0; i < RMAX; ++i) {
-        edge[i] = -1;
+    for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
+  }
+  float peak[V], total[V];
+  if (degree <= RMAXB * PB) {
+    // staged: every row of the segment in registers, one read
+    float value[RMAXB][V];
+    int64_t edge[RMAXB];
 #pragma unroll
-        for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
-        if (static_cast<int64_t>(i) * P < degree) {
-          const int64_t slot = begin + static_cast<int64_t>(i) * P + p;
-          if (slot < end && live) {
-            const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-            if (e >= 0) {
-              edge[i] = e;
-              const float envelope = env[e];
-              const fvec<V> x = load_vec<V>(logit + e * channels + column);
+    for (int i = 0; i < RMAXB; ++i) {
+      edge[i] = -1;
 #pragma unroll
-              for (int v = 0; v < V; ++v) value[i][v] = effective_logit(x.v[v], envelope);
-            }
-          }
-        }
+      for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
+      const int64_t slot = begin + static_cast<int64_t>(i) * PB + L.pb;
+      if (slot < end && L.live) {
+        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+        if (e >= 0) {
+          edge[i] = e;
+          const float envelope = a.env[e];
+          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
 #pragma unroll
-        for (int v = 0; v < V; ++v) peak[v] = fmaxf(peak[v], value[i][v]);
-      }
-      float null_value[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        peak[v] = across_max<LC>(peak[v]);
-        null_value[v] = -INFINITY;
-      }
-      if (kNull && live) {
-        const fvec<V> n0 = load_vec<V>(null_logit + segment * channels + column);
-#pragma unroll
-        for (int v = 0; v < V; ++v) null_value[v] = n0.v[v];
-      }
-      float total[V], null_weight[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        if (kNull) peak[v] = fmaxf(peak[v], null_value[v]);
-        total[v] = 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < RMAX; ++i) {
-        if (static_cast<int64_t>(i) * P < degree) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float w = peak[v] > -INFINITY ? expf(value[i][v] - peak[v]) : 0.0f;
-            value[i][v] = w;
-            total[v] += w;
-          }
+          for (int v = 0; v < V; ++v) value[i][v] = log2_weight(x.v[v], envelope);
         }
       }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      peak[v] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < RMAXB; ++i) peak[v] = fmaxf(peak[v], value[i][v]);
+      peak[v] = span_max<LC, 64>(peak[v]);
+    }
+    if ((L.lane >> LOG_LC) == 0)
+#pragma unroll
+      for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = peak[v];
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float m = partial[0][0][L.k * V + v];
+      for (int q = 1; q < kWaves; ++q) m = fmaxf(m, partial[q][0][L.k * V + v]);
+      peak[v] = kNull ? fmaxf(m, nv[v]) : m;
+      total[v] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < RMAXB; ++i)
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        total[v] = across_sum<LC>(total[v]);
-        null_weight[v] = kNull && peak[v] > -INFINITY ? expf(null_value[v] - peak[v]) : 0.0f;
-        total[v] = total[v] + null_weight[v];
-        if (!(total[v] > 0.0f)) total[v] = 1.0f;
+        const float w = weight_of(value[i][v], peak[v]);
+        value[i][v] = w;
+        total[v] += w;
       }
 #pragma unroll
-      for (int i = 0; i < RMAX; ++i) {
-        if (static_cast<int64_t>(i) * P < degree && edge[i] >= 0) {
-          fvec<V> out;
+    for (int v = 0; v < V; ++v) total[v] = span_sum<LC, 64>(total[v]);
+    if ((L.lane >> LOG_LC) == 0)
 #pragma unroll
-          for (int v = 0; v < V; ++v) out.v[v] = value[i][v] / total[v];
-          store_vec_stream<V>(alpha + edge[i] * channels + column, out);
-        }
-      }
-      if (kNull && p == 0 && live) {
+      for (int v = 0; v < V; ++v) partial[L.wave][1][L.k * V + v] = total[v];
+    __syncthreads();
+    float nw[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float sum = partial[0][1][L.k * V + v];
+      for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][1][L.k * V + v];
+      nw[v] = kNull ? weight_of(nv[v], peak[v]) : 0.0f;
+      total[v] = inverse_total(sum + nw[v]);
+    }
+#pragma unroll
+    for (int i = 0; i < RMAXB; ++i) {
+      if (edge[i] >= 0) {
         fvec<V> out;
 #pragma unroll
-        for (int v = 0; v < V; ++v) out.v[v] = null_weight[v] / total[v];
-        store_vec<V>(null_alpha + segment * channels + column, out);
+        for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
+        store_vec_stream<V>(a.alpha + edge[i] * a.channels + L.column, out);
+      }
+    }
+    if (kNull && threadIdx.x < LC && L.live) {
+      fvec<V> out;
+#pragma unroll
+      for (int v = 0; v < V; ++v) out.v[v] = nw[v] * total[v];
+      store_vec<V>(a.null_alpha + segment * a.channels + L.column, out);
+    }
+    __syncthreads();  // partial[] is reused by the next long segment
+    return;
+  }
+
+  // streaming: online max/sum pass, then the write pass
+  float run_sum[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    peak[v] = -INFINITY;
+    run_sum[v] = 0.0f;
+  }
+  for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
+    float value[S::UNROLL][V];
+#pragma unroll
+    for (int u = 0; u < S::UNROLL; ++u) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) value[u][v] = -INFINITY;
+      const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
+      if (slot < end && L.live) {
+        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+        if (e >= 0) {
+          const float envelope = a.env[e];
+          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
+#pragma unroll
+          for (int v = 0; v < V; ++v) value[u][v] = log2_weight(x.v[v], envelope);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < S::UNROLL; ++u)
+#pragma unroll
+      for (int v = 0; v < V; ++v) online_add(peak[v], run_sum[v], value[u][v]);
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) span_merge<LC, 64>(peak[v], run_sum[v]);
+  if ((L.lane >> LOG_LC) == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      partial[L.wave][0][L.k * V + v] = peak[v];
+      partial[L.wave][1][L.k * V + v] = run_sum[v];
+    }
+  __syncthreads();
+  float nw[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    float m = partial[0][0][L.k * V + v];
+    float s = partial[0][1][L.k * V + v];
+    for (int q = 1; q < kWaves; ++q) online_merge(m, s, partial[q][0][L.k * V + v], partial[q][1][L.k * V + v]);
+    if (kNull) online_add(m, s, nv[v]);
+    peak[v] = m;
+    nw[v] = kNull ? weight_of(nv[v], m) : 0.0f;
+    total[v] = inverse_total(s);
+  }
+  for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
+#pragma unroll
+    for (int u = 0; u < S::UNROLL; ++u) {
+      const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
+      if (slot < end && L.live) {
+        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+        if (e >= 0) {
+          const float envelope = a.env[e];
+          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
+          fvec<V> out;
+#pragma unroll
+          for (int v = 0; v < V; ++v) out.v[v] = weight_of(log2_weight(x.v[v], envelope), peak[v]) * total[v];
+          store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
+        }
       }
     }
   }
-
-  // ---- long segments: the whole block, three streaming passes -----------
-  for (int w = 0; w < kWaves; ++w) {
-    const int64_t segment = first + w;
-    if (segment >= n_nodes) break;
-    int64_t begin, end;
-    segment_bounds(offsets, segment, n_edges, begin, end);
-    if (end - begin <= RMAX * P) continue;
-    const int64_t tiles = (end - begin + P - 1) / P;
-
-    float peak[V];
+  if (kNull && threadIdx.x < LC && L.live) {
+    fvec<V> out;
 #pragma unroll
-    for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
-    for (int64_t t = wave; t < tiles; t += kWaves) {
-      const int64_t slot = begin + t * P + p;
-      if (slot < end && live) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) {
-          const float envelope = env[e];
-          const fvec<V> x = load_vec<V>(logit + e * channels + column);
+    for (int v = 0; v < V; ++v) out.v[v] = nw[v] * total[v];
+    store_vec<V>(a.null_alpha + segment * a.channels + L.column, out);
+  }
+  __syncthreads();
+}
+
+// Short segment of this lane's group (degree <= CAP), all in registers.
+template <int V, int LOG_LC, bool kNull, bool kOrdered>
+__device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
+  using S = Geo<V, LOG_LC>;
+  constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
+  const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t degree = end - begin;
+  float nv[V];
 #pragma unroll
-          for (int v = 0; v < V; ++v) peak[v] = fmaxf(peak[v], effective_logit(x.v[v], envelope));
-        }
+  for (int v = 0; v < V; ++v) nv[v] = -INFINITY;
+  if (kNull && L.live) {
+    const fvec<V> n0 = load_vec<V>(a.null_logit + segment * a.channels + L.column);
+#pragma unroll
+    for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
+  }
+  float value[RMAX][V];
+  int64_t edge[RMAX];
+  float peak[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+    edge[i] = -1;
+#pragma unroll
+    for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
+    const int64_t slot = begin + static_cast<int64_t>(i) * PG + L.p;
+    if (slot < end && L.live) {
+      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+      if (e >= 0) {
+        edge[i] = e;
+        const float envelope = a.env[e];
+        const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
+#pragma unroll
+        for (int v = 0; v < V; ++v) value[i][v] = log2_weight(x.v[v], envelope);
       }
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) peak[v] = across_max<LC>(peak[v]);
-    if (p == 0)
+    for (int v = 0; v < V; ++v) peak[v] = fmaxf(peak[v], value[i][v]);
+  }
+  float total[V], nw[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) partial[wave][k * V + v] = peak[v];
-    __syncthreads();
-    float null_value[V];
+  for (int v = 0; v < V; ++v) {
+    peak[v] = span_max<LC, G>(peak[v]);
+    if (kNull) peak[v] = fmaxf(peak[v], nv[v]);
+    total[v] = 0.0f;
+  }
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      float m = partial[0][k * V + v];
-      for (int q = 1; q < kWaves; ++q) m = fmaxf(m, partial[q][k * V + v]);
-      peak[v] = m;
-      null_value[v] = -INFINITY;
-    }
-    if (kNull && live) {
-      const fvec<V> n0 = load_vec<V>(null_logit + segment * channels + column);
+  for (int i = 0; i < RMAX; ++i) {
+    if (static_cast<int64_t>(i) * PG < degree) {
 #pragma unroll
-      for (int v = 0; v < V; ++v) null_value[v] = n0.v[v];
-    }
-    if (kNull)
-#pragma unroll
-      for (int v = 0; v < V; ++v) peak[v] = fmaxf(peak[v], null_value[v]);
-    __syncthreads();
-
-    float total[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) total[v] = 0.0f;
-    for (int64_t t = wave; t < tiles; t += kWaves) {
-      const int64_t slot = begin + t * P + p;
-      if (slot < end && live) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) {
-          const float envelope = env[e];
-          const fvec<V> x = load_vec<V>(logit + e * channels + column);
-#pragma unroll
-          for (int v = 0; v < V; ++v)
-            if (peak[v] > -INFINITY) total[v] += expf(effective_logit(x.v[v], envelope) - peak[v]);
-        }
+      for (int v = 0; v < V; ++v) {
+        const float w = weight_of(value[i][v], peak[v]);
+        value[i][v] = w;
+        total[v] += w;
       }
     }
+  }
 #pragma unroll
-    for (int v = 0; v < V; ++v) total[v] = across_sum<LC>(total[v]);
-    if (p == 0)
+  for (int v = 0; v < V; ++v) {
+    total[v] = span_sum<LC, G>(total[v]);
+    nw[v] = kNull ? weight_of(nv[v], peak[v]) : 0.0f;
+    total[v] = inverse_total(total[v] + nw[v]);
+  }
 #pragma unroll
-      for (int v = 0; v < V; ++v) partial[wave][k * V + v] = total[v];
-    __syncthreads();
-    float null_weight[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-      float sum = partial[0][k * V + v];
-      for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][k * V + v];
-      null_weight[v] = kNull && peak[v] > -INFINITY ? expf(null_value[v] - peak[v]) : 0.0f;
-      sum = sum + null_weight[v];
-      total[v] = sum > 0.0f ? sum : 1.0f;
-    }
-    __syncthreads();
-
-    for (int64_t t = wave; t < tiles; t += kWaves) {
-      const int64_t slot = begin + t * P + p;
-      if (slot < end && live) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) {
-          const float envelope = env[e];
-          const fvec<V> x = load_vec<V>(logit + e * channels + column);
-          fvec<V> out;
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float w8 = peak[v] > -INFINITY
-                                 ? expf(effective_logit(x.v[v], envelope) - peak[v])
-                                 : 0.0f;
-            out.v[v] = w8 / total[v];
-          }
-          store_vec_stream<V>(alpha + e * channels + column, out);
-        }
-      }
-    }
-    if (kNull && wave == 0 && p == 0 && live) {
+  for (int i = 0; i < RMAX; ++i) {
+    if (edge[i] >= 0) {
       fvec<V> out;
 #pragma unroll
-      for (int v = 0; v < V; ++v) out.v[v] = null_weight[v] / total[v];
-      store_vec<V>(null_alpha + segment * channels + column, out);
+      for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
+      store_vec_stream<V>(a.alpha + edge[i] * a.channels + L.column, out);
     }
+  }
+  if (kNull && L.p == 0 && L.live) {
+    fvec<V> out;
+#pragma unroll
+    for (int v = 0; v < V; ++v) out.v[v] = nw[v] * total[v];
+    store_vec<V>(a.null_alpha + segment * a.channels + L.column, out);
+  }
+}
+
+// Workgroups [0, n_long) take the planned long segments; the others take SPB
+// consecutive segments each.  Without a plan (or with a plan built for
+// another capacity, detected from its header) the first n_long workgroups
+// exit and every other workgroup also runs its own long segments.
+template <int V, int LOG_LC, bool kNull, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, const int64_t* __restrict__ plan,
+                                                                 int64_t n_long) {
+  using S = Geo<V, LOG_LC>;
+  __shared__ float partial[kWaves][2][S::LC * V];
+  const bool planned = plan != nullptr && plan[0] == S::CAP;
+  if (static_cast<int64_t>(blockIdx.x) < n_long) {
+    if (!planned) return;
+    const int64_t segment = plan[kPlanHeader + blockIdx.x];
+    if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
+    int64_t begin, end;
+    segment_bounds(a.offsets, segment, a.n_edges, begin, end);
+    forward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
+    return;
+  }
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) - n_long) * S::SPB;
+  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
+  const int gidx = threadIdx.x >> S::LOG_G;
+  const int64_t begin = __shfl(bb.lo, gidx);
+  const int64_t end = __shfl(bb.hi, gidx);
+  const int64_t segment = first + gidx;
+  if (segment < a.n_nodes && end - begin <= S::CAP)
+    forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
+  if (planned) return;
+  // no plan: this workgroup's long segments, one at a time
+  const int lane = threadIdx.x & 63;
+  unsigned long long longs =
+      __ballot(lane < S::SPB && first + lane < a.n_nodes && bb.hi - bb.lo > S::CAP);
+  while (longs != 0ull) {
+    const int s = __ffsll(static_cast<long long>(longs)) - 1;
+    longs &= longs - 1ull;
+    forward_long<V, LOG_LC, kNull, kOrdered>(a, first + s, __shfl(bb.lo, s), __shfl(bb.hi, s), partial);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+
+struct BackwardArgs {
+  const float* alpha;
+  const float* grad_alpha;
+  const float* env;
+  const int64_t* offsets;
+  const float* null_alpha;
+  const float* grad_null_alpha;
+  const int64_t* order;
+  float* grad_logit;
+  float* grad_null_logit;
+  float* grad_env;
+  int64_t n_edges, n_nodes, channels;
+};
+
+// grad_logit row of edge e from alpha, grad_alpha and the segment's S;
+// grad_env[e] from the row sum over the LC lanes of the row.
+template <int V, int LOG_LC>
+__device__ __forceinline__ void backward_row(const BackwardArgs& a, const Lanes<V, LOG_LC>& L, int64_t e,
+                                             const float (&x)[V], const float (&g)[V], const float (&expect)[V],
+                                             float envelope) {
+  fvec<V> out;
+  float row = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    out.v[v] = x[v] * (g[v] - expect[v]);
+    row += out.v[v];
+  }
+  row = span_sum<1, Geo<V, LOG_LC>::LC>(e >= 0 && L.live ? row : 0.0f);
+  if (e >= 0) {
+    if (L.live) store_vec_stream<V>(a.grad_logit + e * a.channels + L.column, out);
+    if (L.k == 0) a.grad_env[e] = env_gradient(row, envelope);
   }
 }
 
 template <int V, int LOG_LC, bool kNull, bool kOrdered>
-__global__ __launch_bounds__(kBlock) void softmax_backward_kernel(
-    const float* __restrict__ alpha, const float* __restrict__ grad_alpha,
-    const float* __restrict__ env, const int64_t* __restrict__ offsets,
-    const float* __restrict__ null_alpha, const float* __restrict__ grad_null_alpha,
-    const int64_t* __restrict__ order, float* __restrict__ grad_logit,
-    float* __restrict__ grad_null_logit, float* __restrict__ grad_env, int64_t n_edges,
-    int64_t n_nodes, int64_t channels) {
-  using S = Shape<LOG_LC>;
-  constexpr int LC = S::LC, P = S::P, RMAX = S::RMAX;
-  __shared__ float partial[kWaves][LC * V];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int k = lane & (LC - 1);
-  const int p = lane >> LOG_LC;
-  const bool live = k < channels / V;
-  const int64_t column = static_cast<int64_t>(k) * V;
-  const int64_t first = static_cast<int64_t>(blockIdx.x) * kWaves;
-
-  {
-    const int64_t segment = first + wave;
-    int64_t begin = 0, end = 0;
-    if (segment < n_nodes) segment_bounds(offsets, segment, n_edges, begin, end);
-    if (segment < n_nodes && end - begin <= RMAX * P) {
-      const int64_t degree = end - begin;
-      float a[RMAX][V], ga[RMAX][V];
-      int64_t edge[RMAX];
-      float expect[V];
+__device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end,
+                              float (*partial)[2][Geo<V, LOG_LC>::LC * V]) {
+  using S = Geo<V, LOG_LC>;
+  constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
+  const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t degree = end - begin;
+  float a0[V], g0[V], expect[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) expect[v] = 0.0f;
+  for (int v = 0; v < V; ++v) a0[v] = g0[v] = expect[v] = 0.0f;
+  if (kNull && L.live) {
+    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + L.column);
+    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + L.column);
 #pragma unroll
-      for (int i = 0; i < RMAX; ++i) {
-        edge[i] = -1;
+    for (int v = 0; v < V; ++v) {
+      a0[v] = x.v[v];
+      g0[v] = g.v[v];
+    }
+  }
+  const bool staged = degree <= RMAXB * PB;
+  float xs[RMAXB][V], gs[RMAXB][V], envs[RMAXB];
+  int64_t edge[RMAXB];
+  if (staged) {
 #pragma unroll
-        for (int v = 0; v < V; ++v) a[i][v] = ga[i][v] = 0.0f;
-        if (static_cast<int64_t>(i) * P < degree) {
-          const int64_t slot = begin + static_cast<int64_t>(i) * P + p;
-          if (slot < end && live) {
-            const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-            if (e >= 0) {
-              edge[i] = e;
-              const fvec<V> x = load_vec<V>(alpha + e * channels + column);
-              const fvec<V> g = load_vec<V>(grad_alpha + e * channels + column);
+    for (int i = 0; i < RMAXB; ++i) {
+      edge[i] = -1;
+      envs[i] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
+      const int64_t slot = begin + static_cast<int64_t>(i) * PB + L.pb;
+      if (slot < end) {
+        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+        if (e >= 0) {
+          edge[i] = e;
+          envs[i] = a.env[e];
+          if (L.live) {
+            const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
+            const fvec<V> g = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              xs[i][v] = x.v[v];
+              gs[i][v] = g.v[v];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
+    }
+  } else {
+    for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
+      float x[S::UNROLL][V], g[S::UNROLL][V];
+#pragma unroll
+      for (int u = 0; u < S::UNROLL; ++u) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[u][v] = g[u][v] = 0.0f;
+        const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
+        if (slot < end && L.live) {
+          const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+          if (e >= 0) {
+            const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + L.column);
+            const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              x[u][v] = xv.v[v];
+              g[u][v] = gv.v[v];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < S::UNROLL; ++u)
+#pragma unroll
+        for (int v = 0; v < V; ++v) expect[v] = expect[v] + x[u][v] * g[u][v];
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v]);
+  if ((L.lane >> LOG_LC) == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = expect[v];
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    float sum = partial[0][0][L.k * V + v];
+    for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][0][L.k * V + v];
+    expect[v] = kNull ? sum + a0[v] * g0[v] : sum;
+  }
+  if (staged) {
+#pragma unroll
+    for (int i = 0; i < RMAXB; ++i) backward_row<V, LOG_LC>(a, L, edge[i], xs[i], gs[i], expect, envs[i]);
+  } else {
+    for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
+#pragma unroll
+      for (int u = 0; u < S::UNROLL; ++u) {
+        const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
+        int64_t e = -1;
+        float x[V], g[V], envelope = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[v] = g[v] = 0.0f;
+        if (slot < end) {
+          e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+          if (e >= 0) {
+            envelope = a.env[e];
+            if (L.live) {
+              const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + L.column);
+              const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                a[i][v] = x.v[v];
-                ga[i][v] = g.v[v];
+                x[v] = xv.v[v];
+                g[v] = gv.v[v];
               }
             }
           }
         }
-#pragma unroll
-        for (int v = 0; v < V; ++v) expect[v] = expect[v] + a[i][v] * ga[i][v];
-      }
-      float a0[V], g0[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        expect[v] = across_sum<LC>(expect[v]);
-        a0[v] = g0[v] = 0.0f;
-      }
-      if (kNull && live) {
-        const fvec<V> x = load_vec<V>(null_alpha + segment * channels + column);
-        const fvec<V> g = load_vec<V>(grad_null_alpha + segment * channels + column);
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          a0[v] = x.v[v];
-          g0[v] = g.v[v];
-        }
-      }
-      if (kNull)
-#pragma unroll
-        for (int v = 0; v < V; ++v) expect[v] = expect[v] + a0[v] * g0[v];
-#pragma unroll
-      for (int i = 0; i < RMAX; ++i) {
-        if (static_cast<int64_t>(i) * P < degree) {
-          fvec<V> out;
-          float row = 0.0f;
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            out.v[v] = a[i][v] * (ga[i][v] - expect[v]);
-            row += out.v[v];
-          }
-          row = group_sum<LC>(edge[i] >= 0 ? row : 0.0f);
-          if (edge[i] >= 0) {
-            store_vec_stream<V>(grad_logit + edge[i] * channels + column, out);
-            if (k == 0) grad_env[edge[i]] = env_gradient(row, env[edge[i]]);
-          }
-        }
-      }
-      if (kNull && p == 0 && live) {
-        fvec<V> out;
-#pragma unroll
-        for (int v = 0; v < V; ++v) out.v[v] = a0[v] * (g0[v] - expect[v]);
-        store_vec<V>(grad_null_logit + segment * channels + column, out);
+        backward_row<V, LOG_LC>(a, L, e, x, g, expect, envelope);
       }
     }
   }
+  if (kNull && threadIdx.x < LC && L.live) {
+    fvec<V> out;
+#pragma unroll
+    for (int v = 0; v < V; ++v) out.v[v] = a0[v] * (g0[v] - expect[v]);
+    store_vec<V>(a.grad_null_logit + segment * a.channels + L.column, out);
+  }
+  __syncthreads();
+}
 
-  for (int w = 0; w < kWaves; ++w) {
-    const int64_t segment = first + w;
-    if (segment >= n_nodes) break;
-    int64_t begin, end;
-    segment_bounds(offsets, segment, n_edges, begin, end);
-    if (end - begin <= RMAX * P) continue;
-    const int64_t tiles = (end - begin + P - 1) / P;
-
-    float expect[V];
+template <int V, int LOG_LC, bool kNull, bool kOrdered>
+__device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
+  using S = Geo<V, LOG_LC>;
+  constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
+  const Lanes<V, LOG_LC> L(a.channels / V);
+  float a0[V], g0[V], expect[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) expect[v] = 0.0f;
-    for (int64_t t = wave; t < tiles; t += kWaves) {
-      const int64_t slot = begin + t * P + p;
-      if (slot < end && live) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) {
-          const fvec<V> x = load_vec<V>(alpha + e * channels + column);
-          const fvec<V> g = load_vec<V>(grad_alpha + e * channels + column);
-#pragma unroll
-          for (int v = 0; v < V; ++v) expect[v] = expect[v] + x.v[v] * g.v[v];
-        }
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < V; ++v) expect[v] = across_sum<LC>(expect[v]);
-    if (p == 0)
-#pragma unroll
-      for (int v = 0; v < V; ++v) partial[wave][k * V + v] = expect[v];
-    __syncthreads();
-    float a0[V], g0[V];
+  for (int v = 0; v < V; ++v) a0[v] = g0[v] = expect[v] = 0.0f;
+  if (kNull && L.live) {
+    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + L.column);
+    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + L.column);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      float sum = partial[0][k * V + v];
-      for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][k * V + v];
-      expect[v] = sum;
-      a0[v] = g0[v] = 0.0f;
+      a0[v] = x.v[v];
+      g0[v] = g.v[v];
     }
-    __syncthreads();
-    if (kNull && live) {
-      const fvec<V> x = load_vec<V>(null_alpha + segment * channels + column);
-      const fvec<V> g = load_vec<V>(grad_null_alpha + segment * channels + column);
+  }
+  float xs[RMAX][V], gs[RMAX][V], envs[RMAX];
+  int64_t edge[RMAX];
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        a0[v] = x.v[v];
-        g0[v] = g.v[v];
-      }
-    }
-    if (kNull)
+  for (int i = 0; i < RMAX; ++i) {
+    edge[i] = -1;
+    envs[i] = 0.0f;
 #pragma unroll
-      for (int v = 0; v < V; ++v) expect[v] = expect[v] + a0[v] * g0[v];
-
-    for (int64_t t = wave; t < tiles; t += kWaves) {
-      const int64_t slot = begin + t * P + p;
-      int64_t e = -1;
-      fvec<V> out;
-      float row = 0.0f;
-      if (slot < end && live) {
-        e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) {
-          const fvec<V> x = load_vec<V>(alpha + e * channels + column);
-          const fvec<V> g = load_vec<V>(grad_alpha + e * channels + column);
+    for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
+    const int64_t slot = begin + static_cast<int64_t>(i) * PG + L.p;
+    if (slot < end) {
+      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+      if (e >= 0) {
+        edge[i] = e;
+        envs[i] = a.env[e];
+        if (L.live) {
+          const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
+          const fvec<V> g = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
 #pragma unroll
           for (int v = 0; v < V; ++v) {
-            out.v[v] = x.v[v] * (g.v[v] - expect[v]);
-            row += out.v[v];
+            xs[i][v] = x.v[v];
+            gs[i][v] = g.v[v];
           }
         }
       }
-      row = group_sum<LC>(row);
-      if (e >= 0) {
-        store_vec_stream<V>(grad_logit + e * channels + column, out);
-        if (k == 0) grad_env[e] = env_gradient(row, env[e]);
-      }
     }
-    if (kNull && wave == 0 && p == 0 && live) {
-      fvec<V> out;
 #pragma unroll
-      for (int v = 0; v < V; ++v) out.v[v] = a0[v] * (g0[v] - expect[v]);
-      store_vec<V>(grad_null_logit + segment * channels + column, out);
-    }
+    for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    expect[v] = span_sum<LC, G>(expect[v]);
+    if (kNull) expect[v] = expect[v] + a0[v] * g0[v];
+  }
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) backward_row<V, LOG_LC>(a, L, edge[i], xs[i], gs[i], expect, envs[i]);
+  if (kNull && L.p == 0 && L.live) {
+    fvec<V> out;
+#pragma unroll
+    for (int v = 0; v < V; ++v) out.v[v] = a0[v] * (g0[v] - expect[v]);
+    store_vec<V>(a.grad_null_logit + segment * a.channels + L.column, out);
   }
 }
 
-// ---- rows wider than 64 chunks: one wave per segment, lane per chunk ----
+template <int V, int LOG_LC, bool kNull, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a, const int64_t* __restrict__ plan,
+                                                                  int64_t n_long) {
+  using S = Geo<V, LOG_LC>;
+  __shared__ float partial[kWaves][2][S::LC * V];
+  const bool planned = plan != nullptr && plan[0] == S::CAP;
+  if (static_cast<int64_t>(blockIdx.x) < n_long) {
+    if (!planned) return;
+    const int64_t segment = plan[kPlanHeader + blockIdx.x];
+    if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
+    int64_t begin, end;
+    segment_bounds(a.offsets, segment, a.n_edges, begin, end);
+    backward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
+    return;
+  }
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) - n_long) * S::SPB;
+  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
+  const int gidx = threadIdx.x >> S::LOG_G;
+  const int64_t begin = __shfl(bb.lo, gidx);
+  const int64_t end = __shfl(bb.hi, gidx);
+  const int64_t segment = first + gidx;
+  if (segment < a.n_nodes && end - begin <= S::CAP)
+    backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
+  if (planned) return;
+  const int lane = threadIdx.x & 63;
+  unsigned long long longs =
+      __ballot(lane < S::SPB && first + lane < a.n_nodes && bb.hi - bb.lo > S::CAP);
+  while (longs != 0ull) {
+    const int s = __ffsll(static_cast<long long>(longs)) - 1;
+    longs &= longs - 1ull;
+    backward_long<V, LOG_LC, kNull, kOrdered>(a, first + s, __shfl(bb.lo, s), __shfl(bb.hi, s), partial);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// rows wider than 64 chunks: one wave per segment, lane per channel
+// ---------------------------------------------------------------------------
 
 template <bool kOrdered>
-__global__ __launch_bounds__(kBlock) void softmax_forward_wide_kernel(
-    const float* __restrict__ logit, const float* __restrict__ env,
-    const int64_t* __restrict__ offsets, const float* __restrict__ null_logit,
-    const int64_t* __restrict__ order, float* __restrict__ alpha, float* __restrict__ null_alpha,
-    int64_t n_edges, int64_t n_nodes, int64_t channels) {
+__global__ __launch_bounds__(kBlock) void softmax_forward_wide_kernel(ForwardArgs a) {
   const int64_t segment = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (segment >= n_nodes) return;
+  if (segment >= a.n_nodes) return;
   const int lane = threadIdx.x & 63;
+  const int64_t channels = a.channels;
   int64_t begin, end;
-  segment_bounds(offsets, segment, n_edges, begin, end);
+  segment_bounds(a.offsets, segment, a.n_edges, begin, end);
   for (int64_t c = lane; c < channels; c += 64) {
-    float peak = -INFINITY;
+    float peak = -INFINITY, sum = 0.0f;
     for (int64_t slot = begin; slot < end; ++slot) {
-      const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-      if (e >= 0) peak = fmaxf(peak, effective_logit(logit[e * channels + c], env[e]));
+      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+      if (e >= 0) online_add(peak, sum, log2_weight(a.logit[e * channels + c], a.env[e]));
     }
-    const float null_value = null_logit != nullptr ? null_logit[segment * channels + c] : -INFINITY;
-    if (null_logit != nullptr) peak = fmaxf(peak, null_value);
-    float total = 0.0f;
-    if (peak > -INFINITY)
-      for (int64_t slot = begin; slot < end; ++slot) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) total = total + expf(effective_logit(logit[e * channels + c], env[e]) - peak);
-      }
-    const float null_weight =
-        null_logit != nullptr && peak > -INFINITY ? expf(null_value - peak) : 0.0f;
-    total = total + null_weight;
-    if (!(total > 0.0f)) total = 1.0f;
+    float null_value = -INFINITY;
+    if (a.null_logit != nullptr) {
+      null_value = a.null_logit[segment * channels + c] * kLog2e;
+      online_add(peak, sum, null_value);
+    }
+    const float inverse = inverse_total(sum);
     for (int64_t slot = begin; slot < end; ++slot) {
-      const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e < 0) continue;
-      const float w = peak > -INFINITY
-                          ? expf(effective_logit(logit[e * channels + c], env[e]) - peak)
-                          : 0.0f;
-      alpha[e * channels + c] = w / total;
+      a.alpha[e * channels + c] = weight_of(log2_weight(a.logit[e * channels + c], a.env[e]), peak) * inverse;
     }
-    if (null_logit != nullptr) null_alpha[segment * channels + c] = null_weight / total;
+    if (a.null_logit != nullptr) a.null_alpha[segment * channels + c] = weight_of(null_value, peak) * inverse;
   }
 }
 
 template <bool kOrdered>
-__global__ __launch_bounds__(kBlock) void softmax_backward_wide_kernel(
-    const float* __restrict__ alpha, const float* __restrict__ grad_alpha,
-    const float* __restrict__ env, const int64_t* __restrict__ offsets,
-    const float* __restrict__ null_alpha, const float* __restrict__ grad_null_alpha,
-    const int64_t* __restrict__ order, float* __restrict__ grad_logit,
-    float* __restrict__ grad_null_logit, float* __restrict__ grad_env, int64_t n_edges,
-    int64_t n_nodes, int64_t channels) {
+__global__ __launch_bounds__(kBlock) void softmax_backward_wide_kernel(BackwardArgs a) {
   const int64_t segment = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (segment >= n_nodes) return;
+  if (segment >= a.n_nodes) return;
   const int lane = threadIdx.x & 63;
+  const int64_t channels = a.channels;
   int64_t begin, end;
-  segment_bounds(offsets, segment, n_edges, begin, end);
-  const bool has_null = null_alpha != nullptr;
+  segment_bounds(a.offsets, segment, a.n_edges, begin, end);
+  const bool has_null = a.null_alpha != nullptr;
   // Channel windows of 64 lanes; grad_env keeps the raw channel sum until the
   // last window, which applies the 2 / env factor.
   for (int64_t base = 0; base < channels; base += 64) {
@@ -502,30 +803,122 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_wide_kernel(
     float expect = 0.0f;
     if (live)
       for (int64_t slot = begin; slot < end; ++slot) {
-        const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-        if (e >= 0) expect = expect + alpha[e * channels + c] * grad_alpha[e * channels + c];
+        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
+        if (e >= 0) expect = expect + a.alpha[e * channels + c] * a.grad_alpha[e * channels + c];
       }
     if (has_null && live)
-      expect = expect + null_alpha[segment * channels + c] * grad_null_alpha[segment * channels + c];
+      expect = expect + a.null_alpha[segment * channels + c] * a.grad_null_alpha[segment * channels + c];
     for (int64_t slot = begin; slot < end; ++slot) {
-      const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e < 0) continue;
       float out = 0.0f;
       if (live) {
-        out = alpha[e * channels + c] * (grad_alpha[e * channels + c] - expect);
-        grad_logit[e * channels + c] = out;
+        out = a.alpha[e * channels + c] * (a.grad_alpha[e * channels + c] - expect);
+        a.grad_logit[e * channels + c] = out;
       }
       float row = group_sum<64>(out);
       if (lane == 0) {
-        if (base > 0) row = grad_env[e] + row;
-        grad_env[e] = last ? env_gradient(row, env[e]) : row;
+        if (base > 0) row = a.grad_env[e] + row;
+        a.grad_env[e] = last ? env_gradient(row, a.env[e]) : row;
       }
     }
     if (has_null && live)
-      grad_null_logit[segment * channels + c] =
-          null_alpha[segment * channels + c] * (grad_null_alpha[segment * channels + c] - expect);
+      a.grad_null_logit[segment * channels + c] =
+          a.null_alpha[segment * channels + c] * (a.grad_null_alpha[segment * channels + c] - expect);
   }
 }
+
+// ---------------------------------------------------------------------------
+// plan: ascending list of the segments longer than the short-path capacity
+// ---------------------------------------------------------------------------
+
+constexpr int kPlanThreads = 256;
+constexpr int kPlanItems = 16;
+constexpr int64_t kPlanTile = kPlanThreads * kPlanItems;
+
+__device__ __forceinline__ bool is_long(const int64_t* __restrict__ offsets, int64_t segment, int64_t n_edges,
+                                        int64_t capacity) {
+  int64_t begin, end;
+  segment_bounds(offsets, segment, n_edges, begin, end);
+  return end - begin > capacity;
+}
+
+__device__ int64_t plan_block_scan(int64_t value, int64_t* lds) {
+  const int t = threadIdx.x;
+  lds[t] = value;
+  __syncthreads();
+  for (int offset = 1; offset < kPlanThreads; offset <<= 1) {
+    const int64_t add = t >= offset ? lds[t - offset] : 0;
+    __syncthreads();
+    lds[t] += add;
+    __syncthreads();
+  }
+  const int64_t result = lds[t];
+  __syncthreads();
+  return result;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(const int64_t* __restrict__ offsets,
+                                                                  int64_t n_nodes, int64_t n_edges,
+                                                                  int64_t capacity, int64_t* __restrict__ counts) {
+  __shared__ int64_t lds[kPlanThreads];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
+  int64_t count = 0;
+  for (int i = 0; i < kPlanItems; ++i)
+    if (base + i < n_nodes && is_long(offsets, base + i, n_edges, capacity)) ++count;
+  const int64_t inclusive = plan_block_scan(count, lds);
+  if (threadIdx.x == kPlanThreads - 1) counts[blockIdx.x] = inclusive;
+}
+
+// Exclusive scan of the tile counts in place (one workgroup); writes the
+// header of the plan.
+__global__ __launch_bounds__(kPlanThreads) void plan_scan_kernel(int64_t* __restrict__ counts, int64_t tiles,
+                                                                 int64_t capacity, int64_t* __restrict__ plan) {
+  __shared__ int64_t lds[kPlanThreads];
+  const int64_t per_thread = (tiles + kPlanThreads - 1) / kPlanThreads;
+  const int64_t begin = static_cast<int64_t>(threadIdx.x) * per_thread;
+  const int64_t end = begin + per_thread < tiles ? begin + per_thread : tiles;
+  int64_t sum = 0;
+  for (int64_t i = begin; i < end; ++i) sum += counts[i];
+  const int64_t inclusive = plan_block_scan(sum, lds);
+  int64_t running = inclusive - sum;
+  for (int64_t i = begin; i < end; ++i) {
+    const int64_t value = counts[i];
+    counts[i] = running;
+    running += value;
+  }
+  if (threadIdx.x == kPlanThreads - 1) {
+    plan[0] = capacity;
+    plan[1] = inclusive;
+  }
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_write_kernel(const int64_t* __restrict__ offsets,
+                                                                  int64_t n_nodes, int64_t n_edges,
+                                                                  int64_t capacity,
+                                                                  const int64_t* __restrict__ tile_prefix,
+                                                                  int64_t* __restrict__ list) {
+  __shared__ int64_t lds[kPlanThreads];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
+  bool flag[kPlanItems];
+  int64_t count = 0;
+#pragma unroll
+  for (int i = 0; i < kPlanItems; ++i) {
+    flag[i] = base + i < n_nodes && is_long(offsets, base + i, n_edges, capacity);
+    count += flag[i] ? 1 : 0;
+  }
+  const int64_t inclusive = plan_block_scan(count, lds);
+  int64_t position = tile_prefix[blockIdx.x] + inclusive - count;
+#pragma unroll
+  for (int i = 0; i < kPlanItems; ++i)
+    if (flag[i]) list[position++] = base + i;
+}
+
+int64_t plan_tiles(int64_t n_nodes) { return (n_nodes + kPlanTile - 1) / kPlanTile; }
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
 
 int lanes_log_for(int64_t chunks) {
   int log = 0;
@@ -533,89 +926,90 @@ int lanes_log_for(int64_t chunks) {
   return log;
 }
 
+// Short-path capacity of the kernel that runs `channels` with (vec4) or
+// without 128-bit rows; 0 for the channel-major kernel (no plan use).
+int64_t capacity_for(int64_t channels, bool vec4) {
+  const int64_t chunks = vec4 ? channels / 4 : channels;
+  if (chunks > 64) return 0;
+  const int log_lc = lanes_log_for(chunks);
+  const int64_t lc = int64_t(1) << log_lc;
+  const int64_t g = lc > 32 ? lc : 32;
+  const int64_t rmax = vec4 ? 24 / 4 : 24;
+  return rmax * (g / lc);
+}
+
+unsigned int short_blocks(int64_t n_nodes, int log_lc) {
+  const int64_t g = log_lc > 5 ? (int64_t(1) << log_lc) : 32;
+  return blocks_for(n_nodes, kBlock / g);
+}
+
 template <int V, int LOG_LC>
-int launch_forward(const float* logit, const float* env, const int64_t* offsets,
-                   const float* null_logit, const int64_t* order, float* alpha, float* null_alpha,
-                   int64_t n_edges, int64_t n_nodes, int64_t channels, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kWaves);
-#define DPA4K_SOFTMAX_FWD(NULLV, ORD)                                                        \
-  softmax_forward_kernel<V, LOG_LC, NULLV, ORD><<<grid, kBlock, 0, stream>>>(               \
-      logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels)
-  if (null_logit != nullptr) {
-    if (order != nullptr) DPA4K_SOFTMAX_FWD(true, true); else DPA4K_SOFTMAX_FWD(true, false);
+int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
+  const int64_t grid = n_long + short_blocks(a.n_nodes, LOG_LC);
+#define DPA4K_SOFTMAX_FWD(NULLV, ORD) \
+  softmax_forward_kernel<V, LOG_LC, NULLV, ORD><<<static_cast<unsigned int>(grid), kBlock, 0, stream>>>(a, plan, n_long)
+  if (a.null_logit != nullptr) {
+    if (a.order != nullptr) DPA4K_SOFTMAX_FWD(true, true); else DPA4K_SOFTMAX_FWD(true, false);
   } else {
-    if (order != nullptr) DPA4K_SOFTMAX_FWD(false, true); else DPA4K_SOFTMAX_FWD(false, false);
+    if (a.order != nullptr) DPA4K_SOFTMAX_FWD(false, true); else DPA4K_SOFTMAX_FWD(false, false);
   }
 #undef DPA4K_SOFTMAX_FWD
   return launched("softmax_forward_kernel");
 }
 
 template <int V, int LOG_LC>
-int launch_backward(const float* alpha, const float* grad_alpha, const float* env,
-                    const int64_t* offsets, const float* null_alpha, const float* grad_null_alpha,
-                    const int64_t* order, float* grad_logit, float* grad_null_logit,
-                    float* grad_env, int64_t n_edges, int64_t n_nodes, int64_t channels,
-                    hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kWaves);
-#define DPA4K_SOFTMAX_BWD(NULLV, ORD)                                                        \
-  softmax_backward_kernel<V, LOG_LC, NULLV, ORD><<<grid, kBlock, 0, stream>>>(              \
-      alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,       \
-      grad_null_logit, grad_env, n_edges, n_nodes, channels)
-  if (null_alpha != nullptr) {
-    if (order != nullptr) DPA4K_SOFTMAX_BWD(true, true); else DPA4K_SOFTMAX_BWD(true, false);
+int launch_backward(const BackwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
+  const int64_t grid = n_long + short_blocks(a.n_nodes, LOG_LC);
+#define DPA4K_SOFTMAX_BWD(NULLV, ORD) \
+  softmax_backward_kernel<V, LOG_LC, NULLV, ORD><<<static_cast<unsigned int>(grid), kBlock, 0, stream>>>(a, plan, n_long)
+  if (a.null_alpha != nullptr) {
+    if (a.order != nullptr) DPA4K_SOFTMAX_BWD(true, true); else DPA4K_SOFTMAX_BWD(true, false);
   } else {
-    if (order != nullptr) DPA4K_SOFTMAX_BWD(false, true); else DPA4K_SOFTMAX_BWD(false, false);
+    if (a.order != nullptr) DPA4K_SOFTMAX_BWD(false, true); else DPA4K_SOFTMAX_BWD(false, false);
   }
 #undef DPA4K_SOFTMAX_BWD
   return launched("softmax_backward_kernel");
 }
 
-template <int V, typename... Args>
-int dispatch_forward(int log_lc, Args... args) {
+template <int V, typename Args>
+int dispatch_forward(int log_lc, const Args& a, const int64_t* list, int64_t n_long, hipStream_t stream) {
   switch (log_lc) {
-    case 0: return launch_forward<V, 0>(args...);
-    case 1: return launch_forward<V, 1>(args...);
-    case 2: return launch_forward<V, 2>(args...);
-    case 3: return launch_forward<V, 3>(args...);
-    case 4: return launch_forward<V, 4>(args...);
-    case 5: return launch_forward<V, 5>(args...);
-    default: return launch_forward<V, 6>(args...);
+    case 0: return launch_forward<V, 0>(a, list, n_long, stream);
+    case 1: return launch_forward<V, 1>(a, list, n_long, stream);
+    case 2: return launch_forward<V, 2>(a, list, n_long, stream);
+    case 3: return launch_forward<V, 3>(a, list, n_long, stream);
+    case 4: return launch_forward<V, 4>(a, list, n_long, stream);
+    case 5: return launch_forward<V, 5>(a, list, n_long, stream);
+    default: return launch_forward<V, 6>(a, list, n_long, stream);
   }
 }
 
-template <int V, typename... Args>
-int dispatch_backward(int log_lc, Args... args) {
+template <int V, typename Args>
+int dispatch_backward(int log_lc, const Args& a, const int64_t* list, int64_t n_long, hipStream_t stream) {
   switch (log_lc) {
-    case 0: return launch_backward<V, 0>(args...);
-    case 1: return launch_backward<V, 1>(args...);
-    case 2: return launch_backward<V, 2>(args...);
-    case 3: return launch_backward<V, 3>(args...);
-    case 4: return launch_backward<V, 4>(args...);
-    case 5: return launch_backward<V, 5>(args...);
-    default: return launch_backward<V, 6>(args...);
+    case 0: return launch_backward<V, 0>(a, list, n_long, stream);
+    case 1: return launch_backward<V, 1>(a, list, n_long, stream);
+    case 2: return launch_backward<V, 2>(a, list, n_long, stream);
+    case 3: return launch_backward<V, 3>(a, list, n_long, stream);
+    case 4: return launch_backward<V, 4>(a, list, n_long, stream);
+    case 5: return launch_backward<V, 5>(a, list, n_long, stream);
+    default: return launch_backward<V, 6>(a, list, n_long, stream);
   }
 }
 
 int check_common(int64_t n_edges, int64_t n_nodes, int64_t channels, const char* what) {
   if (n_edges < 0 || n_nodes < 0) return fail(DPA4K_EINVAL, "%s: negative sizes", what);
   if (channels <= 0) return fail(DPA4K_EINVAL, "%s requires at least one channel", what);
-  if ((n_nodes + kWaves - 1) / kWaves > kMaxGrid)
-    return fail(DPA4K_EINVAL, "%s: segment count too large", what);
+  if (n_nodes > kMaxGrid) return fail(DPA4K_EINVAL, "%s: segment count too large", what);
   return DPA4K_OK;
 }
 
-}  // namespace
-}  // namespace dpa4k
-
-using namespace dpa4k;
-
-extern "C" int dpa4k_segment_softmax_forward(const float* logit, const float* env,
-                                             const int64_t* offsets, const float* null_logit,
-                                             const int64_t* order, float* alpha, float* null_alpha,
-                                             int64_t n_edges, int64_t n_nodes, int64_t channels,
-                                             dpa4k_stream_t stream_handle) {
-  clear_error();
+int softmax_forward(const float* logit, const float* env, const int64_t* offsets, const float* null_logit,
+                    const int64_t* order, float* alpha, float* null_alpha, int64_t n_edges, int64_t n_nodes,
+                    int64_t channels, const void* plan, int64_t n_long, dpa4k_stream_t stream_handle) {
   if (int s = check_common(n_edges, n_nodes, channels, "segment softmax")) return s;
+  if (plan != nullptr && (n_long < 0 || n_long > n_nodes))
+    return fail(DPA4K_EINVAL, "segment softmax: n_long outside [0, n_nodes]");
   if (n_nodes == 0) return DPA4K_OK;
   if (offsets == nullptr || (n_edges > 0 && (logit == nullptr || env == nullptr || alpha == nullptr)))
     return fail(DPA4K_EINVAL, "segment softmax: null pointer");
@@ -625,32 +1019,28 @@ extern "C" int dpa4k_segment_softmax_forward(const float* logit, const float* en
   const bool vec4 = channels % 4 == 0 && aligned16(logit) && aligned16(alpha) &&
                     (null_logit == nullptr || (aligned16(null_logit) && aligned16(null_alpha)));
   const int64_t chunks = vec4 ? channels / 4 : channels;
+  const ForwardArgs a{logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels};
   if (chunks > 64) {
     const unsigned int grid = blocks_for(n_nodes, kWaves);
-    if (order != nullptr)
-      softmax_forward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(
-          logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels);
-    else
-      softmax_forward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(
-          logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels);
+    if (order != nullptr) softmax_forward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(a);
+    else softmax_forward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_forward_wide_kernel");
   }
+  const int64_t* words = static_cast<const int64_t*>(plan);
+  const int64_t used = plan != nullptr ? n_long : 0;
   const int log_lc = lanes_log_for(chunks);
-  return vec4 ? dispatch_forward<4>(log_lc, logit, env, offsets, null_logit, order, alpha,
-                                    null_alpha, n_edges, n_nodes, channels, stream)
-              : dispatch_forward<1>(log_lc, logit, env, offsets, null_logit, order, alpha,
-                                    null_alpha, n_edges, n_nodes, channels, stream);
+  return vec4 ? dispatch_forward<4>(log_lc, a, words, used, stream)
+              : dispatch_forward<1>(log_lc, a, words, used, stream);
 }
 
-extern "C" int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha,
-                                              const float* env, const int64_t* offsets,
-                                              const float* null_alpha, const float* grad_null_alpha,
-                                              const int64_t* order, float* grad_logit,
-                                              float* grad_null_logit, float* grad_env,
-                                              int64_t n_edges, int64_t n_nodes, int64_t channels,
-                                              dpa4k_stream_t stream_handle) {
-  clear_error();
+int softmax_backward(const float* alpha, const float* grad_alpha, const float* env, const int64_t* offsets,
+                     const float* null_alpha, const float* grad_null_alpha, const int64_t* order,
+                     float* grad_logit, float* grad_null_logit, float* grad_env, int64_t n_edges,
+                     int64_t n_nodes, int64_t channels, const void* plan, int64_t n_long,
+                     dpa4k_stream_t stream_handle) {
   if (int s = check_common(n_edges, n_nodes, channels, "segment softmax backward")) return s;
+  if (plan != nullptr && (n_long < 0 || n_long > n_nodes))
+    return fail(DPA4K_EINVAL, "segment softmax backward: n_long outside [0, n_nodes]");
   if (n_nodes == 0) return DPA4K_OK;
   if (offsets == nullptr ||
       (n_edges > 0 && (alpha == nullptr || grad_alpha == nullptr || env == nullptr ||
@@ -658,31 +1048,112 @@ extern "C" int dpa4k_segment_softmax_backward(const float* alpha, const float* g
     return fail(DPA4K_EINVAL, "segment softmax backward: null pointer");
   const bool has_null = null_alpha != nullptr;
   if (has_null != (grad_null_alpha != nullptr) || has_null != (grad_null_logit != nullptr))
-    return fail(DPA4K_EINVAL,
-                "segment softmax requires null_alpha and grad_null_alpha together");
+    return fail(DPA4K_EINVAL, "segment softmax requires null_alpha and grad_null_alpha together");
   hipStream_t stream = as_stream(stream_handle);
-  const bool vec4 = channels % 4 == 0 && aligned16(alpha) && aligned16(grad_alpha) &&
-                    aligned16(grad_logit) &&
+  const bool vec4 = channels % 4 == 0 && aligned16(alpha) && aligned16(grad_alpha) && aligned16(grad_logit) &&
                     (!has_null || (aligned16(null_alpha) && aligned16(grad_null_alpha) &&
                                    aligned16(grad_null_logit)));
   const int64_t chunks = vec4 ? channels / 4 : channels;
+  const BackwardArgs a{alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order,
+                       grad_logit, grad_null_logit, grad_env, n_edges, n_nodes, channels};
   if (chunks > 64) {
     const unsigned int grid = blocks_for(n_nodes, kWaves);
-    if (order != nullptr)
-      softmax_backward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(
-          alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
-          grad_null_logit, grad_env, n_edges, n_nodes, channels);
-    else
-      softmax_backward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(
-          alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
-          grad_null_logit, grad_env, n_edges, n_nodes, channels);
+    if (order != nullptr) softmax_backward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(a);
+    else softmax_backward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_backward_wide_kernel");
   }
+  const int64_t* words = static_cast<const int64_t*>(plan);
+  const int64_t used = plan != nullptr ? n_long : 0;
   const int log_lc = lanes_log_for(chunks);
-  return vec4 ? dispatch_backward<4>(log_lc, alpha, grad_alpha, env, offsets, null_alpha,
-                                     grad_null_alpha, order, grad_logit, grad_null_logit,
-                                     grad_env, n_edges, n_nodes, channels, stream)
-              : dispatch_backward<1>(log_lc, alpha, grad_alpha, env, offsets, null_alpha,
-                                     grad_null_alpha, order, grad_logit, grad_null_logit,
-                                     grad_env, n_edges, n_nodes, channels, stream);
+  return vec4 ? dispatch_backward<4>(log_lc, a, words, used, stream)
+              : dispatch_backward<1>(log_lc, a, words, used, stream);
+}
+
+}  // namespace
+}  // namespace dpa4k
+
+using namespace dpa4k;
+
+extern "C" int dpa4k_segment_softmax_forward(const float* logit, const float* env, const int64_t* offsets,
+                                             const float* null_logit, const int64_t* order, float* alpha,
+                                             float* null_alpha, int64_t n_edges, int64_t n_nodes,
+                                             int64_t channels, dpa4k_stream_t stream) {
+  clear_error();
+  return softmax_forward(logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels,
+                         nullptr, 0, stream);
+}
+
+extern "C" int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha, const float* env,
+                                              const int64_t* offsets, const float* null_alpha,
+                                              const float* grad_null_alpha, const int64_t* order,
+                                              float* grad_logit, float* grad_null_logit, float* grad_env,
+                                              int64_t n_edges, int64_t n_nodes, int64_t channels,
+                                              dpa4k_stream_t stream) {
+  clear_error();
+  return softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
+                          grad_null_logit, grad_env, n_edges, n_nodes, channels, nullptr, 0, stream);
+}
+
+extern "C" size_t dpa4k_segment_softmax_plan_size(int64_t n_nodes) {
+  if (n_nodes < 0) return 0;
+  return round_up_256(static_cast<size_t>(kPlanHeader + n_nodes + plan_tiles(n_nodes)) * sizeof(int64_t));
+}
+
+extern "C" int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edges, int64_t n_nodes,
+                                          int64_t channels, void* plan, size_t plan_bytes, int64_t* n_long,
+                                          dpa4k_stream_t stream_handle) {
+  clear_error();
+  if (int s = check_common(n_edges, n_nodes, channels, "segment softmax plan")) return s;
+  if (offsets == nullptr || plan == nullptr || n_long == nullptr)
+    return fail(DPA4K_EINVAL, "segment softmax plan: null pointer");
+  if (plan_bytes < dpa4k_segment_softmax_plan_size(n_nodes))
+    return fail(DPA4K_EWORKSPACE, "segment softmax plan: %zu bytes given, %zu needed", plan_bytes,
+                dpa4k_segment_softmax_plan_size(n_nodes));
+  hipStream_t stream = as_stream(stream_handle);
+  // The plan is for the 128-bit row kernel when C % 4 == 0 (operands from
+  // torch's allocator are 16-byte aligned), for the scalar one otherwise.
+  const int64_t capacity = capacity_for(channels, channels % 4 == 0);
+  int64_t* words = static_cast<int64_t*>(plan);
+  const int64_t tiles = plan_tiles(n_nodes);
+  int64_t* counts = words + kPlanHeader + n_nodes;
+  if (tiles > 0) {
+    plan_count_kernel<<<static_cast<unsigned int>(tiles), kPlanThreads, 0, stream>>>(offsets, n_nodes, n_edges,
+                                                                                     capacity, counts);
+    if (int s = launched("plan_count_kernel")) return s;
+  }
+  plan_scan_kernel<<<1, kPlanThreads, 0, stream>>>(counts, tiles, capacity, words);
+  if (int s = launched("plan_scan_kernel")) return s;
+  if (tiles > 0) {
+    plan_write_kernel<<<static_cast<unsigned int>(tiles), kPlanThreads, 0, stream>>>(
+        offsets, n_nodes, n_edges, capacity, counts, words + kPlanHeader);
+    if (int s = launched("plan_write_kernel")) return s;
+  }
+  int64_t header[2] = {0, 0};
+  if (int s = hip_status(hipMemcpyAsync(header, words, sizeof(header), hipMemcpyDeviceToHost, stream),
+                         "hipMemcpyAsync(plan header)"))
+    return s;
+  if (int s = hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize")) return s;
+  *n_long = header[1];
+  return DPA4K_OK;
+}
+
+extern "C" int dpa4k_segment_softmax_forward_planned(const float* logit, const float* env, const int64_t* offsets,
+                                                     const float* null_logit, const int64_t* order, float* alpha,
+                                                     float* null_alpha, int64_t n_edges, int64_t n_nodes,
+                                                     int64_t channels, const void* plan, int64_t n_long,
+                                                     dpa4k_stream_t stream) {
+  clear_error();
+  return softmax_forward(logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels,
+                         plan, n_long, stream);
+}
+
+extern "C" int dpa4k_segment_softmax_backward_planned(const float* alpha, const float* grad_alpha, const float* env,
+                                                      const int64_t* offsets, const float* null_alpha,
+                                                      const float* grad_null_alpha, const int64_t* order,
+                                                      float* grad_logit, float* grad_null_logit, float* grad_env,
+                                                      int64_t n_edges, int64_t n_nodes, int64_t channels,
+                                                      const void* plan, int64_t n_long, dpa4k_stream_t stream) {
+  clear_error();
+  return softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
+                          grad_null_logit, grad_env, n_edges, n_nodes, channels, plan, n_long, stream);
 }

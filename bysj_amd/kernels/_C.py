@@ -13,7 +13,9 @@ Extensions over the reference, all keyword-only or additional symbols:
 ``segment_sum_backward(..., want_edge_scale_grad=True)`` returns a third
 tensor, the ``edge_scale`` gradient; ``force_assembly`` also takes float64
 inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
-``*_csr`` GIE entry points expose the device-side CSR construction.
+``*_csr`` GIE entry points expose the device-side CSR construction;
+``segment_softmax_plan`` builds the degree plan that
+``segment_softmax_forward/backward(..., plan=...)`` accept.
 """
 from __future__ import annotations
 
@@ -218,10 +220,45 @@ def _null_checks(tensor, nodes, channels, what):
     _check(tensor.numel() == nodes * channels, f"{what} must have shape (n_nodes, channels)")
 
 
-def segment_softmax_forward(logit, env, offsets, null_logit=None, order=None):
+class SoftmaxPlan:
+    """Degree plan of one CSR (the long segments of ``offsets``) for one channel count."""
+
+    __slots__ = ("words", "n_long", "n_edges", "channels")
+
+    def __init__(self, words: torch.Tensor, n_long: int, n_edges: int, channels: int):
+        self.words, self.n_long, self.n_edges, self.channels = words, n_long, n_edges, channels
+
+
+def segment_softmax_plan(offsets, n_edges: int, channels: int) -> SoftmaxPlan:
+    """Build the degree plan of ``offsets`` on its device (synchronises once)."""
+    nodes = _offsets(offsets, "segment softmax offsets")
+    _check(int(channels) > 0, "segment softmax requires at least one channel")
+    nbytes = _LIB.dpa4k_segment_softmax_plan_size(nodes)
+    words = torch.empty((max(int(nbytes), 8) + 7) // 8, dtype=torch.int64, device=offsets.device)
+    n_long = _lib.ctypes.c_int64(0)
+    with _on(offsets.device) as stream:
+        status = _LIB.dpa4k_segment_softmax_plan(
+            offsets.data_ptr(), int(n_edges), nodes, int(channels), words.data_ptr(), words.numel() * 8,
+            _lib.ctypes.byref(n_long), stream,
+        )
+    _lib.check(status)
+    return SoftmaxPlan(words, int(n_long.value), int(n_edges), int(channels))
+
+
+def _plan_args(plan, offsets, edges, channels):
+    if plan is None:
+        return None
+    _check(isinstance(plan, SoftmaxPlan) and plan.words.device == offsets.device
+           and plan.n_edges == edges and plan.channels == channels,
+           "segment softmax plan was built for another graph, device or channel count")
+    return plan
+
+
+def segment_softmax_forward(logit, env, offsets, null_logit=None, order=None, *, plan=None):
     edges, nodes, channels = _softmax_checks(logit, env, offsets, order)
     _null_checks(null_logit, nodes, channels, "segment softmax null_logit")
     _same_device(logit, null_logit)
+    plan = _plan_args(plan, offsets, edges, channels)
     alpha = torch.empty((edges, channels), dtype=torch.float32, device=logit.device)
     null_alpha = None
     if null_logit is not None:
@@ -229,17 +266,24 @@ def segment_softmax_forward(logit, env, offsets, null_logit=None, order=None):
     if nodes == 0:
         return alpha, null_alpha
     with _on(logit.device) as stream:
-        status = _LIB.dpa4k_segment_softmax_forward(
-            _ptr(logit), _ptr(env), offsets.data_ptr(), _ptr(null_logit), _ptr(order), _ptr(alpha),
-            _ptr(null_alpha), edges, nodes, channels, stream,
-        )
+        if plan is None:
+            status = _LIB.dpa4k_segment_softmax_forward(
+                _ptr(logit), _ptr(env), offsets.data_ptr(), _ptr(null_logit), _ptr(order), _ptr(alpha),
+                _ptr(null_alpha), edges, nodes, channels, stream,
+            )
+        else:
+            status = _LIB.dpa4k_segment_softmax_forward_planned(
+                _ptr(logit), _ptr(env), offsets.data_ptr(), _ptr(null_logit), _ptr(order), _ptr(alpha),
+                _ptr(null_alpha), edges, nodes, channels, plan.words.data_ptr(), plan.n_long, stream,
+            )
     _lib.check(status)
     return alpha, null_alpha
 
 
 def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
-                             grad_null_alpha=None, order=None):
+                             grad_null_alpha=None, order=None, *, plan=None):
     edges, nodes, channels = _softmax_checks(alpha, env, offsets, order)
+    plan = _plan_args(plan, offsets, edges, channels)
     _f32(grad_alpha, "segment softmax grad_alpha")
     _check(tuple(grad_alpha.shape) == tuple(alpha.shape), "segment softmax grad_alpha must match alpha")
     _same_device(alpha, grad_alpha)
@@ -255,11 +299,18 @@ def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
     if nodes == 0:
         return grad_logit, grad_null, grad_env
     with _on(alpha.device) as stream:
-        status = _LIB.dpa4k_segment_softmax_backward(
-            _ptr(alpha), _ptr(grad_alpha), _ptr(env), offsets.data_ptr(), _ptr(null_alpha),
-            _ptr(grad_null_alpha), _ptr(order), _ptr(grad_logit), _ptr(grad_null), _ptr(grad_env),
-            edges, nodes, channels, stream,
-        )
+        if plan is None:
+            status = _LIB.dpa4k_segment_softmax_backward(
+                _ptr(alpha), _ptr(grad_alpha), _ptr(env), offsets.data_ptr(), _ptr(null_alpha),
+                _ptr(grad_null_alpha), _ptr(order), _ptr(grad_logit), _ptr(grad_null), _ptr(grad_env),
+                edges, nodes, channels, stream,
+            )
+        else:
+            status = _LIB.dpa4k_segment_softmax_backward_planned(
+                _ptr(alpha), _ptr(grad_alpha), _ptr(env), offsets.data_ptr(), _ptr(null_alpha),
+                _ptr(grad_null_alpha), _ptr(order), _ptr(grad_logit), _ptr(grad_null), _ptr(grad_env),
+                edges, nodes, channels, plan.words.data_ptr(), plan.n_long, stream,
+            )
     _lib.check(status)
     return grad_logit, grad_null, grad_env
 

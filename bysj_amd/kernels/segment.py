@@ -22,6 +22,7 @@ propagates a gradient to ``edge_scale``; DeepMD's envelope seam passes
 from __future__ import annotations
 
 import os
+import weakref
 
 import torch
 
@@ -212,6 +213,52 @@ def _check_csr(dst, offsets, n_nodes, name):
 
 
 # ---------------------------------------------------------------------------
+# degree plans of the softmax kernels
+# ---------------------------------------------------------------------------
+
+class _PlanCache:
+    """Softmax degree plans, kept per ``offsets`` tensor object.
+
+    A plan lists the segments of a CSR too long for the register path; the
+    kernels give each of them a workgroup of its own.  Building one costs a
+    device pass and a host synchronisation, so it is done once per graph:
+    entries are keyed by the identity of the ``offsets`` tensor and
+    invalidated when its storage or version counter changes (an in-place
+    write) or the tensor is freed.  During HIP graph capture a missing plan
+    is not built; the kernels then run without one (same results).
+    """
+
+    def __init__(self):
+        self._entries: dict[int, tuple] = {}
+
+    def get(self, offsets: torch.Tensor, n_edges: int, channels: int):
+        stamp = (offsets.data_ptr(), offsets._version, offsets.numel(), offsets.device)
+        key = id(offsets)
+        entry = self._entries.get(key)
+        if entry is not None and (entry[0]() is not offsets or entry[1] != stamp):
+            entry = None
+        plans = entry[2] if entry is not None else {}
+        plan = plans.get((n_edges, channels))
+        if plan is not None:
+            return plan
+        if offsets.is_cuda and torch.cuda.is_current_stream_capturing():
+            return None
+        plan = _extension("segment_softmax_plan").segment_softmax_plan(offsets, n_edges, channels)
+        if entry is None:
+            reference = weakref.ref(offsets, lambda _, key=key: self._entries.pop(key, None))
+            entry = (reference, stamp, plans)
+            self._entries[key] = entry
+        plans[(n_edges, channels)] = plan
+        return plan
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+
+_PLANS = _PlanCache()
+
+
+# ---------------------------------------------------------------------------
 # autograd functions
 # ---------------------------------------------------------------------------
 
@@ -245,12 +292,18 @@ class _SegmentSumFunction(torch.autograd.Function):
         )
 
 
+def _softmax_plan(offsets, logit):
+    return _PLANS.get(offsets, int(logit.shape[0]), int(logit.shape[1]))
+
+
 class _SegmentSoftmaxFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, logit, env, offsets, order):
         native = _extension("segment_softmax_forward")
-        alpha, _ = native.segment_softmax_forward(logit, env, offsets, None, order)
+        plan = _softmax_plan(offsets, logit)
+        alpha, _ = native.segment_softmax_forward(logit, env, offsets, None, order, plan=plan)
         ctx.save_for_backward(alpha, env, offsets, order)
+        ctx.plan = plan
         return alpha
 
     @staticmethod
@@ -258,7 +311,7 @@ class _SegmentSoftmaxFunction(torch.autograd.Function):
         alpha, env, offsets, order = ctx.saved_tensors
         native = _extension("segment_softmax_backward")
         grad_logit, _, grad_env = native.segment_softmax_backward(
-            alpha, grad_alpha.contiguous(), env, offsets, None, None, order
+            alpha, grad_alpha.contiguous(), env, offsets, None, None, order, plan=ctx.plan
         )
         return grad_logit, grad_env, None, None
 
@@ -267,8 +320,10 @@ class _SegmentSoftmaxNullFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, logit, env, offsets, null_logit, order):
         native = _extension("segment_softmax_forward")
-        alpha, null_alpha = native.segment_softmax_forward(logit, env, offsets, null_logit, order)
+        plan = _softmax_plan(offsets, logit)
+        alpha, null_alpha = native.segment_softmax_forward(logit, env, offsets, null_logit, order, plan=plan)
         ctx.save_for_backward(alpha, null_alpha, env, offsets, order)
+        ctx.plan = plan
         return alpha, null_alpha
 
     @staticmethod
@@ -280,7 +335,7 @@ class _SegmentSoftmaxNullFunction(torch.autograd.Function):
         )
         native = _extension("segment_softmax_backward")
         grad_logit, grad_null_logit, grad_env = native.segment_softmax_backward(
-            alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order
+            alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, plan=ctx.plan
         )
         return grad_logit, grad_env, None, grad_null_logit, None
 
@@ -310,6 +365,8 @@ def segment_softmax(logit, env, offsets, null_logit=None, *, order=None, check_g
     when ``null_logit`` ``(n_nodes, channels)`` is given.  Edges with a
     non-positive envelope carry no mass.  ``check_grouping`` is accepted for
     signature compatibility; the softmax has no ``dst`` to check against.
+    The first call on an ``offsets`` tensor builds its degree plan (one host
+    synchronisation); reuse the tensor across calls.
     """
     _validate_segment_softmax(logit, env, offsets, null_logit, order)
     require_dcu(logit, env, offsets, null_logit, order)

@@ -138,23 +138,31 @@ def segment_sum_config(n_nodes: int = 1024, channels: int = 128, seed: int = 0, 
     return case
 
 
+def segment_softmax_features(n_edges: int, n_nodes: int, channels: int = 8, seed: int = 0, device="cpu",
+                             null: bool = True, masked_fraction: float = 0.0):
+    """Config-2 features of one graph: logits ~ N(0, 4) with 0.1 % of entries at +-40,
+    env ~ U(0.1, 1.1) (a fraction set to -0.5 when masked_fraction > 0), null ~ N(0, 1)."""
+    generator = _generator(device, seed)
+    logit = torch.randn((n_edges, channels), generator=generator, device=device) * 2.0
+    flat = logit.view(-1)
+    extreme = torch.rand(flat.shape, generator=generator, device=device) < 1e-3
+    sign = torch.where(torch.rand(flat.shape, generator=generator, device=device) < 0.5, -40.0, 40.0)
+    flat[extreme] = sign[extreme]
+    env = torch.rand((n_edges,), generator=generator, device=device) + 0.1
+    if masked_fraction > 0:
+        env[torch.rand((n_edges,), generator=generator, device=device) < masked_fraction] = -0.5
+    null_logit = torch.randn((n_nodes, channels), generator=generator, device=device) if null else None
+    return {"logit": logit, "env": env, "null_logit": null_logit}
+
+
 def segment_softmax_config(n_nodes: int = 16384, channels: int = 8, seed: int = 0, device="cpu",
                            null: bool = True, masked_fraction: float = 0.0):
     degrees = poisson_degrees(n_nodes, 48.0, seed, hub_fraction=0.01, hub_degree=512)
     edges = int(degrees.sum())
     dst = torch.from_numpy(dst_from_degrees(degrees)).to(device)
     offsets = torch.from_numpy(offsets_from_degrees(degrees)).to(device)
-    generator = _generator(device, seed)
-    logit = torch.randn((edges, channels), generator=generator, device=device) * 2.0
-    flat = logit.view(-1)
-    extreme = torch.rand(flat.shape, generator=generator, device=device) < 1e-3
-    sign = torch.where(torch.rand(flat.shape, generator=generator, device=device) < 0.5, -40.0, 40.0)
-    flat[extreme] = sign[extreme]
-    env = torch.rand((edges,), generator=generator, device=device) + 0.1
-    if masked_fraction > 0:
-        env[torch.rand((edges,), generator=generator, device=device) < masked_fraction] = -0.5
-    null_logit = torch.randn((n_nodes, channels), generator=generator, device=device) if null else None
-    return {"logit": logit, "env": env, "dst": dst, "offsets": offsets, "null_logit": null_logit}
+    features = segment_softmax_features(edges, n_nodes, channels, seed, device, null, masked_fraction)
+    return {"dst": dst, "offsets": offsets, **features}
 
 
 def gie_config(graph: WaterGraph, seed: int = 0, device="cpu", *, primary: bool = True, channels: int = 64):

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 1
+#define DPA4K_ABI_VERSION 2
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -126,6 +126,8 @@ int dpa4k_segment_sum_backward(const float* grad_out, const float* src,
  * env[e] > 0 (other edges carry no mass), m = max(null_logit[n, c], max_e l_e),
  * w_e = exp(l_e - m), D = exp(null - m) + sum_e w_e, alpha = w_e / D,
  * null_alpha = exp(null - m) / D; a segment with no mass gives zeros.
+ * Evaluated in base 2 with the hardware exp2/log2/reciprocal (relative error
+ * below 1e-6 against the natural-base chain).
  * logit[E, C], env[E], null_logit[N, C] or NULL, order[E] or NULL,
  * alpha[E, C], null_alpha[N, C] (required iff null_logit is given). */
 int dpa4k_segment_softmax_forward(const float* logit, const float* env,
@@ -148,6 +150,37 @@ int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha,
                                    float* grad_null_logit, float* grad_env,
                                    int64_t n_edges, int64_t n_nodes,
                                    int64_t channels, dpa4k_stream_t stream);
+
+/* Degree plan of a CSR for the segment softmax (no reference counterpart: it
+ * is the degree-binned schedule of the gfx950 kernels).  Lists, in ascending
+ * order, the segments longer than the register capacity of the kernel that
+ * runs `channels` channels; the planned entry points below give each of them
+ * a workgroup of its own ahead of the short segments.  Build it once per
+ * graph and reuse it for every forward and backward on the same offsets and
+ * channel count.  plan >= dpa4k_segment_softmax_plan_size(N) bytes of device
+ * memory (8-byte aligned); *n_long (host) receives the number of listed
+ * segments.  Synchronises (to read n_long back). */
+size_t dpa4k_segment_softmax_plan_size(int64_t n_nodes);
+int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edges,
+                               int64_t n_nodes, int64_t channels, void* plan,
+                               size_t plan_bytes, int64_t* n_long,
+                               dpa4k_stream_t stream);
+
+/* dpa4k_segment_softmax_forward / _backward with a plan from
+ * dpa4k_segment_softmax_plan on the same offsets (0 <= n_long <= N).  Same
+ * results as the unplanned calls.  A plan built for another channel count
+ * (or alignment) is detected from its header and ignored. */
+int dpa4k_segment_softmax_forward_planned(
+    const float* logit, const float* env, const int64_t* offsets,
+    const float* null_logit, const int64_t* order, float* alpha,
+    float* null_alpha, int64_t n_edges, int64_t n_nodes, int64_t channels,
+    const void* plan, int64_t n_long, dpa4k_stream_t stream);
+int dpa4k_segment_softmax_backward_planned(
+    const float* alpha, const float* grad_alpha, const float* env,
+    const int64_t* offsets, const float* null_alpha,
+    const float* grad_null_alpha, const int64_t* order, float* grad_logit,
+    float* grad_null_logit, float* grad_env, int64_t n_edges, int64_t n_nodes,
+    int64_t channels, const void* plan, int64_t n_long, dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * force_assembly

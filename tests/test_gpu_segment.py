@@ -263,6 +263,67 @@ def test_segment_softmax_with_hubs(channels, null, use_order):
         assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
 
 
+@pytest.mark.parametrize("channels", [1, 3, 8, 16, 64, 256])
+@pytest.mark.parametrize("use_order", [False, True])
+def test_segment_softmax_planned_and_unplanned_paths(channels, use_order):
+    """Degrees straddle every path boundary: the register path of a lane group,
+    the staged and the streaming workgroup paths.  The degree plan must not
+    change a single bit, and both must match the oracle."""
+    from bysj_amd.kernels import _C
+
+    announce("softmax paths", channels, use_order)
+    degrees = np.array([0, 1, 5, 6, 7, 12, 13, 16, 17, 47, 48, 49, 95, 96, 97, 191, 192, 193, 255, 256, 257,
+                        300, 511, 512, 513, 700, 1023, 1024, 1025, 2000, 3, 9], dtype=np.int64)
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    n = degrees.size
+    if use_order:
+        dst, order, offsets = _shuffled(dst_sorted, seed=channels)
+    else:
+        dst, order, offsets = dst_sorted, None, ref.segment_offsets(dst_sorted, n)
+    gen = torch.Generator().manual_seed(channels)
+    logit = torch.randn(dst.numel(), channels, generator=gen) * 2.0
+    logit.view(-1)[::101] = 40.0
+    env = torch.rand(dst.numel(), generator=gen) + 0.1
+    env[::11] = -1.0
+    null_logit = torch.randn(n, channels, generator=gen)
+    up = torch.randn(dst.numel(), channels, generator=gen)
+    up_null = torch.randn(n, channels, generator=gen)
+    d_logit, d_env, d_off = logit.to(DEV), env.to(DEV), offsets.to(DEV)
+    d_order = None if order is None else order.to(DEV)
+    plan = _C.segment_softmax_plan(d_off, dst.numel(), channels)
+    a0, n0 = _C.segment_softmax_forward(d_logit, d_env, d_off, null_logit.to(DEV), d_order)
+    a1, n1 = _C.segment_softmax_forward(d_logit, d_env, d_off, null_logit.to(DEV), d_order, plan=plan)
+    assert_bitwise(a1, a0, "planned alpha")
+    assert_bitwise(n1, n0, "planned null_alpha")
+    e_alpha, e_null = ref.segment_softmax_reference(logit, env, dst, offsets, null_logit)
+    assert_close_scaled(a1, e_alpha, what="alpha")
+    assert_close_scaled(n1, e_null, what="null_alpha")
+    nn = _C.segment_softmax_forward(d_logit, d_env, d_off, None, d_order, plan=plan)[0]
+    assert_close_scaled(nn, ref.segment_softmax_reference(logit, env, dst, offsets)[0], what="alpha without null")
+    g0 = _C.segment_softmax_backward(a1, up.to(DEV), d_env, d_off, n1, up_null.to(DEV), d_order)
+    g1 = _C.segment_softmax_backward(a1, up.to(DEV), d_env, d_off, n1, up_null.to(DEV), d_order, plan=plan)
+    for x, y, what in zip(g1, g0, ("grad_logit", "grad_null", "grad_env")):
+        assert_bitwise(x, y, f"planned {what}")
+    e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
+    assert_close_scaled(g1[0], e_gl, rtol=2e-5, what="grad_logit")
+    assert_close_scaled(g1[1], e_gn, rtol=2e-5, what="grad_null")
+    assert_close_scaled(g1[2], e_ge, rtol=2e-5, what="grad_env")
+
+
+def test_segment_softmax_plan_lists_the_long_segments():
+    from bysj_amd.kernels import _C
+
+    announce("softmax plan")
+    degrees = workloads.poisson_degrees(20000, 48.0, seed=3, hub_fraction=0.01, hub_degree=512)
+    offsets = torch.from_numpy(workloads.offsets_from_degrees(degrees)).to(DEV)
+    plan = _C.segment_softmax_plan(offsets, int(degrees.sum()), 8)
+    words = plan.words.cpu()
+    capacity = int(words[0])
+    expected = np.nonzero(degrees > capacity)[0]
+    assert capacity == 96 and plan.n_long == int(words[1]) == expected.size
+    assert words[2:2 + plan.n_long].tolist() == expected.tolist()
+
+
 def test_segment_softmax_empty_and_masked_segments():
     announce("softmax empty/masked")
     dst, offsets = _graph([0, 2, 3])

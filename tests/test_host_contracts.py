@@ -200,12 +200,17 @@ class _OracleNative:
             return grad_src, grad_node, grad_edge
         return grad_src, grad_node
 
-    def segment_softmax_forward(self, logit, env, offsets, null_logit=None, order=None):
+    def segment_softmax_plan(self, offsets, n_edges, channels):
+        return ("plan", n_edges, channels)
+
+    def segment_softmax_forward(self, logit, env, offsets, null_logit=None, order=None, *, plan=None):
+        assert plan == ("plan", logit.shape[0], logit.shape[1])
         return ref.segment_softmax_reference(logit, env, self._dst(offsets, order, logit.shape[0]), offsets,
                                              null_logit)
 
     def segment_softmax_backward(self, alpha, grad_alpha, env, offsets, null_alpha=None, grad_null_alpha=None,
-                                 order=None):
+                                 order=None, *, plan=None):
+        assert plan == ("plan", alpha.shape[0], alpha.shape[1])
         dst = self._dst(offsets, order, alpha.shape[0])
         expectation = torch.zeros(offsets.numel() - 1, alpha.shape[1]).index_add_(0, dst, alpha * grad_alpha)
         if null_alpha is not None:
