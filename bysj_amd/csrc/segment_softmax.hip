@@ -145,7 +145,21 @@ struct Geo {
   static constexpr int RMAX = 24 / V;                  // register tiles, short path
   static constexpr int RMAXB = 16 / V;                 // register tiles, staged long path
   static constexpr int CAP = RMAX * PG;                // longest short segment
-  static constexpr int UNROLL = 4;                     // loads in flight, streaming path
+  static constexpr int UNROLL = 2;                     // loads in flight per thread, streaming path
+};
+
+// Edge of register tile i: the slot itself in natural order (recomputed, no
+// register), the stored order entry otherwise (-1 for none).
+template <bool kOrdered, int R>
+struct TileEdges {
+  int64_t e[kOrdered ? R : 1];
+  __device__ __forceinline__ void set(int i, int64_t edge) {
+    if constexpr (kOrdered) e[i] = edge;
+  }
+  __device__ __forceinline__ int64_t get(int i, int64_t slot, int64_t end) const {
+    if constexpr (kOrdered) return e[i];
+    return slot < end ? slot : -1;
+  }
 };
 
 // Lane roles inside a workgroup for rows of LC lanes.
@@ -221,17 +235,17 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   if (degree <= RMAXB * PB) {
     // staged: every row of the segment in registers, one read
     float value[RMAXB][V];
-    int64_t edge[RMAXB];
+    TileEdges<kOrdered, RMAXB> edge;
 #pragma unroll
     for (int i = 0; i < RMAXB; ++i) {
-      edge[i] = -1;
+      edge.set(i, -1);
 #pragma unroll
       for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
       const int64_t slot = begin + static_cast<int64_t>(i) * PB + L.pb;
       if (slot < end && L.live) {
         const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
         if (e >= 0) {
-          edge[i] = e;
+          edge.set(i, e);
           const float envelope = a.env[e];
           const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
 #pragma unroll
@@ -281,11 +295,12 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
     }
 #pragma unroll
     for (int i = 0; i < RMAXB; ++i) {
-      if (edge[i] >= 0) {
+      const int64_t e = edge.get(i, begin + static_cast<int64_t>(i) * PB + L.pb, end);
+      if (e >= 0 && L.live) {
         fvec<V> out;
 #pragma unroll
         for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
-        store_vec_stream<V>(a.alpha + edge[i] * a.channels + L.column, out);
+        store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
       }
     }
     if (kNull && threadIdx.x < LC && L.live) {
@@ -389,20 +404,20 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
     for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
   }
   float value[RMAX][V];
-  int64_t edge[RMAX];
+  TileEdges<kOrdered, RMAX> edge;
   float peak[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
 #pragma unroll
   for (int i = 0; i < RMAX; ++i) {
-    edge[i] = -1;
+    edge.set(i, -1);
 #pragma unroll
     for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
     const int64_t slot = begin + static_cast<int64_t>(i) * PG + L.p;
     if (slot < end && L.live) {
       const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e >= 0) {
-        edge[i] = e;
+        edge.set(i, e);
         const float envelope = a.env[e];
         const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
 #pragma unroll
@@ -438,11 +453,12 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
   }
 #pragma unroll
   for (int i = 0; i < RMAX; ++i) {
-    if (edge[i] >= 0) {
+    const int64_t e = edge.get(i, begin + static_cast<int64_t>(i) * PG + L.p, end);
+    if (e >= 0 && L.live) {
       fvec<V> out;
 #pragma unroll
       for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
-      store_vec_stream<V>(a.alpha + edge[i] * a.channels + L.column, out);
+      store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
     }
   }
   if (kNull && L.p == 0 && L.live) {
@@ -453,18 +469,17 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
   }
 }
 
-// Workgroups [0, n_long) take the planned long segments; the others take SPB
-// consecutive segments each.  Without a plan (or with a plan built for
-// another capacity, detected from its header) the first n_long workgroups
-// exit and every other workgroup also runs its own long segments.
-template <int V, int LOG_LC, bool kNull, bool kOrdered>
+// Planned: workgroups [0, n_long) take the listed long segments, the others
+// SPB consecutive segments each, skipping the long ones.  Unplanned: every
+// workgroup takes SPB consecutive segments and runs its own long segments
+// after its short ones.
+template <int V, int LOG_LC, bool kNull, bool kOrdered, bool kPlanned>
 __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, const int64_t* __restrict__ plan,
                                                                  int64_t n_long) {
   using S = Geo<V, LOG_LC>;
   __shared__ float partial[kWaves][2][S::LC * V];
-  const bool planned = plan != nullptr && plan[0] == S::CAP;
-  if (static_cast<int64_t>(blockIdx.x) < n_long) {
-    if (!planned) return;
+  constexpr bool planned = kPlanned;
+  if (planned && static_cast<int64_t>(blockIdx.x) < n_long) {
     const int64_t segment = plan[kPlanHeader + blockIdx.x];
     if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
     int64_t begin, end;
@@ -472,7 +487,7 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, 
     forward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
     return;
   }
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) - n_long) * S::SPB;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
   const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t begin = __shfl(bb.lo, gidx);
@@ -480,7 +495,7 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, 
   const int64_t segment = first + gidx;
   if (segment < a.n_nodes && end - begin <= S::CAP)
     forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-  if (planned) return;
+  if constexpr (planned) return;
   // no plan: this workgroup's long segments, one at a time
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
@@ -551,11 +566,11 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
   }
   const bool staged = degree <= RMAXB * PB;
   float xs[RMAXB][V], gs[RMAXB][V], envs[RMAXB];
-  int64_t edge[RMAXB];
+  TileEdges<kOrdered, RMAXB> edge;
   if (staged) {
 #pragma unroll
     for (int i = 0; i < RMAXB; ++i) {
-      edge[i] = -1;
+      edge.set(i, -1);
       envs[i] = 0.0f;
 #pragma unroll
       for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
@@ -563,7 +578,7 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
       if (slot < end) {
         const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
         if (e >= 0) {
-          edge[i] = e;
+          edge.set(i, e);
           envs[i] = a.env[e];
           if (L.live) {
             const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
@@ -620,7 +635,9 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
   }
   if (staged) {
 #pragma unroll
-    for (int i = 0; i < RMAXB; ++i) backward_row<V, LOG_LC>(a, L, edge[i], xs[i], gs[i], expect, envs[i]);
+    for (int i = 0; i < RMAXB; ++i)
+      backward_row<V, LOG_LC>(a, L, edge.get(i, begin + static_cast<int64_t>(i) * PB + L.pb, end), xs[i], gs[i],
+                              expect, envs[i]);
   } else {
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
 #pragma unroll
@@ -676,10 +693,10 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
     }
   }
   float xs[RMAX][V], gs[RMAX][V], envs[RMAX];
-  int64_t edge[RMAX];
+  TileEdges<kOrdered, RMAX> edge;
 #pragma unroll
   for (int i = 0; i < RMAX; ++i) {
-    edge[i] = -1;
+    edge.set(i, -1);
     envs[i] = 0.0f;
 #pragma unroll
     for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
@@ -687,7 +704,7 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
     if (slot < end) {
       const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e >= 0) {
-        edge[i] = e;
+        edge.set(i, e);
         envs[i] = a.env[e];
         if (L.live) {
           const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
@@ -709,7 +726,9 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
     if (kNull) expect[v] = expect[v] + a0[v] * g0[v];
   }
 #pragma unroll
-  for (int i = 0; i < RMAX; ++i) backward_row<V, LOG_LC>(a, L, edge[i], xs[i], gs[i], expect, envs[i]);
+  for (int i = 0; i < RMAX; ++i)
+    backward_row<V, LOG_LC>(a, L, edge.get(i, begin + static_cast<int64_t>(i) * PG + L.p, end), xs[i], gs[i], expect,
+                            envs[i]);
   if (kNull && L.p == 0 && L.live) {
     fvec<V> out;
 #pragma unroll
@@ -718,14 +737,13 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
   }
 }
 
-template <int V, int LOG_LC, bool kNull, bool kOrdered>
+template <int V, int LOG_LC, bool kNull, bool kOrdered, bool kPlanned>
 __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a, const int64_t* __restrict__ plan,
                                                                   int64_t n_long) {
   using S = Geo<V, LOG_LC>;
   __shared__ float partial[kWaves][2][S::LC * V];
-  const bool planned = plan != nullptr && plan[0] == S::CAP;
-  if (static_cast<int64_t>(blockIdx.x) < n_long) {
-    if (!planned) return;
+  constexpr bool planned = kPlanned;
+  if (planned && static_cast<int64_t>(blockIdx.x) < n_long) {
     const int64_t segment = plan[kPlanHeader + blockIdx.x];
     if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
     int64_t begin, end;
@@ -733,7 +751,7 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
     backward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
     return;
   }
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) - n_long) * S::SPB;
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
   const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t begin = __shfl(bb.lo, gidx);
@@ -741,7 +759,7 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
   const int64_t segment = first + gidx;
   if (segment < a.n_nodes && end - begin <= S::CAP)
     backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-  if (planned) return;
+  if constexpr (planned) return;
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
       __ballot(lane < S::SPB && first + lane < a.n_nodes && bb.hi - bb.lo > S::CAP);
@@ -945,9 +963,12 @@ unsigned int short_blocks(int64_t n_nodes, int log_lc) {
 
 template <int V, int LOG_LC>
 int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = n_long + short_blocks(a.n_nodes, LOG_LC);
-#define DPA4K_SOFTMAX_FWD(NULLV, ORD) \
-  softmax_forward_kernel<V, LOG_LC, NULLV, ORD><<<static_cast<unsigned int>(grid), kBlock, 0, stream>>>(a, plan, n_long)
+  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, LOG_LC);
+#define DPA4K_SOFTMAX_FWD(NULLV, ORD)                                                                      \
+  (plan != nullptr                                                                                        \
+       ? softmax_forward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
+       : softmax_forward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<static_cast<unsigned int>(grid), kBlock, 0, \
+                                                                 stream>>>(a, plan, n_long)
   if (a.null_logit != nullptr) {
     if (a.order != nullptr) DPA4K_SOFTMAX_FWD(true, true); else DPA4K_SOFTMAX_FWD(true, false);
   } else {
@@ -959,9 +980,12 @@ int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hi
 
 template <int V, int LOG_LC>
 int launch_backward(const BackwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = n_long + short_blocks(a.n_nodes, LOG_LC);
-#define DPA4K_SOFTMAX_BWD(NULLV, ORD) \
-  softmax_backward_kernel<V, LOG_LC, NULLV, ORD><<<static_cast<unsigned int>(grid), kBlock, 0, stream>>>(a, plan, n_long)
+  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, LOG_LC);
+#define DPA4K_SOFTMAX_BWD(NULLV, ORD)                                                                       \
+  (plan != nullptr                                                                                         \
+       ? softmax_backward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
+       : softmax_backward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<static_cast<unsigned int>(grid), kBlock, 0, \
+                                                                  stream>>>(a, plan, n_long)
   if (a.null_alpha != nullptr) {
     if (a.order != nullptr) DPA4K_SOFTMAX_BWD(true, true); else DPA4K_SOFTMAX_BWD(true, false);
   } else {
@@ -1006,7 +1030,8 @@ int check_common(int64_t n_edges, int64_t n_nodes, int64_t channels, const char*
 
 int softmax_forward(const float* logit, const float* env, const int64_t* offsets, const float* null_logit,
                     const int64_t* order, float* alpha, float* null_alpha, int64_t n_edges, int64_t n_nodes,
-                    int64_t channels, const void* plan, int64_t n_long, dpa4k_stream_t stream_handle) {
+                    int64_t channels, const void* plan, int64_t n_long, int64_t plan_capacity,
+                    dpa4k_stream_t stream_handle) {
   if (int s = check_common(n_edges, n_nodes, channels, "segment softmax")) return s;
   if (plan != nullptr && (n_long < 0 || n_long > n_nodes))
     return fail(DPA4K_EINVAL, "segment softmax: n_long outside [0, n_nodes]");
@@ -1026,18 +1051,19 @@ int softmax_forward(const float* logit, const float* env, const int64_t* offsets
     else softmax_forward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_forward_wide_kernel");
   }
-  const int64_t* words = static_cast<const int64_t*>(plan);
-  const int64_t used = plan != nullptr ? n_long : 0;
+  // a plan applies only to the geometry it was built for; otherwise run unplanned
+  const bool use_plan = plan != nullptr && plan_capacity == capacity_for(channels, vec4);
+  const int64_t* words = use_plan ? static_cast<const int64_t*>(plan) : nullptr;
   const int log_lc = lanes_log_for(chunks);
-  return vec4 ? dispatch_forward<4>(log_lc, a, words, used, stream)
-              : dispatch_forward<1>(log_lc, a, words, used, stream);
+  return vec4 ? dispatch_forward<4>(log_lc, a, words, use_plan ? n_long : 0, stream)
+              : dispatch_forward<1>(log_lc, a, words, use_plan ? n_long : 0, stream);
 }
 
 int softmax_backward(const float* alpha, const float* grad_alpha, const float* env, const int64_t* offsets,
                      const float* null_alpha, const float* grad_null_alpha, const int64_t* order,
                      float* grad_logit, float* grad_null_logit, float* grad_env, int64_t n_edges,
                      int64_t n_nodes, int64_t channels, const void* plan, int64_t n_long,
-                     dpa4k_stream_t stream_handle) {
+                     int64_t plan_capacity, dpa4k_stream_t stream_handle) {
   if (int s = check_common(n_edges, n_nodes, channels, "segment softmax backward")) return s;
   if (plan != nullptr && (n_long < 0 || n_long > n_nodes))
     return fail(DPA4K_EINVAL, "segment softmax backward: n_long outside [0, n_nodes]");
@@ -1062,11 +1088,11 @@ int softmax_backward(const float* alpha, const float* grad_alpha, const float* e
     else softmax_backward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_backward_wide_kernel");
   }
-  const int64_t* words = static_cast<const int64_t*>(plan);
-  const int64_t used = plan != nullptr ? n_long : 0;
+  const bool use_plan = plan != nullptr && plan_capacity == capacity_for(channels, vec4);
+  const int64_t* words = use_plan ? static_cast<const int64_t*>(plan) : nullptr;
   const int log_lc = lanes_log_for(chunks);
-  return vec4 ? dispatch_backward<4>(log_lc, a, words, used, stream)
-              : dispatch_backward<1>(log_lc, a, words, used, stream);
+  return vec4 ? dispatch_backward<4>(log_lc, a, words, use_plan ? n_long : 0, stream)
+              : dispatch_backward<1>(log_lc, a, words, use_plan ? n_long : 0, stream);
 }
 
 }  // namespace
@@ -1080,7 +1106,7 @@ extern "C" int dpa4k_segment_softmax_forward(const float* logit, const float* en
                                              int64_t channels, dpa4k_stream_t stream) {
   clear_error();
   return softmax_forward(logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels,
-                         nullptr, 0, stream);
+                         nullptr, 0, 0, stream);
 }
 
 extern "C" int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha, const float* env,
@@ -1091,7 +1117,7 @@ extern "C" int dpa4k_segment_softmax_backward(const float* alpha, const float* g
                                               dpa4k_stream_t stream) {
   clear_error();
   return softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
-                          grad_null_logit, grad_env, n_edges, n_nodes, channels, nullptr, 0, stream);
+                          grad_null_logit, grad_env, n_edges, n_nodes, channels, nullptr, 0, 0, stream);
 }
 
 extern "C" size_t dpa4k_segment_softmax_plan_size(int64_t n_nodes) {
@@ -1101,10 +1127,10 @@ extern "C" size_t dpa4k_segment_softmax_plan_size(int64_t n_nodes) {
 
 extern "C" int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edges, int64_t n_nodes,
                                           int64_t channels, void* plan, size_t plan_bytes, int64_t* n_long,
-                                          dpa4k_stream_t stream_handle) {
+                                          int64_t* plan_capacity, dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_common(n_edges, n_nodes, channels, "segment softmax plan")) return s;
-  if (offsets == nullptr || plan == nullptr || n_long == nullptr)
+  if (offsets == nullptr || plan == nullptr || n_long == nullptr || plan_capacity == nullptr)
     return fail(DPA4K_EINVAL, "segment softmax plan: null pointer");
   if (plan_bytes < dpa4k_segment_softmax_plan_size(n_nodes))
     return fail(DPA4K_EWORKSPACE, "segment softmax plan: %zu bytes given, %zu needed", plan_bytes,
@@ -1134,6 +1160,7 @@ extern "C" int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edge
     return s;
   if (int s = hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize")) return s;
   *n_long = header[1];
+  *plan_capacity = header[0];
   return DPA4K_OK;
 }
 
@@ -1141,10 +1168,10 @@ extern "C" int dpa4k_segment_softmax_forward_planned(const float* logit, const f
                                                      const float* null_logit, const int64_t* order, float* alpha,
                                                      float* null_alpha, int64_t n_edges, int64_t n_nodes,
                                                      int64_t channels, const void* plan, int64_t n_long,
-                                                     dpa4k_stream_t stream) {
+                                                     int64_t plan_capacity, dpa4k_stream_t stream) {
   clear_error();
   return softmax_forward(logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels,
-                         plan, n_long, stream);
+                         plan, n_long, plan_capacity, stream);
 }
 
 extern "C" int dpa4k_segment_softmax_backward_planned(const float* alpha, const float* grad_alpha, const float* env,
@@ -1152,8 +1179,10 @@ extern "C" int dpa4k_segment_softmax_backward_planned(const float* alpha, const 
                                                       const float* grad_null_alpha, const int64_t* order,
                                                       float* grad_logit, float* grad_null_logit, float* grad_env,
                                                       int64_t n_edges, int64_t n_nodes, int64_t channels,
-                                                      const void* plan, int64_t n_long, dpa4k_stream_t stream) {
+                                                      const void* plan, int64_t n_long, int64_t plan_capacity,
+                                                      dpa4k_stream_t stream) {
   clear_error();
   return softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order, grad_logit,
-                          grad_null_logit, grad_env, n_edges, n_nodes, channels, plan, n_long, stream);
+                          grad_null_logit, grad_env, n_edges, n_nodes, channels, plan, n_long, plan_capacity,
+                          stream);
 }

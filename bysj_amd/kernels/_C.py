@@ -223,10 +223,11 @@ def _null_checks(tensor, nodes, channels, what):
 class SoftmaxPlan:
     """Degree plan of one CSR (the long segments of ``offsets``) for one channel count."""
 
-    __slots__ = ("words", "n_long", "n_edges", "channels")
+    __slots__ = ("words", "n_long", "capacity", "n_edges", "channels")
 
-    def __init__(self, words: torch.Tensor, n_long: int, n_edges: int, channels: int):
-        self.words, self.n_long, self.n_edges, self.channels = words, n_long, n_edges, channels
+    def __init__(self, words: torch.Tensor, n_long: int, capacity: int, n_edges: int, channels: int):
+        self.words, self.n_long, self.capacity = words, n_long, capacity
+        self.n_edges, self.channels = n_edges, channels
 
 
 def segment_softmax_plan(offsets, n_edges: int, channels: int) -> SoftmaxPlan:
@@ -235,14 +236,14 @@ def segment_softmax_plan(offsets, n_edges: int, channels: int) -> SoftmaxPlan:
     _check(int(channels) > 0, "segment softmax requires at least one channel")
     nbytes = _LIB.dpa4k_segment_softmax_plan_size(nodes)
     words = torch.empty((max(int(nbytes), 8) + 7) // 8, dtype=torch.int64, device=offsets.device)
-    n_long = _lib.ctypes.c_int64(0)
+    n_long, capacity = _lib.ctypes.c_int64(0), _lib.ctypes.c_int64(0)
     with _on(offsets.device) as stream:
         status = _LIB.dpa4k_segment_softmax_plan(
             offsets.data_ptr(), int(n_edges), nodes, int(channels), words.data_ptr(), words.numel() * 8,
-            _lib.ctypes.byref(n_long), stream,
+            _lib.ctypes.byref(n_long), _lib.ctypes.byref(capacity), stream,
         )
     _lib.check(status)
-    return SoftmaxPlan(words, int(n_long.value), int(n_edges), int(channels))
+    return SoftmaxPlan(words, int(n_long.value), int(capacity.value), int(n_edges), int(channels))
 
 
 def _plan_args(plan, offsets, edges, channels):
@@ -274,7 +275,7 @@ def segment_softmax_forward(logit, env, offsets, null_logit=None, order=None, *,
         else:
             status = _LIB.dpa4k_segment_softmax_forward_planned(
                 _ptr(logit), _ptr(env), offsets.data_ptr(), _ptr(null_logit), _ptr(order), _ptr(alpha),
-                _ptr(null_alpha), edges, nodes, channels, plan.words.data_ptr(), plan.n_long, stream,
+                _ptr(null_alpha), edges, nodes, channels, plan.words.data_ptr(), plan.n_long, plan.capacity, stream,
             )
     _lib.check(status)
     return alpha, null_alpha
@@ -309,7 +310,7 @@ def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
             status = _LIB.dpa4k_segment_softmax_backward_planned(
                 _ptr(alpha), _ptr(grad_alpha), _ptr(env), offsets.data_ptr(), _ptr(null_alpha),
                 _ptr(grad_null_alpha), _ptr(order), _ptr(grad_logit), _ptr(grad_null), _ptr(grad_env),
-                edges, nodes, channels, plan.words.data_ptr(), plan.n_long, stream,
+                edges, nodes, channels, plan.words.data_ptr(), plan.n_long, plan.capacity, stream,
             )
     _lib.check(status)
     return grad_logit, grad_null, grad_env

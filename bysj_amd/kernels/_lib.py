@@ -38,11 +38,12 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_segment_softmax_backward": (
         _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "dpa4k_segment_softmax_plan_size": (_SZ, [_I64]),
-    "dpa4k_segment_softmax_plan": (_INT, [_P, _I64, _I64, _I64, _P, _SZ, ctypes.POINTER(ctypes.c_int64), _P]),
+    "dpa4k_segment_softmax_plan": (
+        _INT, [_P, _I64, _I64, _I64, _P, _SZ, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64), _P]),
     "dpa4k_segment_softmax_forward_planned": (
-        _INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I64, _P]),
     "dpa4k_segment_softmax_backward_planned": (
-        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]),
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I64, _P]),
     "dpa4k_force_assembly_f32": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "dpa4k_force_assembly_f64": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "dpa4k_gie_group_workspace_size": (_SZ, [_I64, _I64]),

@@ -158,29 +158,34 @@ int dpa4k_segment_softmax_backward(const float* alpha, const float* grad_alpha,
  * a workgroup of its own ahead of the short segments.  Build it once per
  * graph and reuse it for every forward and backward on the same offsets and
  * channel count.  plan >= dpa4k_segment_softmax_plan_size(N) bytes of device
- * memory (8-byte aligned); *n_long (host) receives the number of listed
- * segments.  Synchronises (to read n_long back). */
+ * memory (8-byte aligned); *n_long and *plan_capacity (host) receive the
+ * number of listed segments and the degree threshold the list was built for.
+ * Synchronises (to read them back). */
 size_t dpa4k_segment_softmax_plan_size(int64_t n_nodes);
 int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edges,
                                int64_t n_nodes, int64_t channels, void* plan,
                                size_t plan_bytes, int64_t* n_long,
-                               dpa4k_stream_t stream);
+                               int64_t* plan_capacity, dpa4k_stream_t stream);
 
 /* dpa4k_segment_softmax_forward / _backward with a plan from
- * dpa4k_segment_softmax_plan on the same offsets (0 <= n_long <= N).  Same
- * results as the unplanned calls.  A plan built for another channel count
- * (or alignment) is detected from its header and ignored. */
+ * dpa4k_segment_softmax_plan on the same offsets, and the n_long and
+ * plan_capacity it returned (0 <= n_long <= N).  Same results as the
+ * unplanned calls, bit for bit.  When plan_capacity does not match the
+ * kernel chosen for these channels and pointer alignments, the plan is
+ * ignored and the call runs unplanned. */
 int dpa4k_segment_softmax_forward_planned(
     const float* logit, const float* env, const int64_t* offsets,
     const float* null_logit, const int64_t* order, float* alpha,
     float* null_alpha, int64_t n_edges, int64_t n_nodes, int64_t channels,
-    const void* plan, int64_t n_long, dpa4k_stream_t stream);
+    const void* plan, int64_t n_long, int64_t plan_capacity,
+    dpa4k_stream_t stream);
 int dpa4k_segment_softmax_backward_planned(
     const float* alpha, const float* grad_alpha, const float* env,
     const int64_t* offsets, const float* null_alpha,
     const float* grad_null_alpha, const int64_t* order, float* grad_logit,
     float* grad_null_logit, float* grad_env, int64_t n_edges, int64_t n_nodes,
-    int64_t channels, const void* plan, int64_t n_long, dpa4k_stream_t stream);
+    int64_t channels, const void* plan, int64_t n_long, int64_t plan_capacity,
+    dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * force_assembly
