@@ -349,6 +349,12 @@ def main() -> int:
                                                            bb["dst_offsets"], bb["src_offsets"]),
                 job["edges"], f"config 4 full input ({dtype_name}), oracle two index_add_ + outer product")
             print(f"[bench] force config 4 {dtype_name} done", file=sys.stderr, flush=True)
+        # the same box with atoms numbered in spatial (Morton) order, as MD engines sort them
+        water4s = workloads.water_graph(65536, seed=0, spatial_order=True)
+        for dtype_name in ("f32", "f64"):
+            job, _, _ = force_job(65536, steps, warm, graph, dtype_name, water=water4s)
+            ops[f"force_assembly_config4_{dtype_name}_spatial"] = op_line("force_assembly", job, job["edges"])
+        print("[bench] force config 4 spatial order done", file=sys.stderr, flush=True)
         if args.roofline_shapes:
             job = segment_sum_job(262144, steps, warm, graph)
             ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])

@@ -5,24 +5,68 @@
 // as a gather over two CSR views: the natural (dst-grouped) edge order and
 // the src_order permutation.  No atomics, no materialised (E, 9) product.
 //
-// Layout: a group of G = 16 lanes owns one atom (16 atoms per 256-thread
-// block).  On the destination side the group streams the contiguous span
-// grad_edge[3*begin, 3*end) as scalars (fully coalesced, the component of
-// scalar f is f mod 3, advanced incrementally); on the source side each lane
-// gathers whole edges through src_order.  Every lane accumulates all twelve
-// outputs in double precision, then a fixed DPP/swizzle butterfly over the
-// 16 lanes produces the totals, and lanes 0..11 store one component each.
-// The summation order depends only on the CSR, so results are reproducible;
-// fp32 inputs round once on output (double products of two floats are
-// exact), fp64 inputs keep double outputs.
+// Layout: a group of G = 32 lanes owns one atom (8 atoms per 256-thread
+// workgroup).  Every load of the atom is issued before any arithmetic:
+//   * the source side gathers whole 12- or 24-byte rows g_e, v_e through
+//     src_order (one row pair per lane, SRC_R rounds held in registers);
+//   * the destination side streams the contiguous span grad_edge[3*begin,
+//     3*end) as scalars (DST_R rounds in registers), the component of
+//     scalar f being f mod 3.
+// Longer segments continue in loops.  Every lane accumulates all twelve
+// outputs in double precision, a fixed DPP/swizzle butterfly over the 32
+// lanes produces the totals and lanes 0..11 store one component each.  The
+// summation order depends only on the CSR, so results are reproducible;
+// fp32 inputs round once on output (products of two floats are exact in
+// double), fp64 inputs keep double outputs.
+//
+// The source side is a random gather when atom numbering has no spatial
+// locality: each 12-byte row then costs a whole cache line, which bounds the
+// kernel well below the HBM roofline of its algorithmic bytes.
 #include "common.h"
 
 namespace dpa4k {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kGroup = 16;
+constexpr int kLogGroup = 5;
+constexpr int kGroup = 1 << kLogGroup;
 constexpr int kAtoms = kBlock / kGroup;
+constexpr int kSrcRounds = 3;   // source rows per lane held in registers
+constexpr int kDstRounds = 9;   // destination scalars per lane held in registers
+
+template <typename T>
+struct Row3 {
+  T x, y, z;
+};
+
+template <typename T>
+__device__ __forceinline__ Row3<T> load_row(const T* __restrict__ base, int64_t e) {
+  return *reinterpret_cast<const Row3<T>*>(base + 3 * e);
+}
+
+__device__ __forceinline__ void add_component(double (&acc)[12], int64_t f, double value) {
+  const int component = static_cast<int>(f % 3);
+  acc[0] += component == 0 ? value : 0.0;
+  acc[1] += component == 1 ? value : 0.0;
+  acc[2] += component == 2 ? value : 0.0;
+}
+
+template <typename T>
+__device__ __forceinline__ void add_source(double (&acc)[12], const Row3<T>& g, const Row3<T>& v) {
+  const double g0 = g.x, g1 = g.y, g2 = g.z, v0 = v.x, v1 = v.y, v2 = v.z;
+  acc[0] -= g0;
+  acc[1] -= g1;
+  acc[2] -= g2;
+  acc[3] -= g0 * v0;
+  acc[4] -= g0 * v1;
+  acc[5] -= g0 * v2;
+  acc[6] -= g1 * v0;
+  acc[7] -= g1 * v1;
+  acc[8] -= g1 * v2;
+  acc[9] -= g2 * v0;
+  acc[10] -= g2 * v1;
+  acc[11] -= g2 * v2;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
@@ -30,49 +74,53 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
     const int64_t* __restrict__ dst_offsets, const int64_t* __restrict__ src_offsets,
     const int64_t* __restrict__ src_order, T* __restrict__ force, T* __restrict__ virial,
     int64_t n_edges, int64_t n_nodes) {
-  const int64_t atom = static_cast<int64_t>(blockIdx.x) * kAtoms + threadIdx.x / kGroup;
+  const int64_t atom = static_cast<int64_t>(blockIdx.x) * kAtoms + (threadIdx.x >> kLogGroup);
   if (atom >= n_nodes) return;
-  const int lane = threadIdx.x % kGroup;
+  const int lane = threadIdx.x & (kGroup - 1);
+  int64_t dst_begin, dst_end, src_begin, src_end;
+  segment_bounds(dst_offsets, atom, n_edges, dst_begin, dst_end);
+  segment_bounds(src_offsets, atom, n_edges, src_begin, src_end);
 
+  // ---- issue the loads ----
+  int64_t edge[kSrcRounds];
+#pragma unroll
+  for (int r = 0; r < kSrcRounds; ++r) {
+    const int64_t slot = src_begin + r * kGroup + lane;
+    edge[r] = slot < src_end ? edge_of<true>(src_order, slot, n_edges) : -1;
+  }
+  Row3<T> g[kSrcRounds], v[kSrcRounds];
+#pragma unroll
+  for (int r = 0; r < kSrcRounds; ++r) {
+    if (edge[r] >= 0) {
+      g[r] = load_row(grad_edge, edge[r]);
+      v[r] = load_row(edge_vec, edge[r]);
+    } else {
+      g[r] = v[r] = Row3<T>{T(0), T(0), T(0)};
+    }
+  }
+  const int64_t dst_stop = 3 * dst_end;
+  T d[kDstRounds];
+#pragma unroll
+  for (int r = 0; r < kDstRounds; ++r) {
+    const int64_t f = 3 * dst_begin + r * kGroup + lane;
+    d[r] = f < dst_stop ? grad_edge[f] : T(0);
+  }
+
+  // ---- accumulate ----
   double acc[12];
 #pragma unroll
   for (int i = 0; i < 12; ++i) acc[i] = 0.0;
-
-  int64_t begin, end;
-  segment_bounds(dst_offsets, atom, n_edges, begin, end);
-  {
-    constexpr int kStep = kGroup % 3;
-    const int64_t stop = 3 * end;
-    int64_t f = 3 * begin + lane;
-    int component = static_cast<int>(f % 3);
-    for (; f < stop; f += kGroup) {
-      const double value = static_cast<double>(grad_edge[f]);
-      acc[0] += component == 0 ? value : 0.0;
-      acc[1] += component == 1 ? value : 0.0;
-      acc[2] += component == 2 ? value : 0.0;
-      component += kStep;
-      if (component >= 3) component -= 3;
-    }
-  }
-
-  segment_bounds(src_offsets, atom, n_edges, begin, end);
-  for (int64_t slot = begin + lane; slot < end; slot += kGroup) {
+#pragma unroll
+  for (int r = 0; r < kDstRounds; ++r)
+    add_component(acc, 3 * dst_begin + r * kGroup + lane, static_cast<double>(d[r]));
+  for (int64_t f = 3 * dst_begin + kDstRounds * kGroup + lane; f < dst_stop; f += kGroup)
+    add_component(acc, f, static_cast<double>(grad_edge[f]));
+#pragma unroll
+  for (int r = 0; r < kSrcRounds; ++r) add_source(acc, g[r], v[r]);
+  for (int64_t slot = src_begin + kSrcRounds * kGroup + lane; slot < src_end; slot += kGroup) {
     const int64_t e = edge_of<true>(src_order, slot, n_edges);
     if (e < 0) continue;
-    const double g0 = grad_edge[3 * e], g1 = grad_edge[3 * e + 1], g2 = grad_edge[3 * e + 2];
-    const double v0 = edge_vec[3 * e], v1 = edge_vec[3 * e + 1], v2 = edge_vec[3 * e + 2];
-    acc[0] -= g0;
-    acc[1] -= g1;
-    acc[2] -= g2;
-    acc[3] -= g0 * v0;
-    acc[4] -= g0 * v1;
-    acc[5] -= g0 * v2;
-    acc[6] -= g1 * v0;
-    acc[7] -= g1 * v1;
-    acc[8] -= g1 * v2;
-    acc[9] -= g2 * v0;
-    acc[10] -= g2 * v1;
-    acc[11] -= g2 * v2;
+    add_source(acc, load_row(grad_edge, e), load_row(edge_vec, e));
   }
 
 #pragma unroll

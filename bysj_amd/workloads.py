@@ -70,14 +70,33 @@ class WaterGraph:
         return offsets_from_degrees(self.degrees())
 
 
-def water_graph(n_atoms: int, seed: int, *, rcut: float = 6.0, density: float = 0.1) -> WaterGraph:
-    """Uniform random positions in a periodic cube; O:H = 1:2 types shuffled by the seed."""
+def morton_order(positions: np.ndarray, box: float, bin_size: float) -> np.ndarray:
+    """Permutation sorting atoms by the Z-order (Morton) key of their spatial bin,
+    the kind of periodic spatial sort MD engines apply to their atom arrays."""
+    bins = np.minimum((positions // bin_size).astype(np.int64), max(1, int(box // bin_size)) - 1)
+    key = np.zeros(positions.shape[0], dtype=np.int64)
+    for bit in range(21):
+        for axis in range(3):
+            key |= ((bins[:, axis] >> bit) & 1) << (3 * bit + axis)
+    return np.argsort(key, kind="stable")
+
+
+def water_graph(n_atoms: int, seed: int, *, rcut: float = 6.0, density: float = 0.1,
+                spatial_order: bool = False) -> WaterGraph:
+    """Uniform random positions in a periodic cube; O:H = 1:2 types shuffled by the seed.
+
+    Atom indices follow the draw order (no spatial locality) unless
+    ``spatial_order`` renumbers them by the Morton key of rcut/2 bins.
+    """
     generator = rng(seed)
     box = (n_atoms / density) ** (1.0 / 3.0)
     types = np.ones(n_atoms, dtype=np.int64)
     types[: n_atoms // 3] = 0
     types = types[generator.permutation(n_atoms)]
     positions = generator.uniform(0.0, box, size=(n_atoms, 3))
+    if spatial_order:
+        permutation = morton_order(positions, box, rcut / 2.0)
+        positions, types = positions[permutation], types[permutation]
 
     n_cell = int(box // rcut)
     if n_cell < 3:
