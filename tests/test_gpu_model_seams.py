@@ -1,0 +1,84 @@
+"""The DeepMD seams with the real gfx950 operators (kernels.* -> libdpa4k.so) on cuda:0.
+
+Each seam runs on a destination list that is grouped by segment but not
+sorted (DeepMD's layout, so the CSR view carries an ``order``), and is compared
+with DeepMD's stock path restated in tests/seam_fakes.py -- values and the
+gradients that forces need (message, logits, envelope, source gate, bias).
+Shapes follow the reference's opt-in parity test
+(tests/csrc/accuracy/test_fused_deepmd_parity.py:45-110 of lipengfei1409/bysj).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from bysj_amd.model import fused_deepmd
+from parity import announce, assert_close_scaled
+from seam_fakes import FakeBlock, FakeModel, softmax_namespace
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _shuffled_dst(n_nodes, n_edges, seed):
+    gen = torch.Generator().manual_seed(seed)
+    dst = torch.randint(0, n_nodes, (n_edges,), generator=gen)
+    return dst.to(DEV)
+
+
+@pytest.fixture
+def clean():
+    yield
+    fused_deepmd.uninstall()
+
+
+def test_softmax_seam_on_gfx950(clean):
+    announce("seam softmax 512 nodes / 8192 edges / F*H = 16")
+    space = softmax_namespace()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), namespaces=[space], envelope=False, verbose=False)
+    assert stats.bound_softmax, "the gfx950 operators should be usable on this device"
+    gen = torch.Generator().manual_seed(1)
+    dst = _shuffled_dst(512, 8192, seed=2)
+    logits = (torch.randn(8192, 4, 4, generator=gen) * 2).to(DEV).requires_grad_(True)
+    env = (torch.rand(8192, 1, generator=gen) + 0.05).to(DEV).requires_grad_(True)
+    bias = torch.randn(4, 4, generator=gen).to(DEV).requires_grad_(True)
+    upstream = torch.randn(8192, 4, 4, generator=gen).to(DEV)
+    leaves = (logits, env, bias)
+    alpha = space.segment_envelope_gated_softmax(logits, env, dst, 512, bias, 1e-6)
+    grads = torch.autograd.grad(alpha, leaves, upstream)
+    assert stats.softmax_hits == 1 and stats.softmax_fallbacks == 0, stats
+    fused_deepmd.uninstall()
+    expected = space.segment_envelope_gated_softmax(logits, env, dst, 512, bias, 1e-6)
+    want = torch.autograd.grad(expected, leaves, upstream)
+    assert_close_scaled(alpha, expected, what="alpha")
+    for got, ref, name in zip(grads, want, ("grad_logits", "grad_env", "grad_bias")):
+        assert_close_scaled(got, ref, rtol=2e-5, scale=2e-5, what=name)
+
+
+@pytest.mark.parametrize("gate", [False, True])
+def test_envelope_seam_on_gfx950(clean, gate):
+    announce("seam envelope 64 nodes / 4096 edges / D=4 C=32", gate)
+    gen = torch.Generator().manual_seed(3)
+    n_nodes, n_edges = 64, 4096
+    dst = _shuffled_dst(n_nodes, n_edges, seed=4)
+    cache = type("EdgeCache", (), {})()
+    cache.dst = dst
+    cache.edge_env = (torch.rand(n_edges, 1, generator=gen) + 0.1).to(DEV).requires_grad_(True)
+    cache.inv_sqrt_deg = torch.rsqrt(torch.bincount(dst.cpu(), minlength=n_nodes).float() + 1).reshape(-1, 1, 1).to(DEV)
+    cache.edge_src_gate = (torch.rand(n_edges, 1, generator=gen) + 0.5).to(DEV).requires_grad_(True) if gate else None
+    message = torch.randn(n_edges, 4, 32, generator=gen).to(DEV).requires_grad_(True)
+    block = FakeBlock(message)
+    stats = fused_deepmd.deepmd_patch(FakeModel([block]), softmax=False, verbose=False)
+    assert stats.bound_envelope
+    x = torch.zeros(n_nodes, 4, 32, device=DEV)
+    upstream = torch.randn(n_nodes, 4, 32, generator=gen).to(DEV)
+    leaves = (message, cache.edge_env) + ((cache.edge_src_gate,) if gate else ())
+    out = block.forward_envelope(x, cache, None)
+    grads = torch.autograd.grad(out, leaves, upstream)
+    assert stats.envelope_hits == 1 and stats.envelope_fallbacks == 0, stats
+    fused_deepmd.uninstall()
+    expected = block.forward_envelope(x, cache, None)
+    want = torch.autograd.grad(expected, leaves, upstream)
+    assert_close_scaled(out, expected, what="aggregation")
+    for got, ref, name in zip(grads, want, ("grad_message", "grad_edge_env", "grad_gate")):
+        assert_close_scaled(got, ref, rtol=2e-5, scale=2e-5, what=name)
