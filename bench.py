@@ -43,6 +43,7 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--headline-only", action="store_true", help="skip the per-operator lines")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-backward", action="store_true", help="skip the backward and CSR-build lines")
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
     parser.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
     parser.add_argument("--roofline-shapes", action="store_true",
@@ -228,6 +229,116 @@ def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: st
             "dtype": dtype_name}, water, base
 
 
+def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+    """segment_softmax backward (with the null logit) on the config-2 graph."""
+    import torch
+
+    from bysj_amd import kernels, workloads
+    from bysj_amd.kernels import _C
+
+    base = workloads.segment_softmax_config(n_nodes=n_nodes, seed=0, device="cuda")
+    edges, channels = base["logit"].shape
+    offsets = base["offsets"]
+    alpha, null_alpha = kernels.segment_softmax(base["logit"], base["env"], offsets, base["null_logit"])
+    plan = _C.segment_softmax_plan(offsets, edges, channels)
+    reads = 2 * edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + 2 * n_nodes * channels * 4
+    writes = edges * channels * 4 + n_nodes * channels * 4 + edges * 4
+    n_sets = n_sets_for(reads + writes)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(7)
+    cotangents = [(torch.randn(alpha.shape, generator=generator, device="cuda"),
+                   torch.randn(null_alpha.shape, generator=generator, device="cuda")) for _ in range(n_sets)]
+
+    def step(i):
+        grad_alpha, grad_null = cotangents[i]
+        return _C.segment_softmax_backward(alpha, grad_alpha, base["env"], offsets, null_alpha, grad_null,
+                                           plan=plan)
+
+    ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
+            "bytes": reads + writes}
+
+
+def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+    """segment_sum backward with edge_scale and node_scale: grad_src, grad_edge_scale, grad_node_scale."""
+    import torch
+
+    from bysj_amd import workloads
+    from bysj_amd.kernels import _C
+
+    base = workloads.segment_sum_config(n_nodes=n_nodes, seed=0, device="cuda", scales=True)
+    edges, channels = base["src"].shape
+    reads = n_nodes * channels * 4 + edges * channels * 4 + edges * 4 + n_nodes * 4 + (n_nodes + 1) * 8
+    writes = edges * channels * 4 + edges * 4 + n_nodes * 4
+    n_sets = n_sets_for(reads + writes)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(8)
+    grads = [torch.randn((n_nodes, channels), generator=generator, device="cuda") for _ in range(n_sets)]
+
+    def step(i):
+        return _C.segment_sum_backward(grads[i], base["src"], base["dst"], base["offsets"], base["edge_scale"],
+                                       base["node_scale"], True, None, want_edge_scale_grad=True)
+
+    ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
+            "bytes": reads + writes}
+
+
+def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool):
+    """GIE backward (zonal, radial and inverse-degree gradients) and RMSNorm backward on config 3."""
+    import torch
+
+    from bysj_amd.kernels import _C
+
+    n_atoms, edges = water.n_atoms, water.n_edges
+    offsets, order, info = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, 16)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(9)
+    grad_out = torch.randn((n_atoms, 16, 64), generator=generator, device="cuda")
+
+    def gie_step(_):
+        return _C.gie_zonal_scatter_backward_csr(grad_out, case["zonal"], case["radial"], offsets, order,
+                                                 case["radial_slot"], case["inv_sqrt_deg"], bool(info & 2))
+
+    gie_reads = n_atoms * 15 * 64 * 4 + edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 \
+        + n_atoms * 4
+    gie_writes = edges * 15 * 4 + edges * 16 * 64 * 4 + n_atoms * 4
+    gie_ms = time_steps(gie_step, 1, max(4, steps // 10), min(warmup, 3), graph=graph)
+    del grad_out
+
+    x = torch.randn((n_atoms, 1024), generator=generator, device="cuda")
+    _, inverse_rms = _C.rmsnorm_forward(x, case["rms_scale"], 1e-6)
+    rms_bytes = 3 * n_atoms * 1024 * 4 + 2 * 1024 * 4 + n_atoms * 4
+    n_sets = n_sets_for(rms_bytes)
+    grads = [torch.randn((n_atoms, 1024), generator=generator, device="cuda") for _ in range(n_sets)]
+
+    def rms_step(i):
+        return _C.rmsnorm_backward(grads[i], x, case["rms_scale"], inverse_rms, True)
+
+    rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
+    gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_reads + gie_writes, "sets": 1}
+    rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
+    return gie, rms
+
+
+def csr_job(water, steps: int):
+    """Device CSR build of a source list (group_by_source: offsets + stable order) on the config-4 graph.
+
+    The call synchronises (index range check), so it is timed eagerly, per call.
+    """
+    import torch
+
+    from bysj_amd import kernels
+
+    src = torch.from_numpy(water.src).to("cuda")
+    n_atoms, edges = water.n_atoms, water.n_edges
+    ms = time_steps(lambda _: kernels.group_by_source(src, n_atoms), 1, steps, 2, graph=False)
+    torch_ms = time_steps(lambda _: (torch.argsort(src, stable=True),
+                                     torch.bincount(src, minlength=n_atoms).cumsum(0)), 1, steps, 2, graph=False)
+    return {"edges": edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": edges * 8 + edges * 8 + (n_atoms + 1) * 8,
+            "sets": 1, "torch_ms_per_call": torch_ms}
+
+
 def op_line(name: str, job: dict, unit_count: int, unit: str = "edges/s") -> dict:
     line = {"op": name, "value": round(unit_count / (job["ms_per_step"] * 1e-3), 1), "unit": unit,
             "ms_per_step": round(job["ms_per_step"], 5), "input_sets": job.get("sets", 1),
@@ -355,6 +466,23 @@ def main() -> int:
             job, _, _ = force_job(65536, steps, warm, graph, dtype_name, water=water4s)
             ops[f"force_assembly_config4_{dtype_name}_spatial"] = op_line("force_assembly", job, job["edges"])
         print("[bench] force config 4 spatial order done", file=sys.stderr, flush=True)
+        if not args.no_backward:
+            job = softmax_backward_job(16384, steps, warm, graph)
+            ops["segment_softmax_bwd_config2"] = op_line("segment_softmax_bwd", job, job["edges"])
+            job = segment_sum_backward_job(1024, steps, warm, graph)
+            ops["segment_sum_bwd_config1"] = op_line("segment_sum_bwd", job, job["edges"])
+            job = segment_sum_backward_job(262144, max(4, steps // 4), warm, graph)
+            ops["segment_sum_bwd_config1R"] = op_line("segment_sum_bwd", job, job["edges"])
+            case3 = workloads.gie_config(water3, seed=0, device="cuda", primary=True)
+            gie_b, rms_b = gie_rmsnorm_backward_jobs(water3, case3, steps, warm, graph)
+            del case3
+            ops["gie_bwd_config3"] = op_line("gie_zonal_scatter_bwd", gie_b, gie_b["edges"])
+            ops["rmsnorm_bwd_config3"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
+            job = csr_job(water4, max(5, steps // 5))
+            line_csr = op_line("group_by_source", job, job["edges"])
+            line_csr["torch_argsort_bincount_ms"] = round(job["torch_ms_per_call"], 5)
+            ops["group_by_source_config4"] = line_csr
+            print("[bench] backward kernels and CSR build done", file=sys.stderr, flush=True)
         if args.roofline_shapes:
             job = segment_sum_job(262144, steps, warm, graph)
             ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])

@@ -14,9 +14,11 @@
 //
 // Backward is segment-parallel too: the group loads grad_out[n] once, writes
 // grad_src for every edge of the segment, and reduces the per-edge channel
-// dot product for grad_edge_scale with a fixed butterfly.  The reference's
-// edge-parallel grad_src kernel needs `dst`; here the CSR names each edge's
-// segment, which the grouping contract makes identical.
+// dot product (grad_edge_scale, and summed over the segment grad_node_scale)
+// with a fixed butterfly.  The reference's edge-parallel grad_src kernel
+// needs `dst`; here the CSR names each edge's segment, which the grouping
+// contract makes identical.  Grids too small to fill the chip (few segments)
+// keep up to 32 rows per lane in flight.
 #include "common.h"
 
 namespace dpa4k {
@@ -24,14 +26,13 @@ namespace {
 
 constexpr int kBlock = 256;
 
-template <int V, int G, int CPL, bool kScaleEdge, bool kOrdered>
+template <int V, int G, int CPL, int U, bool kScaleEdge, bool kOrdered>
 __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
     const float* __restrict__ src, const int64_t* __restrict__ offsets,
     const float* __restrict__ edge_scale, const float* __restrict__ node_scale,
     const int64_t* __restrict__ order, float* __restrict__ out, int64_t n_edges, int64_t n_nodes,
     int64_t channels, int64_t chunk_base) {
   constexpr int kSegments = kBlock / G;
-  constexpr int U = CPL >= 8 ? 2 : (CPL >= 4 ? 4 : 8);
   const int64_t segment = static_cast<int64_t>(blockIdx.x) * kSegments + threadIdx.x / G;
   if (segment >= n_nodes) return;
   const int lane = threadIdx.x % G;
@@ -55,16 +56,18 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[j].v[i] = 0.0f;
 
-  int64_t slot = begin;
-  for (; slot + U <= end; slot += U) {
+  // U slots per round, all loads of a round issued before any add; the adds
+  // then run in slot order, so each element is a sequential sum.
+  for (int64_t slot = begin; slot < end; slot += U) {
     int64_t edge[U];
     float weight[U];
     fvec<V> x[U][CPL];
 #pragma unroll
-    for (int u = 0; u < U; ++u) edge[u] = edge_of<kOrdered>(order, slot + u, n_edges);
+    for (int u = 0; u < U; ++u)
+      edge[u] = slot + u < end ? edge_of<kOrdered>(order, slot + u, n_edges) : -1;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool ok = !kOrdered || edge[u] >= 0;
+      const bool ok = edge[u] >= 0;
       weight[u] = kScaleEdge && ok ? edge_scale[edge[u]] : 1.0f;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
@@ -78,24 +81,12 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (kOrdered && edge[u] < 0) continue;
+      if (edge[u] < 0) continue;
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int i = 0; i < V; ++i)
           acc[j].v[i] = acc[j].v[i] + (kScaleEdge ? x[u][j].v[i] * weight[u] : x[u][j].v[i]);
-    }
-  }
-  for (; slot < end; ++slot) {
-    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-    if (kOrdered && e < 0) continue;
-    const float w = kScaleEdge ? edge_scale[e] : 1.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      if (!live[j]) continue;
-      const fvec<V> x = load_vec<V>(src + e * channels + column[j]);
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + (kScaleEdge ? x.v[i] * w : x.v[i]);
     }
   }
 
@@ -111,13 +102,17 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
   }
 }
 
-// grad_src[e] = (grad_out[n] * node_scale[n]) * edge_scale[e];
-// grad_edge_scale[e] = sum_c (grad_out[n, c] * node_scale[n]) * src[e, c];
-// grad_node_scale[n] = sum_c grad_out[n, c] * prefix[n, c],
-// prefix = sum_e edge_scale[e] * src[e] (recomputed in slot order).
-// `accumulate` adds the channel partial of this chunk window to the value
+// With g = grad_out[n], s = node_scale[n], w = edge_scale[e] and the raw
+// channel dot d_e = sum_c g[c] * src[e, c]:
+//   grad_src[e]        = (g * s) * w
+//   grad_edge_scale[e] = s * d_e
+//   grad_node_scale[n] = sum_e w * d_e
+// (the reference recomputes the prefix sum_e w src[e] for the node-scale
+// gradient; the per-edge dots give the same sum without it).  Each edge row
+// is read once; U edges per round are loaded before any arithmetic.
+// `accumulate` adds the partial dots of this channel window to the values
 // written by the previous window (channels wider than one window).
-template <int V, int G, int CPL, bool kOrdered>
+template <int V, int G, int CPL, int U, bool kOrdered>
 __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
     const float* __restrict__ grad_out, const float* __restrict__ src,
     const int64_t* __restrict__ offsets, const float* __restrict__ edge_scale,
@@ -132,6 +127,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
   const int64_t chunks = channels / V;
   const bool want_edge = grad_edge_scale != nullptr;
   const bool want_node = grad_node_scale != nullptr;
+  const bool need_dot = want_edge || want_node;
   const bool has_edge_scale = edge_scale != nullptr;
 
   int64_t column[CPL];
@@ -144,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
   }
 
   const float scale = node_scale != nullptr ? node_scale[segment] : 1.0f;
-  fvec<V> g[CPL], gs[CPL], prefix[CPL];
+  fvec<V> g[CPL], gs[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     if (live[j]) {
@@ -154,65 +150,67 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
       for (int i = 0; i < V; ++i) g[j].v[i] = 0.0f;
     }
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      gs[j].v[i] = node_scale != nullptr ? g[j].v[i] * scale : g[j].v[i];
-      prefix[j].v[i] = 0.0f;
-    }
+    for (int i = 0; i < V; ++i) gs[j].v[i] = node_scale != nullptr ? g[j].v[i] * scale : g[j].v[i];
   }
 
   int64_t begin, end;
   segment_bounds(offsets, segment, n_edges, begin, end);
-  for (int64_t slot = begin; slot < end; ++slot) {
-    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
-    if (kOrdered && e < 0) continue;
-    const float w = has_edge_scale ? edge_scale[e] : 1.0f;
-    fvec<V> x[CPL];
-    if (want_edge || want_node) {
+  float node_sum = 0.0f;
+  for (int64_t slot = begin; slot < end; slot += U) {
+    int64_t edge[U];
+    float weight[U], dot[U];
+    fvec<V> x[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      edge[u] = slot + u < end ? edge_of<kOrdered>(order, slot + u, n_edges) : -1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      weight[u] = has_edge_scale && edge[u] >= 0 ? edge_scale[edge[u]] : 1.0f;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        if (live[j]) {
-          x[j] = load_vec<V>(src + e * channels + column[j]);
+        if (need_dot && live[j] && edge[u] >= 0) {
+          x[u][j] = load_vec<V>(src + edge[u] * channels + column[j]);
         } else {
 #pragma unroll
-          for (int i = 0; i < V; ++i) x[j].v[i] = 0.0f;
+          for (int i = 0; i < V; ++i) x[u][j].v[i] = 0.0f;
         }
       }
     }
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      if (!live[j]) continue;
-      fvec<V> out;
+    for (int u = 0; u < U; ++u) {
+      if (edge[u] < 0) continue;
 #pragma unroll
-      for (int i = 0; i < V; ++i) out.v[i] = has_edge_scale ? gs[j].v[i] * w : gs[j].v[i];
-      store_vec_stream<V>(grad_src + e * channels + column[j], out);
+      for (int j = 0; j < CPL; ++j) {
+        if (!live[j]) continue;
+        fvec<V> out;
+#pragma unroll
+        for (int i = 0; i < V; ++i) out.v[i] = has_edge_scale ? gs[j].v[i] * weight[u] : gs[j].v[i];
+        store_vec_stream<V>(grad_src + edge[u] * channels + column[j], out);
+      }
     }
-    if (want_edge) {
-      float dot = 0.0f;
+    if (need_dot) {
 #pragma unroll
-      for (int j = 0; j < CPL; ++j)
+      for (int u = 0; u < U; ++u) {
+        float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < V; ++i) dot = dot + gs[j].v[i] * x[j].v[i];
-      dot = group_sum<G>(dot);
-      if (lane == 0) grad_edge_scale[e] = accumulate ? grad_edge_scale[e] + dot : dot;
-    }
-    if (want_node) {
+        for (int j = 0; j < CPL; ++j)
 #pragma unroll
-      for (int j = 0; j < CPL; ++j)
+          for (int i = 0; i < V; ++i) d = d + g[j].v[i] * x[u][j].v[i];
+        dot[u] = group_sum<G>(d);
+      }
 #pragma unroll
-        for (int i = 0; i < V; ++i)
-          prefix[j].v[i] = prefix[j].v[i] + (has_edge_scale ? x[j].v[i] * w : x[j].v[i]);
+      for (int u = 0; u < U; ++u) {
+        if (edge[u] < 0) continue;
+        if (want_edge && lane == 0) {
+          const float value = scale * dot[u];
+          grad_edge_scale[edge[u]] = accumulate ? grad_edge_scale[edge[u]] + value : value;
+        }
+        node_sum = node_sum + weight[u] * dot[u];
+      }
     }
   }
-  if (want_node) {
-    float dot = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-      for (int i = 0; i < V; ++i) dot = dot + g[j].v[i] * prefix[j].v[i];
-    dot = group_sum<G>(dot);
-    if (lane == 0)
-      grad_node_scale[segment] = accumulate ? grad_node_scale[segment] + dot : dot;
-  }
+  if (want_node && lane == 0)
+    grad_node_scale[segment] = accumulate ? grad_node_scale[segment] + node_sum : node_sum;
 }
 
 // Lane-group geometry for a row of `chunks` vector chunks.
@@ -232,27 +230,61 @@ Geometry geometry_for(int64_t chunks) {
   return g;
 }
 
+// Slots per round: about 32 loaded floats per lane, or 128 when the grid is
+// too small to fill the chip (then each lane must keep more bytes in flight).
+template <int V, int CPL>
+constexpr int unroll_for(bool small_grid) {
+  return small_grid ? (CPL * V >= 8 ? 16 : 32) : (CPL * V >= 16 ? 2 : (CPL * V >= 8 ? 4 : 8));
+}
+
+template <int V, int G, int CPL, int U>
+int launch_forward_u(const float* src, const int64_t* offsets, const float* edge_scale,
+                     const float* node_scale, const int64_t* order, float* out, int64_t n_edges,
+                     int64_t n_nodes, int64_t channels, int64_t chunk_base, hipStream_t stream) {
+  const unsigned int grid = blocks_for(n_nodes, kBlock / G);
+#define DPA4K_SUM_FWD(SCALE, ORD)                                                                     \
+  segment_sum_forward_kernel<V, G, CPL, U, SCALE, ORD><<<grid, kBlock, 0, stream>>>(                \
+      src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base)
+  if (edge_scale != nullptr) {
+    if (order != nullptr) DPA4K_SUM_FWD(true, true); else DPA4K_SUM_FWD(true, false);
+  } else {
+    if (order != nullptr) DPA4K_SUM_FWD(false, true); else DPA4K_SUM_FWD(false, false);
+  }
+#undef DPA4K_SUM_FWD
+  return launched("segment_sum_forward_kernel");
+}
+
+// A grid of fewer waves than the chip holds at once (256 CUs x 8 waves).
+bool small_grid(int64_t n_nodes, int group) { return n_nodes * group / 64 < 2048; }
+
 template <int V, int G, int CPL>
 int launch_forward(const float* src, const int64_t* offsets, const float* edge_scale,
                    const float* node_scale, const int64_t* order, float* out, int64_t n_edges,
                    int64_t n_nodes, int64_t channels, int64_t chunk_base, hipStream_t stream) {
+  if (small_grid(n_nodes, G))
+    return launch_forward_u<V, G, CPL, unroll_for<V, CPL>(true)>(src, offsets, edge_scale, node_scale, order,
+                                                                 out, n_edges, n_nodes, channels, chunk_base,
+                                                                 stream);
+  return launch_forward_u<V, G, CPL, unroll_for<V, CPL>(false)>(src, offsets, edge_scale, node_scale, order, out,
+                                                                n_edges, n_nodes, channels, chunk_base, stream);
+}
+
+template <int V, int G, int CPL, int U>
+int launch_backward_u(const float* grad_out, const float* src, const int64_t* offsets,
+                      const float* edge_scale, const float* node_scale, const int64_t* order,
+                      float* grad_src, float* grad_edge_scale, float* grad_node_scale,
+                      int64_t n_edges, int64_t n_nodes, int64_t channels, int64_t chunk_base,
+                      int accumulate, hipStream_t stream) {
   const unsigned int grid = blocks_for(n_nodes, kBlock / G);
-  if (edge_scale != nullptr) {
-    if (order != nullptr)
-      segment_sum_forward_kernel<V, G, CPL, true, true><<<grid, kBlock, 0, stream>>>(
-          src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base);
-    else
-      segment_sum_forward_kernel<V, G, CPL, true, false><<<grid, kBlock, 0, stream>>>(
-          src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base);
-  } else {
-    if (order != nullptr)
-      segment_sum_forward_kernel<V, G, CPL, false, true><<<grid, kBlock, 0, stream>>>(
-          src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base);
-    else
-      segment_sum_forward_kernel<V, G, CPL, false, false><<<grid, kBlock, 0, stream>>>(
-          src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base);
-  }
-  return launched("segment_sum_forward_kernel");
+  if (order != nullptr)
+    segment_sum_backward_kernel<V, G, CPL, U, true><<<grid, kBlock, 0, stream>>>(
+        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
+        grad_node_scale, n_edges, n_nodes, channels, chunk_base, accumulate);
+  else
+    segment_sum_backward_kernel<V, G, CPL, U, false><<<grid, kBlock, 0, stream>>>(
+        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
+        grad_node_scale, n_edges, n_nodes, channels, chunk_base, accumulate);
+  return launched("segment_sum_backward_kernel");
 }
 
 template <int V, int G, int CPL>
@@ -261,16 +293,14 @@ int launch_backward(const float* grad_out, const float* src, const int64_t* offs
                     float* grad_src, float* grad_edge_scale, float* grad_node_scale,
                     int64_t n_edges, int64_t n_nodes, int64_t channels, int64_t chunk_base,
                     int accumulate, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kBlock / G);
-  if (order != nullptr)
-    segment_sum_backward_kernel<V, G, CPL, true><<<grid, kBlock, 0, stream>>>(
-        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
-        grad_node_scale, n_edges, n_nodes, channels, chunk_base, accumulate);
-  else
-    segment_sum_backward_kernel<V, G, CPL, false><<<grid, kBlock, 0, stream>>>(
-        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
-        grad_node_scale, n_edges, n_nodes, channels, chunk_base, accumulate);
-  return launched("segment_sum_backward_kernel");
+  // the backward holds its rows for the dot products: half the forward's depth
+  if (small_grid(n_nodes, G))
+    return launch_backward_u<V, G, CPL, unroll_for<V, CPL>(true) / 2>(
+        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
+        n_edges, n_nodes, channels, chunk_base, accumulate, stream);
+  return launch_backward_u<V, G, CPL, (unroll_for<V, CPL>(false) > 2 ? unroll_for<V, CPL>(false) / 2 : 2)>(
+      grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale, n_edges,
+      n_nodes, channels, chunk_base, accumulate, stream);
 }
 
 // Dispatches a launcher template over the (V, G, CPL) geometry.
