@@ -9,8 +9,9 @@
 // once; the row sum is a DPP / swizzle / bpermute butterfly.  Wider rows take
 // a two-pass streaming kernel.  The reference accumulates grad_scale with one
 // float atomic per (row, column); here each wave keeps per-column partials
-// for its fixed set of rows, the partials go to the workspace and a two-level
-// column reduction sums them in a fixed order.
+// for its fixed set of rows (two rows loaded per round), the four waves of a
+// workgroup add theirs in LDS, the workgroup partials go to the workspace and
+// one wave per group of columns sums them -- every order fixed.
 #include "common.h"
 
 namespace dpa4k {
@@ -18,8 +19,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
-constexpr int kPartialWaves = 2048;   // waves of the grad_scale backward
-constexpr int kLevel = 32;            // partial rows summed per thread per level
+constexpr int kPartialWaves = 3072;   // waves of the grad_scale backward (resident at 3 per SIMD)
 
 __device__ __forceinline__ float inverse_rms_of(float sum_squares, int64_t width, float eps) {
   return 1.0f / sqrtf(sum_squares / static_cast<float>(width) + eps);
@@ -36,20 +36,23 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_forward_kernel(
   const float* xr = x + row * width;
   float* yr = y + row * width;
   if constexpr (CPL > 0) {
-    fvec<V> value[CPL];
+    // the row and the scale chunks are loaded before the reduction
+    fvec<V> value[CPL], s[CPL];
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int64_t q = lane + 64 * j;
+#pragma unroll
+      for (int i = 0; i < V; ++i) value[j].v[i] = s[j].v[i] = 0.0f;
       if (q < chunks) {
         value[j] = load_vec<V>(xr + q * V);
-      } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) value[j].v[i] = 0.0f;
+        if (scale != nullptr) s[j] = load_vec<V>(scale + q * V);
       }
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
       for (int i = 0; i < V; ++i) sum = sum + value[j].v[i] * value[j].v[i];
-    }
     sum = group_sum<64>(sum);
     const float inv = inverse_rms_of(sum, width, eps);
 #pragma unroll
@@ -57,14 +60,12 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_forward_kernel(
       const int64_t q = lane + 64 * j;
       if (q >= chunks) continue;
       fvec<V> out;
-      fvec<V> s;
-      if (scale != nullptr) s = load_vec<V>(scale + q * V);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         out.v[i] = value[j].v[i] * inv;
-        if (scale != nullptr) out.v[i] = out.v[i] * s.v[i];
+        if (scale != nullptr) out.v[i] = out.v[i] * s[j].v[i];
       }
-      store_vec<V>(yr + q * V, out);
+      store_vec_stream<V>(yr + q * V, out);
     }
     if (lane == 0) inverse_rms[row] = inv;
   } else {
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_forward_kernel(
   }
 }
 
-// Register path (CPL > 0): wave w handles rows w, w + waves, ...; with
+// Register path (CPL > 0): wave w handles rows w, w + waves, ... (two per round); with
 // `partial` non-null it also stores its per-column sum of grad * (x * inv)
 // as row w of the [waves, W] partial matrix.
 template <int V, int CPL>
@@ -117,51 +118,98 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_backward_kernel(
     if (scale != nullptr && q < chunks) s[j] = load_vec<V>(scale + q * V);
   }
 
-  for (int64_t row = wave_id; row < rows; row += waves) {
-    const float* gr = grad + row * width;
-    const float* xr = x + row * width;
-    fvec<V> g[CPL], xv[CPL], u[CPL];
-    float dot = 0.0f;
+  // Rows wave_id, wave_id + waves, ... two per round: both rows' loads are
+  // issued before either is reduced.
+  for (int64_t first = wave_id; first < rows; first += 2 * waves) {
+    fvec<V> g[2][CPL], xv[2][CPL];
+    float inv[2];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int64_t q = lane + 64 * j;
-      if (q < chunks) {
-        g[j] = load_vec<V>(gr + q * V);
-        xv[j] = load_vec<V>(xr + q * V);
-      } else {
+    for (int r = 0; r < 2; ++r) {
+      const int64_t row = first + r * waves;
+      const bool ok = row < rows;
+      inv[r] = ok ? inverse_rms[row] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < V; ++i) g[j].v[i] = xv[j].v[i] = 0.0f;
-      }
+      for (int j = 0; j < CPL; ++j) {
+        const int64_t q = lane + 64 * j;
+        if (ok && q < chunks) {
+          g[r][j] = load_vec<V>(grad + row * width + q * V);
+          xv[r][j] = load_vec<V>(x + row * width + q * V);
+        } else {
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        u[j].v[i] = scale != nullptr ? g[j].v[i] * s[j].v[i] : g[j].v[i];
-        dot = dot + xv[j].v[i] * u[j].v[i];
+          for (int i = 0; i < V; ++i) g[r][j].v[i] = xv[r][j].v[i] = 0.0f;
+        }
       }
     }
-    dot = group_sum<64>(dot);
-    const float mean_dot = dot / static_cast<float>(width);
-    const float inv = inverse_rms[row];
-    const float inv3 = inv * inv * inv;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int64_t q = lane + 64 * j;
-      if (q >= chunks) continue;
-      fvec<V> out;
+    for (int r = 0; r < 2; ++r) {
+      const int64_t row = first + r * waves;
+      fvec<V> u[CPL];
+      float dot = 0.0f;
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        out.v[i] = inv * u[j].v[i] - xv[j].v[i] * inv3 * mean_dot;
-        if (partial != nullptr) column[j].v[i] = column[j].v[i] + g[j].v[i] * (xv[j].v[i] * inv);
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          u[j].v[i] = scale != nullptr ? g[r][j].v[i] * s[j].v[i] : g[r][j].v[i];
+          dot = dot + xv[r][j].v[i] * u[j].v[i];
+        }
+      dot = group_sum<64>(dot);
+      if (row >= rows) continue;
+      const float mean_dot = dot / static_cast<float>(width);
+      const float inv3 = inv[r] * inv[r] * inv[r];
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int64_t q = lane + 64 * j;
+        if (q >= chunks) continue;
+        fvec<V> out;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          out.v[i] = inv[r] * u[j].v[i] - xv[r][j].v[i] * inv3 * mean_dot;
+          if (partial != nullptr) column[j].v[i] = column[j].v[i] + g[r][j].v[i] * (xv[r][j].v[i] * inv[r]);
+        }
+        store_vec_stream<V>(grad_x + row * width + q * V, out);
       }
-      store_vec<V>(grad_x + row * width + q * V, out);
     }
   }
   if (partial != nullptr) {
+    // the four waves' column sums meet in LDS and are added in wave order;
+    // the workgroup writes one row of the [workgroups, W] partial matrix
+    extern __shared__ float columns[];  // [kWaves][CPL * 64 * V]
+    constexpr int kSpan = CPL * 64 * V;
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int64_t q = lane + 64 * j;
-      if (q < chunks) store_vec<V>(partial + wave_id * width + q * V, column[j]);
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < V; ++i) columns[wave * kSpan + (lane + 64 * j) * V + i] = column[j].v[i];
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < width; c += kBlock) {
+      float sum = columns[c];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) sum = sum + columns[w * kSpan + c];
+      partial[static_cast<int64_t>(blockIdx.x) * width + c] = sum;
     }
   }
+}
+
+// grad_scale[w] = sum over the workgroup partial rows, one wave per group of
+// V columns: lane l adds rows l, l + 64, ... in order, then a fixed butterfly.
+template <int V>
+__global__ __launch_bounds__(kBlock) void partial_columns_kernel(const float* __restrict__ partial, int64_t n,
+                                                                 int64_t width, float* __restrict__ grad_scale) {
+  const int64_t group = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (group * V >= width) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t column = group * V;
+  fvec<V> sum;
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum.v[i] = 0.0f;
+  for (int64_t r = lane; r < n; r += 64) {
+    const fvec<V> value = load_vec<V>(partial + r * width + column);
+#pragma unroll
+    for (int i = 0; i < V; ++i) sum.v[i] = sum.v[i] + value.v[i];
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum.v[i] = group_sum<64>(sum.v[i]);
+  if (lane == 0) store_vec<V>(grad_scale + column, sum);
 }
 
 // Streaming grad_x for wide rows: two passes over the row.
@@ -217,21 +265,6 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_scale_columns_kernel(
   grad_scale[col] = sum;
 }
 
-// out[b, w] = sum_{i < group, b*group + i < n} in[b*group + i, w]
-__global__ __launch_bounds__(kBlock) void reduce_rows_kernel(const float* __restrict__ in,
-                                                             int64_t n, int64_t width,
-                                                             int64_t group,
-                                                             float* __restrict__ out) {
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  const int64_t b = blockIdx.y;
-  if (col >= width) return;
-  const int64_t first = b * group;
-  const int64_t last = first + group < n ? first + group : n;
-  float sum = 0.0f;
-  for (int64_t r = first; r < last; ++r) sum = sum + in[r * width + col];
-  out[b * width + col] = sum;
-}
-
 int per_lane_for(int64_t chunks) {
   int cpl = 1;
   while (cpl < 16 && 64 * cpl < chunks) cpl <<= 1;
@@ -261,9 +294,9 @@ template <int V>
 int launch_backward(int cpl, unsigned int grid, const float* grad, const float* x,
                     const float* scale, const float* inverse_rms, float* grad_x, float* partial,
                     int64_t rows, int64_t width, hipStream_t stream) {
-#define DPA4K_RMS_BWD(C)                                                                      \
-  rmsnorm_backward_kernel<V, C><<<grid, kBlock, 0, stream>>>(grad, x, scale, inverse_rms,      \
-                                                             grad_x, partial, rows, width)
+#define DPA4K_RMS_BWD(C)                                                                              \
+  rmsnorm_backward_kernel<V, C><<<grid, kBlock, partial != nullptr ? kWaves * C * 64 * V * sizeof(float) : 0, \
+                                  stream>>>(grad, x, scale, inverse_rms, grad_x, partial, rows, width)
   switch (cpl) {
     case 1: DPA4K_RMS_BWD(1); break;
     case 2: DPA4K_RMS_BWD(2); break;
@@ -310,10 +343,7 @@ extern "C" int dpa4k_rmsnorm_forward(const float* x, const float* scale, float* 
 
 extern "C" size_t dpa4k_rmsnorm_backward_workspace_size(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return 0;
-  const int64_t waves = static_cast<int64_t>(partial_blocks(rows)) * kWaves;
-  const int64_t level = (waves + kLevel - 1) / kLevel;
-  return round_up_256(static_cast<size_t>(waves * width) * 4) +
-         round_up_256(static_cast<size_t>(level * width) * 4);
+  return round_up_256(static_cast<size_t>(partial_blocks(rows)) * static_cast<size_t>(width) * 4);
 }
 
 extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const float* scale,
@@ -364,20 +394,16 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
     return fail(DPA4K_EWORKSPACE, "RMSNorm backward: workspace of %zu bytes is smaller than %zu",
                 workspace_bytes, needed);
   const unsigned int grid = partial_blocks(rows);
-  const int64_t waves = static_cast<int64_t>(grid) * kWaves;
-  const int64_t level = (waves + kLevel - 1) / kLevel;
-  Carver carver{static_cast<char*>(workspace), workspace_bytes};
-  float* partial = carver.take<float>(static_cast<size_t>(waves * width));
-  float* partial2 = carver.take<float>(static_cast<size_t>(level * width));
+  float* partial = static_cast<float*>(workspace);
   int s = vec4 ? launch_backward<4>(cpl, grid, grad, x, scale, inverse_rms, grad_x, partial, rows,
                                     width, stream)
                : launch_backward<1>(cpl, grid, grad, x, scale, inverse_rms, grad_x, partial, rows,
                                     width, stream);
   if (s) return s;
-  reduce_rows_kernel<<<dim3(blocks_for(width, kBlock), static_cast<unsigned int>(level)), kBlock, 0,
-                       stream>>>(partial, waves, width, kLevel, partial2);
-  if (int t = launched("reduce_rows_kernel")) return t;
-  reduce_rows_kernel<<<dim3(blocks_for(width, kBlock), 1), kBlock, 0, stream>>>(
-      partial2, level, width, level, grad_scale);
-  return launched("reduce_rows_kernel");
+  const int64_t groups = vec4 ? width / 4 : width;
+  if (vec4 && aligned16(grad_scale))
+    partial_columns_kernel<4><<<blocks_for(groups, kWaves), kBlock, 0, stream>>>(partial, grid, width, grad_scale);
+  else
+    partial_columns_kernel<1><<<blocks_for(width, kWaves), kBlock, 0, stream>>>(partial, grid, width, grad_scale);
+  return launched("partial_columns_kernel");
 }
