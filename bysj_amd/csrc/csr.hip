@@ -1,136 +1,77 @@
-// CSR construction on the device: per-key counts, exclusive prefix sum,
-// stable grouping order and the GIE grouping step.
+// CSR construction on the device: offsets, stable grouping order and the GIE
+// grouping step.
 //
 // Restates python/kernels/segment.py:46-71 (segment_offsets = [0] ++
-// cumsum(bincount(keys)), group_by_source = stable argsort + offsets) as
-// device passes:
-//   1. fill      counts[N] = 0, flags = 0
-//   2. histogram counts[k] += 1 per key (64-bit integer atomics: integer
-//                addition commutes, so the counts are exact whatever the
-//                interleaving), range and sortedness flags
-//   3. scan      offsets[n + 1] = sum_{m <= n} counts[m], in three passes
-//                (tile totals, scan of the totals, tile scans)
-//   4. order     stable radix sort of the keys (sort.hip), only when needed.
-// The integer results are bit-exact.  Functions that report an index-range
-// error read the flags back and therefore synchronise the stream.
+// cumsum(bincount(keys)), group_by_source = stable argsort + offsets) without
+// a histogram:
+//   1. check     one streaming pass over the keys: range and sortedness
+//                flags (at most one integer OR per workgroup); the host
+//                reads them back, as the reference's dst.min()/dst.max()
+//                check does, and raises on out-of-range keys;
+//   2. sort      keys that are not already non-decreasing are sorted by a
+//                stable LSD radix sort (sort.hip), alone or with their
+//                positions (the grouping order);
+//   3. bounds    offsets from the sorted keys: position e writes
+//                offsets[k] = e for every k in (key[e-1], key[e]] (with
+//                key[-1] = -1 and key[E] = N), so every entry is written
+//                exactly once, by the first edge of its segment.
+// Sorted keys (DeepMD's usual layout) need only passes 1 and 3.  Integer
+// results are bit-exact; nothing depends on scheduling.
 #include "common.h"
 
 namespace dpa4k {
 
-// Stable argsort of int64 keys known to lie in [0, n_nodes) (sort.hip).
-size_t stable_order_workspace(int64_t n_edges, int64_t n_nodes);
-int stable_order(const int64_t* keys, int64_t n_edges, int64_t n_nodes, int64_t* order,
-                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Stable sort of keys in [0, n_nodes) (sort.hip).
+size_t sort_workspace(int64_t n_edges, int64_t n_nodes);
+int sort_keys(const int64_t* keys, int64_t n_edges, int64_t n_nodes, uint32_t* sorted_keys, int64_t* order,
+              void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 namespace {
 
-constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
-constexpr int64_t kScanTile = kScanThreads * kScanItems;
-
 enum : int32_t { kFlagOutOfRange = 1, kFlagUnsorted = 2, kFlagSlotRange = 4, kFlagSlotShared = 8 };
 
-__global__ __launch_bounds__(256) void fill_i64_kernel(int64_t* __restrict__ data, int64_t n,
-                                                       int32_t* __restrict__ flags) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-    data[i] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0 && flags != nullptr) *flags = 0;
+unsigned int grid_stride_blocks(int64_t items, int64_t cap = 8192) {
+  const int64_t wanted = (items + 255) / 256;
+  return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > cap ? cap : wanted));
 }
 
-__global__ __launch_bounds__(256) void histogram_kernel(const int64_t* __restrict__ keys,
-                                                        int64_t n_edges, int64_t n_nodes,
-                                                        int64_t* __restrict__ counts,
-                                                        int32_t* __restrict__ flags) {
+__global__ __launch_bounds__(64) void clear_flags_kernel(int32_t* __restrict__ flags) {
+  if (threadIdx.x == 0) *flags = 0;
+}
+
+__global__ __launch_bounds__(256) void check_keys_kernel(const int64_t* __restrict__ keys, int64_t n_edges,
+                                                         int64_t n_nodes, int32_t* __restrict__ flags) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   int32_t local = 0;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_edges;
-       i += stride) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_edges; i += stride) {
     const int64_t key = keys[i];
-    if (static_cast<uint64_t>(key) >= static_cast<uint64_t>(n_nodes)) {
-      local |= kFlagOutOfRange;
-    } else {
-      atomicAdd(reinterpret_cast<unsigned long long*>(counts + key), 1ull);
-    }
+    if (static_cast<uint64_t>(key) >= static_cast<uint64_t>(n_nodes)) local |= kFlagOutOfRange;
     if (i + 1 < n_edges && keys[i + 1] < key) local |= kFlagUnsorted;
   }
-  if (local != 0) atomicOr(flags, local);
+  // one OR per workgroup, skipped when another workgroup already set the bits
+  // (many workgroups hitting one word would serialise in the L2)
+  const int32_t found = (__syncthreads_or(local & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
+                        (__syncthreads_or(local & kFlagUnsorted) ? kFlagUnsorted : 0);
+  if (threadIdx.x == 0 && found != 0 && (__atomic_load_n(flags, __ATOMIC_RELAXED) & found) != found)
+    atomicOr(flags, found);
 }
 
-// Block-wide inclusive scan of one int64 per thread (Hillis-Steele in LDS).
-__device__ int64_t block_inclusive_scan(int64_t value, int64_t* lds) {
-  const int t = threadIdx.x;
-  lds[t] = value;
-  __syncthreads();
-  for (int offset = 1; offset < kScanThreads; offset <<= 1) {
-    const int64_t add = t >= offset ? lds[t - offset] : 0;
-    __syncthreads();
-    lds[t] += add;
-    __syncthreads();
-  }
-  const int64_t result = lds[t];
-  __syncthreads();
-  return result;
-}
-
-__global__ __launch_bounds__(kScanThreads) void tile_total_kernel(const int64_t* __restrict__ counts,
-                                                                  int64_t n, int64_t* __restrict__ totals) {
-  __shared__ int64_t lds[kScanThreads];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-  int64_t sum = 0;
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t index = base + static_cast<int64_t>(i) * kScanThreads + threadIdx.x;
-    if (index < n) sum += counts[index];
-  }
-  const int64_t inclusive = block_inclusive_scan(sum, lds);
-  if (threadIdx.x == kScanThreads - 1) totals[blockIdx.x] = inclusive;
-}
-
-// Exclusive scan of the tile totals in place, by one block; each thread owns
-// a contiguous run of ceil(n / 256) totals.
-__global__ __launch_bounds__(kScanThreads) void scan_totals_kernel(int64_t* __restrict__ totals,
-                                                                   int64_t n) {
-  __shared__ int64_t lds[kScanThreads];
-  const int64_t per_thread = (n + kScanThreads - 1) / kScanThreads;
-  const int64_t begin = static_cast<int64_t>(threadIdx.x) * per_thread;
-  const int64_t end = begin + per_thread < n ? begin + per_thread : n;
-  int64_t sum = 0;
-  for (int64_t i = begin; i < end; ++i) sum += totals[i];
-  const int64_t inclusive = block_inclusive_scan(sum, lds);
-  int64_t running = inclusive - sum;
-  for (int64_t i = begin; i < end; ++i) {
-    const int64_t value = totals[i];
-    totals[i] = running;
-    running += value;
+// offsets[k] = first position e with key[e] >= k, for k in [0, n_nodes], of
+// non-decreasing keys in [0, n_nodes).
+template <typename K>
+__global__ __launch_bounds__(256) void offsets_from_sorted_kernel(const K* __restrict__ keys, int64_t n_edges,
+                                                                  int64_t n_nodes, int64_t* __restrict__ offsets) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e <= n_edges; e += stride) {
+    const int64_t previous = e > 0 ? static_cast<int64_t>(keys[e - 1]) : -1;
+    const int64_t current = e < n_edges ? static_cast<int64_t>(keys[e]) : n_nodes;
+    for (int64_t k = previous + 1; k <= current && k <= n_nodes; ++k) offsets[k] = e;
   }
 }
 
-// offsets[i + 1] = prefix(tile) + inclusive scan of counts inside the tile.
-// Thread t owns the kScanItems consecutive counts [base + t*items, ...).
-__global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(const int64_t* __restrict__ counts,
-                                                                 int64_t n,
-                                                                 const int64_t* __restrict__ tile_prefix,
-                                                                 int64_t* __restrict__ offsets) {
-  __shared__ int64_t lds[kScanThreads];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
-                       static_cast<int64_t>(threadIdx.x) * kScanItems;
-  int64_t values[kScanItems];
-  int64_t sum = 0;
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t index = base + i;
-    values[i] = index < n ? counts[index] : 0;
-    sum += values[i];
-  }
-  const int64_t inclusive = block_inclusive_scan(sum, lds);
-  int64_t running = tile_prefix[blockIdx.x] + inclusive - sum;
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t index = base + i;
-    running += values[i];
-    if (index < n) offsets[index + 1] = running;
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0) offsets[0] = 0;
+__global__ __launch_bounds__(256) void iota_kernel(int64_t* __restrict__ order, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) order[i] = i;
 }
 
 // Range and sharing checks of the GIE radial slots (one small block).
@@ -147,64 +88,76 @@ __global__ __launch_bounds__(64) void slot_check_kernel(const int64_t* __restric
   if (local != 0) atomicOr(flags, local);
 }
 
-struct OffsetsScratch {
-  int64_t* counts;
-  int64_t* totals;
-  int32_t* flags;
+// Workspace: the flags word, the sorted 32-bit keys, the sort's scratch.
+struct Scratch {
+  int32_t* flags = nullptr;
+  uint32_t* sorted = nullptr;
+  void* sort = nullptr;
+  size_t sort_bytes = 0;
 };
 
-int64_t tiles_for(int64_t n_nodes) { return (n_nodes + kScanTile - 1) / kScanTile; }
-
-size_t offsets_scratch_bytes(int64_t n_nodes) {
-  return round_up_256(static_cast<size_t>(n_nodes) * 8) +
-         round_up_256(static_cast<size_t>(tiles_for(n_nodes)) * 8) + 256;
+size_t scratch_bytes(int64_t n_edges, int64_t n_nodes) {
+  const size_t edges = static_cast<size_t>(n_edges > 0 ? n_edges : 1);
+  const size_t sort = sort_workspace(n_edges, n_nodes);
+  return 256 + round_up_256(edges * sizeof(uint32_t)) + round_up_256(sort > 0 ? sort : 1);
 }
 
-bool carve_offsets(Carver& carver, int64_t n_nodes, OffsetsScratch& out) {
-  out.counts = carver.take<int64_t>(static_cast<size_t>(n_nodes));
-  out.totals = carver.take<int64_t>(static_cast<size_t>(tiles_for(n_nodes)));
+bool carve(void* workspace, size_t bytes, int64_t n_edges, int64_t n_nodes, Scratch& out) {
+  if (workspace == nullptr || bytes < scratch_bytes(n_edges, n_nodes)) return false;
+  Carver carver{static_cast<char*>(workspace), bytes};
   out.flags = carver.take<int32_t>(1);
-  return out.counts && out.totals && out.flags;
+  out.sorted = carver.take<uint32_t>(static_cast<size_t>(n_edges > 0 ? n_edges : 1));
+  out.sort_bytes = sort_workspace(n_edges, n_nodes);
+  out.sort = carver.take<char>(out.sort_bytes > 0 ? out.sort_bytes : 1);
+  return out.flags && out.sorted && out.sort;
 }
 
-unsigned int grid_stride_blocks(int64_t items) {
-  const int64_t wanted = (items + 255) / 256;
-  return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > 8192 ? 8192 : wanted));
-}
-
-// Enqueues fill + histogram + scan.  No synchronisation.
-int enqueue_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes, int64_t* offsets,
-                    const OffsetsScratch& scratch, hipStream_t stream) {
-  fill_i64_kernel<<<grid_stride_blocks(n_nodes), 256, 0, stream>>>(scratch.counts, n_nodes,
-                                                                    scratch.flags);
-  if (int s = launched("fill_i64_kernel")) return s;
+// Pass 1 (+ optional slot checks), then the flags are read back.  Synchronises.
+int check_keys(const int64_t* keys, int64_t n_edges, int64_t n_nodes, const int64_t* radial_slot, int64_t n_rows,
+               int64_t n_radial, const Scratch& scratch, int32_t& flags, hipStream_t stream) {
+  clear_flags_kernel<<<1, 64, 0, stream>>>(scratch.flags);
+  if (int s = launched("clear_flags_kernel")) return s;
   if (n_edges > 0) {
-    histogram_kernel<<<grid_stride_blocks(n_edges), 256, 0, stream>>>(keys, n_edges, n_nodes,
-                                                                      scratch.counts, scratch.flags);
-    if (int s = launched("histogram_kernel")) return s;
+    check_keys_kernel<<<grid_stride_blocks(n_edges, 2048), 256, 0, stream>>>(keys, n_edges, n_nodes,
+                                                                             scratch.flags);
+    if (int s = launched("check_keys_kernel")) return s;
   }
-  const int64_t tiles = tiles_for(n_nodes);
-  tile_total_kernel<<<static_cast<unsigned int>(tiles), kScanThreads, 0, stream>>>(
-      scratch.counts, n_nodes, scratch.totals);
-  if (int s = launched("tile_total_kernel")) return s;
-  scan_totals_kernel<<<1, kScanThreads, 0, stream>>>(scratch.totals, tiles);
-  if (int s = launched("scan_totals_kernel")) return s;
-  tile_scan_kernel<<<static_cast<unsigned int>(tiles), kScanThreads, 0, stream>>>(
-      scratch.counts, n_nodes, scratch.totals, offsets);
-  return launched("tile_scan_kernel");
-}
-
-int read_flags(const int32_t* flags, int32_t& host, hipStream_t stream) {
-  if (int s = hip_status(hipMemcpyAsync(&host, flags, sizeof(int32_t), hipMemcpyDeviceToHost, stream),
+  if (n_rows > 0) {
+    slot_check_kernel<<<1, 64, 0, stream>>>(radial_slot, n_rows, n_radial, scratch.flags);
+    if (int s = launched("slot_check_kernel")) return s;
+  }
+  int32_t host = 0;
+  if (int s = hip_status(hipMemcpyAsync(&host, scratch.flags, sizeof(int32_t), hipMemcpyDeviceToHost, stream),
                          "hipMemcpyAsync(flags)"))
     return s;
-  return hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  if (int s = hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize")) return s;
+  flags = host;
+  return DPA4K_OK;
+}
+
+// Passes 2 and 3 for checked keys: offsets always, the order when `order` is
+// given (the identity for sorted keys).
+int build(const int64_t* keys, int64_t n_edges, int64_t n_nodes, bool sorted, int64_t* offsets, int64_t* order,
+          const Scratch& scratch, hipStream_t stream) {
+  const unsigned int blocks = grid_stride_blocks(n_edges + 1);
+  if (sorted || n_edges == 0) {
+    if (order != nullptr && n_edges > 0) {
+      iota_kernel<<<grid_stride_blocks(n_edges), 256, 0, stream>>>(order, n_edges);
+      if (int s = launched("iota_kernel")) return s;
+    }
+    offsets_from_sorted_kernel<int64_t><<<blocks, 256, 0, stream>>>(keys, n_edges, n_nodes, offsets);
+    return launched("offsets_from_sorted_kernel");
+  }
+  if (int s = sort_keys(keys, n_edges, n_nodes, scratch.sorted, order, scratch.sort, scratch.sort_bytes, stream))
+    return s;
+  offsets_from_sorted_kernel<uint32_t><<<blocks, 256, 0, stream>>>(scratch.sorted, n_edges, n_nodes, offsets);
+  return launched("offsets_from_sorted_kernel");
 }
 
 int check_sizes(int64_t n_edges, int64_t n_nodes, const char* what) {
   if (n_edges < 0) return fail(DPA4K_EINVAL, "%s: negative edge count", what);
   if (n_nodes <= 0) return fail(DPA4K_EINVAL, "%s require a positive node count", what);
-  if (tiles_for(n_nodes) > kMaxGrid) return fail(DPA4K_EINVAL, "%s: node count too large", what);
+  if (n_nodes > (int64_t(1) << 32)) return fail(DPA4K_EINVAL, "%s supports at most 2^32 nodes", what);
   return DPA4K_OK;
 }
 
@@ -214,101 +167,73 @@ int check_sizes(int64_t n_edges, int64_t n_nodes, const char* what) {
 using namespace dpa4k;
 
 extern "C" size_t dpa4k_segment_offsets_workspace_size(int64_t n_edges, int64_t n_nodes) {
-  (void)n_edges;
-  return n_nodes > 0 ? offsets_scratch_bytes(n_nodes) : 0;
+  return n_nodes > 0 ? scratch_bytes(n_edges, n_nodes) : 0;
 }
 
-extern "C" int dpa4k_segment_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
-                                     int64_t* offsets, void* workspace, size_t workspace_bytes,
-                                     dpa4k_stream_t stream_handle) {
+extern "C" int dpa4k_segment_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes, int64_t* offsets,
+                                     void* workspace, size_t workspace_bytes, dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_sizes(n_edges, n_nodes, "segment offsets")) return s;
-  if (offsets == nullptr || (n_edges > 0 && keys == nullptr))
-    return fail(DPA4K_EINVAL, "segment offsets: null pointer");
-  Carver carver{static_cast<char*>(workspace), workspace_bytes};
-  OffsetsScratch scratch{};
-  if (workspace == nullptr || !carve_offsets(carver, n_nodes, scratch))
-    return fail(DPA4K_EWORKSPACE, "segment offsets: workspace of %zu bytes is smaller than %zu",
-                workspace_bytes, offsets_scratch_bytes(n_nodes));
+  if (offsets == nullptr || (n_edges > 0 && keys == nullptr)) return fail(DPA4K_EINVAL, "segment offsets: null pointer");
+  Scratch scratch;
+  if (!carve(workspace, workspace_bytes, n_edges, n_nodes, scratch))
+    return fail(DPA4K_EWORKSPACE, "segment offsets: workspace of %zu bytes is smaller than %zu", workspace_bytes,
+                scratch_bytes(n_edges, n_nodes));
   hipStream_t stream = as_stream(stream_handle);
-  if (int s = enqueue_offsets(keys, n_edges, n_nodes, offsets, scratch, stream)) return s;
   int32_t flags = 0;
-  if (int s = read_flags(scratch.flags, flags, stream)) return s;
-  if (flags & kFlagOutOfRange)
-    return fail(DPA4K_EINVAL, "destination values must be within the node range");
-  return DPA4K_OK;
+  if (int s = check_keys(keys, n_edges, n_nodes, nullptr, 0, 0, scratch, flags, stream)) return s;
+  if (flags & kFlagOutOfRange) return fail(DPA4K_EINVAL, "destination values must be within the node range");
+  return build(keys, n_edges, n_nodes, !(flags & kFlagUnsorted), offsets, nullptr, scratch, stream);
 }
 
 extern "C" size_t dpa4k_group_by_key_workspace_size(int64_t n_edges, int64_t n_nodes) {
-  if (n_nodes <= 0) return 0;
-  const size_t a = offsets_scratch_bytes(n_nodes);
-  const size_t b = stable_order_workspace(n_edges, n_nodes);
-  return a > b ? a : b;
+  return n_nodes > 0 ? scratch_bytes(n_edges, n_nodes) : 0;
 }
 
-extern "C" int dpa4k_group_by_key(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
-                                  int64_t* order, int64_t* offsets, void* workspace,
-                                  size_t workspace_bytes, dpa4k_stream_t stream_handle) {
+extern "C" int dpa4k_group_by_key(const int64_t* keys, int64_t n_edges, int64_t n_nodes, int64_t* order,
+                                  int64_t* offsets, void* workspace, size_t workspace_bytes,
+                                  dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_sizes(n_edges, n_nodes, "group_by_source")) return s;
   if (offsets == nullptr || (n_edges > 0 && (keys == nullptr || order == nullptr)))
     return fail(DPA4K_EINVAL, "group_by_source: null pointer");
-  const size_t needed = dpa4k_group_by_key_workspace_size(n_edges, n_nodes);
-  if (workspace == nullptr || workspace_bytes < needed)
-    return fail(DPA4K_EWORKSPACE, "group_by_source: workspace of %zu bytes is smaller than %zu",
-                workspace_bytes, needed);
+  Scratch scratch;
+  if (!carve(workspace, workspace_bytes, n_edges, n_nodes, scratch))
+    return fail(DPA4K_EWORKSPACE, "group_by_source: workspace of %zu bytes is smaller than %zu", workspace_bytes,
+                scratch_bytes(n_edges, n_nodes));
   hipStream_t stream = as_stream(stream_handle);
-  Carver carver{static_cast<char*>(workspace), workspace_bytes};
-  OffsetsScratch scratch{};
-  carve_offsets(carver, n_nodes, scratch);
-  if (int s = enqueue_offsets(keys, n_edges, n_nodes, offsets, scratch, stream)) return s;
   int32_t flags = 0;
-  if (int s = read_flags(scratch.flags, flags, stream)) return s;
-  if (flags & kFlagOutOfRange)
-    return fail(DPA4K_EINVAL, "source values must be within the node range");
-  if (n_edges == 0) return DPA4K_OK;
-  // The offsets scratch is dead once the flags are read: the sort reuses the
-  // whole workspace.
-  return stable_order(keys, n_edges, n_nodes, order, workspace, workspace_bytes, stream);
+  if (int s = check_keys(keys, n_edges, n_nodes, nullptr, 0, 0, scratch, flags, stream)) return s;
+  if (flags & kFlagOutOfRange) return fail(DPA4K_EINVAL, "source values must be within the node range");
+  return build(keys, n_edges, n_nodes, !(flags & kFlagUnsorted), offsets, order, scratch, stream);
 }
 
 extern "C" size_t dpa4k_gie_group_workspace_size(int64_t n_edges, int64_t n_nodes) {
   return dpa4k_group_by_key_workspace_size(n_edges, n_nodes);
 }
 
-extern "C" int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot, int64_t n_edges,
-                               int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t* offsets,
-                               int64_t* order, int32_t* host_info, void* workspace,
-                               size_t workspace_bytes, dpa4k_stream_t stream_handle) {
+extern "C" int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot, int64_t n_edges, int64_t n_nodes,
+                               int64_t n_rows, int64_t n_radial, int64_t* offsets, int64_t* order,
+                               int32_t* host_info, void* workspace, size_t workspace_bytes,
+                               dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_sizes(n_edges, n_nodes, "GIE grouping")) return s;
   if (n_rows < 0 || n_radial < 0) return fail(DPA4K_EINVAL, "GIE grouping: negative sizes");
-  if (offsets == nullptr || (n_edges > 0 && dst == nullptr) ||
-      (n_rows > 0 && radial_slot == nullptr))
+  if (offsets == nullptr || (n_edges > 0 && dst == nullptr) || (n_rows > 0 && radial_slot == nullptr))
     return fail(DPA4K_EINVAL, "GIE grouping: null pointer");
-  const size_t needed = dpa4k_gie_group_workspace_size(n_edges, n_nodes);
-  if (workspace == nullptr || workspace_bytes < needed)
-    return fail(DPA4K_EWORKSPACE, "GIE grouping: workspace of %zu bytes is smaller than %zu",
-                workspace_bytes, needed);
+  Scratch scratch;
+  if (!carve(workspace, workspace_bytes, n_edges, n_nodes, scratch))
+    return fail(DPA4K_EWORKSPACE, "GIE grouping: workspace of %zu bytes is smaller than %zu", workspace_bytes,
+                scratch_bytes(n_edges, n_nodes));
   hipStream_t stream = as_stream(stream_handle);
-  Carver carver{static_cast<char*>(workspace), workspace_bytes};
-  OffsetsScratch scratch{};
-  carve_offsets(carver, n_nodes, scratch);
-  if (int s = enqueue_offsets(dst, n_edges, n_nodes, offsets, scratch, stream)) return s;
-  if (n_rows > 0) {
-    slot_check_kernel<<<1, 64, 0, stream>>>(radial_slot, n_rows, n_radial, scratch.flags);
-    if (int s = launched("slot_check_kernel")) return s;
-  }
   int32_t flags = 0;
-  if (int s = read_flags(scratch.flags, flags, stream)) return s;
+  if (int s = check_keys(dst, n_edges, n_nodes, radial_slot, n_rows, n_radial, scratch, flags, stream)) return s;
   if (flags & kFlagOutOfRange) return fail(DPA4K_EINVAL, "GIE dst values must be within the node range");
-  if (flags & kFlagSlotRange)
-    return fail(DPA4K_EINVAL, "GIE radial_slot values must be within the radial range");
-  int32_t info = 0;
-  if (!(flags & kFlagUnsorted)) info |= 1;
-  if (!(flags & kFlagSlotShared)) info |= 2;
+  if (flags & kFlagSlotRange) return fail(DPA4K_EINVAL, "GIE radial_slot values must be within the radial range");
+  const bool sorted = !(flags & kFlagUnsorted);
+  const int32_t info = (sorted ? 1 : 0) | ((flags & kFlagSlotShared) ? 0 : 2);
   if (host_info != nullptr) *host_info = info;
-  if ((info & 1) || n_edges == 0) return DPA4K_OK;
-  if (order == nullptr) return fail(DPA4K_EINVAL, "GIE grouping: unsorted dst needs an order buffer");
-  return stable_order(dst, n_edges, n_nodes, order, workspace, workspace_bytes, stream);
+  if (!sorted && n_edges > 0 && order == nullptr)
+    return fail(DPA4K_EINVAL, "GIE grouping: unsorted dst needs an order buffer");
+  return build(dst, n_edges, n_nodes, sorted, offsets, sorted ? nullptr : order, scratch, stream);
 }
