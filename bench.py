@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2**20
 ROTATION_BYTES = 1 << 30  # distinct input bytes cycled through per op
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
 def parse_args():
@@ -94,10 +95,28 @@ def n_sets_for(bytes_per_set: int) -> int:
     return max(1, min(64, -(-ROTATION_BYTES // max(1, bytes_per_set))))
 
 
-def roofline(bytes_per_launch: int, ms_per_launch: float) -> dict:
+def measured_traffic(key: str | None, bytes_per_launch: int) -> int | None:
+    """HBM bytes per launch from the committed FETCH_SIZE + WRITE_SIZE summary, when it is for this workload.
+
+    profiles/traffic.json holds the calibrated counter totals of one rocprofv3 --pmc pass per
+    counter; an entry counts only when its algorithmic byte total equals this run's, so a changed
+    workload reports null instead of a stale figure.
+    """
+    if key is None:
+        return None
+    try:
+        entry = json.loads(TRAFFIC_FILE.read_text())[key]
+    except (OSError, ValueError, KeyError):
+        return None
+    if int(entry.get("algorithmic_bytes", -1)) != int(bytes_per_launch):
+        return None
+    return int(entry["bytes_per_launch"])
+
+
+def roofline(bytes_per_launch: int, ms_per_launch: float, traffic_key: str | None = None) -> dict:
     achieved = bytes_per_launch / (ms_per_launch * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(traffic_key, bytes_per_launch),
             "algorithmic_bytes": int(bytes_per_launch)}
 
 
@@ -418,7 +437,7 @@ def main() -> int:
                    "channels": head["channels"], "hub_fraction": 0.01, "hub_degree": 512, "null_logit": True,
                    "input_sets": head["sets"], "timing": "hip-graph replay" if graph else "eager",
                    "parallelism": "single-gpu"},
-        "roofline": roofline(head["bytes"], head["ms_per_step"]),
+        "roofline": roofline(head["bytes"], head["ms_per_step"], "segment_softmax_fwd_config2"),
     }
     print(f"[bench] headline done: {head['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
 

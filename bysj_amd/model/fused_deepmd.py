@@ -19,8 +19,8 @@ S2  ``SO2Convolution.forward_envelope(self, x, edge_cache, radial_feat)`` --
     coordinates, so forces need it).
 
 Both seams need the destination CSR view of ``dst``.  It is built once per
-neighbour graph on the device (``kernels.group_by_source``: histogram, scan
-and stable radix sort) and cached per ``dst`` tensor object; an entry is
+neighbour graph on the device (``kernels.group_by_source``: a check pass,
+a stable radix sort when the list is unsorted, a boundary pass) and cached per ``dst`` tensor object; an entry is
 dropped when the tensor is freed or written in place (its version counter
 moves), so a recycled storage address can never return a stale view.
 
