@@ -233,4 +233,88 @@ __device__ __forceinline__ void store_vec_stream(float* __restrict__ p, const fv
   }
 }
 
+// ---------------------------------------------------------------------------
+// Device: buffer views
+// ---------------------------------------------------------------------------
+//
+// A buffer view is a buffer resource over a byte range starting at a
+// wave-uniform address.  A load at an offset at or past the end of the range
+// returns zeros and a store there is dropped, both without a memory access.
+// A lane that has no row therefore issues the same instruction as its
+// neighbours with the offset kNoRow instead of branching around it.  This
+// matters for latency: arithmetic on a value loaded inside a branch is
+// placed in that branch by the compiler, which must then wait for the load
+// before the branch ends, and the loads of consecutive tiles stop
+// overlapping.  Offsets are 32-bit, and callers rebase views so that the
+// offsets they use stay below 2^31.
+constexpr uint32_t kNoRow = 0x80000000u;
+
+// Word 3 of a gfx9-family buffer resource: 32-bit data format, no swizzle.
+constexpr int kBufferFlags = 0x00020000;
+
+typedef __amdgpu_buffer_rsrc_t BufferView;
+
+__device__ __forceinline__ BufferView buffer_view(const void* base, int64_t bytes) {
+  const int64_t records = bytes < 0 ? 0 : (bytes > int64_t(kNoRow) ? int64_t(kNoRow) : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(static_cast<uint32_t>(records)), kBufferFlags);
+}
+
+// The rows [base, n_rows) of a row-major float array with `width` floats per
+// row; `base` must be wave-uniform.
+__device__ __forceinline__ BufferView row_view(const float* p, int64_t base, int64_t n_rows, int64_t width) {
+  return buffer_view(p + base * width, (n_rows - base) * width * 4);
+}
+
+// `value` of the lowest active lane, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int64_t uniform_i64(int64_t value) {
+  const uint64_t bits = static_cast<uint64_t>(value);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bits));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bits >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ float buffer_load_f32(BufferView view, uint32_t offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(view, static_cast<int>(offset), 0, 0));
+}
+
+template <int N>
+__device__ __forceinline__ fvec<N> buffer_load_vec(BufferView view, uint32_t offset) {
+  fvec<N> out;
+  if constexpr (N == 4) {
+    const f32x4 raw = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(offset),
+                                                                                        0, 0));
+    out.v[0] = raw.x;
+    out.v[1] = raw.y;
+    out.v[2] = raw.z;
+    out.v[3] = raw.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out.v[i] = buffer_load_f32(view, offset == kNoRow ? kNoRow : offset + 4u * i);
+  }
+  return out;
+}
+
+// Non-temporal (cache policy nt) store of N floats; dropped at kNoRow.
+template <int N>
+__device__ __forceinline__ void buffer_store_vec_stream(BufferView view, uint32_t offset, const fvec<N>& value) {
+  constexpr int kNonTemporal = 2;
+  if constexpr (N == 4) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 raw = {value.v[0], value.v[1], value.v[2], value.v[3]};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, raw), view, static_cast<int>(offset), 0,
+                                           kNonTemporal);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value.v[i]), view,
+                                            static_cast<int>(offset == kNoRow ? kNoRow : offset + 4u * i), 0,
+                                            kNonTemporal);
+  }
+}
+
+__device__ __forceinline__ void buffer_store_f32(BufferView view, uint32_t offset, float value) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), view, static_cast<int>(offset), 0, 0);
+}
+
 }  // namespace dpa4k

@@ -43,6 +43,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 // [1] n_long, [2, 2 + n_long) ascending ids of the long segments, then
 // scratch (one count per tile of segments).
 constexpr int64_t kPlanHeader = 2;
+// Short-path geometry: a short segment belongs to a group of at least
+// 2^kShortGroupLog lanes, and each lane stages up to kShortFloats values.
+constexpr int kShortGroupLog = 5;
+constexpr int kShortFloats = 24;
 
 // ---------------------------------------------------------------------------
 // arithmetic
@@ -137,28 +141,73 @@ __device__ __forceinline__ void span_merge(float& peak, float& sum) {
 template <int V, int LOG_LC>
 struct Geo {
   static constexpr int LC = 1 << LOG_LC;               // lanes per edge row
-  static constexpr int LOG_G = LOG_LC > 5 ? LOG_LC : 5;
+  static constexpr int LOG_G = LOG_LC > kShortGroupLog ? LOG_LC : kShortGroupLog;
   static constexpr int G = 1 << LOG_G;                 // lanes per short segment
   static constexpr int PG = G / LC;                    // rows per group load
   static constexpr int SPB = kBlock / G;               // segments per short workgroup
   static constexpr int PB = kBlock / LC;               // rows per workgroup load
-  static constexpr int RMAX = 24 / V;                  // register tiles, short path
+  static constexpr int RMAX = kShortFloats / V;        // register tiles, short path
   static constexpr int RMAXB = 16 / V;                 // register tiles, staged long path
   static constexpr int CAP = RMAX * PG;                // longest short segment
   static constexpr int UNROLL = 2;                     // loads in flight per thread, streaming path
 };
 
-// Edge of register tile i: the slot itself in natural order (recomputed, no
-// register), the stored order entry otherwise (-1 for none).
-template <bool kOrdered, int R>
-struct TileEdges {
+// Register tiles of rows: tile i holds, for this lane, the row of CSR slot
+// first + i * STEP + row_lane when that slot is below `end` and the lane is
+// live (its column lies inside the row).
+//
+// Natural order (slot = edge): rows are read and written through buffer
+// views rebased at `base`, the lowest first slot of the active lanes (wave-
+// uniform), and a lane without a row uses kNoRow; callers keep every slot of
+// the window within 2^31 bytes of `base`.  No load sits in a branch.
+// With an order: the order entries of every tile are loaded first (at slot 0
+// for lanes without a row), then the rows they name at a clamped index; `e`
+// keeps the edge id, or -1 where there is no row.  Callers guard the ordered
+// loads with n_edges > 0, so index 0 exists.  A lane that is not live reads
+// column 0 instead of its own (null rows included); its results are neither
+// stored nor reduced into the live lanes' results.
+template <int R, int STEP, bool kOrdered>
+struct Tiles {
+  int64_t first, base;
+  int32_t rows_left;  // min(end - first, 2^31 - 1)
+  int row_lane;
+  bool live;
+  uint32_t row_bytes, col_bytes;
   int64_t e[kOrdered ? R : 1];
-  __device__ __forceinline__ void set(int i, int64_t edge) {
-    if constexpr (kOrdered) e[i] = edge;
+
+  __device__ __forceinline__ Tiles(int64_t first_, int64_t end, int row_lane_, bool live_, int64_t column,
+                                   int64_t channels)
+      : first(first_), row_lane(row_lane_), live(live_) {
+    base = kOrdered ? 0 : uniform_i64(first_);
+    const int64_t left = end - first_;
+    rows_left = static_cast<int32_t>(left < 0 ? 0 : (left > 0x7fffffff ? 0x7fffffff : left));
+    row_bytes = static_cast<uint32_t>(channels) * 4u;
+    col_bytes = static_cast<uint32_t>(column) * 4u;
   }
-  __device__ __forceinline__ int64_t get(int i, int64_t slot, int64_t end) const {
-    if constexpr (kOrdered) return e[i];
-    return slot < end ? slot : -1;
+  __device__ __forceinline__ bool row(int i) const { return live & (i * STEP + row_lane < rows_left); }
+  // kNoRow without a row, 0 with one; folded into offsets by an OR, which keeps
+  // the offset arithmetic free of selects (a select here becomes a branch).
+  __device__ __forceinline__ uint32_t miss(int i) const { return (static_cast<uint32_t>(row(i)) - 1u) & kNoRow; }
+  __device__ __forceinline__ int64_t slot(int i) const { return first + static_cast<int64_t>(i) * STEP + row_lane; }
+  // natural order: byte offsets of this lane's chunk and of its row's scalar
+  __device__ __forceinline__ uint32_t rel(int i) const {
+    return static_cast<uint32_t>(first - base) + static_cast<uint32_t>(i * STEP + row_lane);
+  }
+  __device__ __forceinline__ uint32_t at(int i) const { return (rel(i) * row_bytes + col_bytes) | miss(i); }
+  __device__ __forceinline__ uint32_t scalar_at(int i) const { return (rel(i) * 4u) | miss(i); }
+  // ordered: edge ids of every tile
+  __device__ __forceinline__ void gather_ids(const int64_t* __restrict__ order, int64_t n_edges) {
+    if constexpr (kOrdered) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) e[i] = order[row(i) ? slot(i) : 0];
+#pragma unroll
+      for (int i = 0; i < R; ++i) e[i] = row(i) && e[i] >= 0 && e[i] < n_edges ? e[i] : -1;
+    }
+  }
+  __device__ __forceinline__ void clear_ids() {
+    if constexpr (kOrdered)
+#pragma unroll
+      for (int i = 0; i < R; ++i) e[i] = -1;
   }
 };
 
@@ -215,6 +264,86 @@ struct ForwardArgs {
   int64_t n_edges, n_nodes, channels;
 };
 
+// Loads tile i of the forward input for this lane: the logit chunk and the
+// envelope (0, hence no mass, where the lane has no row).  Natural order
+// reads through the views; with an order the caller has gathered the ids.
+template <int V, int R, int STEP, bool kOrdered>
+__device__ __forceinline__ void forward_loads(const ForwardArgs& a, const Tiles<R, STEP, kOrdered>& t,
+                                              int64_t column, float (&value)[R][V], float (&envelope)[R]) {
+  if constexpr (!kOrdered) {
+    const BufferView logit = row_view(a.logit, t.base, a.n_edges, a.channels);
+    const BufferView env = row_view(a.env, t.base, a.n_edges, 1);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const fvec<V> x = buffer_load_vec<V>(logit, t.at(i));
+      envelope[i] = buffer_load_f32(env, t.scalar_at(i));
+#pragma unroll
+      for (int v = 0; v < V; ++v) value[i][v] = x.v[v];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any use
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t e = t.e[i] >= 0 ? t.e[i] : 0;
+      const fvec<V> x = load_vec<V>(a.logit + e * a.channels + column);
+      const float env = a.env[e];
+      envelope[i] = t.e[i] >= 0 ? env : 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) value[i][v] = x.v[v];
+    }
+  }
+}
+
+// Stores alpha of tile i where the lane has a row.
+template <int V, int R, int STEP, bool kOrdered>
+__device__ __forceinline__ void forward_stores(const ForwardArgs& a, const Tiles<R, STEP, kOrdered>& t,
+                                               int64_t column, const float (&alpha)[R][V]) {
+  if constexpr (!kOrdered) {
+    const BufferView out = row_view(a.alpha, t.base, a.n_edges, a.channels);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      fvec<V> row;
+#pragma unroll
+      for (int v = 0; v < V; ++v) row.v[v] = alpha[i][v];
+      buffer_store_vec_stream<V>(out, t.at(i), row);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (t.e[i] >= 0) {
+        fvec<V> row;
+#pragma unroll
+        for (int v = 0; v < V; ++v) row.v[v] = alpha[i][v];
+        store_vec_stream<V>(a.alpha + t.e[i] * a.channels + column, row);
+      }
+    }
+  }
+}
+
+// Tiles of [first, end) with every load issued before any arithmetic.
+template <int V, int R, int STEP, bool kOrdered>
+__device__ __forceinline__ Tiles<R, STEP, kOrdered> forward_tiles(const ForwardArgs& a, int64_t first, int64_t end,
+                                                                  int row_lane, bool live, int64_t column,
+                                                                  float (&value)[R][V], float (&envelope)[R]) {
+  Tiles<R, STEP, kOrdered> t(first, end, row_lane, live, column, a.channels);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    envelope[i] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) value[i][v] = 0.0f;
+  }
+  if constexpr (kOrdered) {
+    t.clear_ids();
+    if (a.n_edges > 0) {
+      t.gather_ids(a.order, a.n_edges);
+      forward_loads<V>(a, t, column, value, envelope);
+    }
+  } else {
+    forward_loads<V>(a, t, column, value, envelope);
+  }
+  return t;
+}
+
 // One long segment [begin, end) of `segment`, processed by the whole workgroup.
 template <int V, int LOG_LC, bool kNull, bool kOrdered>
 __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end,
@@ -222,44 +351,31 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   using S = Geo<V, LOG_LC>;
   constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
   const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t column = L.live ? L.column : 0;
   const int64_t degree = end - begin;
+  fvec<V> n0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) n0.v[v] = -INFINITY;
+  if constexpr (kNull) n0 = load_vec<V>(a.null_logit + segment * a.channels + column);
   float nv[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) nv[v] = -INFINITY;
-  if (kNull && L.live) {
-    const fvec<V> n0 = load_vec<V>(a.null_logit + segment * a.channels + L.column);
-#pragma unroll
-    for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
-  }
+  for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
   float peak[V], total[V];
   if (degree <= RMAXB * PB) {
     // staged: every row of the segment in registers, one read
-    float value[RMAXB][V];
-    TileEdges<kOrdered, RMAXB> edge;
+    float value[RMAXB][V], envelope[RMAXB];
+    const auto t = forward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, L.pb, L.live, column, value, envelope);
 #pragma unroll
-    for (int i = 0; i < RMAXB; ++i) {
-      edge.set(i, -1);
+    for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
 #pragma unroll
-      for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
-      const int64_t slot = begin + static_cast<int64_t>(i) * PB + L.pb;
-      if (slot < end && L.live) {
-        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-        if (e >= 0) {
-          edge.set(i, e);
-          const float envelope = a.env[e];
-          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
+    for (int i = 0; i < RMAXB; ++i)
 #pragma unroll
-          for (int v = 0; v < V; ++v) value[i][v] = log2_weight(x.v[v], envelope);
-        }
+      for (int v = 0; v < V; ++v) {
+        value[i][v] = log2_weight(value[i][v], envelope[i]);
+        peak[v] = fmaxf(peak[v], value[i][v]);
       }
-    }
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      peak[v] = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < RMAXB; ++i) peak[v] = fmaxf(peak[v], value[i][v]);
-      peak[v] = span_max<LC, 64>(peak[v]);
-    }
+    for (int v = 0; v < V; ++v) peak[v] = span_max<LC, 64>(peak[v]);
     if ((L.lane >> LOG_LC) == 0)
 #pragma unroll
       for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = peak[v];
@@ -294,15 +410,10 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
       total[v] = inverse_total(sum + nw[v]);
     }
 #pragma unroll
-    for (int i = 0; i < RMAXB; ++i) {
-      const int64_t e = edge.get(i, begin + static_cast<int64_t>(i) * PB + L.pb, end);
-      if (e >= 0 && L.live) {
-        fvec<V> out;
+    for (int i = 0; i < RMAXB; ++i)
 #pragma unroll
-        for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
-        store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
-      }
-    }
+      for (int v = 0; v < V; ++v) value[i][v] *= total[v];
+    forward_stores<V>(a, t, column, value);
     if (kNull && threadIdx.x < LC && L.live) {
       fvec<V> out;
 #pragma unroll
@@ -321,26 +432,12 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
     run_sum[v] = 0.0f;
   }
   for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
-    float value[S::UNROLL][V];
-#pragma unroll
-    for (int u = 0; u < S::UNROLL; ++u) {
-#pragma unroll
-      for (int v = 0; v < V; ++v) value[u][v] = -INFINITY;
-      const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
-      if (slot < end && L.live) {
-        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-        if (e >= 0) {
-          const float envelope = a.env[e];
-          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
-#pragma unroll
-          for (int v = 0; v < V; ++v) value[u][v] = log2_weight(x.v[v], envelope);
-        }
-      }
-    }
+    float value[S::UNROLL][V], envelope[S::UNROLL];
+    forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, value, envelope);
 #pragma unroll
     for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
-      for (int v = 0; v < V; ++v) online_add(peak[v], run_sum[v], value[u][v]);
+      for (int v = 0; v < V; ++v) online_add(peak[v], run_sum[v], log2_weight(value[u][v], envelope[u]));
   }
 #pragma unroll
   for (int v = 0; v < V; ++v) span_merge<LC, 64>(peak[v], run_sum[v]);
@@ -363,21 +460,13 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
     total[v] = inverse_total(s);
   }
   for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
+    float value[S::UNROLL][V], envelope[S::UNROLL];
+    const auto t = forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, value, envelope);
 #pragma unroll
-    for (int u = 0; u < S::UNROLL; ++u) {
-      const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
-      if (slot < end && L.live) {
-        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-        if (e >= 0) {
-          const float envelope = a.env[e];
-          const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
-          fvec<V> out;
+    for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
-          for (int v = 0; v < V; ++v) out.v[v] = weight_of(log2_weight(x.v[v], envelope), peak[v]) * total[v];
-          store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
-        }
-      }
-    }
+      for (int v = 0; v < V; ++v) value[u][v] = weight_of(log2_weight(value[u][v], envelope[u]), peak[v]) * total[v];
+    forward_stores<V>(a, t, column, value);
   }
   if (kNull && threadIdx.x < LC && L.live) {
     fvec<V> out;
@@ -388,45 +477,36 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   __syncthreads();
 }
 
-// Short segment of this lane's group (degree <= CAP), all in registers.
+// Short segment of this lane's group (degree <= CAP), all in registers.  The
+// rows of a wave's (at most two) short groups lie within 2 CAP slots of the
+// first one's begin, which keeps the buffer offsets small.
 template <int V, int LOG_LC, bool kNull, bool kOrdered>
 __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
   using S = Geo<V, LOG_LC>;
   constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
+  static_assert(G >= 32, "the row window of a wave assumes at most two short groups per wave");
   const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t column = L.live ? L.column : 0;
   const int64_t degree = end - begin;
-  float nv[V];
+  fvec<V> n0;
 #pragma unroll
-  for (int v = 0; v < V; ++v) nv[v] = -INFINITY;
-  if (kNull && L.live) {
-    const fvec<V> n0 = load_vec<V>(a.null_logit + segment * a.channels + L.column);
+  for (int v = 0; v < V; ++v) n0.v[v] = -INFINITY;
+  if constexpr (kNull) n0 = load_vec<V>(a.null_logit + segment * a.channels + column);
+  float value[RMAX][V], envelope[RMAX];
+  const auto t = forward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, L.p, L.live, column, value, envelope);
+  float nv[V], peak[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) nv[v] = n0.v[v] * kLog2e;
+  for (int v = 0; v < V; ++v) {
+    nv[v] = n0.v[v] * kLog2e;
+    peak[v] = -INFINITY;
   }
-  float value[RMAX][V];
-  TileEdges<kOrdered, RMAX> edge;
-  float peak[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
+  for (int i = 0; i < RMAX; ++i)
 #pragma unroll
-  for (int i = 0; i < RMAX; ++i) {
-    edge.set(i, -1);
-#pragma unroll
-    for (int v = 0; v < V; ++v) value[i][v] = -INFINITY;
-    const int64_t slot = begin + static_cast<int64_t>(i) * PG + L.p;
-    if (slot < end && L.live) {
-      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-      if (e >= 0) {
-        edge.set(i, e);
-        const float envelope = a.env[e];
-        const fvec<V> x = load_vec<V>(a.logit + e * a.channels + L.column);
-#pragma unroll
-        for (int v = 0; v < V; ++v) value[i][v] = log2_weight(x.v[v], envelope);
-      }
+    for (int v = 0; v < V; ++v) {
+      value[i][v] = log2_weight(value[i][v], envelope[i]);
+      peak[v] = fmaxf(peak[v], value[i][v]);
     }
-#pragma unroll
-    for (int v = 0; v < V; ++v) peak[v] = fmaxf(peak[v], value[i][v]);
-  }
   float total[V], nw[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -452,15 +532,10 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
     total[v] = inverse_total(total[v] + nw[v]);
   }
 #pragma unroll
-  for (int i = 0; i < RMAX; ++i) {
-    const int64_t e = edge.get(i, begin + static_cast<int64_t>(i) * PG + L.p, end);
-    if (e >= 0 && L.live) {
-      fvec<V> out;
+  for (int i = 0; i < RMAX; ++i)
 #pragma unroll
-      for (int v = 0; v < V; ++v) out.v[v] = value[i][v] * total[v];
-      store_vec_stream<V>(a.alpha + e * a.channels + L.column, out);
-    }
-  }
+    for (int v = 0; v < V; ++v) value[i][v] *= total[v];
+  forward_stores<V>(a, t, column, value);
   if (kNull && L.p == 0 && L.live) {
     fvec<V> out;
 #pragma unroll
@@ -525,23 +600,92 @@ struct BackwardArgs {
   int64_t n_edges, n_nodes, channels;
 };
 
-// grad_logit row of edge e from alpha, grad_alpha and the segment's S;
-// grad_env[e] from the row sum over the LC lanes of the row.
-template <int V, int LOG_LC>
-__device__ __forceinline__ void backward_row(const BackwardArgs& a, const Lanes<V, LOG_LC>& L, int64_t e,
-                                             const float (&x)[V], const float (&g)[V], const float (&expect)[V],
-                                             float envelope) {
-  fvec<V> out;
-  float row = 0.0f;
+// Tiles of [first, end) for the backward: alpha, grad_alpha and the envelope
+// of every row (zeros without a row), every load issued before any arithmetic.
+template <int V, int R, int STEP, bool kOrdered>
+__device__ __forceinline__ Tiles<R, STEP, kOrdered> backward_tiles(const BackwardArgs& a, int64_t first, int64_t end,
+                                                                   int row_lane, bool live, int64_t column,
+                                                                   float (&x)[R][V], float (&g)[R][V],
+                                                                   float (&envelope)[R]) {
+  Tiles<R, STEP, kOrdered> t(first, end, row_lane, live, column, a.channels);
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    out.v[v] = x[v] * (g[v] - expect[v]);
-    row += out.v[v];
+  for (int i = 0; i < R; ++i) {
+    envelope[i] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) x[i][v] = g[i][v] = 0.0f;
   }
-  row = span_sum<1, Geo<V, LOG_LC>::LC>(e >= 0 && L.live ? row : 0.0f);
-  if (e >= 0) {
-    if (L.live) store_vec_stream<V>(a.grad_logit + e * a.channels + L.column, out);
-    if (L.k == 0) a.grad_env[e] = env_gradient(row, envelope);
+  if constexpr (!kOrdered) {
+    const BufferView alpha = row_view(a.alpha, t.base, a.n_edges, a.channels);
+    const BufferView grad = row_view(a.grad_alpha, t.base, a.n_edges, a.channels);
+    const BufferView env = row_view(a.env, t.base, a.n_edges, 1);
+    // envelopes first: they are consumed last, after the row sums
+#pragma unroll
+    for (int i = 0; i < R; ++i) envelope[i] = buffer_load_f32(env, t.scalar_at(i));
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const fvec<V> xv = buffer_load_vec<V>(alpha, t.at(i));
+      const fvec<V> gv = buffer_load_vec<V>(grad, t.at(i));
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        x[i][v] = xv.v[v];
+        g[i][v] = gv.v[v];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any use
+  } else {
+    t.clear_ids();
+    if (a.n_edges > 0) {
+      t.gather_ids(a.order, a.n_edges);
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int64_t e = t.e[i] >= 0 ? t.e[i] : 0;
+        const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + column);
+        const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + column);
+        const float env = a.env[e];
+        const bool has = t.e[i] >= 0;
+        envelope[i] = has ? env : 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          x[i][v] = has ? xv.v[v] : 0.0f;
+          g[i][v] = has ? gv.v[v] : 0.0f;
+        }
+      }
+    }
+  }
+  return t;
+}
+
+// grad_logit rows of the tiles from alpha, grad_alpha and the segment's S;
+// grad_env of each row from the row sum over the LC lanes of the row.
+template <int V, int LOG_LC, int R, int STEP, bool kOrdered>
+__device__ __forceinline__ void backward_rows(const BackwardArgs& a, const Lanes<V, LOG_LC>& L,
+                                              const Tiles<R, STEP, kOrdered>& t, int64_t column,
+                                              const float (&x)[R][V], const float (&g)[R][V],
+                                              const float (&expect)[V], const float (&envelope)[R]) {
+  // natural order only (unused, and dropped by the compiler, with an order)
+  const BufferView grad_logit = row_view(a.grad_logit, t.base, a.n_edges, a.channels);
+  const BufferView grad_env = row_view(a.grad_env, t.base, a.n_edges, 1);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const bool has = kOrdered ? t.e[i] >= 0 : t.row(i);
+    fvec<V> out;
+    float row = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      out.v[v] = x[i][v] * (g[i][v] - expect[v]);
+      row += out.v[v];
+    }
+    row = span_sum<1, Geo<V, LOG_LC>::LC>(has ? row : 0.0f);
+    const float d_env = env_gradient(row, envelope[i]);
+    if constexpr (!kOrdered) {
+      buffer_store_vec_stream<V>(grad_logit, t.at(i), out);
+      buffer_store_f32(grad_env, L.k == 0 ? t.scalar_at(i) : kNoRow, d_env);
+    } else {
+      if (has) {
+        store_vec_stream<V>(a.grad_logit + t.e[i] * a.channels + column, out);
+        if (L.k == 0) a.grad_env[t.e[i]] = d_env;
+      }
+    }
   }
 }
 
@@ -551,119 +695,67 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
   using S = Geo<V, LOG_LC>;
   constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
   const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t column = L.live ? L.column : 0;
   const int64_t degree = end - begin;
   float a0[V], g0[V], expect[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) a0[v] = g0[v] = expect[v] = 0.0f;
-  if (kNull && L.live) {
-    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + L.column);
-    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + L.column);
+  if constexpr (kNull) {
+    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + column);
+    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + column);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       a0[v] = x.v[v];
       g0[v] = g.v[v];
     }
   }
-  const bool staged = degree <= RMAXB * PB;
-  float xs[RMAXB][V], gs[RMAXB][V], envs[RMAXB];
-  TileEdges<kOrdered, RMAXB> edge;
-  if (staged) {
+  if (degree <= RMAXB * PB) {
+    // staged: every row of the segment in registers, one read
+    float xs[RMAXB][V], gs[RMAXB][V], envs[RMAXB];
+    const auto t = backward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, L.pb, L.live, column, xs, gs, envs);
 #pragma unroll
-    for (int i = 0; i < RMAXB; ++i) {
-      edge.set(i, -1);
-      envs[i] = 0.0f;
-#pragma unroll
-      for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
-      const int64_t slot = begin + static_cast<int64_t>(i) * PB + L.pb;
-      if (slot < end) {
-        const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-        if (e >= 0) {
-          edge.set(i, e);
-          envs[i] = a.env[e];
-          if (L.live) {
-            const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
-            const fvec<V> g = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
-#pragma unroll
-            for (int v = 0; v < V; ++v) {
-              xs[i][v] = x.v[v];
-              gs[i][v] = g.v[v];
-            }
-          }
-        }
-      }
+    for (int i = 0; i < RMAXB; ++i)
 #pragma unroll
       for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
+#pragma unroll
+    for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v]);
+    if ((L.lane >> LOG_LC) == 0)
+#pragma unroll
+      for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = expect[v];
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float sum = partial[0][0][L.k * V + v];
+      for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][0][L.k * V + v];
+      expect[v] = kNull ? sum + a0[v] * g0[v] : sum;
     }
+    backward_rows<V, LOG_LC>(a, L, t, column, xs, gs, expect, envs);
   } else {
+    // streaming: the dot-product pass, then the gradient pass
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
-      float x[S::UNROLL][V], g[S::UNROLL][V];
-#pragma unroll
-      for (int u = 0; u < S::UNROLL; ++u) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) x[u][v] = g[u][v] = 0.0f;
-        const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
-        if (slot < end && L.live) {
-          const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-          if (e >= 0) {
-            const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + L.column);
-            const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
-#pragma unroll
-            for (int v = 0; v < V; ++v) {
-              x[u][v] = xv.v[v];
-              g[u][v] = gv.v[v];
-            }
-          }
-        }
-      }
+      float x[S::UNROLL][V], g[S::UNROLL][V], envs[S::UNROLL];
+      backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, x, g, envs);
 #pragma unroll
       for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
         for (int v = 0; v < V; ++v) expect[v] = expect[v] + x[u][v] * g[u][v];
     }
-  }
 #pragma unroll
-  for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v]);
-  if ((L.lane >> LOG_LC) == 0)
+    for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v]);
+    if ((L.lane >> LOG_LC) == 0)
 #pragma unroll
-    for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = expect[v];
-  __syncthreads();
+      for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = expect[v];
+    __syncthreads();
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    float sum = partial[0][0][L.k * V + v];
-    for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][0][L.k * V + v];
-    expect[v] = kNull ? sum + a0[v] * g0[v] : sum;
-  }
-  if (staged) {
-#pragma unroll
-    for (int i = 0; i < RMAXB; ++i)
-      backward_row<V, LOG_LC>(a, L, edge.get(i, begin + static_cast<int64_t>(i) * PB + L.pb, end), xs[i], gs[i],
-                              expect, envs[i]);
-  } else {
+    for (int v = 0; v < V; ++v) {
+      float sum = partial[0][0][L.k * V + v];
+      for (int q = 1; q < kWaves; ++q) sum = sum + partial[q][0][L.k * V + v];
+      expect[v] = kNull ? sum + a0[v] * g0[v] : sum;
+    }
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
-#pragma unroll
-      for (int u = 0; u < S::UNROLL; ++u) {
-        const int64_t slot = base + static_cast<int64_t>(u) * PB + L.pb;
-        int64_t e = -1;
-        float x[V], g[V], envelope = 0.0f;
-#pragma unroll
-        for (int v = 0; v < V; ++v) x[v] = g[v] = 0.0f;
-        if (slot < end) {
-          e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-          if (e >= 0) {
-            envelope = a.env[e];
-            if (L.live) {
-              const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + L.column);
-              const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                x[v] = xv.v[v];
-                g[v] = gv.v[v];
-              }
-            }
-          }
-        }
-        backward_row<V, LOG_LC>(a, L, e, x, g, expect, envelope);
-      }
+      float x[S::UNROLL][V], g[S::UNROLL][V], envs[S::UNROLL];
+      const auto t = backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, x, g, envs);
+      backward_rows<V, LOG_LC>(a, L, t, column, x, g, expect, envs);
     }
   }
   if (kNull && threadIdx.x < LC && L.live) {
@@ -679,13 +771,15 @@ template <int V, int LOG_LC, bool kNull, bool kOrdered>
 __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
   using S = Geo<V, LOG_LC>;
   constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
+  static_assert(G >= 32, "the row window of a wave assumes at most two short groups per wave");
   const Lanes<V, LOG_LC> L(a.channels / V);
+  const int64_t column = L.live ? L.column : 0;
   float a0[V], g0[V], expect[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) a0[v] = g0[v] = expect[v] = 0.0f;
-  if (kNull && L.live) {
-    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + L.column);
-    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + L.column);
+  if constexpr (kNull) {
+    const fvec<V> x = load_vec<V>(a.null_alpha + segment * a.channels + column);
+    const fvec<V> g = load_vec<V>(a.grad_null_alpha + segment * a.channels + column);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       a0[v] = x.v[v];
@@ -693,42 +787,17 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
     }
   }
   float xs[RMAX][V], gs[RMAX][V], envs[RMAX];
-  TileEdges<kOrdered, RMAX> edge;
+  const auto t = backward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, L.p, L.live, column, xs, gs, envs);
 #pragma unroll
-  for (int i = 0; i < RMAX; ++i) {
-    edge.set(i, -1);
-    envs[i] = 0.0f;
-#pragma unroll
-    for (int v = 0; v < V; ++v) xs[i][v] = gs[i][v] = 0.0f;
-    const int64_t slot = begin + static_cast<int64_t>(i) * PG + L.p;
-    if (slot < end) {
-      const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-      if (e >= 0) {
-        edge.set(i, e);
-        envs[i] = a.env[e];
-        if (L.live) {
-          const fvec<V> x = load_vec<V>(a.alpha + e * a.channels + L.column);
-          const fvec<V> g = load_vec<V>(a.grad_alpha + e * a.channels + L.column);
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            xs[i][v] = x.v[v];
-            gs[i][v] = g.v[v];
-          }
-        }
-      }
-    }
+  for (int i = 0; i < RMAX; ++i)
 #pragma unroll
     for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
-  }
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     expect[v] = span_sum<LC, G>(expect[v]);
     if (kNull) expect[v] = expect[v] + a0[v] * g0[v];
   }
-#pragma unroll
-  for (int i = 0; i < RMAX; ++i)
-    backward_row<V, LOG_LC>(a, L, edge.get(i, begin + static_cast<int64_t>(i) * PG + L.p, end), xs[i], gs[i], expect,
-                            envs[i]);
+  backward_rows<V, LOG_LC>(a, L, t, column, xs, gs, expect, envs);
   if (kNull && L.p == 0 && L.live) {
     fvec<V> out;
 #pragma unroll
@@ -951,13 +1020,13 @@ int64_t capacity_for(int64_t channels, bool vec4) {
   if (chunks > 64) return 0;
   const int log_lc = lanes_log_for(chunks);
   const int64_t lc = int64_t(1) << log_lc;
-  const int64_t g = lc > 32 ? lc : 32;
-  const int64_t rmax = vec4 ? 24 / 4 : 24;
+  const int64_t g = lc > (int64_t(1) << kShortGroupLog) ? lc : (int64_t(1) << kShortGroupLog);
+  const int64_t rmax = vec4 ? kShortFloats / 4 : kShortFloats;
   return rmax * (g / lc);
 }
 
 unsigned int short_blocks(int64_t n_nodes, int log_lc) {
-  const int64_t g = log_lc > 5 ? (int64_t(1) << log_lc) : 32;
+  const int64_t g = int64_t(1) << (log_lc > kShortGroupLog ? log_lc : kShortGroupLog);
   return blocks_for(n_nodes, kBlock / g);
 }
 
