@@ -64,6 +64,21 @@ __device__ __forceinline__ float weight_of(float y, float peak) {
   return peak > -INFINITY ? exp2_of(y - peak) : 0.0f;
 }
 
+// The per-row part of y: 2 log2(max(env, 1e-30)) for env > 0, -inf otherwise.
+__device__ __forceinline__ float row_term(float env) {
+  return env > 0.0f ? 2.0f * __builtin_amdgcn_logf(fmaxf(env, 1e-30f)) : -INFINITY;
+}
+
+// y of one value from its row's term: -inf for a row without mass, whatever
+// the logit.
+__device__ __forceinline__ float log2_weight_of_row(float logit, float term) {
+  return term > -INFINITY ? __builtin_fmaf(logit, kLog2e, term) : -INFINITY;
+}
+
+// The exponent shift of a column: its peak, or 0 when it has no mass (every
+// y is then -inf and 2^(y - 0) = 0).
+__device__ __forceinline__ float shift_of(float peak) { return peak > -INFINITY ? peak : 0.0f; }
+
 // 1 / D, with D = 1 for a segment without mass.
 __device__ __forceinline__ float inverse_total(float total) {
   return __builtin_amdgcn_rcpf(total > 0.0f ? total : 1.0f);
@@ -249,6 +264,34 @@ __device__ __forceinline__ BlockBounds block_bounds(const int64_t* __restrict__ 
   return {lo, hi};
 }
 
+// Bounds of this lane's group among the 64 / G consecutive segments of its
+// wave (segments first + wave * 64 / G + j), read with scalar loads: the
+// addresses are wave-uniform, so no vector load and no lane shuffle stands
+// between the kernel's start and the first row loads.
+template <int LOG_G>
+__device__ __forceinline__ void group_bounds(const int64_t* __restrict__ offsets, int64_t first, int64_t n_nodes,
+                                             int64_t n_edges, int64_t& begin, int64_t& end) {
+  constexpr int GPW = 64 >> LOG_G;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t s0 = first + static_cast<int64_t>(wave) * GPW;
+  int64_t o[GPW + 1];
+#pragma unroll
+  for (int j = 0; j <= GPW; ++j) o[j] = offsets[s0 + j < n_nodes ? s0 + j : n_nodes];
+  __builtin_amdgcn_sched_barrier(0);  // the loads above overlap; clamps follow
+#pragma unroll
+  for (int j = 0; j <= GPW; ++j) o[j] = o[j] < 0 ? 0 : (o[j] > n_edges ? n_edges : o[j]);
+  const int g = static_cast<int>(threadIdx.x & 63) >> LOG_G;
+  begin = o[0];
+  end = o[1];
+#pragma unroll
+  for (int j = 1; j < GPW; ++j)
+    if (g == j) {
+      begin = o[j];
+      end = o[j + 1];
+    }
+  if (end < begin) end = begin;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -294,14 +337,16 @@ __device__ __forceinline__ void forward_loads(const ForwardArgs& a, const Tiles<
   }
 }
 
-// Stores alpha of tile i where the lane has a row.
+// Stores alpha of tile i where the lane has a row (tiles [0, tiles) hold
+// every row of the lane).
 template <int V, int R, int STEP, bool kOrdered>
 __device__ __forceinline__ void forward_stores(const ForwardArgs& a, const Tiles<R, STEP, kOrdered>& t,
-                                               int64_t column, const float (&alpha)[R][V]) {
+                                               int64_t column, const float (&alpha)[R][V], int tiles = R) {
   if constexpr (!kOrdered) {
     const BufferView out = row_view(a.alpha, t.base, a.n_edges, a.channels);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
+      if (i >= tiles) continue;
       fvec<V> row;
 #pragma unroll
       for (int v = 0; v < V; ++v) row.v[v] = alpha[i][v];
@@ -494,6 +539,9 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
   if constexpr (kNull) n0 = load_vec<V>(a.null_logit + segment * a.channels + column);
   float value[RMAX][V], envelope[RMAX];
   const auto t = forward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, L.p, L.live, column, value, envelope);
+  // Only the tiles that hold rows of the group are computed (the wave runs
+  // the larger count of its groups).
+  const int tiles = static_cast<int>((degree + PG - 1) / PG);
   float nv[V], peak[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -501,25 +549,30 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
     peak[v] = -INFINITY;
   }
 #pragma unroll
-  for (int i = 0; i < RMAX; ++i)
+  for (int i = 0; i < RMAX; ++i) {
+    if (i < tiles) {
+      const float term = row_term(envelope[i]);
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      value[i][v] = log2_weight(value[i][v], envelope[i]);
-      peak[v] = fmaxf(peak[v], value[i][v]);
+      for (int v = 0; v < V; ++v) {
+        value[i][v] = log2_weight_of_row(value[i][v], term);
+        peak[v] = fmaxf(peak[v], value[i][v]);
+      }
     }
-  float total[V], nw[V];
+  }
+  float total[V], nw[V], shift[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     peak[v] = span_max<LC, G>(peak[v]);
     if (kNull) peak[v] = fmaxf(peak[v], nv[v]);
+    shift[v] = shift_of(peak[v]);
     total[v] = 0.0f;
   }
 #pragma unroll
   for (int i = 0; i < RMAX; ++i) {
-    if (static_cast<int64_t>(i) * PG < degree) {
+    if (i < tiles) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float w = weight_of(value[i][v], peak[v]);
+        const float w = exp2_of(value[i][v] - shift[v]);
         value[i][v] = w;
         total[v] += w;
       }
@@ -528,14 +581,15 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     total[v] = span_sum<LC, G>(total[v]);
-    nw[v] = kNull ? weight_of(nv[v], peak[v]) : 0.0f;
+    nw[v] = kNull ? exp2_of(nv[v] - shift[v]) : 0.0f;
     total[v] = inverse_total(total[v] + nw[v]);
   }
 #pragma unroll
   for (int i = 0; i < RMAX; ++i)
+    if (i < tiles)
 #pragma unroll
-    for (int v = 0; v < V; ++v) value[i][v] *= total[v];
-  forward_stores<V>(a, t, column, value);
+      for (int v = 0; v < V; ++v) value[i][v] *= total[v];
+  forward_stores<V>(a, t, column, value, tiles);
   if (kNull && L.p == 0 && L.live) {
     fvec<V> out;
 #pragma unroll
@@ -563,14 +617,20 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, 
     return;
   }
   const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
-  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int gidx = threadIdx.x >> S::LOG_G;
+  const int64_t segment = first + gidx;
+  if constexpr (planned) {
+    int64_t begin, end;
+    group_bounds<S::LOG_G>(a.offsets, first, a.n_nodes, a.n_edges, begin, end);
+    if (segment < a.n_nodes && end - begin <= S::CAP)
+      forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
+    return;
+  }
+  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int64_t begin = __shfl(bb.lo, gidx);
   const int64_t end = __shfl(bb.hi, gidx);
-  const int64_t segment = first + gidx;
   if (segment < a.n_nodes && end - begin <= S::CAP)
     forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-  if constexpr (planned) return;
   // no plan: this workgroup's long segments, one at a time
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
@@ -821,14 +881,20 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
     return;
   }
   const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
-  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int gidx = threadIdx.x >> S::LOG_G;
+  const int64_t segment = first + gidx;
+  if constexpr (planned) {
+    int64_t begin, end;
+    group_bounds<S::LOG_G>(a.offsets, first, a.n_nodes, a.n_edges, begin, end);
+    if (segment < a.n_nodes && end - begin <= S::CAP)
+      backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
+    return;
+  }
+  const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
   const int64_t begin = __shfl(bb.lo, gidx);
   const int64_t end = __shfl(bb.hi, gidx);
-  const int64_t segment = first + gidx;
   if (segment < a.n_nodes && end - begin <= S::CAP)
     backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-  if constexpr (planned) return;
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
       __ballot(lane < S::SPB && first + lane < a.n_nodes && bb.hi - bb.lo > S::CAP);
