@@ -43,10 +43,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 // [1] n_long, [2, 2 + n_long) ascending ids of the long segments, then
 // scratch (one count per tile of segments).
 constexpr int64_t kPlanHeader = 2;
-// Short-path geometry: a short segment belongs to a group of at least
-// 2^kShortGroupLog lanes, and each lane stages up to kShortFloats values.
-constexpr int kShortGroupLog = 5;
-constexpr int kShortFloats = 24;
 
 // ---------------------------------------------------------------------------
 // arithmetic
@@ -153,17 +149,31 @@ __device__ __forceinline__ void span_merge(float& peak, float& sum) {
 // geometry
 // ---------------------------------------------------------------------------
 
-template <int V, int LOG_LC>
+// Short-path capacity (rows) for rows of LC lanes: 24 / V tiles of a
+// 32-lane group.  Forward and backward share it, so one plan serves both.
+constexpr int short_capacity(int v, int lc) { return (24 / v) * ((lc > 32 ? lc : 32) / lc); }
+
+// Lanes per short group: 32, or LC when a row is wider.  (16-lane groups
+// with twice the tiles fit a config-2-like graph into one dispatch round
+// but need over 96 VGPRs, which halves the occupancy, and ran slower.)
+constexpr int short_group_log(int v, int log_lc, bool backward) {
+  (void)v;
+  (void)backward;
+  return log_lc > 5 ? log_lc : 5;
+}
+
+template <int V, int LOG_LC, bool kBackward = false>
 struct Geo {
   static constexpr int LC = 1 << LOG_LC;               // lanes per edge row
-  static constexpr int LOG_G = LOG_LC > kShortGroupLog ? LOG_LC : kShortGroupLog;
+  static constexpr int LOG_G = short_group_log(V, LOG_LC, kBackward);
   static constexpr int G = 1 << LOG_G;                 // lanes per short segment
+  static constexpr int GPW = 64 / G;                   // short segments per wave
   static constexpr int PG = G / LC;                    // rows per group load
   static constexpr int SPB = kBlock / G;               // segments per short workgroup
   static constexpr int PB = kBlock / LC;               // rows per workgroup load
-  static constexpr int RMAX = kShortFloats / V;        // register tiles, short path
+  static constexpr int CAP = short_capacity(V, LC);    // longest short segment
+  static constexpr int RMAX = CAP / PG;                // register tiles, short path
   static constexpr int RMAXB = 16 / V;                 // register tiles, staged long path
-  static constexpr int CAP = RMAX * PG;                // longest short segment
   static constexpr int UNROLL = 2;                     // loads in flight per thread, streaming path
 };
 
@@ -172,9 +182,9 @@ struct Geo {
 // live (its column lies inside the row).
 //
 // Natural order (slot = edge): rows are read and written through buffer
-// views rebased at `base`, the lowest first slot of the active lanes (wave-
-// uniform), and a lane without a row uses kNoRow; callers keep every slot of
-// the window within 2^31 bytes of `base`.  No load sits in a branch.
+// views rebased at `base` (wave-uniform, at most the lowest slot of the
+// active lanes), and a lane without a row uses kNoRow; callers keep every
+// slot of the window within 2^31 bytes of `base`.  No load sits in a branch.
 // With an order: the order entries of every tile are loaded first (at slot 0
 // for lanes without a row), then the rows they name at a clamped index; `e`
 // keeps the edge id, or -1 where there is no row.  Callers guard the ordered
@@ -190,10 +200,9 @@ struct Tiles {
   uint32_t row_bytes, col_bytes;
   int64_t e[kOrdered ? R : 1];
 
-  __device__ __forceinline__ Tiles(int64_t first_, int64_t end, int row_lane_, bool live_, int64_t column,
-                                   int64_t channels)
-      : first(first_), row_lane(row_lane_), live(live_) {
-    base = kOrdered ? 0 : uniform_i64(first_);
+  __device__ __forceinline__ Tiles(int64_t first_, int64_t end, int64_t base_, int row_lane_, bool live_,
+                                   int64_t column, int64_t channels)
+      : first(first_), base(kOrdered ? 0 : base_), row_lane(row_lane_), live(live_) {
     const int64_t left = end - first_;
     rows_left = static_cast<int32_t>(left < 0 ? 0 : (left > 0x7fffffff ? 0x7fffffff : left));
     row_bytes = static_cast<uint32_t>(channels) * 4u;
@@ -226,10 +235,11 @@ struct Tiles {
   }
 };
 
-// Lane roles inside a workgroup for rows of LC lanes.
-template <int V, int LOG_LC>
+// Lane roles inside a workgroup for rows of LC lanes (short groups of the
+// forward or the backward geometry).
+template <int V, int LOG_LC, bool kBackward = false>
 struct Lanes {
-  using S = Geo<V, LOG_LC>;
+  using S = Geo<V, LOG_LC, kBackward>;
   int lane, wave, k, p, pb, gidx;
   bool live;
   int64_t column;
@@ -368,9 +378,10 @@ __device__ __forceinline__ void forward_stores(const ForwardArgs& a, const Tiles
 // Tiles of [first, end) with every load issued before any arithmetic.
 template <int V, int R, int STEP, bool kOrdered>
 __device__ __forceinline__ Tiles<R, STEP, kOrdered> forward_tiles(const ForwardArgs& a, int64_t first, int64_t end,
-                                                                  int row_lane, bool live, int64_t column,
-                                                                  float (&value)[R][V], float (&envelope)[R]) {
-  Tiles<R, STEP, kOrdered> t(first, end, row_lane, live, column, a.channels);
+                                                                  int64_t base, int row_lane, bool live,
+                                                                  int64_t column, float (&value)[R][V],
+                                                                  float (&envelope)[R]) {
+  Tiles<R, STEP, kOrdered> t(first, end, base, row_lane, live, column, a.channels);
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     envelope[i] = 0.0f;
@@ -394,6 +405,8 @@ template <int V, int LOG_LC, bool kNull, bool kOrdered>
 __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end,
                              float (*partial)[2][Geo<V, LOG_LC>::LC * V]) {
   using S = Geo<V, LOG_LC>;
+  begin = uniform_i64(begin);  // one segment per workgroup
+  end = uniform_i64(end);
   constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
   const Lanes<V, LOG_LC> L(a.channels / V);
   const int64_t column = L.live ? L.column : 0;
@@ -409,7 +422,7 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   if (degree <= RMAXB * PB) {
     // staged: every row of the segment in registers, one read
     float value[RMAXB][V], envelope[RMAXB];
-    const auto t = forward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, L.pb, L.live, column, value, envelope);
+    const auto t = forward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, begin, L.pb, L.live, column, value, envelope);
 #pragma unroll
     for (int v = 0; v < V; ++v) peak[v] = -INFINITY;
 #pragma unroll
@@ -478,7 +491,7 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   }
   for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
     float value[S::UNROLL][V], envelope[S::UNROLL];
-    forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, value, envelope);
+    forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, base, L.pb, L.live, column, value, envelope);
 #pragma unroll
     for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
@@ -506,7 +519,7 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   }
   for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
     float value[S::UNROLL][V], envelope[S::UNROLL];
-    const auto t = forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, value, envelope);
+    const auto t = forward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, base, L.pb, L.live, column, value, envelope);
 #pragma unroll
     for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
@@ -522,14 +535,13 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   __syncthreads();
 }
 
-// Short segment of this lane's group (degree <= CAP), all in registers.  The
-// rows of a wave's (at most two) short groups lie within 2 CAP slots of the
-// first one's begin, which keeps the buffer offsets small.
+// Short segment of this lane's group (degree <= CAP), all in registers; rows
+// are addressed from `base` (see Tiles).
 template <int V, int LOG_LC, bool kNull, bool kOrdered>
-__device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
+__device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segment, int64_t begin, int64_t end,
+                                              int64_t base) {
   using S = Geo<V, LOG_LC>;
   constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
-  static_assert(G >= 32, "the row window of a wave assumes at most two short groups per wave");
   const Lanes<V, LOG_LC> L(a.channels / V);
   const int64_t column = L.live ? L.column : 0;
   const int64_t degree = end - begin;
@@ -538,7 +550,7 @@ __device__ __forceinline__ void forward_short(const ForwardArgs& a, int64_t segm
   for (int v = 0; v < V; ++v) n0.v[v] = -INFINITY;
   if constexpr (kNull) n0 = load_vec<V>(a.null_logit + segment * a.channels + column);
   float value[RMAX][V], envelope[RMAX];
-  const auto t = forward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, L.p, L.live, column, value, envelope);
+  const auto t = forward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, base, L.p, L.live, column, value, envelope);
   // Only the tiles that hold rows of the group are computed (the wave runs
   // the larger count of its groups).
   const int tiles = static_cast<int>((degree + PG - 1) / PG);
@@ -619,18 +631,17 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, 
   const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t segment = first + gidx;
-  if constexpr (planned) {
+  {
     int64_t begin, end;
     group_bounds<S::LOG_G>(a.offsets, first, a.n_nodes, a.n_edges, begin, end);
+    // The rows of a wave's short groups (at most two) lie within 2 CAP slots
+    // of the lowest short group's begin: one buffer window serves the wave.
+    static_assert(S::GPW <= 2, "one row window per wave needs at most two short groups per wave");
     if (segment < a.n_nodes && end - begin <= S::CAP)
-      forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-    return;
+      forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, uniform_i64(begin));
   }
+  if constexpr (planned) return;
   const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
-  const int64_t begin = __shfl(bb.lo, gidx);
-  const int64_t end = __shfl(bb.hi, gidx);
-  if (segment < a.n_nodes && end - begin <= S::CAP)
-    forward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
   // no plan: this workgroup's long segments, one at a time
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
@@ -664,10 +675,10 @@ struct BackwardArgs {
 // of every row (zeros without a row), every load issued before any arithmetic.
 template <int V, int R, int STEP, bool kOrdered>
 __device__ __forceinline__ Tiles<R, STEP, kOrdered> backward_tiles(const BackwardArgs& a, int64_t first, int64_t end,
-                                                                   int row_lane, bool live, int64_t column,
-                                                                   float (&x)[R][V], float (&g)[R][V],
-                                                                   float (&envelope)[R]) {
-  Tiles<R, STEP, kOrdered> t(first, end, row_lane, live, column, a.channels);
+                                                                   int64_t base, int row_lane, bool live,
+                                                                   int64_t column, float (&x)[R][V],
+                                                                   float (&g)[R][V], float (&envelope)[R]) {
+  Tiles<R, STEP, kOrdered> t(first, end, base, row_lane, live, column, a.channels);
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     envelope[i] = 0.0f;
@@ -718,15 +729,17 @@ __device__ __forceinline__ Tiles<R, STEP, kOrdered> backward_tiles(const Backwar
 // grad_logit rows of the tiles from alpha, grad_alpha and the segment's S;
 // grad_env of each row from the row sum over the LC lanes of the row.
 template <int V, int LOG_LC, int R, int STEP, bool kOrdered>
-__device__ __forceinline__ void backward_rows(const BackwardArgs& a, const Lanes<V, LOG_LC>& L,
+__device__ __forceinline__ void backward_rows(const BackwardArgs& a, const Lanes<V, LOG_LC, true>& L,
                                               const Tiles<R, STEP, kOrdered>& t, int64_t column,
                                               const float (&x)[R][V], const float (&g)[R][V],
-                                              const float (&expect)[V], const float (&envelope)[R]) {
+                                              const float (&expect)[V], const float (&envelope)[R],
+                                              int tiles = R) {
   // natural order only (unused, and dropped by the compiler, with an order)
   const BufferView grad_logit = row_view(a.grad_logit, t.base, a.n_edges, a.channels);
   const BufferView grad_env = row_view(a.grad_env, t.base, a.n_edges, 1);
 #pragma unroll
   for (int i = 0; i < R; ++i) {
+    if (i >= tiles) continue;  // no row of the lane's group in this tile or later ones
     const bool has = kOrdered ? t.e[i] >= 0 : t.row(i);
     fvec<V> out;
     float row = 0.0f;
@@ -753,8 +766,10 @@ template <int V, int LOG_LC, bool kNull, bool kOrdered>
 __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end,
                               float (*partial)[2][Geo<V, LOG_LC>::LC * V]) {
   using S = Geo<V, LOG_LC>;
+  begin = uniform_i64(begin);  // one segment per workgroup
+  end = uniform_i64(end);
   constexpr int LC = S::LC, PB = S::PB, RMAXB = S::RMAXB;
-  const Lanes<V, LOG_LC> L(a.channels / V);
+  const Lanes<V, LOG_LC, true> L(a.channels / V);
   const int64_t column = L.live ? L.column : 0;
   const int64_t degree = end - begin;
   float a0[V], g0[V], expect[V];
@@ -772,7 +787,7 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
   if (degree <= RMAXB * PB) {
     // staged: every row of the segment in registers, one read
     float xs[RMAXB][V], gs[RMAXB][V], envs[RMAXB];
-    const auto t = backward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, L.pb, L.live, column, xs, gs, envs);
+    const auto t = backward_tiles<V, RMAXB, PB, kOrdered>(a, begin, end, begin, L.pb, L.live, column, xs, gs, envs);
 #pragma unroll
     for (int i = 0; i < RMAXB; ++i)
 #pragma unroll
@@ -794,7 +809,7 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
     // streaming: the dot-product pass, then the gradient pass
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
       float x[S::UNROLL][V], g[S::UNROLL][V], envs[S::UNROLL];
-      backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, x, g, envs);
+      backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, base, L.pb, L.live, column, x, g, envs);
 #pragma unroll
       for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
@@ -814,7 +829,7 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
     }
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
       float x[S::UNROLL][V], g[S::UNROLL][V], envs[S::UNROLL];
-      const auto t = backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, L.pb, L.live, column, x, g, envs);
+      const auto t = backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, base, L.pb, L.live, column, x, g, envs);
       backward_rows<V, LOG_LC>(a, L, t, column, x, g, expect, envs);
     }
   }
@@ -828,11 +843,11 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
 }
 
 template <int V, int LOG_LC, bool kNull, bool kOrdered>
-__device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end) {
-  using S = Geo<V, LOG_LC>;
+__device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t segment, int64_t begin, int64_t end,
+                                               int64_t base) {
+  using S = Geo<V, LOG_LC, true>;
   constexpr int LC = S::LC, G = S::G, PG = S::PG, RMAX = S::RMAX;
-  static_assert(G >= 32, "the row window of a wave assumes at most two short groups per wave");
-  const Lanes<V, LOG_LC> L(a.channels / V);
+  const Lanes<V, LOG_LC, true> L(a.channels / V);
   const int64_t column = L.live ? L.column : 0;
   float a0[V], g0[V], expect[V];
 #pragma unroll
@@ -847,17 +862,19 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
     }
   }
   float xs[RMAX][V], gs[RMAX][V], envs[RMAX];
-  const auto t = backward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, L.p, L.live, column, xs, gs, envs);
+  const auto t = backward_tiles<V, RMAX, PG, kOrdered>(a, begin, end, base, L.p, L.live, column, xs, gs, envs);
+  const int tiles = static_cast<int>((end - begin + PG - 1) / PG);
 #pragma unroll
   for (int i = 0; i < RMAX; ++i)
+    if (i < tiles)
 #pragma unroll
-    for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
+      for (int v = 0; v < V; ++v) expect[v] = expect[v] + xs[i][v] * gs[i][v];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     expect[v] = span_sum<LC, G>(expect[v]);
     if (kNull) expect[v] = expect[v] + a0[v] * g0[v];
   }
-  backward_rows<V, LOG_LC>(a, L, t, column, xs, gs, expect, envs);
+  backward_rows<V, LOG_LC>(a, L, t, column, xs, gs, expect, envs, tiles);
   if (kNull && L.p == 0 && L.live) {
     fvec<V> out;
 #pragma unroll
@@ -869,7 +886,7 @@ __device__ __forceinline__ void backward_short(const BackwardArgs& a, int64_t se
 template <int V, int LOG_LC, bool kNull, bool kOrdered, bool kPlanned>
 __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a, const int64_t* __restrict__ plan,
                                                                   int64_t n_long) {
-  using S = Geo<V, LOG_LC>;
+  using S = Geo<V, LOG_LC, true>;
   __shared__ float partial[kWaves][2][S::LC * V];
   constexpr bool planned = kPlanned;
   if (planned && static_cast<int64_t>(blockIdx.x) < n_long) {
@@ -883,18 +900,17 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
   const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t segment = first + gidx;
-  if constexpr (planned) {
+  {
     int64_t begin, end;
     group_bounds<S::LOG_G>(a.offsets, first, a.n_nodes, a.n_edges, begin, end);
+    // The rows of a wave's short groups (at most two) lie within 2 CAP slots
+    // of the lowest short group's begin: one buffer window serves the wave.
+    static_assert(S::GPW <= 2, "one row window per wave needs at most two short groups per wave");
     if (segment < a.n_nodes && end - begin <= S::CAP)
-      backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
-    return;
+      backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, uniform_i64(begin));
   }
+  if constexpr (planned) return;
   const BlockBounds bb = block_bounds<S::SPB>(a.offsets, first, a.n_nodes, a.n_edges);
-  const int64_t begin = __shfl(bb.lo, gidx);
-  const int64_t end = __shfl(bb.hi, gidx);
-  if (segment < a.n_nodes && end - begin <= S::CAP)
-    backward_short<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end);
   const int lane = threadIdx.x & 63;
   unsigned long long longs =
       __ballot(lane < S::SPB && first + lane < a.n_nodes && bb.hi - bb.lo > S::CAP);
@@ -1084,21 +1100,16 @@ int lanes_log_for(int64_t chunks) {
 int64_t capacity_for(int64_t channels, bool vec4) {
   const int64_t chunks = vec4 ? channels / 4 : channels;
   if (chunks > 64) return 0;
-  const int log_lc = lanes_log_for(chunks);
-  const int64_t lc = int64_t(1) << log_lc;
-  const int64_t g = lc > (int64_t(1) << kShortGroupLog) ? lc : (int64_t(1) << kShortGroupLog);
-  const int64_t rmax = vec4 ? kShortFloats / 4 : kShortFloats;
-  return rmax * (g / lc);
+  return short_capacity(vec4 ? 4 : 1, 1 << lanes_log_for(chunks));
 }
 
-unsigned int short_blocks(int64_t n_nodes, int log_lc) {
-  const int64_t g = int64_t(1) << (log_lc > kShortGroupLog ? log_lc : kShortGroupLog);
-  return blocks_for(n_nodes, kBlock / g);
+unsigned int short_blocks(int64_t n_nodes, int v, int log_lc, bool backward) {
+  return blocks_for(n_nodes, kBlock >> short_group_log(v, log_lc, backward));
 }
 
 template <int V, int LOG_LC>
 int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, LOG_LC);
+  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, false);
 #define DPA4K_SOFTMAX_FWD(NULLV, ORD)                                                                      \
   (plan != nullptr                                                                                        \
        ? softmax_forward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
@@ -1115,7 +1126,7 @@ int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hi
 
 template <int V, int LOG_LC>
 int launch_backward(const BackwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, LOG_LC);
+  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, true);
 #define DPA4K_SOFTMAX_BWD(NULLV, ORD)                                                                       \
   (plan != nullptr                                                                                         \
        ? softmax_backward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
