@@ -99,8 +99,9 @@ def measured_traffic(key: str | None, bytes_per_launch: int) -> int | None:
     """HBM bytes per launch from the committed FETCH_SIZE + WRITE_SIZE summary, when it is for this workload.
 
     profiles/traffic.json holds the calibrated counter totals of one rocprofv3 --pmc pass per
-    counter; an entry counts only when its algorithmic byte total equals this run's, so a changed
-    workload reports null instead of a stale figure.
+    counter for every bench line (the headline and each entry of `ops`); an entry counts only when
+    its algorithmic byte total equals this run's, so a changed workload reports null instead of a
+    stale figure.
     """
     if key is None:
         return None
@@ -510,6 +511,8 @@ def main() -> int:
             job, _, _ = force_job(131072, steps, warm, graph, "f32")
             ops["force_assembly_config4R_f32"] = op_line("force_assembly", job, job["edges"])
             print("[bench] roofline shapes done", file=sys.stderr, flush=True)
+        for key, op in ops.items():
+            op["roofline"]["traffic"] = measured_traffic(key, op["roofline"]["algorithmic_bytes"])
         line["ops"] = ops
 
     if args.calibrate_copy:
