@@ -73,6 +73,27 @@ inline unsigned int blocks_for(int64_t items, int64_t per_block) {
 constexpr int64_t kMaxGrid = 2147483647;
 
 // ---------------------------------------------------------------------------
+// Device: XCD-aware block order
+// ---------------------------------------------------------------------------
+
+// gfx950 deals the workgroups of a launch to its 8 XCDs round-robin
+// (workgroup b runs on XCD b mod 8), and each XCD has its own L2.  This
+// bijection on [0, blocks) renumbers them so that every XCD runs one
+// contiguous range of logical blocks: XCD x gets blocks/8 logical blocks
+// (plus one for the first blocks mod 8 XCDs) starting at
+// x * (blocks/8) + min(x, blocks mod 8).  Kernels whose neighbouring blocks
+// share data then find it in their own L2.
+constexpr unsigned int kXcds = 8;
+
+__device__ __forceinline__ unsigned int xcd_block(unsigned int block, unsigned int blocks) {
+  const unsigned int xcd = block % kXcds;
+  const unsigned int index = block / kXcds;
+  const unsigned int whole = blocks / kXcds;
+  const unsigned int extra = blocks % kXcds;
+  return xcd * whole + (xcd < extra ? xcd : extra) + index;
+}
+
+// ---------------------------------------------------------------------------
 // Device: CSR bounds
 // ---------------------------------------------------------------------------
 

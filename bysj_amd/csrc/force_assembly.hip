@@ -74,7 +74,9 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
     const int64_t* __restrict__ dst_offsets, const int64_t* __restrict__ src_offsets,
     const int64_t* __restrict__ src_order, T* __restrict__ force, T* __restrict__ virial,
     int64_t n_edges, int64_t n_nodes) {
-  const int64_t atom = static_cast<int64_t>(blockIdx.x) * kAtoms + (threadIdx.x >> kLogGroup);
+  // Neighbouring atoms gather rows from the same destination segments when
+  // atom numbering follows space, so each XCD takes a contiguous atom range.
+  const int64_t atom = static_cast<int64_t>(xcd_block(blockIdx.x, gridDim.x)) * kAtoms + (threadIdx.x >> kLogGroup);
   if (atom >= n_nodes) return;
   const int lane = threadIdx.x & (kGroup - 1);
   int64_t dst_begin, dst_end, src_begin, src_end;
