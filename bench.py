@@ -236,11 +236,17 @@ def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: st
     n_sets = n_sets_for(bytes_per_step)
     generator = torch.Generator(device="cuda")
     generator.manual_seed(5)
-    grads = [base["grad_edge"]] + [torch.randn(base["grad_edge"].shape, generator=generator, device="cuda",
-                                               dtype=dtype) for _ in range(1, n_sets)]
+    # every set has its own gradients and edge vectors (the same geometry, jittered): each step reads
+    # both from HBM; the graph (offsets, src_order) is fixed, as within one neighbour-list lifetime
+    sets = [(base["grad_edge"], base["edge_vec"])] + [
+        (torch.randn(base["grad_edge"].shape, generator=generator, device="cuda", dtype=dtype),
+         base["edge_vec"] + 0.01 * torch.randn(base["edge_vec"].shape, generator=generator, device="cuda",
+                                               dtype=dtype))
+        for _ in range(1, n_sets)]
 
     def step(i):
-        return kernels.force_assembly(grads[i], base["edge_vec"], base["src"], base["dst"], base["dst_offsets"],
+        grad_edge, edge_vec = sets[i]
+        return kernels.force_assembly(grad_edge, edge_vec, base["src"], base["dst"], base["dst_offsets"],
                                       base["src_offsets"], base["src_order"])
 
     with torch.no_grad():
@@ -250,7 +256,11 @@ def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: st
 
 
 def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
-    """segment_softmax backward (with the null logit) on the config-2 graph."""
+    """segment_softmax backward (with the null logit) on the config-2 graph.
+
+    Every input set holds its own alpha, null alpha (forward outputs of fresh logits), envelope
+    and cotangents, so each step reads them from HBM.
+    """
     import torch
 
     from bysj_amd import kernels, workloads
@@ -259,20 +269,26 @@ def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
     base = workloads.segment_softmax_config(n_nodes=n_nodes, seed=0, device="cuda")
     edges, channels = base["logit"].shape
     offsets = base["offsets"]
-    alpha, null_alpha = kernels.segment_softmax(base["logit"], base["env"], offsets, base["null_logit"])
     plan = _C.segment_softmax_plan(offsets, edges, channels)
     reads = 2 * edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + 2 * n_nodes * channels * 4
     writes = edges * channels * 4 + n_nodes * channels * 4 + edges * 4
     n_sets = n_sets_for(reads + writes)
     generator = torch.Generator(device="cuda")
     generator.manual_seed(7)
-    cotangents = [(torch.randn(alpha.shape, generator=generator, device="cuda"),
-                   torch.randn(null_alpha.shape, generator=generator, device="cuda")) for _ in range(n_sets)]
+    sets = []
+    for s in range(n_sets):
+        features = base if s == 0 else workloads.segment_softmax_features(edges, n_nodes, channels, seed=s,
+                                                                          device="cuda")
+        with torch.no_grad():
+            alpha, null_alpha = kernels.segment_softmax(features["logit"], features["env"], offsets,
+                                                        features["null_logit"])
+        sets.append((alpha, null_alpha, features["env"], torch.randn(alpha.shape, generator=generator, device="cuda"),
+                     torch.randn(null_alpha.shape, generator=generator, device="cuda")))
+        del features
 
     def step(i):
-        grad_alpha, grad_null = cotangents[i]
-        return _C.segment_softmax_backward(alpha, grad_alpha, base["env"], offsets, null_alpha, grad_null,
-                                           plan=plan)
+        alpha, null_alpha, env, grad_alpha, grad_null = sets[i]
+        return _C.segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null, plan=plan)
 
     ms = time_steps(step, n_sets, steps, warmup, graph=graph)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
@@ -280,7 +296,10 @@ def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
 
 
 def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
-    """segment_sum backward with edge_scale and node_scale: grad_src, grad_edge_scale, grad_node_scale."""
+    """segment_sum backward with edge_scale and node_scale: grad_src, grad_edge_scale, grad_node_scale.
+
+    Every input set holds its own src, scales and grad_out, so each step reads them from HBM.
+    """
     import torch
 
     from bysj_amd import workloads
@@ -293,11 +312,18 @@ def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool)
     n_sets = n_sets_for(reads + writes)
     generator = torch.Generator(device="cuda")
     generator.manual_seed(8)
-    grads = [torch.randn((n_nodes, channels), generator=generator, device="cuda") for _ in range(n_sets)]
+    sets = []
+    for s in range(n_sets):
+        src = base["src"] if s == 0 else torch.randn(base["src"].shape, generator=generator, device="cuda")
+        edge_scale = torch.rand(edges, generator=generator, device="cuda") + 0.5
+        node_scale = torch.rand(n_nodes, generator=generator, device="cuda") + 0.5
+        grad = torch.randn((n_nodes, channels), generator=generator, device="cuda")
+        sets.append((grad, src, edge_scale, node_scale))
 
     def step(i):
-        return _C.segment_sum_backward(grads[i], base["src"], base["dst"], base["offsets"], base["edge_scale"],
-                                       base["node_scale"], True, None, want_edge_scale_grad=True)
+        grad, src, edge_scale, node_scale = sets[i]
+        return _C.segment_sum_backward(grad, src, base["dst"], base["offsets"], edge_scale, node_scale, True, None,
+                                       want_edge_scale_grad=True)
 
     ms = time_steps(step, n_sets, steps, warmup, graph=graph)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
@@ -326,14 +352,17 @@ def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool)
     gie_ms = time_steps(gie_step, 1, max(4, steps // 10), min(warmup, 3), graph=graph)
     del grad_out
 
-    x = torch.randn((n_atoms, 1024), generator=generator, device="cuda")
-    _, inverse_rms = _C.rmsnorm_forward(x, case["rms_scale"], 1e-6)
     rms_bytes = 3 * n_atoms * 1024 * 4 + 2 * 1024 * 4 + n_atoms * 4
     n_sets = n_sets_for(rms_bytes)
-    grads = [torch.randn((n_atoms, 1024), generator=generator, device="cuda") for _ in range(n_sets)]
+    rms_sets = []
+    for _ in range(n_sets):
+        x = torch.randn((n_atoms, 1024), generator=generator, device="cuda")
+        _, inverse_rms = _C.rmsnorm_forward(x, case["rms_scale"], 1e-6)
+        rms_sets.append((torch.randn((n_atoms, 1024), generator=generator, device="cuda"), x, inverse_rms))
 
     def rms_step(i):
-        return _C.rmsnorm_backward(grads[i], x, case["rms_scale"], inverse_rms, True)
+        grad, x, inverse_rms = rms_sets[i]
+        return _C.rmsnorm_backward(grad, x, case["rms_scale"], inverse_rms, True)
 
     rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
     gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_reads + gie_writes, "sets": 1}

@@ -213,6 +213,232 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
     grad_node_scale[segment] = accumulate ? grad_node_scale[segment] + node_sum : node_sum;
 }
 
+// ---------------------------------------------------------------------------
+// Small grids: one segment per workgroup
+// ---------------------------------------------------------------------------
+//
+// With few segments (config 1: 1,024 segments of ~40 rows of 128 floats) the
+// lane-group kernels above leave the chip mostly empty and walk a segment in
+// several dependent memory round trips.  These kernels give each segment a
+// whole 256-thread workgroup instead.
+
+constexpr int kStageChunks = 2048;  // float4 chunks of LDS staging (32 KB)
+constexpr int kStageItems = kStageChunks / kBlock;
+
+// Forward: the workgroup loads up to kStageChunks / chunks rows of the
+// segment into LDS at once (every thread's loads in flight together), then
+// thread c < channels sums column c of the staged rows in slot order, eight
+// rows of LDS reads ahead of its adds -- the same sequential fp32 sum as the
+// lane-group kernel, so the result is bit-identical.  Longer segments repeat
+// the load/sum step.  Rows of 16 to 64 chunks (64 to 256 floats).
+template <bool kScaleEdge, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
+    const float* __restrict__ src, const int64_t* __restrict__ offsets,
+    const float* __restrict__ edge_scale, const float* __restrict__ node_scale,
+    const int64_t* __restrict__ order, float* __restrict__ out, int64_t n_edges, int64_t n_nodes,
+    int64_t channels) {
+  constexpr int kAhead = 8;
+  __shared__ fvec<4> stage[kStageChunks];
+  __shared__ float weight[kStageChunks / 16 + kAhead];  // rows per batch (chunks >= 16), padded
+  const int64_t segment = blockIdx.x;
+  const int chunks = static_cast<int>(channels / 4);
+  const int width = chunks * 4;
+  const int rows_per_batch = kStageChunks / chunks;
+  int64_t begin, end;
+  segment_bounds(offsets, segment, n_edges, begin, end);
+  const int t = threadIdx.x;
+  const float* staged = reinterpret_cast<const float*>(stage);
+  float acc = 0.0f;
+
+  for (int64_t first = begin; first < end; first += rows_per_batch) {
+    const int rows = static_cast<int>(end - first < rows_per_batch ? end - first : rows_per_batch);
+    const int items = rows * chunks;
+    fvec<4> x[kStageItems];
+#pragma unroll
+    for (int k = 0; k < kStageItems; ++k) {
+      const int item = t + k * kBlock;
+      const int row = item / chunks;
+      const int64_t e = item < items ? edge_of<kOrdered>(order, first + row, n_edges) : -1;
+      if (e >= 0) {
+        x[k] = load_vec<4>(src + e * channels + static_cast<int64_t>(item - row * chunks) * 4);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[k].v[i] = 0.0f;
+      }
+    }
+    // weight of each staged row; NaN marks a row whose order entry is out of range (skipped)
+    for (int row = t; row < rows; row += kBlock) {
+      const int64_t e = edge_of<kOrdered>(order, first + row, n_edges);
+      weight[row] = e < 0 ? __builtin_nanf("") : (kScaleEdge ? edge_scale[e] : 1.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < kStageItems; ++k)
+      if (t + k * kBlock < items) stage[t + k * kBlock] = x[k];
+    __syncthreads();
+    if (t < width) {
+      for (int row = 0; row < rows; row += kAhead) {
+        float v[kAhead], w[kAhead];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+          const int r = row + k < rows ? row + k : row;
+          v[k] = staged[r * width + t];
+          w[k] = weight[r];
+        }
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) {
+          if (row + k >= rows || (kOrdered && w[k] != w[k])) continue;
+          acc = acc + (kScaleEdge ? v[k] * w[k] : v[k]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (t < width) out[segment * channels + t] = node_scale != nullptr ? acc * node_scale[segment] : acc;
+}
+
+// Backward: SG = 256 / G lane groups of G lanes (G >= chunks) take the
+// segment's rows round-robin, U rows per group per round with every load of
+// a round issued first.  grad_edge_scale is per edge; the groups' partial
+// grad_node_scale sums meet in LDS in group order.  Rows of at most 64 chunks.
+template <int G, int U, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void segment_sum_backward_wide_kernel(
+    const float* __restrict__ grad_out, const float* __restrict__ src,
+    const int64_t* __restrict__ offsets, const float* __restrict__ edge_scale,
+    const float* __restrict__ node_scale, const int64_t* __restrict__ order,
+    float* __restrict__ grad_src, float* __restrict__ grad_edge_scale,
+    float* __restrict__ grad_node_scale, int64_t n_edges, int64_t n_nodes, int64_t channels) {
+  constexpr int SG = kBlock / G;
+  __shared__ float partial[SG];
+  const int64_t segment = blockIdx.x;
+  const int lane = threadIdx.x % G;
+  const int group = threadIdx.x / G;
+  const int chunks = static_cast<int>(channels / 4);
+  const bool live = lane < chunks;
+  const int64_t column = static_cast<int64_t>(live ? lane : 0) * 4;
+  const bool want_edge = grad_edge_scale != nullptr;
+  const bool want_node = grad_node_scale != nullptr;
+  const bool need_dot = want_edge || want_node;
+  const bool has_edge_scale = edge_scale != nullptr;
+
+  const float scale = node_scale != nullptr ? node_scale[segment] : 1.0f;
+  fvec<4> g, gs;
+  if (live) {
+    g = load_vec<4>(grad_out + segment * channels + column);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) g.v[i] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gs.v[i] = node_scale != nullptr ? g.v[i] * scale : g.v[i];
+
+  int64_t begin, end;
+  segment_bounds(offsets, segment, n_edges, begin, end);
+  float node_sum = 0.0f;
+  for (int64_t base = begin + group; base < end; base += static_cast<int64_t>(SG) * U) {
+    int64_t edge[U];
+    float weight[U];
+    fvec<4> x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t slot = base + static_cast<int64_t>(u) * SG;
+      edge[u] = slot < end ? edge_of<kOrdered>(order, slot, n_edges) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      weight[u] = has_edge_scale && edge[u] >= 0 ? edge_scale[edge[u]] : 1.0f;
+      if (need_dot && live && edge[u] >= 0) {
+        x[u] = load_vec<4>(src + edge[u] * channels + column);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[u].v[i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (edge[u] < 0 || !live) continue;
+      fvec<4> o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o.v[i] = has_edge_scale ? gs.v[i] * weight[u] : gs.v[i];
+      store_vec_stream<4>(grad_src + edge[u] * channels + column, o);
+    }
+    if (need_dot) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d = d + g.v[i] * x[u].v[i];
+        d = group_sum<G>(d);
+        if (edge[u] < 0) continue;
+        if (want_edge && lane == 0) grad_edge_scale[edge[u]] = scale * d;
+        node_sum = node_sum + weight[u] * d;
+      }
+    }
+  }
+  if (want_node) {
+    if (lane == 0) partial[group] = node_sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float total = partial[0];
+      for (int q = 1; q < SG; ++q) total = total + partial[q];
+      grad_node_scale[segment] = total;
+    }
+  }
+}
+
+int launch_staged_forward(const float* src, const int64_t* offsets, const float* edge_scale,
+                          const float* node_scale, const int64_t* order, float* out, int64_t n_edges,
+                          int64_t n_nodes, int64_t channels, hipStream_t stream) {
+  const unsigned int grid = static_cast<unsigned int>(n_nodes);
+#define DPA4K_SUM_STAGED(SCALE, ORD)                                                                  \
+  segment_sum_staged_kernel<SCALE, ORD><<<grid, kBlock, 0, stream>>>(src, offsets, edge_scale, node_scale, \
+                                                                      order, out, n_edges, n_nodes, channels)
+  if (edge_scale != nullptr) {
+    if (order != nullptr) DPA4K_SUM_STAGED(true, true); else DPA4K_SUM_STAGED(true, false);
+  } else {
+    if (order != nullptr) DPA4K_SUM_STAGED(false, true); else DPA4K_SUM_STAGED(false, false);
+  }
+#undef DPA4K_SUM_STAGED
+  return launched("segment_sum_staged_kernel");
+}
+
+template <int G>
+int launch_wide_backward_g(const float* grad_out, const float* src, const int64_t* offsets,
+                           const float* edge_scale, const float* node_scale, const int64_t* order,
+                           float* grad_src, float* grad_edge_scale, float* grad_node_scale, int64_t n_edges,
+                           int64_t n_nodes, int64_t channels, hipStream_t stream) {
+  constexpr int U = 8;
+  const unsigned int grid = static_cast<unsigned int>(n_nodes);
+  if (order != nullptr)
+    segment_sum_backward_wide_kernel<G, U, true><<<grid, kBlock, 0, stream>>>(
+        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
+        n_edges, n_nodes, channels);
+  else
+    segment_sum_backward_wide_kernel<G, U, false><<<grid, kBlock, 0, stream>>>(
+        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
+        n_edges, n_nodes, channels);
+  return launched("segment_sum_backward_wide_kernel");
+}
+
+int launch_wide_backward(const float* grad_out, const float* src, const int64_t* offsets, const float* edge_scale,
+                         const float* node_scale, const int64_t* order, float* grad_src, float* grad_edge_scale,
+                         float* grad_node_scale, int64_t n_edges, int64_t n_nodes, int64_t channels,
+                         hipStream_t stream) {
+  const int64_t chunks = channels / 4;
+  if (chunks <= 16)
+    return launch_wide_backward_g<16>(grad_out, src, offsets, edge_scale, node_scale, order, grad_src,
+                                      grad_edge_scale, grad_node_scale, n_edges, n_nodes, channels, stream);
+  if (chunks <= 32)
+    return launch_wide_backward_g<32>(grad_out, src, offsets, edge_scale, node_scale, order, grad_src,
+                                      grad_edge_scale, grad_node_scale, n_edges, n_nodes, channels, stream);
+  return launch_wide_backward_g<64>(grad_out, src, offsets, edge_scale, node_scale, order, grad_src,
+                                    grad_edge_scale, grad_node_scale, n_edges, n_nodes, channels, stream);
+}
+
+// The workgroup-per-segment kernels serve grids of fewer than this many
+// segments, with float4 rows of 16 to 64 chunks (64 to 256 channels).
+constexpr int64_t kWideSegments = 4096;
+bool use_wide(int64_t n_nodes, int64_t chunks) { return n_nodes < kWideSegments && chunks >= 16 && chunks <= 64; }
+
 // Lane-group geometry for a row of `chunks` vector chunks.
 struct Geometry {
   int group;   // lanes per segment (power of two, <= 64)
@@ -360,6 +586,9 @@ extern "C" int dpa4k_segment_sum_forward(const float* src, const int64_t* offset
   hipStream_t stream = as_stream(stream_handle);
   const bool vec4 = channels % 4 == 0 && aligned16(src) && aligned16(out);
   const int64_t chunks = vec4 ? channels / 4 : channels;
+  if (vec4 && use_wide(n_nodes, chunks))
+    return launch_staged_forward(src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels,
+                                 stream);
   const Geometry geo = geometry_for(chunks);
   for (int64_t base = 0; base < chunks; base += geo.window()) {
     const int status =
@@ -395,6 +624,9 @@ extern "C" int dpa4k_segment_sum_backward(const float* grad_out, const float* sr
   const bool vec4 = channels % 4 == 0 && aligned16(grad_out) && aligned16(grad_src) &&
                     (src == nullptr || aligned16(src));
   const int64_t chunks = vec4 ? channels / 4 : channels;
+  if (vec4 && use_wide(n_nodes, chunks))
+    return launch_wide_backward(grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
+                                grad_node_scale, n_edges, n_nodes, channels, stream);
   const Geometry geo = geometry_for(chunks);
   int accumulate = 0;
   for (int64_t base = 0; base < chunks; base += geo.window()) {

@@ -141,7 +141,53 @@ def test_segment_sum_config1_full_size_and_determinism():
     assert_bitwise(first, ref.segment_sum_reference(case["src"], case["dst"], case["offsets"]), "config 1")
 
 
-@pytest.mark.parametrize("channels", [3, 8, 128, 640])
+@pytest.mark.parametrize("channels", [64, 128, 256])
+@pytest.mark.parametrize("use_order", [False, True])
+def test_segment_sum_workgroup_path_long_segments(channels, use_order):
+    """Small grids take the workgroup-per-segment kernels; segments longer than one LDS batch
+    repeat the staging step.  The same graph padded past the small-grid limit with empty segments
+    takes the lane-group kernels, and both must agree bit for bit (forward, grad_src)."""
+    announce("segment_sum workgroup path", channels, use_order)
+    gen = torch.Generator().manual_seed(channels + int(use_order))
+    degrees = np.array([0, 1, 2, 300, 1000, 45, 0, 129, 64, 33, 7, 511], dtype=np.int64)
+    nodes = degrees.size
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    if use_order:
+        dst, order, offsets = _shuffled(dst_sorted, seed=channels)
+    else:
+        dst, order, offsets = dst_sorted, None, ref.segment_offsets(dst_sorted, nodes)
+    edges = dst.numel()
+    src = torch.randn(edges, channels, generator=gen)
+    w = torch.rand(edges, generator=gen) + 0.5
+    s = torch.rand(nodes, generator=gen) + 0.5
+    g = torch.randn(nodes, channels, generator=gen)
+    o = None if order is None else order.to(DEV)
+    x = src.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    sd = s.to(DEV).requires_grad_(True)
+    out = kernels.segment_sum(x, dst.to(DEV), offsets.to(DEV), wd, sd, order=o)
+    assert_bitwise(out, ref.segment_sum_reference(src, dst, offsets, w, s), "workgroup-path forward")
+    grads = torch.autograd.grad(out, (x, wd, sd), g.to(DEV))
+    e_src, e_w, e_s = ref.segment_sum_backward_reference(g, src, dst, offsets, w, s)
+    assert_bitwise(grads[0], e_src, "workgroup-path grad_src")
+    assert_close_scaled(grads[1], e_w, what="workgroup-path grad_edge_scale")
+    assert_close_scaled(grads[2], e_s, what="workgroup-path grad_node_scale")
+    # the same edges under 5000 more (empty) segments: the lane-group kernels
+    pad = 5000
+    offsets_big = torch.cat([offsets, offsets[-1:].expand(pad)])
+    s_big = torch.cat([s, torch.ones(pad)])
+    g_big = torch.cat([g, torch.zeros(pad, channels)])
+    native = kernels._C
+    big = native.segment_sum_forward(src.to(DEV), offsets_big.to(DEV), w.to(DEV), s_big.to(DEV), o)
+    assert_bitwise(big[:nodes], out, "lane-group vs workgroup forward")
+    grads_big = native.segment_sum_backward(g_big.to(DEV), src.to(DEV), dst.to(DEV), offsets_big.to(DEV), w.to(DEV),
+                                            s_big.to(DEV), True, o, want_edge_scale_grad=True)
+    assert_bitwise(grads_big[0], grads[0], "lane-group vs workgroup grad_src")
+    assert_close_scaled(grads_big[2], grads[1], what="lane-group vs workgroup grad_edge_scale")
+    assert_close_scaled(grads_big[1][:nodes], grads[2], what="lane-group vs workgroup grad_node_scale")
+
+
+@pytest.mark.parametrize("channels", [3, 8, 64, 128, 256, 640])
 @pytest.mark.parametrize("use_order", [False, True])
 def test_segment_sum_backward_matches_autograd(channels, use_order):
     announce("segment_sum bwd", channels, use_order)
