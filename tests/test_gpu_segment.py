@@ -145,8 +145,9 @@ def test_segment_sum_config1_full_size_and_determinism():
 @pytest.mark.parametrize("use_order", [False, True])
 def test_segment_sum_workgroup_path_long_segments(channels, use_order):
     """Small grids take the workgroup-per-segment kernels; segments longer than one LDS batch
-    repeat the staging step.  The same graph padded past the small-grid limit with empty segments
-    takes the lane-group kernels, and both must agree bit for bit (forward, grad_src)."""
+    repeat the forward's staging step.  The same graph padded past the small-grid limit with empty
+    segments takes the lane-group forward (the backward keeps its workgroup kernel), and the
+    results must agree bit for bit (forward, grad_src)."""
     announce("segment_sum workgroup path", channels, use_order)
     gen = torch.Generator().manual_seed(channels + int(use_order))
     degrees = np.array([0, 1, 2, 300, 1000, 45, 0, 129, 64, 33, 7, 511], dtype=np.int64)
@@ -182,9 +183,9 @@ def test_segment_sum_workgroup_path_long_segments(channels, use_order):
     assert_bitwise(big[:nodes], out, "lane-group vs workgroup forward")
     grads_big = native.segment_sum_backward(g_big.to(DEV), src.to(DEV), dst.to(DEV), offsets_big.to(DEV), w.to(DEV),
                                             s_big.to(DEV), True, o, want_edge_scale_grad=True)
-    assert_bitwise(grads_big[0], grads[0], "lane-group vs workgroup grad_src")
-    assert_close_scaled(grads_big[2], grads[1], what="lane-group vs workgroup grad_edge_scale")
-    assert_close_scaled(grads_big[1][:nodes], grads[2], what="lane-group vs workgroup grad_node_scale")
+    assert_bitwise(grads_big[0], grads[0], "padded grid vs small grid grad_src")
+    assert_close_scaled(grads_big[2], grads[1], what="padded grid vs small grid grad_edge_scale")
+    assert_close_scaled(grads_big[1][:nodes], grads[2], what="padded grid vs small grid grad_node_scale")
 
 
 @pytest.mark.parametrize("channels", [3, 8, 64, 128, 256, 640])
