@@ -186,13 +186,13 @@ def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool):
             "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
 
 
-def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool):
+def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool, water=None, gie_steps=None):
     import torch
 
     from bysj_amd import workloads
     from bysj_amd.kernels import _C
 
-    water = workloads.water_graph(n_atoms, seed=0)
+    water = water or workloads.water_graph(n_atoms, seed=0)
     case = workloads.gie_config(water, seed=0, device="cuda", primary=True)
     edges = water.n_edges
     offsets, order, _ = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, 16)
@@ -204,7 +204,7 @@ def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool):
     gie_bytes = edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 + n_atoms * 4 \
         + n_atoms * 16 * 64 * 4
     with torch.no_grad():
-        gie_ms = time_steps(gie_step, 1, max(4, steps // 10), min(warmup, 3), graph=graph)
+        gie_ms = time_steps(gie_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
         rows = gie_step(0).reshape(n_atoms, 1024)
     rms_bytes = 2 * n_atoms * 1024 * 4 + 1024 * 4 + n_atoms * 4
     n_sets = n_sets_for(rms_bytes)
@@ -330,8 +330,8 @@ def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool)
             "bytes": reads + writes}
 
 
-def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool):
-    """GIE backward (zonal, radial and inverse-degree gradients) and RMSNorm backward on config 3."""
+def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool, gie_steps=None):
+    """GIE backward (zonal, radial and inverse-degree gradients) and RMSNorm backward on a water box."""
     import torch
 
     from bysj_amd.kernels import _C
@@ -349,7 +349,7 @@ def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool)
     gie_reads = n_atoms * 15 * 64 * 4 + edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 \
         + n_atoms * 4
     gie_writes = edges * 15 * 4 + edges * 16 * 64 * 4 + n_atoms * 4
-    gie_ms = time_steps(gie_step, 1, max(4, steps // 10), min(warmup, 3), graph=graph)
+    gie_ms = time_steps(gie_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
     del grad_out
 
     rms_bytes = 3 * n_atoms * 1024 * 4 + 2 * 1024 * 4 + n_atoms * 4
@@ -368,6 +368,32 @@ def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool)
     gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_reads + gie_writes, "sets": 1}
     rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
     return gie, rms
+
+
+def rmsnorm_jobs(rows: int, steps: int, warmup: int, graph: bool):
+    """RMSNorm forward and backward over `rows` random rows of width 1024 (eps 1e-6, scale ~U(0.5, 1.5))."""
+    import torch
+
+    from bysj_amd.kernels import _C
+
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(13)
+    scale = torch.rand(1024, generator=generator, device="cuda") + 0.5
+    fwd_bytes = 2 * rows * 1024 * 4 + 1024 * 4 + rows * 4
+    bwd_bytes = 3 * rows * 1024 * 4 + 2 * 1024 * 4 + rows * 4
+    n_sets = n_sets_for(bwd_bytes)
+    sets = []
+    for _ in range(n_sets):
+        x = torch.randn((rows, 1024), generator=generator, device="cuda")
+        _, inverse_rms = _C.rmsnorm_forward(x, scale, 1e-6)
+        sets.append((x, inverse_rms, torch.randn((rows, 1024), generator=generator, device="cuda")))
+    with torch.no_grad():
+        fwd_ms = time_steps(lambda i: _C.rmsnorm_forward(sets[i][0], scale, 1e-6), n_sets, steps, warmup, graph=graph)
+    bwd_ms = time_steps(lambda i: _C.rmsnorm_backward(sets[i][2], sets[i][0], scale, sets[i][1], True), n_sets,
+                        steps, warmup, graph=graph)
+    fwd = {"rows": rows, "width": 1024, "ms_per_step": fwd_ms, "bytes": fwd_bytes, "sets": n_sets}
+    bwd = {"rows": rows, "width": 1024, "ms_per_step": bwd_ms, "bytes": bwd_bytes, "sets": n_sets}
+    return fwd, bwd
 
 
 def csr_job(water, steps: int):
@@ -537,8 +563,31 @@ def main() -> int:
             ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])
             job = softmax_job(210000, steps, warm, graph)
             ops["segment_softmax_config2R"] = op_line("segment_softmax_fwd", job, job["edges"])
-            job, _, _ = force_job(131072, steps, warm, graph, "f32")
-            ops["force_assembly_config4R_f32"] = op_line("force_assembly", job, job["edges"])
+            if not args.no_backward:
+                job = softmax_backward_job(210000, steps, warm, graph)
+                ops["segment_softmax_bwd_config2R"] = op_line("segment_softmax_bwd", job, job["edges"])
+            print("[bench] roofline shapes 1R, 2R done", file=sys.stderr, flush=True)
+            water4r = workloads.water_graph(131072, seed=0)
+            for dtype_name in ("f32", "f64"):
+                job, _, _ = force_job(131072, steps, warm, graph, dtype_name, water=water4r)
+                ops[f"force_assembly_config4R_{dtype_name}"] = op_line("force_assembly", job, job["edges"])
+            del water4r
+            print("[bench] roofline shape 4R done", file=sys.stderr, flush=True)
+            # config 3R: 114,688 atoms (E ~ 10.4M; GIE radial [E, 16, 64] is 42.6 GB), two GIE steps
+            water3r = workloads.water_graph(114688, seed=0)
+            gie, rms, _, case3r = gie_rmsnorm_jobs(114688, steps, warm, graph, water=water3r, gie_steps=2)
+            ops["gie_config3R"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
+            ops["rmsnorm_config3R"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
+            if not args.no_backward:
+                gie_b, rms_b = gie_rmsnorm_backward_jobs(water3r, case3r, steps, warm, graph, gie_steps=2)
+                ops["gie_bwd_config3R"] = op_line("gie_zonal_scatter_bwd", gie_b, gie_b["edges"])
+                ops["rmsnorm_bwd_config3R"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
+            del case3r, water3r
+            torch.cuda.empty_cache()
+            print("[bench] roofline shape 3R done", file=sys.stderr, flush=True)
+            rms, rms_b = rmsnorm_jobs(1048576, steps, warm, graph)
+            ops["rmsnorm_rows1M"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
+            ops["rmsnorm_bwd_rows1M"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
             print("[bench] roofline shapes done", file=sys.stderr, flush=True)
         for key, op in ops.items():
             op["roofline"]["traffic"] = measured_traffic(key, op["roofline"]["algorithmic_bytes"])
