@@ -203,8 +203,16 @@ def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool, water=N
 
     gie_bytes = edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 + n_atoms * 4 \
         + n_atoms * 16 * 64 * 4
+    width = 16 * 64
+    fused_bytes = gie_bytes - n_atoms * width * 4 + n_atoms * width * 4 + width * 4 + n_atoms * 4
+
+    def fused_step(_):
+        return _C.gie_rmsnorm_forward_csr(case["zonal"], case["radial"], offsets, order, case["radial_slot"],
+                                          case["inv_sqrt_deg"], case["rms_scale"], 1e-6, False)
+
     with torch.no_grad():
         gie_ms = time_steps(gie_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
+        fused_ms = time_steps(fused_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
         rows = gie_step(0).reshape(n_atoms, 1024)
     rms_bytes = 2 * n_atoms * 1024 * 4 + 1024 * 4 + n_atoms * 4
     n_sets = n_sets_for(rms_bytes)
@@ -219,6 +227,8 @@ def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool, water=N
         rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
     gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_bytes, "sets": 1}
     rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
+    gie["fused_rmsnorm"] = {"edges": edges, "nodes": n_atoms, "ms_per_step": fused_ms, "bytes": fused_bytes,
+                            "sets": 1}
     return gie, rms, water, case
 
 
@@ -515,6 +525,8 @@ def main() -> int:
         gie, rms, water3, case3 = gie_rmsnorm_jobs(24576, steps, warm, graph)
         ops["gie_config3"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
         ops["rmsnorm_config3"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
+        ops["gie_rmsnorm_config3"] = op_line("gie_zonal_scatter_rmsnorm_fwd", gie["fused_rmsnorm"], gie["edges"])
+        ops["gie_rmsnorm_config3"]["unfused_ms_per_step"] = round(gie["ms_per_step"] + rms["ms_per_step"], 5)
         sample_nodes = 2048
         cut = int(water3.offsets()[sample_nodes])
         sample = tuple(t.cpu() for t in (case3["zonal"][:cut], case3["radial"][:cut], case3["dst"][:cut],
@@ -578,6 +590,9 @@ def main() -> int:
             gie, rms, _, case3r = gie_rmsnorm_jobs(114688, steps, warm, graph, water=water3r, gie_steps=2)
             ops["gie_config3R"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
             ops["rmsnorm_config3R"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
+            ops["gie_rmsnorm_config3R"] = op_line("gie_zonal_scatter_rmsnorm_fwd", gie["fused_rmsnorm"],
+                                                  gie["edges"])
+            ops["gie_rmsnorm_config3R"]["unfused_ms_per_step"] = round(gie["ms_per_step"] + rms["ms_per_step"], 5)
             if not args.no_backward:
                 gie_b, rms_b = gie_rmsnorm_backward_jobs(water3r, case3r, steps, warm, graph, gie_steps=2)
                 ops["gie_bwd_config3R"] = op_line("gie_zonal_scatter_bwd", gie_b, gie_b["edges"])

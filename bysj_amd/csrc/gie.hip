@@ -128,6 +128,138 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
   }
 }
 
+// Fused GIE -> RMSNorm over each node's flattened row of W = (R + 1) * C
+// floats (no reference counterpart; the reference runs the two operators
+// back to back).  One wave per node, float4 chunks.  Lane l owns the chunks
+// q = l + 64 j of the whole row, row 0 included -- the chunk layout of
+// rmsnorm_forward_kernel -- and accumulates the GIE sum of the chunks it owns
+// exactly as gie_forward_kernel does (slot order, product rounded before the
+// add, normalised by inv_sqrt_deg after the sum).  The sum of squares,
+// 1 / sqrt(mean + eps) and the scaled output then follow the RMSNorm kernel
+// step for step, so y, the pre-norm row x (written only when x_out is
+// given) and inverse_rms equal the two kernels run back to back, bit for bit.
+__device__ __forceinline__ float fused_inverse_rms(float sum_squares, int64_t width, float eps) {
+  return 1.0f / sqrtf(sum_squares / static_cast<float>(width) + eps);
+}
+
+template <int CPL, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_rmsnorm_forward_kernel(
+    const float* __restrict__ zonal, const float* __restrict__ radial,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ order,
+    const int64_t* __restrict__ radial_slot, const float* __restrict__ inv,
+    const float* __restrict__ scale, float eps, float* __restrict__ y, float* __restrict__ x_out,
+    float* __restrict__ inverse_rms, int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+    int64_t channels) {
+  constexpr int V = 4;
+  constexpr int U = CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
+  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (node >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t row_chunks = channels / V;
+  const int64_t chunks = (n_rows + 1) * row_chunks;  // the whole row, row 0 included
+  const int64_t width = (n_rows + 1) * channels;
+  const int64_t edge_stride = n_radial * channels;
+
+  int64_t zonal_col[CPL], radial_col[CPL];
+  bool live[CPL];
+  fvec<V> s[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t q = lane + 64 * j;
+    const int64_t gq = q - row_chunks;  // chunk of rows 1..R
+    const int64_t r = gq >= 0 ? gq / row_chunks : 0;
+    const int64_t c = gq >= 0 ? gq - r * row_chunks : 0;
+    const int64_t slot = (gq >= 0 && q < chunks) ? radial_slot[r] : -1;
+    live[j] = static_cast<uint64_t>(slot) < static_cast<uint64_t>(n_radial);
+    zonal_col[j] = live[j] ? r : 0;
+    radial_col[j] = live[j] ? slot * channels + c * V : 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) s[j].v[i] = 0.0f;
+    if (q < chunks && scale != nullptr) s[j] = load_vec<V>(scale + q * V);
+  }
+
+  fvec<V> acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[j].v[i] = 0.0f;
+
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  int64_t slot = begin;
+  for (; slot + U <= end; slot += U) {
+    int64_t edge[U];
+    float z[U][CPL];
+    fvec<V> x[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) edge[u] = edge_of<kOrdered>(order, slot + u, n_edges);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (live[j] && (!kOrdered || edge[u] >= 0)) {
+          z[u][j] = zonal[edge[u] * n_rows + zonal_col[j]];
+          x[u][j] = load_vec<V>(radial + edge[u] * edge_stride + radial_col[j]);
+        } else {
+          z[u][j] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[u][j].v[i] = 0.0f;
+        }
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kOrdered && edge[u] < 0) continue;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + z[u][j] * x[u][j].v[i];
+    }
+  }
+  for (; slot < end; ++slot) {
+    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+    if (kOrdered && e < 0) continue;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (!live[j]) continue;
+      const float zv = zonal[e * n_rows + zonal_col[j]];
+      const fvec<V> xv = load_vec<V>(radial + e * edge_stride + radial_col[j]);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + zv * xv.v[i];
+    }
+  }
+
+  // the GIE output row (row 0 and absent rows: 0 * inv), then RMSNorm over it
+  const float degree_scale = inv[node];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const bool in_row = lane + 64 * j < chunks;
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[j].v[i] = in_row ? acc[j].v[i] * degree_scale : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int i = 0; i < V; ++i) sum = sum + acc[j].v[i] * acc[j].v[i];
+  sum = group_sum<64>(sum);
+  const float inv_rms = fused_inverse_rms(sum, width, eps);
+  float* y_row = y + node * width;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int64_t q = lane + 64 * j;
+    if (q >= chunks) continue;
+    fvec<V> out;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      out.v[i] = acc[j].v[i] * inv_rms;
+      if (scale != nullptr) out.v[i] = out.v[i] * s[j].v[i];
+    }
+    store_vec_stream<V>(y_row + q * V, out);
+    if (x_out != nullptr) store_vec<V>(x_out + node * width + q * V, acc[j]);
+  }
+  if (lane == 0) inverse_rms[node] = inv_rms;
+}
+
 // Distinct slots: lane owns (slot s, chunk c) pairs q = s * row_chunks + c of
 // one edge's radial block; RC = row_chunks lanes share a slot (power of two).
 template <int V, int CPL, int RC, bool kOrdered>
@@ -648,4 +780,63 @@ extern "C" int dpa4k_gie_zonal_scatter_backward(
       grad_output, zonal, radial, csr.offsets, csr.order, radial_slot, inv_sqrt_deg, grad_zonal,
       grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
       (csr.info & 2) ? 1 : 0, stream);
+}
+
+namespace dpa4k {
+namespace {
+
+template <bool kOrdered>
+int launch_gie_rmsnorm(int cpl, const float* zonal, const float* radial, const int64_t* offsets,
+                       const int64_t* order, const int64_t* radial_slot, const float* inv, const float* scale,
+                       float eps, float* y, float* x_out, float* inverse_rms, int64_t n_edges, int64_t n_nodes,
+                       int64_t n_rows, int64_t n_radial, int64_t channels, hipStream_t stream) {
+  const unsigned int grid = blocks_for(n_nodes, kWaves);
+#define DPA4K_GIE_RMS(C)                                                                              \
+  gie_rmsnorm_forward_kernel<C, kOrdered><<<grid, kBlock, 0, stream>>>(                              \
+      zonal, radial, offsets, order, radial_slot, inv, scale, eps, y, x_out, inverse_rms, n_edges, n_nodes, \
+      n_rows, n_radial, channels)
+  switch (cpl) {
+    case 1: DPA4K_GIE_RMS(1); break;
+    case 2: DPA4K_GIE_RMS(2); break;
+    case 4: DPA4K_GIE_RMS(4); break;
+    default: DPA4K_GIE_RMS(8); break;
+  }
+#undef DPA4K_GIE_RMS
+  return launched("gie_rmsnorm_forward_kernel");
+}
+
+}  // namespace
+}  // namespace dpa4k
+
+extern "C" int dpa4k_gie_rmsnorm_supported(int64_t n_rows, int64_t channels) {
+  return channels > 0 && channels % 4 == 0 && n_rows >= 0 && (n_rows + 1) * (channels / 4) <= 512 ? 1 : 0;
+}
+
+extern "C" int dpa4k_gie_rmsnorm_forward_csr(const float* zonal, const float* radial, const int64_t* offsets,
+                                             const int64_t* order, const int64_t* radial_slot,
+                                             const float* inv_sqrt_deg, const float* scale, float eps, float* y,
+                                             float* x_out, float* inverse_rms, int64_t n_edges, int64_t n_nodes,
+                                             int64_t n_rows, int64_t n_radial, int64_t channels,
+                                             dpa4k_stream_t stream_handle) {
+  clear_error();
+  if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE RMSNorm")) return s;
+  if (!dpa4k_gie_rmsnorm_supported(n_rows, channels))
+    return fail(DPA4K_EINVAL, "GIE RMSNorm: rows of (n_rows + 1) * channels floats need channels %% 4 == 0 and "
+                              "at most 2048 floats");
+  if (!(eps > 0.0f) || eps == INFINITY) return fail(DPA4K_EINVAL, "GIE RMSNorm: eps must be finite and positive");
+  if (n_nodes == 0) return DPA4K_OK;
+  if (offsets == nullptr || inv_sqrt_deg == nullptr || y == nullptr || inverse_rms == nullptr ||
+      (n_rows > 0 && radial_slot == nullptr) ||
+      (n_edges > 0 && n_rows > 0 && (zonal == nullptr || radial == nullptr)))
+    return fail(DPA4K_EINVAL, "GIE RMSNorm: null pointer");
+  if (!aligned16(y) || (x_out != nullptr && !aligned16(x_out)) || (radial != nullptr && !aligned16(radial)) ||
+      (scale != nullptr && !aligned16(scale)))
+    return fail(DPA4K_EINVAL, "GIE RMSNorm: radial, scale and outputs must be 16-byte aligned");
+  hipStream_t stream = as_stream(stream_handle);
+  const int cpl = per_lane_for((n_rows + 1) * (channels / 4));
+  return order != nullptr
+             ? launch_gie_rmsnorm<true>(cpl, zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, scale, eps, y,
+                                        x_out, inverse_rms, n_edges, n_nodes, n_rows, n_radial, channels, stream)
+             : launch_gie_rmsnorm<false>(cpl, zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, scale, eps,
+                                         y, x_out, inverse_rms, n_edges, n_nodes, n_rows, n_radial, channels, stream);
 }

@@ -15,7 +15,8 @@ tensor, the ``edge_scale`` gradient; ``force_assembly`` also takes float64
 inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
 ``*_csr`` GIE entry points expose the device-side CSR construction;
 ``segment_softmax_plan`` builds the degree plan that
-``segment_softmax_forward/backward(..., plan=...)`` accept.
+``segment_softmax_forward/backward(..., plan=...)`` accept;
+``gie_rmsnorm_forward_csr`` is the fused GIE -> RMSNorm forward.
 """
 from __future__ import annotations
 
@@ -409,6 +410,42 @@ def gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, in
         )
     _lib.check(status)
     return out
+
+
+def gie_rmsnorm_supported(n_rows: int, channels: int) -> bool:
+    """Whether the fused GIE -> RMSNorm kernel takes rows of (n_rows + 1) * channels floats."""
+    return bool(_LIB.dpa4k_gie_rmsnorm_supported(int(n_rows), int(channels)))
+
+
+def gie_rmsnorm_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, scale, eps, keep_x=False):
+    """Fused GIE zonal scatter and RMSNorm over each node's flattened (n_rows + 1) * channels row.
+
+    Returns ``(y, x, inverse_rms)``: ``y`` shaped ``(n_nodes, n_rows + 1, channels)``, the pre-norm
+    GIE output ``x`` of the same shape when ``keep_x`` (else None) and ``inverse_rms`` ``(n_nodes,)``.
+    ``scale`` is a ``((n_rows + 1) * channels,)`` tensor or an empty one for no scale.
+    """
+    edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
+    n_radial, channels = int(radial.shape[1]), int(radial.shape[2])
+    nodes = int(inv_sqrt_deg.shape[0])
+    width = (rows + 1) * channels
+    _check(gie_rmsnorm_supported(rows, channels),
+           "GIE RMSNorm needs channels % 4 == 0 and rows of at most 2048 + channels floats")
+    _f32(scale, "GIE RMSNorm scale")
+    _check(scale.numel() in (0, width), f"GIE RMSNorm scale must have shape ({width},) or be empty")
+    _same_device(zonal, radial, offsets, radial_slot, inv_sqrt_deg, scale)
+    y = torch.empty((nodes, rows + 1, channels), dtype=torch.float32, device=zonal.device)
+    x = torch.empty_like(y) if keep_x else None
+    inverse_rms = torch.empty((nodes,), dtype=torch.float32, device=zonal.device)
+    if nodes == 0:
+        return y, x, inverse_rms
+    with _on(zonal.device) as stream:
+        status = _LIB.dpa4k_gie_rmsnorm_forward_csr(
+            _ptr(zonal), _ptr(radial), offsets.data_ptr(), _ptr(order), _ptr(radial_slot), inv_sqrt_deg.data_ptr(),
+            _ptr(scale), float(eps), y.data_ptr(), None if x is None else x.data_ptr(), inverse_rms.data_ptr(),
+            edges, nodes, rows, n_radial, channels, stream,
+        )
+    _lib.check(status)
+    return y, x, inverse_rms
 
 
 def gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, radial_slot,

@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -58,6 +58,9 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_gie_zonal_scatter_backward": (
         _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "dpa4k_gie_workspace_size": (_SZ, [_I64, _I64]),
+    "dpa4k_gie_rmsnorm_supported": (_INT, [_I64, _I64]),
+    "dpa4k_gie_rmsnorm_forward_csr": (
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "dpa4k_rmsnorm_forward": (_INT, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "dpa4k_rmsnorm_backward_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_rmsnorm_backward": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),

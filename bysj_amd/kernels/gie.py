@@ -6,6 +6,9 @@ validation.  The forward groups the (possibly unsorted) ``dst`` into a
 destination CSR on the device once and keeps it for the backward, so neither
 pass uses atomics.  Out-of-range ``dst`` or ``radial_slot`` values raise
 ``ValueError`` instead of being read out of bounds.
+
+``gie_zonal_scatter_rmsnorm`` (an extension, not in ``__all__``) fuses the
+scatter with the RMSNorm that follows it over each node's flattened row.
 """
 from __future__ import annotations
 
@@ -111,6 +114,92 @@ def zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg):
 def gie_zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg):
     """Alias of :func:`zonal_scatter` named after the DPA4 GIE stage."""
     return zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+
+
+class _GIERMSNormFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, zonal, radial, dst, radial_slot, inv_sqrt_deg, scale, eps):
+        native = _extension("gie_zonal_scatter_forward")
+        n_nodes, n_radial = int(inv_sqrt_deg.shape[0]), int(radial.shape[1])
+        offsets, order, info = native.gie_group(dst, radial_slot, n_nodes, n_radial)
+        keep_x = any(ctx.needs_input_grad)
+        y, x, inverse_rms = native.gie_rmsnorm_forward_csr(zonal, radial, offsets, order, radial_slot,
+                                                          inv_sqrt_deg, scale, eps, keep_x)
+        ctx.slots_distinct = bool(info & 2)
+        ctx.has_order = order is not None
+        ctx.has_scale = scale.numel() != 0
+        saved = [zonal, radial, radial_slot, inv_sqrt_deg, scale, inverse_rms, offsets]
+        if keep_x:
+            saved.append(x)
+        if order is not None:
+            saved.append(order)
+        ctx.save_for_backward(*saved)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        saved = ctx.saved_tensors
+        zonal, radial, radial_slot, inv_sqrt_deg, scale, inverse_rms, offsets, x = saved[:8]
+        order = saved[8] if ctx.has_order else None
+        native = _extension("rmsnorm_backward")
+        n_nodes, width = x.shape[0], x.shape[1] * x.shape[2]
+        want_scale = ctx.has_scale and ctx.needs_input_grad[5]
+        grad_x, grad_scale = native.rmsnorm_backward(grad_y.contiguous().reshape(n_nodes, width),
+                                                     x.reshape(n_nodes, width), scale, inverse_rms, want_scale)
+        need = (ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[4])
+        if any(need):
+            grads = native.gie_zonal_scatter_backward_csr(
+                grad_x.reshape(x.shape), zonal, radial, offsets, order, radial_slot, inv_sqrt_deg,
+                ctx.slots_distinct, need=need,
+            )
+        else:
+            grads = (None, None, None)
+        return (
+            grads[0] if need[0] else None,
+            grads[1] if need[1] else None,
+            None,
+            None,
+            grads[2] if need[2] else None,
+            grad_scale if want_scale else None,
+            None,
+        )
+
+
+def gie_zonal_scatter_rmsnorm(zonal, radial, dst, radial_slot, inv_sqrt_deg, scale=None, eps=1e-6):
+    """``rmsnorm(zonal_scatter(...).reshape(n_nodes, -1), scale, eps)`` reshaped back, in one pass.
+
+    An extension of the reference (which runs ``zonal_scatter`` and then
+    ``rmsnorm``): the node rows of ``(n_rows + 1) * channels`` floats are
+    normalised where the GIE kernel forms them, so the pre-norm rows are
+    written only when a gradient is needed (the RMSNorm backward reads them)
+    and never read back in the forward.  Same validation as the two
+    operators; ``scale`` has shape ``((n_rows + 1) * channels,)``.  The
+    result equals the two operators run back to back bit for bit.  Shapes
+    the fused kernel does not take (channels not a multiple of 4, rows over
+    2048 + channels floats, no edges) run the two operators.
+    """
+    from .rmsnorm import _validate as _validate_rmsnorm
+    from .rmsnorm import rmsnorm
+
+    _validate(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    n_nodes = int(inv_sqrt_deg.shape[0])
+    n_edges, n_rows = int(zonal.shape[0]), int(zonal.shape[1])
+    channels = int(radial.shape[2])
+    width = (n_rows + 1) * channels
+    probe = torch.empty((1, width), dtype=torch.float32, device=zonal.device) if width > 0 else None
+    if probe is None:
+        raise ValueError("GIE RMSNorm rows must contain at least one channel")
+    eps = _validate_rmsnorm(probe, scale, eps)
+    require_dcu(zonal, radial, dst, radial_slot, inv_sqrt_deg, scale)
+    native = _extension("gie_zonal_scatter_forward")
+    fused = (n_nodes > 0 and n_edges * n_rows > 0 and native.gie_rmsnorm_supported(n_rows, channels)
+             and radial.data_ptr() % 16 == 0 and (scale is None or scale.data_ptr() % 16 == 0))
+    if not fused:
+        rows = zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+        return rmsnorm(rows.reshape(n_nodes, width), scale, eps).reshape(n_nodes, n_rows + 1, channels)
+    empty = torch.empty((0,), dtype=torch.float32, device=zonal.device)
+    return _GIERMSNormFunction.apply(zonal, radial, dst, radial_slot, inv_sqrt_deg,
+                                     scale if scale is not None else empty, eps)
 
 
 def gie_available() -> bool:

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 2
+#define DPA4K_ABI_VERSION 3
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -286,6 +286,27 @@ int dpa4k_gie_zonal_scatter_backward(
     dpa4k_stream_t stream);
 /* Workspace of the one-call forms (CSR arrays + grouping scratch). */
 size_t dpa4k_gie_workspace_size(int64_t n_edges, int64_t n_nodes);
+
+/* Fused GIE zonal scatter -> RMSNorm (no reference counterpart: the
+ * reference runs gie_zonal_scatter_forward_hip, csrc/gie.cpp:148, and then
+ * rmsnorm_forward_hip, csrc/rmsnorm.cpp:99).  For each node, x = the GIE
+ * output row [R + 1, C] (as dpa4k_gie_zonal_scatter_forward_csr), flattened
+ * to W = (R + 1) * C floats, and y = x * (1 / sqrt(mean(x^2) + eps)) *
+ * scale (as dpa4k_rmsnorm_forward); y[N, W], inverse_rms[N], and x[N, W]
+ * when x_out is not NULL (the backward needs it).  Bit-identical to the two
+ * entry points run back to back.  scale may be NULL.  Needs channels % 4 ==
+ * 0, W <= 2048 + C (dpa4k_gie_rmsnorm_supported) and 16-byte aligned
+ * radial, scale, y and x_out. */
+int dpa4k_gie_rmsnorm_supported(int64_t n_rows, int64_t channels);
+int dpa4k_gie_rmsnorm_forward_csr(const float* zonal, const float* radial,
+                                  const int64_t* offsets, const int64_t* order,
+                                  const int64_t* radial_slot,
+                                  const float* inv_sqrt_deg, const float* scale,
+                                  float eps, float* y, float* x_out,
+                                  float* inverse_rms, int64_t n_edges,
+                                  int64_t n_nodes, int64_t n_rows,
+                                  int64_t n_radial, int64_t channels,
+                                  dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * RMSNorm

@@ -189,3 +189,109 @@ def test_gie_then_rmsnorm_config3_reduced():
     y = kernels.rmsnorm(rows, case["rms_scale"].to(DEV), eps=1e-6)
     assert_close_scaled(y, reference_rmsnorm(expected.reshape(expected.shape[0], -1), case["rms_scale"], 1e-6),
                         what="rmsnorm")
+
+
+# ---------------------------------------------------------------------------
+# fused GIE -> RMSNorm (extension: kernels.gie.gie_zonal_scatter_rmsnorm)
+# ---------------------------------------------------------------------------
+
+def _oracle_gie_rmsnorm(zonal, radial, dst, slots, inverse, scale, eps):
+    rows = gie_ref.zonal_scatter_reference(zonal, radial, dst, slots, inverse)
+    flat = rows.reshape(rows.shape[0], -1)
+    return reference_rmsnorm(flat, scale, eps).reshape(rows.shape)
+
+
+@pytest.mark.parametrize("primary", [True, False])
+@pytest.mark.parametrize("use_scale", [True, False])
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_gie_rmsnorm_fused_matches_two_operators(primary, use_scale, shuffle):
+    """Fused forward == zonal_scatter then rmsnorm (both gfx950) bit for bit; both within the fp32
+    rule of the oracle chain; gradients of every input against autograd through the oracle."""
+    from bysj_amd.kernels import gie as gie_ops
+
+    announce("gie rmsnorm fused", primary, use_scale, shuffle)
+    graph = workloads.water_graph(768, seed=5, rcut=3.0)
+    case = workloads.gie_config(graph, seed=5, primary=primary, channels=64)
+    dst, zonal, radial = case["dst"], case["zonal"], case["radial"]
+    if shuffle:
+        perm = torch.randperm(dst.numel(), generator=torch.Generator().manual_seed(6))
+        dst, zonal, radial = dst[perm].contiguous(), zonal[perm].contiguous(), radial[perm].contiguous()
+    scale = case["rms_scale"] if use_scale else None
+    inputs = (zonal, radial, dst, case["radial_slot"], case["inv_sqrt_deg"])
+    d = _to(inputs)
+    ds = None if scale is None else scale.to(DEV)
+    with torch.no_grad():
+        fused = gie_ops.gie_zonal_scatter_rmsnorm(*d, scale=ds, eps=1e-6)
+        rows = kernels.zonal_scatter(*d)
+        two_step = kernels.rmsnorm(rows.reshape(rows.shape[0], -1), ds, eps=1e-6).reshape(rows.shape)
+    assert_bitwise(fused, two_step, "fused vs zonal_scatter -> rmsnorm")
+    assert_close_scaled(fused, _oracle_gie_rmsnorm(*inputs, scale, 1e-6), what="fused vs oracle")
+    again = gie_ops.gie_zonal_scatter_rmsnorm(*d, scale=ds, eps=1e-6)
+    assert_bitwise(again, fused, "run to run")
+
+    z, r = d[0].clone().requires_grad_(True), d[1].clone().requires_grad_(True)
+    inv = d[4].clone().requires_grad_(True)
+    s = None if ds is None else ds.clone().requires_grad_(True)
+    out = gie_ops.gie_zonal_scatter_rmsnorm(z, r, d[2], d[3], inv, scale=s, eps=1e-6)
+    assert_bitwise(out, fused, "forward with gradients kept")
+    up = torch.randn(out.shape, generator=torch.Generator().manual_seed(7))
+    wrt = (z, r, inv) + (() if s is None else (s,))
+    grads = torch.autograd.grad(out, wrt, up.to(DEV))
+    cz, cr = inputs[0].clone().requires_grad_(True), inputs[1].clone().requires_grad_(True)
+    cinv = inputs[4].clone().requires_grad_(True)
+    cs = None if scale is None else scale.clone().requires_grad_(True)
+    expected_out = _oracle_gie_rmsnorm(cz, cr, inputs[2], inputs[3], cinv, cs, 1e-6)
+    expected = torch.autograd.grad(expected_out, (cz, cr, cinv) + (() if cs is None else (cs,)), up)
+    for label, actual, wanted in zip(("zonal", "radial", "inverse", "scale"), grads, expected):
+        if label == "inverse":
+            continue
+        assert_close_scaled(actual, wanted, rtol=2e-5, scale=2e-5, what=f"grad {label}")
+    # RMSNorm is scale invariant, so d y / d inv_sqrt_deg is a sum of (n_rows + 1) * channels terms
+    # that cancel (exactly, but for eps): fp32 results are rounding noise around a tiny value.  Check
+    # it against the chain in float64, to 2e-5 of the node's sum of absolute terms.
+    truth, terms = _inverse_gradient_fp64(inputs, scale, up, 1e-6)
+    error = (grads[2].double().cpu() - truth).abs()
+    assert bool((error <= 2e-5 * terms + 1e-12).all()), f"grad inverse: worst {float((error / terms).max())}"
+
+
+def _inverse_gradient_fp64(inputs, scale, up, eps):
+    """d(sum up * y)/d inv_sqrt_deg of zonal_scatter -> rmsnorm in float64, and per node the sum
+    of |d(loss)/d x * S| over the row (S the unnormalised scatter), the scale of its terms."""
+    zonal, radial, dst, slots, inverse = (t.double() if t.is_floating_point() else t for t in inputs)
+    n_nodes, n_rows, channels = inverse.shape[0], zonal.shape[1], radial.shape[2]
+    gathered = radial.gather(1, slots.reshape(1, -1, 1).expand(zonal.shape[0], n_rows, channels))
+    summed = torch.zeros((n_nodes, n_rows + 1, channels), dtype=torch.float64)
+    summed[:, 1:, :].index_add_(0, dst, zonal.unsqueeze(-1) * gathered)
+    inv = inverse.reshape(-1).clone().requires_grad_(True)
+    x = (summed * inv.reshape(-1, 1, 1)).reshape(n_nodes, -1)
+    x.retain_grad()
+    y = x * torch.rsqrt(x.pow(2).mean(dim=1, keepdim=True) + eps)
+    if scale is not None:
+        y = y * scale.double()
+    (y * up.double().reshape(n_nodes, -1)).sum().backward()
+    terms = (x.grad * summed.reshape(n_nodes, -1)).abs().sum(dim=1)
+    return inv.grad.detach(), terms.detach()
+
+
+def test_gie_rmsnorm_unfused_shapes_and_empty_edges():
+    """Rows the fused kernel does not take (channels % 4 != 0) and graphs without edges run the two
+    operators; results still follow the oracle chain."""
+    from bysj_amd.kernels import gie as gie_ops
+
+    announce("gie rmsnorm unfused shapes")
+    inputs = _fixture()
+    width = (inputs[0].shape[1] + 1) * inputs[1].shape[2]
+    scale = torch.linspace(0.5, 1.5, width)
+    out = gie_ops.gie_zonal_scatter_rmsnorm(*_to(inputs), scale=scale.to(DEV), eps=1e-6)
+    assert_close_scaled(out, _oracle_gie_rmsnorm(*inputs, scale, 1e-6), what="3 channels")
+    zonal = torch.empty(0, 15)
+    radial = torch.empty(0, 16, 8)
+    dst = torch.empty(0, dtype=torch.int64)
+    slots = torch.arange(1, 16, dtype=torch.int64)
+    inverse = torch.ones(3)
+    out = gie_ops.gie_zonal_scatter_rmsnorm(*_to((zonal, radial, dst, slots, inverse)), eps=1e-6)
+    assert out.shape == (3, 16, 8) and out.count_nonzero().item() == 0
+    with pytest.raises(ValueError):
+        gie_ops.gie_zonal_scatter_rmsnorm(*_to(inputs), scale=torch.ones(3, device=DEV), eps=1e-6)
+    with pytest.raises(ValueError):
+        gie_ops.gie_zonal_scatter_rmsnorm(*_to(inputs), eps=0.0)
