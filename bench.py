@@ -424,6 +424,47 @@ def csr_job(water, steps: int):
             "sets": 1, "torch_ms_per_call": torch_ms}
 
 
+def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
+    """Read-only and copy rates of plain streams on this part, and a copy of one operator's bytes.
+
+    1 GiB read-only and copy passes (dpa4k_stream_calibrate: grid-stride, four 16-byte chunks per
+    thread per round), then a copy that reads `read_bytes` and writes `write_bytes`, rotated
+    through 1 GiB of distinct sources like the operator lines.  Same graph-replay timing.
+    """
+    import torch
+
+    from bysj_amd.kernels import _lib
+
+    library = _lib.load()
+    floats = 256 * 2**20
+    source = torch.randn(floats, device="cuda")
+    target = torch.empty(floats, device="cuda")
+    sink = torch.empty(8192, device="cuda")
+
+    def launch(src, read_floats, dst, write_floats):
+        status = library.dpa4k_stream_calibrate(src.data_ptr(), read_floats, dst.data_ptr(), write_floats,
+                                                torch.cuda.current_stream().cuda_stream)
+        _lib.check(status)
+
+    read_ms = time_steps(lambda _: launch(source, floats, sink, 0), 1, 10, 2)
+    copy_ms = time_steps(lambda _: launch(source, floats, target, floats), 1, 10, 2)
+    del source, target
+    read_floats = (read_bytes // 4 + 3) // 4 * 4
+    write_floats = min(read_floats, (write_bytes // 4 + 3) // 4 * 4)
+    n_sets = n_sets_for(read_bytes + write_bytes)
+    sources = [torch.randn(read_floats, device="cuda") for _ in range(n_sets)]
+    out = torch.empty(max(write_floats, 8192), device="cuda")
+    op_ms = time_steps(lambda i: launch(sources[i], read_floats, out, write_floats), n_sets, steps, 20)
+    moved = (read_floats + write_floats) * 4
+    return {"read_GBps": round(floats * 4 / (read_ms * 1e-3) / 1e9, 1),
+            "copy_GBps": round(2 * floats * 4 / (copy_ms * 1e-3) / 1e9, 1),
+            "same_bytes_copy_us": round(op_ms * 1e3, 3),
+            "same_bytes_copy_GBps": round(moved / (op_ms * 1e-3) / 1e9, 1),
+            "note": "plain HIP streams on this part (1 GiB read, 1 GiB copy, and a copy of the headline's "
+                    "read/write bytes); the headline's ms_per_step over same_bytes_copy_us is its share of "
+                    "what a stream of its own bytes reaches"}
+
+
 def op_line(name: str, job: dict, unit_count: int, unit: str = "edges/s") -> dict:
     line = {"op": name, "value": round(unit_count / (job["ms_per_step"] * 1e-3), 1), "unit": unit,
             "ms_per_step": round(job["ms_per_step"], 5), "input_sets": job.get("sets", 1),
@@ -506,6 +547,13 @@ def main() -> int:
         "roofline": roofline(head["bytes"], head["ms_per_step"], "segment_softmax_fwd_config2"),
     }
     print(f"[bench] headline done: {head['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+    edges, channels, nodes = head["edges"], head["channels"], head["nodes"]
+    head_reads = edges * channels * 4 + edges * 4 + (nodes + 1) * 8 + nodes * channels * 4
+    ceilings = stream_ceilings(head_reads, head["bytes"] - head_reads, args.steps)
+    ceilings["headline_share_of_same_bytes_copy"] = round(ceilings["same_bytes_copy_us"] /
+                                                          (head["ms_per_step"] * 1e3), 4)
+    line["stream_ceilings"] = ceilings
+    print("[bench] stream ceilings done", file=sys.stderr, flush=True)
 
     ops = {}
     extra_cpu = {}

@@ -332,6 +332,18 @@ int dpa4k_rmsnorm_backward(const float* grad, const float* x,
                            int64_t width, void* workspace,
                            size_t workspace_bytes, dpa4k_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Stream calibration (measurement aid; no reference counterpart)
+ * ---------------------------------------------------------------------- */
+
+/* Streams read_floats floats of src and writes the first write_floats of
+ * them to dst (write_floats == 0: read only; dst then receives at most one
+ * word per workgroup and needs 8192 floats).  Counts are multiples of 4,
+ * write_floats <= read_floats, buffers 16-byte aligned.  bench.py times it
+ * to report the read and copy ceilings of the part beside each roofline. */
+int dpa4k_stream_calibrate(const float* src, int64_t read_floats, float* dst,
+                           int64_t write_floats, dpa4k_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
