@@ -38,9 +38,12 @@ _CHECK_GROUPING = os.environ.get("DPA4_CHECK_GROUPING", "0").strip().lower() in 
 def segment_offsets(dst: torch.Tensor, n_nodes: int) -> torch.Tensor:
     """Exclusive prefix sum of the destination group sizes of an edge list.
 
-    gfx950 tensors: histogram + scan kernels (one host sync for the range
-    check, like the reference's ``dst.min()/dst.max()``).  CPU tensors: the
-    same bincount/cumsum with torch on the host, as in the reference.
+    gfx950 tensors: a check pass, a stable radix sort when ``dst`` is not
+    already non-decreasing, and a boundary pass that writes each offset once
+    (one host sync for the range check, like the reference's
+    ``dst.min()/dst.max()``).  CPU tensors never reach the device: the
+    reference's helper is device-agnostic torch (bincount and cumsum), and so
+    is this one for them.
     """
     if not isinstance(dst, torch.Tensor):
         raise TypeError("segment offsets require a tensor of destinations")
