@@ -20,7 +20,6 @@ inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
 """
 from __future__ import annotations
 
-import contextlib
 
 import torch
 
@@ -81,14 +80,35 @@ def _ptr(tensor):
     return None if tensor is None or tensor.numel() == 0 else tensor.data_ptr()
 
 
-@contextlib.contextmanager
-def _on(device: torch.device):
-    """Make `device` current for the launch (the reference's CUDAGuard)."""
-    if device.index is None or device.index == torch.cuda.current_device():
-        yield torch.cuda.current_stream(device).cuda_stream
-        return
-    with torch.cuda.device(device):
-        yield torch.cuda.current_stream(device).cuda_stream
+# The raw handle of a device's current stream, without building a
+# torch.cuda.Stream object per launch (the public call is the fallback).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(index: int) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+class _on:
+    """Make `device` current for the launch (the reference's CUDAGuard); yields its current stream."""
+
+    __slots__ = ("index", "previous")
+
+    def __init__(self, device: torch.device):
+        current = torch.cuda.current_device()
+        self.index = current if device.index is None else device.index
+        self.previous = current
+
+    def __enter__(self) -> int:
+        if self.index != self.previous:
+            torch.cuda.set_device(self.index)
+        return _current_stream(self.index)
+
+    def __exit__(self, *exc) -> None:
+        if self.index != self.previous:
+            torch.cuda.set_device(self.previous)
 
 
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:

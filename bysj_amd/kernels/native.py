@@ -7,18 +7,36 @@ code and tests that patch ``kernels.<op>.require_dcu`` keep working.
 from __future__ import annotations
 
 import importlib
+import sys
 
 import torch
 
 SUPPORTED_ARCHITECTURES = frozenset({"gfx950"})
 _NATIVE_MODULE = __name__.rsplit(".", 1)[0] + "._C"
 
+# Every operator call passes through the gate and the loader, so both keep
+# what they have established: the loaded native module (only the one that is
+# in sys.modules, i.e. the real import) and the device indices whose
+# architecture has been checked.  `importlib.import_module` takes the import
+# system's module lock even for a loaded module, which costs tens of
+# microseconds per call.
+_LOADED = None
+_CHECKED_DEVICES: set[int] = set()
+_RUNTIME_READY = False
+
 
 def _require_hip_runtime() -> None:
+    # A HIP runtime with a visible device stays so for the process; only the
+    # first successful check is paid (torch.cuda.is_available reads the
+    # environment on every call).
+    global _RUNTIME_READY
+    if _RUNTIME_READY:
+        return
     if not torch.version.hip:
         raise RuntimeError("gfx950 operators require a ROCm (HIP) build of PyTorch")
     if not torch.cuda.is_available():
         raise RuntimeError("gfx950 operators require a visible MI355X (gfx950) device")
+    _RUNTIME_READY = True
 
 
 def require_dcu(*tensors) -> torch.device:
@@ -37,28 +55,35 @@ def require_dcu(*tensors) -> torch.device:
             raise RuntimeError("gfx950 operator inputs must share one device")
         device = tensor.device
     index = torch.cuda.current_device() if device is None or device.index is None else device.index
-    try:
-        properties = torch.cuda.get_device_properties(index)
-    except (AssertionError, RuntimeError) as error:
-        raise RuntimeError(f"cannot inspect GPU device {index}") from error
-    architecture = str(getattr(properties, "gcnArchName", "")).split(":", 1)[0]
-    if architecture not in SUPPORTED_ARCHITECTURES:
-        raise RuntimeError(
-            f"unsupported GPU architecture {architecture!r}; these operators are built for gfx950 (MI355X)"
-        )
+    if index not in _CHECKED_DEVICES:
+        try:
+            properties = torch.cuda.get_device_properties(index)
+        except (AssertionError, RuntimeError) as error:
+            raise RuntimeError(f"cannot inspect GPU device {index}") from error
+        architecture = str(getattr(properties, "gcnArchName", "")).split(":", 1)[0]
+        if architecture not in SUPPORTED_ARCHITECTURES:
+            raise RuntimeError(
+                f"unsupported GPU architecture {architecture!r}; these operators are built for gfx950 (MI355X)"
+            )
+        _CHECKED_DEVICES.add(index)
     return torch.device("cuda", index)
 
 
 def _extension(required_symbol: str):
     """Import the native module and require one of its entry points."""
+    global _LOADED
     _require_hip_runtime()
-    try:
-        extension = importlib.import_module(_NATIVE_MODULE)
-    except (ImportError, OSError) as error:
-        raise RuntimeError(
-            "the gfx950 operator library is not built: run __graft_entry__.build() "
-            "(segment, GIE and RMSNorm operators)"
-        ) from error
+    extension = _LOADED
+    if extension is None:
+        try:
+            extension = importlib.import_module(_NATIVE_MODULE)
+        except (ImportError, OSError) as error:
+            raise RuntimeError(
+                "the gfx950 operator library is not built: run __graft_entry__.build() "
+                "(segment, GIE and RMSNorm operators)"
+            ) from error
+        if sys.modules.get(_NATIVE_MODULE) is extension:
+            _LOADED = extension
     if not hasattr(extension, required_symbol):
         raise RuntimeError(f"the loaded {_NATIVE_MODULE} has no {required_symbol!r} entry point")
     return extension

@@ -152,12 +152,12 @@ def test_invalid_inputs_fail_before_the_device_gate():
 
 def test_native_loader_requires_the_entry_point():
     extension = SimpleNamespace(rmsnorm_forward=object())
-    with patch.object(native_mod, "_require_hip_runtime"), \
+    with patch.object(native_mod, "_require_hip_runtime"), patch.object(native_mod, "_LOADED", None), \
             patch.object(native_mod.importlib, "import_module", return_value=extension):
         assert native_mod._extension("rmsnorm_forward") is extension
         with pytest.raises(RuntimeError, match="no 'rmsnorm_backward' entry point"):
             native_mod._extension("rmsnorm_backward")
-    with patch.object(native_mod, "_require_hip_runtime"), \
+    with patch.object(native_mod, "_require_hip_runtime"), patch.object(native_mod, "_LOADED", None), \
             patch.object(native_mod.importlib, "import_module", side_effect=ImportError("absent")):
         with pytest.raises(RuntimeError, match="not built"):
             native_mod._extension("rmsnorm_forward")
