@@ -465,6 +465,72 @@ def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
                     "what a stream of its own bytes reaches"}
 
 
+def reference_shapes(steps: int) -> dict:
+    """The reference's own latency-test shape, timed like its harness and as a kernel.
+
+    tests/csrc/latency/test_segment_ops_latency.py of the reference: 3,000 atoms, 181,838 edges,
+    dst = sorted uniform draws, env ~ U(0.1, 1.1), logits/null logits ~ N(0, 1) at 64 and 256
+    channels, force assembly on uniform random sources.  `eager_ms` follows its `_median_ms`
+    (10 warmup calls, median of 5 repeats of 20 calls between events, same inputs every call);
+    `kernel_ms` is the graph replay of this file.  `dcu_ms` is the reference's published figure
+    on its Hygon DCU (docs/task2-hip-fusion-plan.md:229, :272), other hardware.
+    """
+    import torch
+
+    from bysj_amd import kernels
+
+    atoms, edges = 3000, 181838
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(11)
+    dst = torch.sort(torch.randint(0, atoms, (edges,), generator=generator, device="cuda")).values
+    offsets = kernels.segment_offsets(dst, atoms)
+    env = torch.rand(edges, generator=generator, device="cuda") + 0.1
+
+    def median_eager(function) -> float:
+        for _ in range(10):
+            function()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(5):
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(20):
+                function()
+            stop.record()
+            torch.cuda.synchronize()
+            samples.append(start.elapsed_time(stop) / 20)
+        samples.sort()
+        return samples[2]
+
+    out = {}
+    with torch.no_grad():
+        for channels, dcu in ((64, 0.49), (256, 1.91)):
+            logit = torch.randn(edges, channels, generator=generator, device="cuda")
+            null = torch.randn(atoms, channels, generator=generator, device="cuda")
+            call = lambda _=None, logit=logit, null=null: kernels.segment_softmax(logit, env, offsets, null)
+            out[f"segment_softmax_C{channels}_null"] = {
+                "eager_ms": round(median_eager(call), 4), "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
+                "dcu_ms": dcu, "source": "docs/task2-hip-fusion-plan.md:229"}
+        src = torch.randint(0, atoms, (edges,), generator=generator, device="cuda")
+        src_order, src_offsets = kernels.group_by_source(src, atoms)
+        grad_edge = torch.randn(edges, 3, generator=generator, device="cuda")
+        edge_vec = torch.randn(edges, 3, generator=generator, device="cuda")
+        call = lambda _=None: kernels.force_assembly(grad_edge, edge_vec, src, dst, offsets, src_offsets, src_order)
+        out["force_assembly_f32"] = {"eager_ms": round(median_eager(call), 4),
+                                     "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
+                                     "dcu_ms": 0.182, "source": "docs/task2-hip-fusion-plan.md:272"}
+        node_scale = torch.rand(atoms, generator=generator, device="cuda") + 0.5
+        for channels in (64, 256):
+            src_rows = torch.randn(edges, channels, generator=generator, device="cuda")
+            call = lambda _=None, rows=src_rows: kernels.segment_sum(rows, dst, offsets, None, node_scale)
+            out[f"segment_sum_C{channels}"] = {"eager_ms": round(median_eager(call), 4),
+                                               "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
+                                               "dcu_ms": None, "source": "not published by the reference"}
+    out["note"] = ("same inputs every call, as in the reference's harness, so they stay in the Infinity Cache; "
+                   "eager_ms includes the Python layer's cost per call")
+    return out
+
+
 def op_line(name: str, job: dict, unit_count: int, unit: str = "edges/s") -> dict:
     line = {"op": name, "value": round(unit_count / (job["ms_per_step"] * 1e-3), 1), "unit": unit,
             "ms_per_step": round(job["ms_per_step"], 5), "input_sets": job.get("sets", 1),
@@ -655,6 +721,8 @@ def main() -> int:
         for key, op in ops.items():
             op["roofline"]["traffic"] = measured_traffic(key, op["roofline"]["algorithmic_bytes"])
         line["ops"] = ops
+        line["reference_shapes"] = reference_shapes(steps)
+        print("[bench] reference latency shapes done", file=sys.stderr, flush=True)
 
     # BASELINE.json config 5 (DPA4Model(fused=True) end to end at 32,768 atoms) needs a DPA4/SeZM
     # model created by DeepMD-kit and DeepMD's own DeepPot; without DeepMD there is nothing to run.
