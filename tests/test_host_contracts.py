@@ -236,6 +236,16 @@ class _OracleNative:
         return gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, self._dst(offsets, order, zonal.shape[0]),
                                                         radial_slot, inv)
 
+    def gie_rmsnorm_supported(self, n_rows, channels):
+        return channels % 4 == 0 and (n_rows + 1) * (channels // 4) <= 512
+
+    def gie_rmsnorm_forward_csr(self, zonal, radial, offsets, order, radial_slot, inv, scale, eps, keep_x=False):
+        x = gie_ref.zonal_scatter_reference(zonal, radial, self._dst(offsets, order, zonal.shape[0]), radial_slot,
+                                            inv)
+        flat = x.reshape(x.shape[0], -1)
+        y = rms_ref.rmsnorm(flat, scale if scale.numel() else None, eps).reshape(x.shape)
+        return y, (x if keep_x else None), torch.rsqrt(flat.square().mean(dim=-1) + eps)
+
     def rmsnorm_forward(self, x, scale, eps):
         weight = scale if scale.numel() else None
         inv = torch.rsqrt(x.square().mean(dim=-1) + eps).reshape(-1)
@@ -336,3 +346,25 @@ def test_gie_and_rmsnorm_autograd(fake_native):
         torch.testing.assert_close(a, b)
     out = kernels.rmsnorm(x)
     torch.testing.assert_close(out, rms_ref.rmsnorm(x))
+
+
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_fused_gie_rmsnorm_autograd(fake_native, with_scale):
+    """The fused GIE -> RMSNorm Function: forward and every gradient equal the two operators' chain."""
+    gen = torch.Generator().manual_seed(3)
+    zonal = torch.randn(6, 3, generator=gen, requires_grad=True)
+    radial = torch.randn(6, 2, 4, generator=gen, requires_grad=True)
+    dst, slots = torch.tensor([2, 0, 1, 2, 2, 0]), torch.tensor([0, 1, 1])
+    inv = (torch.rand(3, generator=gen) + 0.5).requires_grad_(True)
+    scale = (torch.rand(16, generator=gen) + 0.5).requires_grad_(True) if with_scale else None
+    out = gie_mod.gie_zonal_scatter_rmsnorm(zonal, radial, dst, slots, inv, scale=scale, eps=1e-5)
+    rows = gie_ref.zonal_scatter_reference(zonal, radial, dst, slots, inv)
+    expected = rms_ref.rmsnorm(rows.reshape(3, 16), scale, 1e-5).reshape(rows.shape)
+    torch.testing.assert_close(out, expected)
+    inputs = (zonal, radial, inv) + ((scale,) if with_scale else ())
+    g = torch.randn(out.shape, generator=gen)
+    for a, b in zip(torch.autograd.grad(out, inputs, g), torch.autograd.grad(expected, inputs, g)):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+    with torch.no_grad():  # no gradient wanted: the pre-norm rows are not kept
+        assert gie_mod.gie_zonal_scatter_rmsnorm(zonal, radial, dst, slots, inv, scale=scale, eps=1e-5).shape \
+            == rows.shape
