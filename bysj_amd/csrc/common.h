@@ -69,8 +69,41 @@ inline unsigned int blocks_for(int64_t items, int64_t per_block) {
   return static_cast<unsigned int>((items + per_block - 1) / per_block);
 }
 
-// Grid-dimension ceiling of a 1-D launch on gfx950.
-constexpr int64_t kMaxGrid = 2147483647;
+// ---------------------------------------------------------------------------
+// Host/device: grids of more blocks than one row holds
+// ---------------------------------------------------------------------------
+//
+// HIP launches fewer than 2^32 work-items along each grid dimension
+// (gridDim.x * blockDim.x < 2^32): at most 16,777,215 blocks of 256 threads
+// along x.  Kernels that take one unit of work per block (a segment, a group
+// of rows) are launched on launch_grid(blocks, threads): a 1-D grid up to that
+// limit, and beyond it rows of equal length along y.  The kernel numbers its
+// blocks with block_index(), which is blockIdx.x in a 1-D grid, and returns
+// from the few blocks of the last row that lie past its work.
+
+// Most blocks of `threads` threads along x (the hardware limit, or the lower
+// limit set with dpa4k_set_launch_row_limit).
+int64_t row_block_limit(int threads);
+
+// Grid of at least `blocks` blocks (blocks >= 1); rows.x * rows.y < blocks +
+// rows.y, so at most rows.y - 1 blocks find no work.
+inline dim3 launch_grid(int64_t blocks, int threads) {
+  const int64_t limit = row_block_limit(threads);
+  if (blocks <= limit) return dim3(static_cast<unsigned int>(blocks), 1u, 1u);
+  const int64_t rows = (blocks + limit - 1) / limit;
+  const int64_t per_row = (blocks + rows - 1) / rows;
+  return dim3(static_cast<unsigned int>(per_row), static_cast<unsigned int>(rows), 1u);
+}
+
+// Whether launch_grid() can express `blocks` (its rows are bounded like its
+// columns).
+inline bool grid_fits(int64_t blocks, int threads) {
+  return blocks / row_block_limit(threads) < 4294967295LL;
+}
+
+__device__ __forceinline__ int64_t block_index() {
+  return static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+}
 
 // ---------------------------------------------------------------------------
 // Device: XCD-aware block order

@@ -75,8 +75,10 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
     const int64_t* __restrict__ src_order, T* __restrict__ force, T* __restrict__ virial,
     int64_t n_edges, int64_t n_nodes) {
   // Neighbouring atoms gather rows from the same destination segments when
-  // atom numbering follows space, so each XCD takes a contiguous atom range.
-  const int64_t atom = static_cast<int64_t>(xcd_block(blockIdx.x, gridDim.x)) * kAtoms + (threadIdx.x >> kLogGroup);
+  // atom numbering follows space, so each XCD takes a contiguous atom range
+  // (of each grid row, when the atoms need more than one row of blocks).
+  const int64_t block = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
+  const int64_t atom = block * kAtoms + (threadIdx.x >> kLogGroup);
   if (atom >= n_nodes) return;
   const int lane = threadIdx.x & (kGroup - 1);
   int64_t dst_begin, dst_end, src_begin, src_end;
@@ -144,13 +146,13 @@ int run(const T* grad_edge, const T* edge_vec, const int64_t* dst_offsets,
   clear_error();
   if (n_edges < 0) return fail(DPA4K_EINVAL, "force assembly: negative edge count");
   if (n_nodes <= 0) return fail(DPA4K_EINVAL, "force assembly requires at least one atom");
-  if ((n_nodes + kAtoms - 1) / kAtoms > kMaxGrid)
-    return fail(DPA4K_EINVAL, "force assembly atom count exceeds the HIP grid limit");
+  if (!grid_fits((n_nodes + kAtoms - 1) / kAtoms, kBlock))
+    return fail(DPA4K_EINVAL, "force assembly atom count exceeds the launch limit");
   if (dst_offsets == nullptr || src_offsets == nullptr || force == nullptr || virial == nullptr ||
       (n_edges > 0 && (grad_edge == nullptr || edge_vec == nullptr || src_order == nullptr)))
     return fail(DPA4K_EINVAL, "force assembly: null pointer");
   hipStream_t stream = as_stream(stream_handle);
-  force_assembly_kernel<T><<<blocks_for(n_nodes, kAtoms), kBlock, 0, stream>>>(
+  force_assembly_kernel<T><<<launch_grid((n_nodes + kAtoms - 1) / kAtoms, kBlock), kBlock, 0, stream>>>(
       grad_edge, edge_vec, dst_offsets, src_offsets, src_order, force, virial, n_edges, n_nodes);
   return launched("force_assembly_kernel");
 }

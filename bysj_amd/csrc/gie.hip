@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
     float* __restrict__ out, int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
     int64_t channels, int64_t chunk_base) {
   constexpr int U = CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
-  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t node = block_index() * kWaves + (threadIdx.x >> 6);
   if (node >= n_nodes) return;
   const int lane = threadIdx.x & 63;
   const int64_t row_chunks = channels / V;
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kBlock) void gie_rmsnorm_forward_kernel(
     int64_t channels) {
   constexpr int V = 4;
   constexpr int U = CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
-  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t node = block_index() * kWaves + (threadIdx.x >> 6);
   if (node >= n_nodes) return;
   const int lane = threadIdx.x & 63;
   const int64_t row_chunks = channels / V;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
     const float* __restrict__ inv, float* __restrict__ grad_zonal, float* __restrict__ grad_radial,
     float* __restrict__ grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
     int64_t n_radial, int64_t channels) {
-  const int64_t node = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t node = block_index() * kWaves + (threadIdx.x >> 6);
   if (node >= n_nodes) return;
   const int lane = threadIdx.x & 63;
   const int64_t chunks = n_radial * RC;
@@ -371,7 +371,8 @@ __global__ __launch_bounds__(64) void gie_backward_general_kernel(
   int* slot_begin = reinterpret_cast<int*>(product + 64 * CPL * V);
   int* slot_rows = slot_begin + n_radial + 1;
 
-  const int64_t node = blockIdx.x;
+  const int64_t node = block_index();
+  if (node >= n_nodes) return;
   const int lane = threadIdx.x;
   const int64_t wc = window_chunks;
   const bool ordered = order != nullptr;
@@ -490,7 +491,7 @@ int launch_forward(int cpl, const float* zonal, const float* radial, const int64
                    const int64_t* order, const int64_t* radial_slot, const float* inv, float* out,
                    int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
                    int64_t channels, int64_t base, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kWaves);
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
 #define DPA4K_GIE_FWD(C)                                                                      \
   gie_forward_kernel<V, C, kOrdered><<<grid, kBlock, 0, stream>>>(                           \
       zonal, radial, offsets, order, radial_slot, inv, out, n_edges, n_nodes, n_rows, n_radial, \
@@ -511,7 +512,7 @@ int launch_distinct(int cpl, const float* grad_output, const float* zonal, const
                     const float* inv, float* grad_zonal, float* grad_radial, float* grad_inv,
                     int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
                     int64_t channels, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kWaves);
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
 #define DPA4K_GIE_DIST(C)                                                                     \
   gie_backward_distinct_kernel<V, C, RC, kOrdered><<<grid, kBlock, 0, stream>>>(             \
       grad_output, zonal, radial, offsets, order, radial_slot, inv, grad_zonal, grad_radial,  \
@@ -557,7 +558,7 @@ int launch_general(int cpl, size_t lds_bytes, const float* grad_output, const fl
                    int64_t n_rows, int64_t n_radial, int64_t channels, int64_t base, int64_t wc,
                    hipStream_t stream) {
 #define DPA4K_GIE_GEN(C)                                                                      \
-  gie_backward_general_kernel<V, C><<<static_cast<unsigned int>(n_nodes), 64, lds_bytes,      \
+  gie_backward_general_kernel<V, C><<<launch_grid(n_nodes, 64), 64, lds_bytes,                \
                                       stream>>>(grad_output, zonal, radial, offsets, order,   \
                                                 radial_slot, inv, grad_zonal, grad_radial,    \
                                                 grad_inv, n_edges, n_nodes, n_rows, n_radial, \
@@ -579,7 +580,7 @@ int check_shapes(int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_rad
   if (n_rows > 0 && n_radial == 0)
     return fail(DPA4K_EINVAL, "GIE radial slots are required for non-scalar rows");
   if (n_edges > 0 && n_nodes == 0) return fail(DPA4K_EINVAL, "GIE edges require destination nodes");
-  if (n_nodes > kMaxGrid) return fail(DPA4K_EINVAL, "GIE node count exceeds the HIP grid limit");
+  if (!grid_fits(n_nodes, 64)) return fail(DPA4K_EINVAL, "GIE node count exceeds the launch limit");
   return DPA4K_OK;
 }
 
@@ -790,7 +791,7 @@ int launch_gie_rmsnorm(int cpl, const float* zonal, const float* radial, const i
                        const int64_t* order, const int64_t* radial_slot, const float* inv, const float* scale,
                        float eps, float* y, float* x_out, float* inverse_rms, int64_t n_edges, int64_t n_nodes,
                        int64_t n_rows, int64_t n_radial, int64_t channels, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kWaves);
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
 #define DPA4K_GIE_RMS(C)                                                                              \
   gie_rmsnorm_forward_kernel<C, kOrdered><<<grid, kBlock, 0, stream>>>(                              \
       zonal, radial, offsets, order, radial_slot, inv, scale, eps, y, x_out, inverse_rms, n_edges, n_nodes, \

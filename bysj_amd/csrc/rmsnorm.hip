@@ -29,7 +29,7 @@ template <int V, int CPL>
 __global__ __launch_bounds__(kBlock) void rmsnorm_forward_kernel(
     const float* __restrict__ x, const float* __restrict__ scale, float* __restrict__ y,
     float* __restrict__ inverse_rms, int64_t rows, int64_t width, float eps) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t row = block_index() * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int64_t chunks = width / V;
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_backward_wide_kernel(
     const float* __restrict__ grad, const float* __restrict__ x, const float* __restrict__ scale,
     const float* __restrict__ inverse_rms, float* __restrict__ grad_x, int64_t rows,
     int64_t width) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t row = block_index() * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int64_t chunks = width / V;
@@ -274,7 +274,7 @@ int per_lane_for(int64_t chunks) {
 template <int V>
 int launch_forward(int cpl, const float* x, const float* scale, float* y, float* inverse_rms,
                    int64_t rows, int64_t width, float eps, hipStream_t stream) {
-  const unsigned int grid = blocks_for(rows, kWaves);
+  const dim3 grid = launch_grid((rows + kWaves - 1) / kWaves, kBlock);
 #define DPA4K_RMS_FWD(C)                                                                  \
   rmsnorm_forward_kernel<V, C><<<grid, kBlock, 0, stream>>>(x, scale, y, inverse_rms, rows, \
                                                             width, eps)
@@ -327,8 +327,8 @@ extern "C" int dpa4k_rmsnorm_forward(const float* x, const float* scale, float* 
   if (width <= 0) return fail(DPA4K_EINVAL, "RMSNorm feature dimension must be positive");
   if (!(eps > 0.0f) || !(eps < INFINITY))
     return fail(DPA4K_EINVAL, "RMSNorm eps must be a finite positive number");
-  if ((rows + kWaves - 1) / kWaves > kMaxGrid)
-    return fail(DPA4K_EINVAL, "RMSNorm row count exceeds the HIP grid limit");
+  if (!grid_fits((rows + kWaves - 1) / kWaves, kBlock))
+    return fail(DPA4K_EINVAL, "RMSNorm row count exceeds the launch limit");
   if (rows == 0) return DPA4K_OK;
   if (x == nullptr || y == nullptr || inverse_rms == nullptr)
     return fail(DPA4K_EINVAL, "RMSNorm: null pointer");
@@ -355,6 +355,9 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
   if (width <= 0) return fail(DPA4K_EINVAL, "RMSNorm feature dimension must be positive");
   if (grad_scale != nullptr && scale == nullptr)
     return fail(DPA4K_EINVAL, "cannot compute a scale gradient when scale is omitted");
+  // the scale gradient takes one thread per column along one grid row
+  if (grad_scale != nullptr && width > 4294967295LL / kBlock * kBlock)
+    return fail(DPA4K_EINVAL, "RMSNorm scale gradient: feature dimension exceeds the launch limit");
   hipStream_t stream = as_stream(stream_handle);
   if (rows == 0) {
     if (grad_scale != nullptr) return zero_fill(grad_scale, width * sizeof(float), stream);
@@ -367,7 +370,7 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
   const int64_t chunks = vec4 ? width / 4 : width;
   const int cpl = per_lane_for(chunks);
   if (cpl == 0) {
-    const unsigned int grid = blocks_for(rows, kWaves);
+    const dim3 grid = launch_grid((rows + kWaves - 1) / kWaves, kBlock);
     if (vec4)
       rmsnorm_backward_wide_kernel<4><<<grid, kBlock, 0, stream>>>(grad, x, scale, inverse_rms,
                                                                     grad_x, rows, width);
@@ -383,7 +386,10 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
     return DPA4K_OK;
   }
   if (grad_scale == nullptr) {
-    const unsigned int grid = blocks_for(rows, kWaves);
+    // the register kernel strides over rows: one row of blocks covers any count
+    const int64_t wanted = (rows + kWaves - 1) / kWaves;
+    const int64_t limit = row_block_limit(kBlock);
+    const unsigned int grid = static_cast<unsigned int>(wanted < limit ? wanted : limit);
     return vec4 ? launch_backward<4>(cpl, grid, grad, x, scale, inverse_rms, grad_x, nullptr, rows,
                                      width, stream)
                 : launch_backward<1>(cpl, grid, grad, x, scale, inverse_rms, grad_x, nullptr, rows,

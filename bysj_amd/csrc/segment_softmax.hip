@@ -96,6 +96,32 @@ __device__ __forceinline__ void online_add(float& peak, float& sum, float y) {
   }
 }
 
+// Compensated accumulation (Neumaier's variant of Kahan summation) for the
+// loops that run over a whole long segment in one lane.  Over millions of
+// rows a plain fp32 running sum drops the many terms far below its own
+// magnitude (each rounds away) and comes out biased low: about 5e-4 for a
+// 67M-row segment of N(0, 4) logits.  `carry` keeps what each addition
+// rounded off; the caller folds it in once, with sum + carry.
+__device__ __forceinline__ void compensated_add(float& sum, float& carry, float x) {
+  const float t = sum + x;
+  carry += fabsf(sum) >= fabsf(x) ? (sum - t) + x : (x - t) + sum;
+  sum = t;
+}
+
+// online_add with a compensated sum; a new maximum rescales both parts.
+__device__ __forceinline__ void online_add(float& peak, float& sum, float& carry, float y) {
+  if (y == -INFINITY) return;
+  if (y > peak) {
+    const float scale = peak == -INFINITY ? 0.0f : exp2_of(peak - y);
+    sum *= scale;
+    carry *= scale;
+    compensated_add(sum, carry, 1.0f);
+    peak = y;
+  } else {
+    compensated_add(sum, carry, exp2_of(y - peak));
+  }
+}
+
 // Merges (peak_b, sum_b) into (peak, sum); symmetric in its operands.
 __device__ __forceinline__ void online_merge(float& peak, float& sum, float peak_b, float sum_b) {
   const float top = fmaxf(peak, peak_b);
@@ -483,11 +509,12 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
   }
 
   // streaming: online max/sum pass, then the write pass
-  float run_sum[V];
+  float run_sum[V], carry[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     peak[v] = -INFINITY;
     run_sum[v] = 0.0f;
+    carry[v] = 0.0f;
   }
   for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
     float value[S::UNROLL][V], envelope[S::UNROLL];
@@ -495,10 +522,13 @@ __device__ void forward_long(const ForwardArgs& a, int64_t segment, int64_t begi
 #pragma unroll
     for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
-      for (int v = 0; v < V; ++v) online_add(peak[v], run_sum[v], log2_weight(value[u][v], envelope[u]));
+      for (int v = 0; v < V; ++v) online_add(peak[v], run_sum[v], carry[v], log2_weight(value[u][v], envelope[u]));
   }
 #pragma unroll
-  for (int v = 0; v < V; ++v) span_merge<LC, 64>(peak[v], run_sum[v]);
+  for (int v = 0; v < V; ++v) {
+    run_sum[v] = run_sum[v] + carry[v];
+    span_merge<LC, 64>(peak[v], run_sum[v]);
+  }
   if ((L.lane >> LOG_LC) == 0)
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -620,15 +650,16 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_kernel(ForwardArgs a, 
   using S = Geo<V, LOG_LC>;
   __shared__ float partial[kWaves][2][S::LC * V];
   constexpr bool planned = kPlanned;
-  if (planned && static_cast<int64_t>(blockIdx.x) < n_long) {
-    const int64_t segment = plan[kPlanHeader + blockIdx.x];
+  const int64_t block = block_index();
+  if (planned && block < n_long) {
+    const int64_t segment = plan[kPlanHeader + block];
     if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
     int64_t begin, end;
     segment_bounds(a.offsets, segment, a.n_edges, begin, end);
     forward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
     return;
   }
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
+  const int64_t first = (block - (planned ? n_long : 0)) * S::SPB;
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t segment = first + gidx;
   {
@@ -806,17 +837,20 @@ __device__ void backward_long(const BackwardArgs& a, int64_t segment, int64_t be
     }
     backward_rows<V, LOG_LC>(a, L, t, column, xs, gs, expect, envs);
   } else {
-    // streaming: the dot-product pass, then the gradient pass
+    // streaming: the dot-product pass (compensated), then the gradient pass
+    float carry[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) carry[v] = 0.0f;
     for (int64_t base = begin; base < end; base += S::UNROLL * PB) {
       float x[S::UNROLL][V], g[S::UNROLL][V], envs[S::UNROLL];
       backward_tiles<V, S::UNROLL, PB, kOrdered>(a, base, end, base, L.pb, L.live, column, x, g, envs);
 #pragma unroll
       for (int u = 0; u < S::UNROLL; ++u)
 #pragma unroll
-        for (int v = 0; v < V; ++v) expect[v] = expect[v] + x[u][v] * g[u][v];
+        for (int v = 0; v < V; ++v) compensated_add(expect[v], carry[v], x[u][v] * g[u][v]);
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v]);
+    for (int v = 0; v < V; ++v) expect[v] = span_sum<LC, 64>(expect[v] + carry[v]);
     if ((L.lane >> LOG_LC) == 0)
 #pragma unroll
       for (int v = 0; v < V; ++v) partial[L.wave][0][L.k * V + v] = expect[v];
@@ -889,15 +923,16 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
   using S = Geo<V, LOG_LC, true>;
   __shared__ float partial[kWaves][2][S::LC * V];
   constexpr bool planned = kPlanned;
-  if (planned && static_cast<int64_t>(blockIdx.x) < n_long) {
-    const int64_t segment = plan[kPlanHeader + blockIdx.x];
+  const int64_t block = block_index();
+  if (planned && block < n_long) {
+    const int64_t segment = plan[kPlanHeader + block];
     if (static_cast<uint64_t>(segment) >= static_cast<uint64_t>(a.n_nodes)) return;
     int64_t begin, end;
     segment_bounds(a.offsets, segment, a.n_edges, begin, end);
     backward_long<V, LOG_LC, kNull, kOrdered>(a, segment, begin, end, partial);
     return;
   }
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) - (planned ? n_long : 0)) * S::SPB;
+  const int64_t first = (block - (planned ? n_long : 0)) * S::SPB;
   const int gidx = threadIdx.x >> S::LOG_G;
   const int64_t segment = first + gidx;
   {
@@ -927,24 +962,24 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_kernel(BackwardArgs a
 
 template <bool kOrdered>
 __global__ __launch_bounds__(kBlock) void softmax_forward_wide_kernel(ForwardArgs a) {
-  const int64_t segment = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t segment = block_index() * kWaves + (threadIdx.x >> 6);
   if (segment >= a.n_nodes) return;
   const int lane = threadIdx.x & 63;
   const int64_t channels = a.channels;
   int64_t begin, end;
   segment_bounds(a.offsets, segment, a.n_edges, begin, end);
   for (int64_t c = lane; c < channels; c += 64) {
-    float peak = -INFINITY, sum = 0.0f;
+    float peak = -INFINITY, sum = 0.0f, carry = 0.0f;
     for (int64_t slot = begin; slot < end; ++slot) {
       const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-      if (e >= 0) online_add(peak, sum, log2_weight(a.logit[e * channels + c], a.env[e]));
+      if (e >= 0) online_add(peak, sum, carry, log2_weight(a.logit[e * channels + c], a.env[e]));
     }
     float null_value = -INFINITY;
     if (a.null_logit != nullptr) {
       null_value = a.null_logit[segment * channels + c] * kLog2e;
-      online_add(peak, sum, null_value);
+      online_add(peak, sum, carry, null_value);
     }
-    const float inverse = inverse_total(sum);
+    const float inverse = inverse_total(sum + carry);
     for (int64_t slot = begin; slot < end; ++slot) {
       const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e < 0) continue;
@@ -956,7 +991,7 @@ __global__ __launch_bounds__(kBlock) void softmax_forward_wide_kernel(ForwardArg
 
 template <bool kOrdered>
 __global__ __launch_bounds__(kBlock) void softmax_backward_wide_kernel(BackwardArgs a) {
-  const int64_t segment = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  const int64_t segment = block_index() * kWaves + (threadIdx.x >> 6);
   if (segment >= a.n_nodes) return;
   const int lane = threadIdx.x & 63;
   const int64_t channels = a.channels;
@@ -969,14 +1004,15 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_wide_kernel(BackwardA
     const int64_t c = base + lane;
     const bool live = c < channels;
     const bool last = base + 64 >= channels;
-    float expect = 0.0f;
+    float expect = 0.0f, carry = 0.0f;
     if (live)
       for (int64_t slot = begin; slot < end; ++slot) {
         const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
-        if (e >= 0) expect = expect + a.alpha[e * channels + c] * a.grad_alpha[e * channels + c];
+        if (e >= 0) compensated_add(expect, carry, a.alpha[e * channels + c] * a.grad_alpha[e * channels + c]);
       }
     if (has_null && live)
-      expect = expect + a.null_alpha[segment * channels + c] * a.grad_null_alpha[segment * channels + c];
+      compensated_add(expect, carry, a.null_alpha[segment * channels + c] * a.grad_null_alpha[segment * channels + c]);
+    expect = expect + carry;
     for (int64_t slot = begin; slot < end; ++slot) {
       const int64_t e = edge_of<kOrdered>(a.order, slot, a.n_edges);
       if (e < 0) continue;
@@ -1031,12 +1067,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(const int64_t*
                                                                   int64_t n_nodes, int64_t n_edges,
                                                                   int64_t capacity, int64_t* __restrict__ counts) {
   __shared__ int64_t lds[kPlanThreads];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
+  const int64_t tile = block_index();
+  if (tile * kPlanTile >= n_nodes) return;
+  const int64_t base = tile * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
   int64_t count = 0;
   for (int i = 0; i < kPlanItems; ++i)
     if (base + i < n_nodes && is_long(offsets, base + i, n_edges, capacity)) ++count;
   const int64_t inclusive = plan_block_scan(count, lds);
-  if (threadIdx.x == kPlanThreads - 1) counts[blockIdx.x] = inclusive;
+  if (threadIdx.x == kPlanThreads - 1) counts[tile] = inclusive;
 }
 
 // Exclusive scan of the tile counts in place (one workgroup); writes the
@@ -1068,7 +1106,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_write_kernel(const int64_t*
                                                                   const int64_t* __restrict__ tile_prefix,
                                                                   int64_t* __restrict__ list) {
   __shared__ int64_t lds[kPlanThreads];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
+  const int64_t tile = block_index();
+  if (tile * kPlanTile >= n_nodes) return;
+  const int64_t base = tile * kPlanTile + static_cast<int64_t>(threadIdx.x) * kPlanItems;
   bool flag[kPlanItems];
   int64_t count = 0;
 #pragma unroll
@@ -1077,7 +1117,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_write_kernel(const int64_t*
     count += flag[i] ? 1 : 0;
   }
   const int64_t inclusive = plan_block_scan(count, lds);
-  int64_t position = tile_prefix[blockIdx.x] + inclusive - count;
+  int64_t position = tile_prefix[tile] + inclusive - count;
 #pragma unroll
   for (int i = 0; i < kPlanItems; ++i)
     if (flag[i]) list[position++] = base + i;
@@ -1103,17 +1143,18 @@ int64_t capacity_for(int64_t channels, bool vec4) {
   return short_capacity(vec4 ? 4 : 1, 1 << lanes_log_for(chunks));
 }
 
-unsigned int short_blocks(int64_t n_nodes, int v, int log_lc, bool backward) {
-  return blocks_for(n_nodes, kBlock >> short_group_log(v, log_lc, backward));
+int64_t short_blocks(int64_t n_nodes, int v, int log_lc, bool backward) {
+  const int64_t per_block = kBlock >> short_group_log(v, log_lc, backward);
+  return (n_nodes + per_block - 1) / per_block;
 }
 
 template <int V, int LOG_LC>
 int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, false);
+  const dim3 grid = launch_grid((plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, false), kBlock);
 #define DPA4K_SOFTMAX_FWD(NULLV, ORD)                                                                      \
   (plan != nullptr                                                                                        \
        ? softmax_forward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
-       : softmax_forward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<static_cast<unsigned int>(grid), kBlock, 0, \
+       : softmax_forward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<grid, kBlock, 0, \
                                                                  stream>>>(a, plan, n_long)
   if (a.null_logit != nullptr) {
     if (a.order != nullptr) DPA4K_SOFTMAX_FWD(true, true); else DPA4K_SOFTMAX_FWD(true, false);
@@ -1126,11 +1167,11 @@ int launch_forward(const ForwardArgs& a, const int64_t* plan, int64_t n_long, hi
 
 template <int V, int LOG_LC>
 int launch_backward(const BackwardArgs& a, const int64_t* plan, int64_t n_long, hipStream_t stream) {
-  const int64_t grid = (plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, true);
+  const dim3 grid = launch_grid((plan != nullptr ? n_long : 0) + short_blocks(a.n_nodes, V, LOG_LC, true), kBlock);
 #define DPA4K_SOFTMAX_BWD(NULLV, ORD)                                                                       \
   (plan != nullptr                                                                                         \
        ? softmax_backward_kernel<V, LOG_LC, NULLV, ORD, true>                                               \
-       : softmax_backward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<static_cast<unsigned int>(grid), kBlock, 0, \
+       : softmax_backward_kernel<V, LOG_LC, NULLV, ORD, false>)<<<grid, kBlock, 0, \
                                                                   stream>>>(a, plan, n_long)
   if (a.null_alpha != nullptr) {
     if (a.order != nullptr) DPA4K_SOFTMAX_BWD(true, true); else DPA4K_SOFTMAX_BWD(true, false);
@@ -1170,7 +1211,7 @@ int dispatch_backward(int log_lc, const Args& a, const int64_t* list, int64_t n_
 int check_common(int64_t n_edges, int64_t n_nodes, int64_t channels, const char* what) {
   if (n_edges < 0 || n_nodes < 0) return fail(DPA4K_EINVAL, "%s: negative sizes", what);
   if (channels <= 0) return fail(DPA4K_EINVAL, "%s requires at least one channel", what);
-  if (n_nodes > kMaxGrid) return fail(DPA4K_EINVAL, "%s: segment count too large", what);
+  if (!grid_fits(n_nodes, kBlock)) return fail(DPA4K_EINVAL, "%s: segment count too large", what);
   return DPA4K_OK;
 }
 
@@ -1192,7 +1233,7 @@ int softmax_forward(const float* logit, const float* env, const int64_t* offsets
   const int64_t chunks = vec4 ? channels / 4 : channels;
   const ForwardArgs a{logit, env, offsets, null_logit, order, alpha, null_alpha, n_edges, n_nodes, channels};
   if (chunks > 64) {
-    const unsigned int grid = blocks_for(n_nodes, kWaves);
+    const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
     if (order != nullptr) softmax_forward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(a);
     else softmax_forward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_forward_wide_kernel");
@@ -1229,7 +1270,7 @@ int softmax_backward(const float* alpha, const float* grad_alpha, const float* e
   const BackwardArgs a{alpha, grad_alpha, env, offsets, null_alpha, grad_null_alpha, order,
                        grad_logit, grad_null_logit, grad_env, n_edges, n_nodes, channels};
   if (chunks > 64) {
-    const unsigned int grid = blocks_for(n_nodes, kWaves);
+    const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
     if (order != nullptr) softmax_backward_wide_kernel<true><<<grid, kBlock, 0, stream>>>(a);
     else softmax_backward_wide_kernel<false><<<grid, kBlock, 0, stream>>>(a);
     return launched("softmax_backward_wide_kernel");
@@ -1289,14 +1330,14 @@ extern "C" int dpa4k_segment_softmax_plan(const int64_t* offsets, int64_t n_edge
   const int64_t tiles = plan_tiles(n_nodes);
   int64_t* counts = words + kPlanHeader + n_nodes;
   if (tiles > 0) {
-    plan_count_kernel<<<static_cast<unsigned int>(tiles), kPlanThreads, 0, stream>>>(offsets, n_nodes, n_edges,
+    plan_count_kernel<<<launch_grid(tiles, kPlanThreads), kPlanThreads, 0, stream>>>(offsets, n_nodes, n_edges,
                                                                                      capacity, counts);
     if (int s = launched("plan_count_kernel")) return s;
   }
   plan_scan_kernel<<<1, kPlanThreads, 0, stream>>>(counts, tiles, capacity, words);
   if (int s = launched("plan_scan_kernel")) return s;
   if (tiles > 0) {
-    plan_write_kernel<<<static_cast<unsigned int>(tiles), kPlanThreads, 0, stream>>>(
+    plan_write_kernel<<<launch_grid(tiles, kPlanThreads), kPlanThreads, 0, stream>>>(
         offsets, n_nodes, n_edges, capacity, counts, words + kPlanHeader);
     if (int s = launched("plan_write_kernel")) return s;
   }

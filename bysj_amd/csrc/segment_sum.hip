@@ -33,7 +33,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
     const int64_t* __restrict__ order, float* __restrict__ out, int64_t n_edges, int64_t n_nodes,
     int64_t channels, int64_t chunk_base) {
   constexpr int kSegments = kBlock / G;
-  const int64_t segment = static_cast<int64_t>(blockIdx.x) * kSegments + threadIdx.x / G;
+  const int64_t segment = block_index() * kSegments + threadIdx.x / G;
   if (segment >= n_nodes) return;
   const int lane = threadIdx.x % G;
   const int64_t chunks = channels / V;
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_kernel(
     float* __restrict__ grad_node_scale, int64_t n_edges, int64_t n_nodes, int64_t channels,
     int64_t chunk_base, int accumulate) {
   constexpr int kSegments = kBlock / G;
-  const int64_t segment = static_cast<int64_t>(blockIdx.x) * kSegments + threadIdx.x / G;
+  const int64_t segment = block_index() * kSegments + threadIdx.x / G;
   if (segment >= n_nodes) return;
   const int lane = threadIdx.x % G;
   const int64_t chunks = channels / V;
@@ -240,7 +240,8 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
   constexpr int kAhead = 8;
   __shared__ fvec<4> stage[kStageChunks];
   __shared__ float weight[kStageChunks / 16 + kAhead];  // rows per batch (chunks >= 16), padded
-  const int64_t segment = blockIdx.x;
+  const int64_t segment = block_index();
+  if (segment >= n_nodes) return;
   const int chunks = static_cast<int>(channels / 4);
   const int width = chunks * 4;
   const int rows_per_batch = kStageChunks / chunks;
@@ -309,7 +310,8 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_wide_kernel(
     float* __restrict__ grad_node_scale, int64_t n_edges, int64_t n_nodes, int64_t channels) {
   constexpr int SG = kBlock / G;
   __shared__ float partial[SG];
-  const int64_t segment = blockIdx.x;
+  const int64_t segment = block_index();
+  if (segment >= n_nodes) return;
   const int lane = threadIdx.x % G;
   const int group = threadIdx.x / G;
   const int chunks = static_cast<int>(channels / 4);
@@ -388,7 +390,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_wide_kernel(
 int launch_staged_forward(const float* src, const int64_t* offsets, const float* edge_scale,
                           const float* node_scale, const int64_t* order, float* out, int64_t n_edges,
                           int64_t n_nodes, int64_t channels, hipStream_t stream) {
-  const unsigned int grid = static_cast<unsigned int>(n_nodes);
+  const dim3 grid = launch_grid(n_nodes, kBlock);
 #define DPA4K_SUM_STAGED(SCALE, ORD)                                                                  \
   segment_sum_staged_kernel<SCALE, ORD><<<grid, kBlock, 0, stream>>>(src, offsets, edge_scale, node_scale, \
                                                                       order, out, n_edges, n_nodes, channels)
@@ -407,7 +409,7 @@ int launch_wide_backward_g(const float* grad_out, const float* src, const int64_
                            float* grad_src, float* grad_edge_scale, float* grad_node_scale, int64_t n_edges,
                            int64_t n_nodes, int64_t channels, hipStream_t stream) {
   constexpr int U = 8;
-  const unsigned int grid = static_cast<unsigned int>(n_nodes);
+  const dim3 grid = launch_grid(n_nodes, kBlock);
   if (order != nullptr)
     segment_sum_backward_wide_kernel<G, U, true><<<grid, kBlock, 0, stream>>>(
         grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
@@ -473,7 +475,7 @@ template <int V, int G, int CPL, int U>
 int launch_forward_u(const float* src, const int64_t* offsets, const float* edge_scale,
                      const float* node_scale, const int64_t* order, float* out, int64_t n_edges,
                      int64_t n_nodes, int64_t channels, int64_t chunk_base, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kBlock / G);
+  const dim3 grid = launch_grid((n_nodes + kBlock / G - 1) / (kBlock / G), kBlock);
 #define DPA4K_SUM_FWD(SCALE, ORD)                                                                     \
   segment_sum_forward_kernel<V, G, CPL, U, SCALE, ORD><<<grid, kBlock, 0, stream>>>(                \
       src, offsets, edge_scale, node_scale, order, out, n_edges, n_nodes, channels, chunk_base)
@@ -507,7 +509,7 @@ int launch_backward_u(const float* grad_out, const float* src, const int64_t* of
                       float* grad_src, float* grad_edge_scale, float* grad_node_scale,
                       int64_t n_edges, int64_t n_nodes, int64_t channels, int64_t chunk_base,
                       int accumulate, hipStream_t stream) {
-  const unsigned int grid = blocks_for(n_nodes, kBlock / G);
+  const dim3 grid = launch_grid((n_nodes + kBlock / G - 1) / (kBlock / G), kBlock);
   if (order != nullptr)
     segment_sum_backward_kernel<V, G, CPL, U, true><<<grid, kBlock, 0, stream>>>(
         grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale,
@@ -570,7 +572,7 @@ struct BackwardLauncher {
 int check_common(int64_t n_edges, int64_t n_nodes, int64_t channels, const char* what) {
   if (n_edges < 0 || n_nodes < 0) return fail(DPA4K_EINVAL, "%s: negative sizes", what);
   if (channels <= 0) return fail(DPA4K_EINVAL, "%s requires at least one channel", what);
-  if ((n_nodes + 3) / 4 > kMaxGrid * 64) return fail(DPA4K_EINVAL, "%s: segment count too large", what);
+  if (!grid_fits(n_nodes, kBlock)) return fail(DPA4K_EINVAL, "%s: segment count too large", what);
   return DPA4K_OK;
 }
 

@@ -1,4 +1,5 @@
 // Error plumbing of the C ABI: status codes plus a thread-local message.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -49,7 +50,25 @@ int zero_fill(void* pointer, size_t bytes, hipStream_t stream) {
   return launched("zero_fill_kernel");
 }
 
+namespace {
+// 0: the hardware limit.  Only dpa4k_set_launch_row_limit changes it.
+std::atomic<int64_t> g_row_limit{0};
+}  // namespace
+
+int64_t row_block_limit(int threads) {
+  const int64_t hardware = 4294967295LL / threads;
+  const int64_t lowered = g_row_limit.load(std::memory_order_relaxed);
+  return lowered > 0 && lowered < hardware ? lowered : hardware;
+}
+
 }  // namespace dpa4k
+
+extern "C" int dpa4k_set_launch_row_limit(int64_t blocks) {
+  dpa4k::clear_error();
+  if (blocks < 0) return dpa4k::fail(DPA4K_EINVAL, "launch row limit must be non-negative");
+  dpa4k::g_row_limit.store(blocks, std::memory_order_relaxed);
+  return DPA4K_OK;
+}
 
 extern "C" const char* dpa4k_last_error(void) { return dpa4k::g_message; }
 

@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -65,6 +65,7 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_rmsnorm_backward_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_rmsnorm_backward": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
     "dpa4k_stream_calibrate": (_INT, [_P, _I64, _P, _I64, _P]),
+    "dpa4k_set_launch_row_limit": (_INT, [_I64]),
 }
 
 _LOCK = threading.Lock()

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 3
+#define DPA4K_ABI_VERSION 4
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -343,6 +343,18 @@ int dpa4k_rmsnorm_backward(const float* grad, const float* x,
  * to report the read and copy ceilings of the part beside each roofline. */
 int dpa4k_stream_calibrate(const float* src, int64_t read_floats, float* dst,
                            int64_t write_floats, dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Launch shape (testing aid; no reference counterpart)
+ * ---------------------------------------------------------------------- */
+
+/* HIP launches fewer than 2^32 work-items along each grid dimension, so a
+ * launch that needs more blocks than one row holds (16,777,215 blocks of 256
+ * threads) continues in rows along y.  This lowers the blocks per row to
+ * `blocks` (0 restores the hardware limit) for every later launch in the
+ * process, so that tests reach the multi-row grids at small sizes.  Results
+ * do not depend on it.  Not meant to be changed while other threads launch. */
+int dpa4k_set_launch_row_limit(int64_t blocks);
 
 #ifdef __cplusplus
 }

@@ -86,6 +86,12 @@ def test_invalid_sizes_fail_before_any_device_call():
         (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (1, 4, ctypes.c_float(0.0), null), "eps"),
         (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 0, null), ""),
         (lib.dpa4k_force_assembly_f64, (null,) * 7 + (-1, 1, null), ""),
+        # beyond what rows of blocks along y can hold
+        (lib.dpa4k_segment_sum_forward, (null,) * 6 + (1, 2**62, 1, null), "segment count too large"),
+        (lib.dpa4k_segment_softmax_forward, (null,) * 7 + (1, 2**62, 8, null), "segment count too large"),
+        (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (2**62, 4, ctypes.c_float(1e-6), null), "launch limit"),
+        (lib.dpa4k_gie_zonal_scatter_forward_csr, (null,) * 7 + (0, 2**62, 0, 0, 4, null), "launch limit"),
+        (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 2**62, null), "launch limit"),
     ]
     for function, args, fragment in cases:
         status = function(*args)
@@ -110,3 +116,21 @@ def test_package_imports_under_the_reference_names():
         "zonal_scatter",
     ]
     assert module == "kernels._C"
+
+
+def test_launch_row_limit_hook():
+    binding = _lib()
+    lib = binding.load()
+    assert lib.dpa4k_set_launch_row_limit(-1) == binding.EINVAL
+    assert "non-negative" in lib.dpa4k_last_error().decode()
+    args = (None,) * 6 + (1, 2**40, 1, None)
+    # 2^40 segments fit in 65,536 rows of the hardware limit (the call then stops at its null pointers) ...
+    assert lib.dpa4k_segment_sum_forward(*args) == binding.EINVAL
+    assert "null pointer" in lib.dpa4k_last_error().decode()
+    # ... but not in rows of 3 blocks
+    assert lib.dpa4k_set_launch_row_limit(3) == binding.OK
+    try:
+        assert lib.dpa4k_segment_sum_forward(*args) == binding.EINVAL
+        assert "segment count too large" in lib.dpa4k_last_error().decode()
+    finally:
+        assert lib.dpa4k_set_launch_row_limit(0) == binding.OK
