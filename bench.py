@@ -545,6 +545,18 @@ def op_line(name: str, job: dict, unit_count: int, unit: str = "edges/s") -> dic
 # CPU baselines (the oracle on the host cores)
 # ---------------------------------------------------------------------------
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name"), read from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as info:
+            for row in info:
+                if row.startswith("model name"):
+                    return row.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baselines(softmax_case, seconds: float, extra_ops: dict | None) -> tuple[dict, dict]:
     import torch
 
@@ -553,15 +565,24 @@ def cpu_baselines(softmax_case, seconds: float, extra_ops: dict | None) -> tuple
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in softmax_case.items()}
-    per_call, samples = cpu_time(
-        lambda: ref.segment_softmax_reference(c["logit"], c["env"], c["dst"], c["offsets"], c["null_logit"]),
-        seconds,
-    )
+
+    def oracle():
+        return ref.segment_softmax_reference(c["logit"], c["env"], c["dst"], c["offsets"], c["null_logit"])
+
+    per_call, samples = cpu_time(oracle, seconds)
     edges = int(c["logit"].shape[0])
     headline = {"value": round(edges / per_call, 1), "unit": "edges/s", "cores": threads, "kind": "port",
                 "sample": f"config 2 full input (E={edges}, C=8, null logit); median of {samples} calls of the "
                           f"oracle ATen chain (torch CPU, {threads} threads)",
-                "ms_per_call": round(per_call * 1e3, 3)}
+                "ms_per_call": round(per_call * 1e3, 3), "cpu_model": cpu_model()}
+    # the same chain on one core
+    torch.set_num_threads(1)
+    try:
+        per_one, samples_one = cpu_time(oracle, min(seconds, 6.0))
+    finally:
+        torch.set_num_threads(threads)
+    headline["single_thread"] = {"value": round(edges / per_one, 1), "ms_per_call": round(per_one * 1e3, 3),
+                                 "calls": samples_one}
     extras = {}
     if extra_ops:
         for name, (function, count, description) in extra_ops.items():
