@@ -3,14 +3,17 @@
 Public surface of python/kernels/gie.py in the reference: ``zonal_scatter``,
 its alias ``gie_zonal_scatter`` and ``gie_available``, with the same
 validation.  The forward groups the (possibly unsorted) ``dst`` into a
-destination CSR on the device once and keeps it for the backward, so neither
-pass uses atomics.  Out-of-range ``dst`` or ``radial_slot`` values raise
+destination CSR on the device and keeps it for the backward, so neither pass
+uses atomics; the grouping is cached per ``dst`` tensor, so later calls on
+the same graph skip it.  Out-of-range ``dst`` or ``radial_slot`` values raise
 ``ValueError`` instead of being read out of bounds.
 
 ``gie_zonal_scatter_rmsnorm`` (an extension, not in ``__all__``) fuses the
 scatter with the RMSNorm that follows it over each node's flattened row.
 """
 from __future__ import annotations
+
+import weakref
 
 import torch
 
@@ -54,6 +57,68 @@ def _validate(zonal, radial, dst, radial_slot, inv_sqrt_deg):
         raise ValueError("all GIE inputs must share a device")
 
 
+def _capturing(tensor: torch.Tensor) -> bool:
+    return tensor.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+class _GroupingCache:
+    """Destination CSRs of live ``dst`` tensors, so that a graph is grouped once.
+
+    Grouping costs a pass over ``dst`` (and a sort when it is unsorted) plus a
+    host synchronisation that reports out-of-range indices.  An entry belongs
+    to the ``dst`` tensor object and, within it, to the ``radial_slot`` tensor
+    object (whose values decide the slot checks and the backward kernel); it
+    is dropped when ``dst`` is freed and rebuilt when either tensor's storage
+    or version counter (an in-place write) changes, or the node or slot count
+    does.  A few ``radial_slot`` objects are kept per ``dst``.  Grouping
+    synchronises, so under HIP graph capture only a cached grouping can be
+    used: run the operator once on the same tensors before capturing it.
+    """
+
+    SLOTS_PER_DST = 4
+
+    def __init__(self):
+        self._entries: dict[int, tuple] = {}
+
+    @staticmethod
+    def _stamp(tensor: torch.Tensor) -> tuple:
+        return (tensor.data_ptr(), tensor._version, tensor.numel(), tensor.device)
+
+    def get(self, native, dst, radial_slot, n_nodes: int, n_radial: int):
+        key = id(dst)
+        stamp = self._stamp(dst) + (n_nodes,)
+        entry = self._entries.get(key)
+        if entry is not None and (entry[0]() is not dst or entry[1] != stamp):
+            entry = None
+        groupings = entry[2] if entry is not None else {}
+        slot_key = (id(radial_slot), n_radial)
+        found = groupings.get(slot_key)
+        if found is not None and found[0]() is radial_slot and found[1] == self._stamp(radial_slot):
+            return found[2]
+        if _capturing(dst):
+            raise RuntimeError("GIE: this dst has no cached grouping, and grouping synchronises; "
+                               "run the operator once on the same tensors before HIP graph capture")
+        grouping = native.gie_group(dst, radial_slot, n_nodes, n_radial)
+        if entry is None:
+            reference = weakref.ref(dst, lambda _, key=key: self._entries.pop(key, None))
+            entry = (reference, stamp, groupings)
+            self._entries[key] = entry
+        groupings.pop(slot_key, None)
+        groupings[slot_key] = (weakref.ref(radial_slot), self._stamp(radial_slot), grouping)
+        while len(groupings) > self.SLOTS_PER_DST:
+            groupings.pop(next(iter(groupings)))
+        return grouping
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+
+_GROUPINGS = _GroupingCache()
+
+
 class _GIEZonalScatterFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, zonal, radial, dst, radial_slot, inv_sqrt_deg):
@@ -64,7 +129,7 @@ class _GIEZonalScatterFunction(torch.autograd.Function):
         if ctx.empty:
             ctx.save_for_backward(zonal, radial, dst, radial_slot, inv_sqrt_deg)
             return torch.zeros((n_nodes, n_rows + 1, channels), dtype=torch.float32, device=zonal.device)
-        offsets, order, info = native.gie_group(dst, radial_slot, n_nodes, n_radial)
+        offsets, order, info = _GROUPINGS.get(native, dst, radial_slot, n_nodes, n_radial)
         out = native.gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg)
         ctx.slots_distinct = bool(info & 2)
         ctx.has_order = order is not None
@@ -121,7 +186,7 @@ class _GIERMSNormFunction(torch.autograd.Function):
     def forward(ctx, zonal, radial, dst, radial_slot, inv_sqrt_deg, scale, eps):
         native = _extension("gie_zonal_scatter_forward")
         n_nodes, n_radial = int(inv_sqrt_deg.shape[0]), int(radial.shape[1])
-        offsets, order, info = native.gie_group(dst, radial_slot, n_nodes, n_radial)
+        offsets, order, info = _GROUPINGS.get(native, dst, radial_slot, n_nodes, n_radial)
         keep_x = any(ctx.needs_input_grad)
         y, x, inverse_rms = native.gie_rmsnorm_forward_csr(zonal, radial, offsets, order, radial_slot,
                                                           inv_sqrt_deg, scale, eps, keep_x)

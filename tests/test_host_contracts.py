@@ -16,6 +16,8 @@ test_rmsnorm.py:107-232, test_native_package.py:25-43):
 """
 from __future__ import annotations
 
+import gc
+
 import importlib
 from types import SimpleNamespace
 from unittest.mock import patch
@@ -346,6 +348,55 @@ def test_gie_and_rmsnorm_autograd(fake_native):
         torch.testing.assert_close(a, b)
     out = kernels.rmsnorm(x)
     torch.testing.assert_close(out, rms_ref.rmsnorm(x))
+
+
+def test_gie_grouping_is_cached_per_dst(fake_native):
+    """One grouping per live dst object; in-place writes, new slot tensors and freeing invalidate it."""
+    calls = []
+    group = fake_native.gie_group
+
+    def counting(*args):
+        calls.append(args[2])
+        return group(*args)
+
+    fake_native.gie_group = counting
+    gie_mod._GROUPINGS.clear()
+    gen = torch.Generator().manual_seed(4)
+    zonal, radial = torch.randn(5, 3, generator=gen), torch.randn(5, 2, 4, generator=gen)
+    dst, slots = torch.tensor([2, 0, 1, 2, 0]), torch.tensor([0, 1, 1])
+    inv = torch.rand(3, generator=gen) + 0.5
+    first = kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+    again = kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+    assert len(calls) == 1
+    torch.testing.assert_close(again, first)
+    gie_mod.gie_zonal_scatter_rmsnorm(zonal, radial, dst, slots, inv)
+    assert len(calls) == 1, "the fused operator shares the cache"
+    dst.copy_(torch.tensor([0, 0, 1, 2, 2]))  # in place: the version counter moves
+    moved = kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+    assert len(calls) == 2
+    torch.testing.assert_close(moved, gie_ref.zonal_scatter_reference(zonal, radial, dst, slots, inv))
+    kernels.zonal_scatter(zonal, radial, dst, slots.clone(), inv)
+    assert len(calls) == 3, "another radial_slot object is grouped again"
+    kernels.zonal_scatter(zonal, radial, dst, slots, torch.rand(4, generator=gen))
+    assert len(calls) == 4, "another node count is grouped again"
+    assert len(gie_mod._GROUPINGS) == 1
+    gie_mod.require_dcu.reset_mock()  # the stand-in gate keeps its call arguments
+    del dst
+    gc.collect()
+    assert len(gie_mod._GROUPINGS) == 0, "freeing dst drops its entry"
+
+
+def test_gie_grouping_is_not_built_under_graph_capture(fake_native):
+    """Grouping synchronises: under capture only a cached one is used, else a clear error."""
+    gie_mod._GROUPINGS.clear()
+    zonal, radial = torch.rand(3, 1), torch.rand(3, 1, 4)
+    dst, slots, inv = torch.tensor([1, 0, 1]), torch.tensor([0]), torch.rand(2)
+    with patch.object(gie_mod, "_capturing", return_value=True):
+        with pytest.raises(RuntimeError, match="before HIP graph capture"):
+            kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+    eager = kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+    with patch.object(gie_mod, "_capturing", return_value=True):
+        torch.testing.assert_close(kernels.zonal_scatter(zonal, radial, dst, slots, inv), eager)
 
 
 @pytest.mark.parametrize("with_scale", [False, True])
