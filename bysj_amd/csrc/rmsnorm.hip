@@ -36,18 +36,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_forward_kernel(
   const float* xr = x + row * width;
   float* yr = y + row * width;
   if constexpr (CPL > 0) {
-    // the row and the scale chunks are loaded before the reduction
+    // The row and the scale chunks are loaded before the reduction, through
+    // views (zeros past the row), so that no load sits in a branch: a load in
+    // a divergent branch is waited for before the branch closes, and the
+    // chunk loads would follow one another instead of overlapping.
+    const BufferView row_x = buffer_view(x + uniform_i64(row) * width, width * 4);
+    const BufferView row_s = buffer_view(scale, scale != nullptr ? width * 4 : 0);
     fvec<V> value[CPL], s[CPL];
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int64_t q = lane + 64 * j;
-#pragma unroll
-      for (int i = 0; i < V; ++i) value[j].v[i] = s[j].v[i] = 0.0f;
-      if (q < chunks) {
-        value[j] = load_vec<V>(xr + q * V);
-        if (scale != nullptr) s[j] = load_vec<V>(scale + q * V);
-      }
+      const uint32_t offset = static_cast<uint32_t>(lane + 64 * j) * (V * 4u);
+      value[j] = buffer_load_vec<V>(row_x, offset);
+      s[j] = buffer_load_vec<V>(row_s, offset);
     }
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
