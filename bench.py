@@ -466,7 +466,7 @@ def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
 
 
 def reference_shapes(steps: int) -> dict:
-    """The reference's own latency-test shape, timed like its harness and as a kernel.
+    """The reference's own latency-test shapes, timed like its harnesses and as kernels.
 
     tests/csrc/latency/test_segment_ops_latency.py of the reference: 3,000 atoms, 181,838 edges,
     dst = sorted uniform draws, env ~ U(0.1, 1.1), logits/null logits ~ N(0, 1) at 64 and 256
@@ -526,8 +526,31 @@ def reference_shapes(steps: int) -> dict:
             out[f"segment_sum_C{channels}"] = {"eager_ms": round(median_eager(call), 4),
                                                "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
                                                "dcu_ms": None, "source": "not published by the reference"}
+        # tests/csrc/latency/test_rmsnorm_latency.py: 20 warmup calls, 7 repeats of 100 calls between
+        # events, median and p95 of the per-call time, scale of ones; no figure is published
+        for rows, width in ((1, 128), (32, 256), (128, 512), (512, 1024)):
+            x = torch.randn(rows, width, generator=generator, device="cuda")
+            scale = torch.ones(width, device="cuda")
+            call = lambda _=None, x=x, scale=scale: kernels.rmsnorm(x, scale)
+            for _ in range(20):
+                call()
+            torch.cuda.synchronize()
+            samples = []
+            for _ in range(7):
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(100):
+                    call()
+                stop.record()
+                stop.synchronize()
+                samples.append(start.elapsed_time(stop) / 100 * 1e3)
+            samples.sort()
+            out[f"rmsnorm_{rows}x{width}"] = {
+                "eager_median_us": round(samples[3], 2), "eager_p95_us": round(samples[min(6, int(0.95 * 7))], 2),
+                "kernel_us": round(time_steps(call, 1, steps, 10) * 1e3, 2),
+                "dcu_ms": None, "source": "tests/csrc/latency/test_rmsnorm_latency.py (no figure published)"}
     out["note"] = ("same inputs every call, as in the reference's harness, so they stay in the Infinity Cache; "
-                   "eager_ms includes the Python layer's cost per call")
+                   "eager times include the Python layer's cost per call")
     return out
 
 

@@ -17,7 +17,7 @@ import weakref
 
 import torch
 
-from .native import _extension, require_dcu
+from .native import apply_function, _extension, require_dcu
 
 
 def _validate(zonal, radial, dst, radial_slot, inv_sqrt_deg):
@@ -173,7 +173,7 @@ def zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg):
     """
     _validate(zonal, radial, dst, radial_slot, inv_sqrt_deg)
     require_dcu(zonal, radial, dst, radial_slot, inv_sqrt_deg)
-    return _GIEZonalScatterFunction.apply(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    return apply_function(_GIEZonalScatterFunction, zonal, radial, dst, radial_slot, inv_sqrt_deg)
 
 
 def gie_zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg):
@@ -263,7 +263,7 @@ def gie_zonal_scatter_rmsnorm(zonal, radial, dst, radial_slot, inv_sqrt_deg, sca
         rows = zonal_scatter(zonal, radial, dst, radial_slot, inv_sqrt_deg)
         return rmsnorm(rows.reshape(n_nodes, width), scale, eps).reshape(n_nodes, n_rows + 1, channels)
     empty = torch.empty((0,), dtype=torch.float32, device=zonal.device)
-    return _GIERMSNormFunction.apply(zonal, radial, dst, radial_slot, inv_sqrt_deg,
+    return apply_function(_GIERMSNormFunction, zonal, radial, dst, radial_slot, inv_sqrt_deg,
                                      scale if scale is not None else empty, eps)
 
 

@@ -87,3 +87,32 @@ def _extension(required_symbol: str):
     if not hasattr(extension, required_symbol):
         raise RuntimeError(f"the loaded {_NATIVE_MODULE} has no {required_symbol!r} entry point")
     return extension
+
+
+class _Untracked:
+    """Stands in for an autograd context when no gradient can flow.
+
+    The operators' ``Function.forward`` methods run unchanged on it: what they
+    would save for the backward is dropped, and ``needs_input_grad`` is all
+    False (so a forward that writes extra state only for its backward skips
+    it).
+    """
+
+    def __init__(self, count: int):
+        self.needs_input_grad = (False,) * count
+
+    def save_for_backward(self, *tensors) -> None:
+        pass
+
+
+def apply_function(function, *args):
+    """``function.apply(*args)``, or its forward alone when no argument needs a gradient.
+
+    Outside grad mode (``torch.no_grad``, ``torch.inference_mode``) or when
+    no tensor argument requires a gradient, ``apply`` would record nothing:
+    calling the forward directly gives the same tensors without the autograd
+    bookkeeping, which is most of the Python layer's cost per eager call.
+    """
+    if torch.is_grad_enabled() and any(isinstance(a, torch.Tensor) and a.requires_grad for a in args):
+        return function.apply(*args)
+    return function.forward(_Untracked(len(args)), *args)

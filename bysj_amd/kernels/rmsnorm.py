@@ -10,7 +10,7 @@ import math
 
 import torch
 
-from .native import _extension, require_dcu
+from .native import apply_function, _extension, require_dcu
 
 
 def _validate(x, scale, eps) -> float:
@@ -73,7 +73,7 @@ def rmsnorm(x: torch.Tensor, scale: torch.Tensor | None = None, eps: float = 1.0
     eps = _validate(x, scale, eps)
     scale_tensor = scale if scale is not None else x.new_empty((0,))
     require_dcu(x, scale_tensor)
-    return _RMSNormFunction.apply(x, scale_tensor, eps)
+    return apply_function(_RMSNormFunction, x, scale_tensor, eps)
 
 
 def rmsnorm_available() -> bool:

@@ -26,7 +26,7 @@ import weakref
 
 import torch
 
-from .native import _extension, require_dcu
+from .native import apply_function, _extension, require_dcu
 
 _CHECK_GROUPING = os.environ.get("DPA4_CHECK_GROUPING", "0").strip().lower() in {"1", "true", "yes", "on"}
 
@@ -358,7 +358,7 @@ def segment_sum(src, dst, offsets, edge_scale=None, node_scale=None, *, order=No
     if _should_check(check_grouping):
         _check_csr(dst, offsets, n_nodes, "segment sum")
     require_dcu(src, dst, offsets, edge_scale, node_scale, order)
-    return _SegmentSumFunction.apply(src, dst, offsets, edge_scale, node_scale, order)
+    return apply_function(_SegmentSumFunction, src, dst, offsets, edge_scale, node_scale, order)
 
 
 def segment_softmax(logit, env, offsets, null_logit=None, *, order=None, check_grouping=None):
@@ -374,8 +374,8 @@ def segment_softmax(logit, env, offsets, null_logit=None, *, order=None, check_g
     _validate_segment_softmax(logit, env, offsets, null_logit, order)
     require_dcu(logit, env, offsets, null_logit, order)
     if null_logit is None:
-        return _SegmentSoftmaxFunction.apply(logit, env, offsets, order)
-    return _SegmentSoftmaxNullFunction.apply(logit, env, offsets, null_logit, order)
+        return apply_function(_SegmentSoftmaxFunction, logit, env, offsets, order)
+    return apply_function(_SegmentSoftmaxNullFunction, logit, env, offsets, null_logit, order)
 
 
 def force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None, src_order=None):

@@ -350,6 +350,36 @@ def test_gie_and_rmsnorm_autograd(fake_native):
     torch.testing.assert_close(out, rms_ref.rmsnorm(x))
 
 
+def test_untracked_calls_match_the_autograd_path(fake_native):
+    """Without a gradient to record, the operators run their forwards directly: same values, no graph."""
+    gen = torch.Generator().manual_seed(5)
+    dst, offsets = torch.tensor([0, 0, 1, 2, 2, 2]), torch.tensor([0, 2, 3, 6])
+    src = torch.randn(6, 4, generator=gen)
+    logit, env = torch.randn(6, 3, generator=gen), torch.rand(6, generator=gen) + 0.1
+    null = torch.randn(3, 3, generator=gen)
+    x, scale = torch.randn(4, 8, generator=gen), torch.rand(8, generator=gen) + 0.5
+    zonal, radial = torch.randn(6, 3, generator=gen), torch.randn(6, 2, 4, generator=gen)
+    slots, inv = torch.tensor([0, 1, 1]), torch.rand(3, generator=gen) + 0.5
+    rows_scale = torch.rand(16, generator=gen) + 0.5
+    calls = {
+        "segment_sum": lambda t: kernels.segment_sum(t(src), dst, offsets),
+        "segment_softmax": lambda t: kernels.segment_softmax(t(logit), env, offsets, null)[0],
+        "rmsnorm": lambda t: kernels.rmsnorm(t(x), scale),
+        "zonal_scatter": lambda t: kernels.zonal_scatter(t(zonal), radial, dst, slots, inv),
+        "gie_rmsnorm": lambda t: gie_mod.gie_zonal_scatter_rmsnorm(t(zonal), radial, dst, slots, inv, rows_scale),
+    }
+    for name, call in calls.items():
+        tracked = call(lambda v: v.clone().requires_grad_(True))
+        assert tracked.grad_fn is not None, name
+        plain = call(lambda v: v)
+        assert plain.grad_fn is None and not plain.requires_grad, name
+        with torch.no_grad():
+            quiet = call(lambda v: v.clone().requires_grad_(True))
+        assert quiet.grad_fn is None, name
+        torch.testing.assert_close(plain, tracked.detach(), rtol=0, atol=0, msg=name)
+        torch.testing.assert_close(quiet, tracked.detach(), rtol=0, atol=0, msg=name)
+
+
 def test_gie_grouping_is_cached_per_dst(fake_native):
     """One grouping per live dst object; in-place writes, new slot tensors and freeing invalidate it."""
     calls = []
