@@ -86,6 +86,39 @@ def group_by_source(src: torch.Tensor, n_nodes: int) -> tuple[torch.Tensor, torc
         raise ValueError("source values must be within the node range") from error
 
 
+def destination_grouping(dst: torch.Tensor, n_nodes: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """``(offsets, order)`` grouping an edge list by destination; ``order`` is None when ``dst`` is sorted.
+
+    An extension of the reference API for callers that cache a CSR per
+    neighbour graph (the seam layer's ``_CsrView``): the reference's seam
+    groups with :func:`group_by_source` and passes its order, which is the
+    identity for an already non-decreasing ``dst``.  Returning None there lets
+    ``segment_sum``/``segment_softmax`` take their natural-order kernels,
+    which read rows without the extra indirection.  Same validation and
+    errors as :func:`group_by_source`; on the device, one check pass (and a
+    sort only when ``dst`` is unsorted).
+    """
+    if not isinstance(dst, torch.Tensor):
+        raise TypeError("destination grouping requires a tensor of destinations")
+    if dst.dtype != torch.int64:
+        raise TypeError("destination grouping requires int64 destinations")
+    if n_nodes <= 0:
+        raise ValueError("destination grouping requires a positive node count")
+    n_nodes = int(n_nodes)
+    if dst.device.type == "cpu":
+        if dst.numel() and (int(dst.min()) < 0 or int(dst.max()) >= n_nodes):
+            raise ValueError("destination values must be within the node range")
+        ordered = dst.numel() < 2 or bool((dst[1:] >= dst[:-1]).all())
+        return segment_offsets(dst, n_nodes), (None if ordered else torch.argsort(dst, stable=True))
+    require_dcu(dst)
+    extension = _extension("gie_group")
+    try:
+        offsets, order, _ = extension.gie_group(dst.contiguous(), dst.new_empty(0), n_nodes, 0)
+    except ValueError as error:
+        raise ValueError("destination values must be within the node range") from error
+    return offsets, order
+
+
 # ---------------------------------------------------------------------------
 # validators (python/kernels/segment.py:74-193)
 # ---------------------------------------------------------------------------

@@ -84,12 +84,12 @@ def _segment_operators():
 
 
 def _group_by_destination(dst: torch.Tensor, n_nodes: int):
+    """``(offsets, order)``, with ``order`` None when ``dst`` is already sorted (natural-order kernels)."""
     try:
-        from ..kernels import group_by_source
+        from ..kernels.segment import destination_grouping
     except ImportError:
-        from kernels import group_by_source
-    order, offsets = group_by_source(dst, n_nodes)
-    return offsets, order
+        from kernels.segment import destination_grouping
+    return destination_grouping(dst, n_nodes)
 
 
 class _CsrView:

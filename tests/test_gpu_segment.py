@@ -8,6 +8,8 @@ device tests (tests/csrc/accuracy/test_segment_ops_accuracy.py).
 """
 from __future__ import annotations
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +21,7 @@ from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
+segment_mod = importlib.import_module("bysj_amd.kernels.segment")
 
 
 def _graph(sizes):
@@ -53,6 +56,25 @@ def test_segment_offsets_and_grouping_bit_exact(edges, nodes, seed):
     e_order, e_offsets = ref.group_by_source(keys, nodes)
     assert_bitwise(order, e_order, "group_by_source order")
     assert_bitwise(src_offsets, e_offsets, "group_by_source offsets")
+
+
+@pytest.mark.parametrize("sort", [False, True])
+def test_destination_grouping(sort):
+    """Offsets equal segment_offsets; the order is None exactly when dst is non-decreasing."""
+    announce("destination grouping", sort)
+    gen = torch.Generator().manual_seed(21)
+    keys = torch.randint(0, 700, (50000,), generator=gen, dtype=torch.int64)
+    if sort:
+        keys = torch.sort(keys).values
+    offsets, order = segment_mod.destination_grouping(keys.to(DEV), 700)
+    e_order, e_offsets = ref.group_by_source(keys, 700)
+    assert_bitwise(offsets, e_offsets, "offsets")
+    if sort:
+        assert order is None
+    else:
+        assert_bitwise(order, e_order, "order")
+    with pytest.raises(ValueError, match="node range"):
+        segment_mod.destination_grouping(torch.tensor([0, 700], device=DEV), 700)
 
 
 def test_grouping_known_answer_and_range_errors():

@@ -257,6 +257,15 @@ def test_csr_view_reuses_and_invalidates_entries():
     assert len(view) == 0                                       # freed tensors drop their entries
 
 
+def test_csr_view_leaves_sorted_destinations_in_natural_order():
+    """A non-decreasing dst needs no order: the operators then take their natural-order kernels."""
+    view = fused_deepmd._CsrView()
+    offsets, order = view.get(torch.tensor([0, 0, 1, 2, 2]), 3)
+    assert order is None and offsets.tolist() == [0, 2, 3, 5]
+    with pytest.raises(ValueError, match="node range"):
+        view.get(torch.tensor([0, 3]), 3)
+
+
 # ---------------------------------------------------------------------------
 # fused= switch and DPA4Model facade
 # ---------------------------------------------------------------------------
