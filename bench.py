@@ -163,7 +163,8 @@ def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
             "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
 
 
-def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool, scaled_shuffled: bool = False):
+    """segment_sum forward; `scaled_shuffled` adds edge and node scales ~U(0.5, 1.5) and a shuffled edge order."""
     import torch
 
     from bysj_amd import kernels, workloads
@@ -171,14 +172,22 @@ def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool):
     base = workloads.segment_sum_config(n_nodes=n_nodes, seed=0, device="cuda")
     edges, channels = base["src"].shape
     bytes_per_step = edges * channels * 4 + (n_nodes + 1) * 8 + n_nodes * channels * 4
-    n_sets = n_sets_for(bytes_per_step)
     generator = torch.Generator(device="cuda")
     generator.manual_seed(1)
+    dst, edge_scale, node_scale, order = base["dst"], None, None, None
+    if scaled_shuffled:
+        edge_scale = torch.rand(edges, generator=generator, device="cuda") + 0.5
+        node_scale = torch.rand(n_nodes, generator=generator, device="cuda") + 0.5
+        order = torch.randperm(edges, generator=generator, device="cuda")  # slot i holds edge order[i]
+        dst = torch.empty_like(base["dst"])
+        dst[order] = base["dst"]
+        bytes_per_step += edges * 4 + n_nodes * 4 + edges * 8
+    n_sets = n_sets_for(bytes_per_step)
     sets = [base["src"]] + [torch.randn(base["src"].shape, generator=generator, device="cuda")
                             for _ in range(1, n_sets)]
 
     def step(i):
-        return kernels.segment_sum(sets[i], base["dst"], base["offsets"])
+        return kernels.segment_sum(sets[i], dst, base["offsets"], edge_scale, node_scale, order=order)
 
     with torch.no_grad():
         ms = time_steps(step, n_sets, steps, warmup, graph=graph)
@@ -731,6 +740,8 @@ def main() -> int:
         if args.roofline_shapes:
             job = segment_sum_job(262144, steps, warm, graph)
             ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])
+            job = segment_sum_job(262144, steps, warm, graph, scaled_shuffled=True)
+            ops["segment_sum_config1R_scaled_shuffled"] = op_line("segment_sum_fwd", job, job["edges"])
             job = softmax_job(210000, steps, warm, graph)
             ops["segment_softmax_config2R"] = op_line("segment_softmax_fwd", job, job["edges"])
             if not args.no_backward:
