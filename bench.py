@@ -474,6 +474,40 @@ def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
                     "what a stream of its own bytes reaches"}
 
 
+def _torch_softmax_chain(logit, env, dst, n_nodes, null_logit):
+    """The reference's PyTorch chain for segment_softmax (python/reference/segment.py:84-118), run on the GPU."""
+    import torch
+
+    valid = (env > 0).unsqueeze(1)
+    eff = torch.where(valid, logit + 2.0 * torch.log(env.clamp_min(1e-30)).unsqueeze(1),
+                      torch.full_like(logit, float("-inf")))
+    peak = torch.full((n_nodes, logit.shape[1]), float("-inf"), device=logit.device)
+    peak = peak.scatter_reduce(0, dst.unsqueeze(1).expand_as(eff), eff, reduce="amax", include_self=True)
+    peak = torch.maximum(peak, null_logit)
+    weight = torch.where(valid, torch.exp(eff - peak[dst]), torch.zeros_like(eff))
+    null_weight = torch.exp(null_logit - peak)
+    total = torch.zeros_like(peak).index_add_(0, dst, weight) + null_weight
+    return weight / total[dst], null_weight / total
+
+
+def _torch_force_chain(grad_edge, edge_vec, src, dst, n_nodes):
+    """The reference's PyTorch chain for force_assembly (python/reference/segment.py:121-142), run on the GPU."""
+    import torch
+
+    force = torch.zeros((n_nodes, 3), device=grad_edge.device).index_add_(0, dst, grad_edge)
+    force.index_add_(0, src, -grad_edge)
+    outer = -(grad_edge.unsqueeze(2) * edge_vec.unsqueeze(1)).reshape(-1, 9)
+    return force, torch.zeros((n_nodes, 9), device=grad_edge.device).index_add_(0, src, outer)
+
+
+def _torch_sum_chain(rows, dst, n_nodes, node_scale):
+    """The reference's PyTorch chain for segment_sum (python/reference/segment.py:39-60), run on the GPU."""
+    import torch
+
+    out = torch.zeros((n_nodes, rows.shape[1]), device=rows.device).index_add_(0, dst, rows)
+    return out * node_scale.unsqueeze(1)
+
+
 def reference_shapes(steps: int) -> dict:
     """The reference's own latency-test shapes, timed like its harnesses and as kernels.
 
@@ -513,27 +547,35 @@ def reference_shapes(steps: int) -> dict:
 
     out = {}
     with torch.no_grad():
-        for channels, dcu in ((64, 0.49), (256, 1.91)):
+        # dcu_ms / dcu_torch_ms: the reference's fused operator and its PyTorch chain on its DCU;
+        # torch_gpu_ms: that PyTorch chain on this GPU, timed like the fused operator
+        for channels, dcu, dcu_torch in ((64, 0.49, 4.42), (256, 1.91, 9.52)):
             logit = torch.randn(edges, channels, generator=generator, device="cuda")
             null = torch.randn(atoms, channels, generator=generator, device="cuda")
             call = lambda _=None, logit=logit, null=null: kernels.segment_softmax(logit, env, offsets, null)
+            chain = lambda _=None, logit=logit, null=null: _torch_softmax_chain(logit, env, dst, atoms, null)
             out[f"segment_softmax_C{channels}_null"] = {
                 "eager_ms": round(median_eager(call), 4), "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
-                "dcu_ms": dcu, "source": "docs/task2-hip-fusion-plan.md:229"}
+                "torch_gpu_ms": round(median_eager(chain), 4), "dcu_ms": dcu, "dcu_torch_ms": dcu_torch,
+                "source": "docs/task2-hip-fusion-plan.md:229"}
         src = torch.randint(0, atoms, (edges,), generator=generator, device="cuda")
         src_order, src_offsets = kernels.group_by_source(src, atoms)
         grad_edge = torch.randn(edges, 3, generator=generator, device="cuda")
         edge_vec = torch.randn(edges, 3, generator=generator, device="cuda")
         call = lambda _=None: kernels.force_assembly(grad_edge, edge_vec, src, dst, offsets, src_offsets, src_order)
+        chain = lambda _=None: _torch_force_chain(grad_edge, edge_vec, src, dst, atoms)
         out["force_assembly_f32"] = {"eager_ms": round(median_eager(call), 4),
                                      "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
-                                     "dcu_ms": 0.182, "source": "docs/task2-hip-fusion-plan.md:272"}
+                                     "torch_gpu_ms": round(median_eager(chain), 4), "dcu_ms": 0.182,
+                                     "dcu_torch_ms": 1.006, "source": "docs/task2-hip-fusion-plan.md:272"}
         node_scale = torch.rand(atoms, generator=generator, device="cuda") + 0.5
         for channels in (64, 256):
             src_rows = torch.randn(edges, channels, generator=generator, device="cuda")
             call = lambda _=None, rows=src_rows: kernels.segment_sum(rows, dst, offsets, None, node_scale)
+            chain = lambda _=None, rows=src_rows: _torch_sum_chain(rows, dst, atoms, node_scale)
             out[f"segment_sum_C{channels}"] = {"eager_ms": round(median_eager(call), 4),
                                                "kernel_ms": round(time_steps(call, 1, steps, 10), 4),
+                                               "torch_gpu_ms": round(median_eager(chain), 4),
                                                "dcu_ms": None, "source": "not published by the reference"}
         # tests/csrc/latency/test_rmsnorm_latency.py: 20 warmup calls, 7 repeats of 100 calls between
         # events, median and p95 of the per-call time, scale of ones; no figure is published
