@@ -86,6 +86,10 @@ def test_invalid_sizes_fail_before_any_device_call():
         (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (1, 4, ctypes.c_float(0.0), null), "eps"),
         (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 0, null), ""),
         (lib.dpa4k_force_assembly_f64, (null,) * 7 + (-1, 1, null), ""),
+        # a scale gradient needs a scale (csrc/rmsnorm.cpp:138-139 of the reference); the output
+        # pointer is never dereferenced
+        (lib.dpa4k_rmsnorm_backward, (null,) * 5 + (ctypes.c_void_p(256), 1, 4, null, 0, null),
+         "scale is omitted"),
         # beyond what rows of blocks along y can hold
         (lib.dpa4k_segment_sum_forward, (null,) * 6 + (1, 2**62, 1, null), "segment count too large"),
         (lib.dpa4k_segment_softmax_forward, (null,) * 7 + (1, 2**62, 8, null), "segment count too large"),

@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from bysj_amd import kernels, workloads
+from bysj_amd.kernels import _C
 from oracle import gie as gie_ref
 from oracle import loops
 from oracle.rmsnorm import rmsnorm as reference_rmsnorm
@@ -175,6 +176,15 @@ def test_rmsnorm_zero_input_no_scale_and_stream():
         out = kernels.rmsnorm(xs.to(DEV), ss.to(DEV))
     torch.cuda.current_stream().wait_stream(stream)
     assert_close_scaled(out, reference_rmsnorm(xs, ss), what="side stream")
+    # a scale gradient needs a scale (csrc/rmsnorm.cpp:138-139 of the reference)
+    empty = torch.empty(0, device=DEV)
+    y, inverse_rms = _C.rmsnorm_forward(xs.to(DEV), empty, 1e-6)
+    with pytest.raises(RuntimeError, match="scale is omitted"):
+        _C.rmsnorm_backward(torch.ones_like(y), xs.to(DEV), empty, inverse_rms, True)
+    grad_x, grad_scale = _C.rmsnorm_backward(torch.ones_like(y), xs.to(DEV), empty, inverse_rms, False)
+    assert grad_scale.numel() == 0
+    e_x, _ = rmsnorm_backward_reference(torch.ones(9, 131), xs, None, 1e-6)
+    assert_close_scaled(grad_x, e_x, rtol=3e-5, what="grad_x without scale")
 
 
 def test_gie_then_rmsnorm_config3_reduced():

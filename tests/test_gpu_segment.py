@@ -301,6 +301,7 @@ def test_segment_softmax_with_hubs(channels, null, use_order):
     env = torch.rand(dst.numel(), generator=gen) + 0.1
     env[::13] = 0.0
     env[7::29] = -1.0
+    env[11::31] = float("nan")  # masked like env <= 0: the mask is !(env > 0), csrc/segment_softmax.cpp:73
     null_logit = torch.randn(67, channels, generator=gen) if null else None
     up = torch.randn(dst.numel(), channels, generator=gen)
     up_null = torch.randn(67, channels, generator=gen) if null else None
