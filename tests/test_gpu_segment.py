@@ -409,6 +409,44 @@ def test_segment_softmax_empty_and_masked_segments():
     torch.testing.assert_close(null_alpha[1].cpu(), torch.ones(4))
 
 
+@pytest.mark.parametrize("channels", [8, 64, 260])
+def test_identity_order_equals_no_order(channels):
+    """order = arange(E) names the natural slots: segment_sum and segment_softmax, forward and
+    backward, must give the same bits as order=None on every path (short, staged and long
+    segments, lane groups and wide rows)."""
+    announce("identity order", channels)
+    n_nodes = 300
+    degrees = workloads.poisson_degrees(n_nodes, 9.0, seed=channels, minimum=0, hub_fraction=0.02,
+                                        hub_degree=900)
+    dst = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    offsets = ref.segment_offsets(dst, n_nodes).to(DEV)
+    edges = dst.numel()
+    identity = torch.arange(edges, dtype=torch.int64, device=DEV)
+    gen = torch.Generator().manual_seed(channels)
+    src = torch.randn(edges, channels, generator=gen)
+    edge_scale = torch.rand(edges, generator=gen) + 0.5
+    node_scale = torch.rand(n_nodes, generator=gen) + 0.5
+    grad_out = torch.randn(n_nodes, channels, generator=gen)
+    logit = torch.randn(edges, channels, generator=gen) * 2.0
+    env = torch.rand(edges, generator=gen) + 0.1
+    env[::11] = 0.0
+    null_logit = torch.randn(n_nodes, channels, generator=gen)
+    up = torch.randn(edges, channels, generator=gen)
+    up_null = torch.randn(n_nodes, channels, generator=gen)
+
+    def run(order):
+        s, w, n = (t.to(DEV).requires_grad_(True) for t in (src, edge_scale, node_scale))
+        out = kernels.segment_sum(s, dst.to(DEV), offsets, w, n, order=order)
+        sum_grads = torch.autograd.grad(out, (s, w, n), grad_out.to(DEV))
+        x, e, nl = (t.to(DEV).requires_grad_(True) for t in (logit, env, null_logit))
+        alpha, null_alpha = kernels.segment_softmax(x, e, offsets, nl, order=order)
+        soft_grads = torch.autograd.grad((alpha, null_alpha), (x, e, nl), (up.to(DEV), up_null.to(DEV)))
+        return (out.detach(), *sum_grads, alpha.detach(), null_alpha.detach(), *soft_grads)
+
+    for i, (got, want) in enumerate(zip(run(identity), run(None))):
+        assert_bitwise(got, want, f"output {i}")
+
+
 def test_segment_softmax_config2_full_size_and_determinism():
     announce("softmax config 2")
     case = workloads.segment_softmax_config(seed=0)
