@@ -17,7 +17,7 @@ import weakref
 
 import torch
 
-from .native import apply_function, _extension, require_dcu
+from .native import apply_function, _extension, require_dcu, version_stamp
 
 
 def _validate(zonal, radial, dst, radial_slot, inv_sqrt_deg):
@@ -73,6 +73,8 @@ class _GroupingCache:
     does.  A few ``radial_slot`` objects are kept per ``dst``.  Grouping
     synchronises, so under HIP graph capture only a cached grouping can be
     used: run the operator once on the same tensors before capturing it.
+    Inference tensors keep no version counter, so a grouping of one is built
+    on every call and not cached.
     """
 
     SLOTS_PER_DST = 4
@@ -80,20 +82,22 @@ class _GroupingCache:
     def __init__(self):
         self._entries: dict[int, tuple] = {}
 
-    @staticmethod
-    def _stamp(tensor: torch.Tensor) -> tuple:
-        return (tensor.data_ptr(), tensor._version, tensor.numel(), tensor.device)
-
     def get(self, native, dst, radial_slot, n_nodes: int, n_radial: int):
         key = id(dst)
-        stamp = self._stamp(dst) + (n_nodes,)
+        dst_stamp, slot_stamp = version_stamp(dst), version_stamp(radial_slot)
+        if dst_stamp is None or slot_stamp is None:
+            if _capturing(dst):
+                raise RuntimeError("GIE: grouping synchronises, and the grouping of an inference tensor is not "
+                                   "cached; make dst and radial_slot outside torch.inference_mode to capture")
+            return native.gie_group(dst, radial_slot, n_nodes, n_radial)
+        stamp = dst_stamp + (n_nodes,)
         entry = self._entries.get(key)
         if entry is not None and (entry[0]() is not dst or entry[1] != stamp):
             entry = None
         groupings = entry[2] if entry is not None else {}
         slot_key = (id(radial_slot), n_radial)
         found = groupings.get(slot_key)
-        if found is not None and found[0]() is radial_slot and found[1] == self._stamp(radial_slot):
+        if found is not None and found[0]() is radial_slot and found[1] == slot_stamp:
             return found[2]
         if _capturing(dst):
             raise RuntimeError("GIE: this dst has no cached grouping, and grouping synchronises; "
@@ -104,7 +108,7 @@ class _GroupingCache:
             entry = (reference, stamp, groupings)
             self._entries[key] = entry
         groupings.pop(slot_key, None)
-        groupings[slot_key] = (weakref.ref(radial_slot), self._stamp(radial_slot), grouping)
+        groupings[slot_key] = (weakref.ref(radial_slot), slot_stamp, grouping)
         while len(groupings) > self.SLOTS_PER_DST:
             groupings.pop(next(iter(groupings)))
         return grouping

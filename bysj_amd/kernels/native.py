@@ -105,6 +105,19 @@ class _Untracked:
         pass
 
 
+def version_stamp(tensor: torch.Tensor):
+    """``(storage address, version counter, numel, device)`` of ``tensor``, or None for an inference tensor.
+
+    The caches of derived data (degree plans, groupings) use the stamp to see
+    in-place writes.  Tensors made under ``torch.inference_mode`` keep no
+    version counter, so their in-place writes cannot be seen: callers derive
+    afresh from them instead of caching.
+    """
+    if tensor.is_inference():
+        return None
+    return (tensor.data_ptr(), tensor._version, tensor.numel(), tensor.device)
+
+
 def apply_function(function, *args):
     """``function.apply(*args)``, or its forward alone when no argument needs a gradient.
 

@@ -26,7 +26,7 @@ import weakref
 
 import torch
 
-from .native import apply_function, _extension, require_dcu
+from .native import apply_function, _extension, require_dcu, version_stamp
 
 _CHECK_GROUPING = os.environ.get("DPA4_CHECK_GROUPING", "0").strip().lower() in {"1", "true", "yes", "on"}
 
@@ -261,14 +261,19 @@ class _PlanCache:
     entries are keyed by the identity of the ``offsets`` tensor and
     invalidated when its storage or version counter changes (an in-place
     write) or the tensor is freed.  During HIP graph capture a missing plan
-    is not built; the kernels then run without one (same results).
+    is not built; the kernels then run without one (same results).  Nor is
+    one built for an inference tensor, whose in-place writes a cached plan
+    could not follow: a plan per call would add a synchronisation to every
+    call.
     """
 
     def __init__(self):
         self._entries: dict[int, tuple] = {}
 
     def get(self, offsets: torch.Tensor, n_edges: int, channels: int):
-        stamp = (offsets.data_ptr(), offsets._version, offsets.numel(), offsets.device)
+        stamp = version_stamp(offsets)
+        if stamp is None:
+            return None
         key = id(offsets)
         entry = self._entries.get(key)
         if entry is not None and (entry[0]() is not offsets or entry[1] != stamp):

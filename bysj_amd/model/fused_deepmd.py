@@ -97,7 +97,8 @@ class _CsrView:
 
     Keyed by the identity of the ``dst`` tensor object; an entry is valid
     while that object is alive and its storage, size, version counter and
-    node count are unchanged.
+    node count are unchanged.  An inference tensor keeps no version counter,
+    so its view is built on every call and not kept.
     """
 
     def __init__(self, capacity: int = _CSR_CAPACITY):
@@ -106,17 +107,22 @@ class _CsrView:
 
     @staticmethod
     def _stamp(dst: torch.Tensor, n_nodes: int):
+        if dst.is_inference():
+            return None
         return (dst.data_ptr(), dst.numel(), dst._version, str(dst.device), int(n_nodes))
 
     def get(self, dst: torch.Tensor, n_nodes: int):
+        stamp = self._stamp(dst, n_nodes)
+        if stamp is None:
+            return _group_by_destination(dst, int(n_nodes))
         key = id(dst)
         entry = self._entries.pop(key, None)
-        if entry is not None and entry[0]() is dst and entry[1] == self._stamp(dst, n_nodes):
+        if entry is not None and entry[0]() is dst and entry[1] == stamp:
             self._entries[key] = entry            # most recently used last
             return entry[2], entry[3]
         offsets, order = _group_by_destination(dst, int(n_nodes))
         reference = weakref.ref(dst, lambda _, key=key: self._entries.pop(key, None))
-        self._entries[key] = (reference, self._stamp(dst, n_nodes), offsets, order)
+        self._entries[key] = (reference, stamp, offsets, order)
         while len(self._entries) > self.capacity:
             self._entries.pop(next(iter(self._entries)))
         return offsets, order

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from bysj_amd import kernels, workloads
+from oracle import gie as gie_ref
 from oracle import loops
 from oracle import segment as ref
 from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
@@ -445,6 +446,41 @@ def test_identity_order_equals_no_order(channels):
 
     for i, (got, want) in enumerate(zip(run(identity), run(None))):
         assert_bitwise(got, want, f"output {i}")
+
+
+def test_operators_on_inference_tensors():
+    """Tensors made under torch.inference_mode keep no version counter: the operators then cache
+    nothing (the softmax runs without its degree plan, GIE groups on every call) and still match
+    the oracle, hubs and an unsorted GIE dst included."""
+    announce("inference tensors")
+    n_nodes = 200
+    degrees = workloads.poisson_degrees(n_nodes, 8.0, seed=3, minimum=0, hub_fraction=0.03, hub_degree=600)
+    dst_cpu = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    offsets_cpu = ref.segment_offsets(dst_cpu, n_nodes)
+    edges = dst_cpu.numel()
+    gen = torch.Generator().manual_seed(3)
+    logit, env = torch.randn(edges, 8, generator=gen) * 2.0, torch.rand(edges, generator=gen) + 0.1
+    null_logit, src = torch.randn(n_nodes, 8, generator=gen), torch.randn(edges, 64, generator=gen)
+    perm = torch.randperm(edges, generator=gen)
+    zonal, radial = torch.randn(edges, 15, generator=gen), torch.randn(edges, 16, 16, generator=gen)
+    slots, inv = torch.arange(1, 16), torch.rand(n_nodes, generator=gen) + 0.2
+    with torch.inference_mode():
+        dst, offsets = dst_cpu.to(DEV), offsets_cpu.to(DEV)
+        assert offsets.is_inference()
+        results = []
+        for _ in range(2):
+            alpha, null_alpha = kernels.segment_softmax(logit.to(DEV), env.to(DEV), offsets, null_logit.to(DEV))
+            summed = kernels.segment_sum(src.to(DEV), dst, offsets)
+            gie = kernels.zonal_scatter(zonal.to(DEV), radial.to(DEV), dst[perm.to(DEV)], slots.to(DEV), inv.to(DEV))
+            results.append((alpha, null_alpha, summed, gie))
+    e_alpha, e_null = ref.segment_softmax_reference(logit, env, dst_cpu, offsets_cpu, null_logit)
+    assert_close_scaled(results[0][0], e_alpha, what="alpha")
+    assert_close_scaled(results[0][1], e_null, what="null_alpha")
+    assert_bitwise(results[0][2], ref.segment_sum_reference(src, dst_cpu, offsets_cpu), "segment_sum")
+    assert_close_scaled(results[0][3], gie_ref.zonal_scatter_reference(zonal, radial, dst_cpu[perm], slots, inv),
+                        what="zonal_scatter")
+    for i, (got, want) in enumerate(zip(results[1], results[0])):
+        assert_bitwise(got, want, f"second call, output {i}")
 
 
 def test_segment_softmax_config2_full_size_and_determinism():

@@ -416,6 +416,42 @@ def test_gie_grouping_is_cached_per_dst(fake_native):
     assert len(gie_mod._GROUPINGS) == 0, "freeing dst drops its entry"
 
 
+def test_inference_tensors_are_not_cached(fake_native):
+    """Tensors made under torch.inference_mode keep no version counter, so no cache can see their
+    in-place writes: the softmax runs without a degree plan (the kernels give the same results
+    either way) and the GIE grouping is built on every call."""
+    plans, groupings = [], []
+    fake_native.segment_softmax_plan = lambda *args: plans.append(args)
+
+    def forward_without_plan(logit, env, offsets, null_logit=None, order=None, *, plan=None):
+        assert plan is None
+        dst = fake_native._dst(offsets, order, logit.shape[0])
+        return ref.segment_softmax_reference(logit, env, dst, offsets, null_logit)
+
+    fake_native.segment_softmax_forward = forward_without_plan
+    group = fake_native.gie_group
+    fake_native.gie_group = lambda *args: groupings.append(args) or group(*args)
+    segment_mod._PLANS.clear()
+    gie_mod._GROUPINGS.clear()
+    gen = torch.Generator().manual_seed(6)
+    with torch.inference_mode():
+        dst = torch.tensor([0, 0, 1, 2, 2])
+        offsets = torch.tensor([0, 2, 3, 5])
+        logit, env = torch.randn(5, 4, generator=gen), torch.rand(5, generator=gen) + 0.1
+        for _ in range(2):
+            alpha = kernels.segment_softmax(logit, env, offsets)
+        expected, _ = ref.segment_softmax_reference(logit, env, dst, offsets)
+        zonal, radial = torch.randn(5, 3, generator=gen), torch.randn(5, 2, 4, generator=gen)
+        slots, inv = torch.tensor([0, 1, 1]), torch.rand(3, generator=gen) + 0.5
+        for _ in range(2):
+            out = kernels.zonal_scatter(zonal, radial, dst, slots, inv)
+        expected_gie = gie_ref.zonal_scatter_reference(zonal, radial, dst, slots, inv)
+    torch.testing.assert_close(alpha, expected)
+    torch.testing.assert_close(out, expected_gie)
+    assert plans == [] and len(segment_mod._PLANS._entries) == 0
+    assert len(groupings) == 2 and len(gie_mod._GROUPINGS) == 0
+
+
 def test_gie_grouping_is_not_built_under_graph_capture(fake_native):
     """Grouping synchronises: under capture only a cached one is used, else a clear error."""
     gie_mod._GROUPINGS.clear()

@@ -266,6 +266,17 @@ def test_csr_view_leaves_sorted_destinations_in_natural_order():
         view.get(torch.tensor([0, 3]), 3)
 
 
+def test_csr_view_of_inference_tensors_is_built_per_call():
+    """Inference tensors keep no version counter, so their views are not kept (and do not raise)."""
+    view = fused_deepmd._CsrView()
+    with torch.inference_mode():
+        dst = torch.tensor([1, 0, 1, 2])
+        offsets, order = view.get(dst, 3)
+        again = view.get(dst, 3)
+    assert offsets.tolist() == [0, 1, 3, 4] and order.tolist() == [1, 0, 2, 3]
+    assert again[0].tolist() == offsets.tolist() and len(view) == 0
+
+
 # ---------------------------------------------------------------------------
 # fused= switch and DPA4Model facade
 # ---------------------------------------------------------------------------
