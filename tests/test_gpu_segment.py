@@ -483,6 +483,45 @@ def test_operators_on_inference_tensors():
         assert_bitwise(got, want, f"second call, output {i}")
 
 
+@pytest.mark.parametrize("channels", [8, 260])
+def test_segment_softmax_fully_masked_long_segments(channels):
+    """Hub segments whose envelopes are all <= 0 or NaN (staged and streamed long paths): alpha is
+    zero there, the null logit takes all the mass, and the gradients match the oracle."""
+    announce("softmax masked hubs", channels)
+    dst, offsets = _graph([5, 700, 3, 5000, 0, 2])
+    edges = dst.numel()
+    gen = torch.Generator().manual_seed(channels)
+    logit = torch.randn(edges, channels, generator=gen) * 2.0
+    env = torch.rand(edges, generator=gen) + 0.1
+    env[5:705] = -0.5
+    env[708:5708] = 0.0
+    env[708:5708:7] = float("nan")
+    up = torch.randn(edges, channels, generator=gen)
+    for null in (False, True):
+        null_logit = torch.randn(6, channels, generator=gen) if null else None
+        up_null = torch.randn(6, channels, generator=gen) if null else None
+        x, e = logit.to(DEV).requires_grad_(True), env.to(DEV).requires_grad_(True)
+        nd = null_logit.to(DEV).requires_grad_(True) if null else None
+        result = kernels.segment_softmax(x, e, offsets.to(DEV), nd)
+        alpha = result[0] if null else result
+        e_alpha, e_null = ref.segment_softmax_reference(logit, env, dst, offsets, null_logit)
+        assert_close_scaled(alpha, e_alpha, what=f"alpha (null={null})")
+        assert alpha[5:705].count_nonzero().item() == 0 and alpha[708:5708].count_nonzero().item() == 0
+        if null:
+            torch.testing.assert_close(result[1][1].cpu(), torch.ones(channels))
+            torch.testing.assert_close(result[1][3].cpu(), torch.ones(channels))
+            outputs, cotangents, inputs = (result[0], result[1]), (up.to(DEV), up_null.to(DEV)), (x, e, nd)
+        else:
+            outputs, cotangents, inputs = (alpha,), (up.to(DEV),), (x, e)
+        grads = torch.autograd.grad(outputs, inputs, cotangents)
+        e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
+        assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
+        assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
+        assert grads[1][5:705].count_nonzero().item() == 0 and grads[1][708:5708].count_nonzero().item() == 0
+        if null:
+            assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+
+
 def test_segment_softmax_config2_full_size_and_determinism():
     announce("softmax config 2")
     case = workloads.segment_softmax_config(seed=0)
