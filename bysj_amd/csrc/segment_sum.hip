@@ -240,6 +240,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
   constexpr int kAhead = 8;
   __shared__ fvec<4> stage[kStageChunks];
   __shared__ float weight[kStageChunks / 16 + kAhead];  // rows per batch (chunks >= 16), padded
+  __shared__ unsigned char skip[kStageChunks / 16 + kAhead];  // 1: the row's order entry is out of range
   const int64_t segment = block_index();
   if (segment >= n_nodes) return;
   const int chunks = static_cast<int>(channels / 4);
@@ -267,10 +268,12 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
         for (int i = 0; i < 4; ++i) x[k].v[i] = 0.0f;
       }
     }
-    // weight of each staged row; NaN marks a row whose order entry is out of range (skipped)
+    // weight of each staged row, and whether it is skipped (order entry out of range); the
+    // flag lives apart from the weight so that a NaN edge_scale still propagates into the sum
     for (int row = t; row < rows; row += kBlock) {
       const int64_t e = edge_of<kOrdered>(order, first + row, n_edges);
-      weight[row] = e < 0 ? __builtin_nanf("") : (kScaleEdge ? edge_scale[e] : 1.0f);
+      weight[row] = e < 0 ? 0.0f : (kScaleEdge ? edge_scale[e] : 1.0f);
+      skip[row] = e < 0 ? 1 : 0;
     }
 #pragma unroll
     for (int k = 0; k < kStageItems; ++k)
@@ -279,15 +282,17 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
     if (t < width) {
       for (int row = 0; row < rows; row += kAhead) {
         float v[kAhead], w[kAhead];
+        bool dropped[kAhead];
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
           const int r = row + k < rows ? row + k : row;
           v[k] = staged[r * width + t];
           w[k] = weight[r];
+          dropped[k] = kOrdered && skip[r] != 0;
         }
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) {
-          if (row + k >= rows || (kOrdered && w[k] != w[k])) continue;
+          if (row + k >= rows || dropped[k]) continue;
           acc = acc + (kScaleEdge ? v[k] * w[k] : v[k]);
         }
       }

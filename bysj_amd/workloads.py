@@ -82,11 +82,18 @@ def morton_order(positions: np.ndarray, box: float, bin_size: float) -> np.ndarr
 
 
 def water_graph(n_atoms: int, seed: int, *, rcut: float = 6.0, density: float = 0.1,
-                spatial_order: bool = False) -> WaterGraph:
+                spatial_order: bool = False, device: str | torch.device = "cpu") -> WaterGraph:
     """Uniform random positions in a periodic cube; O:H = 1:2 types shuffled by the seed.
 
     Atom indices follow the draw order (no spatial locality) unless
     ``spatial_order`` renumbers them by the Morton key of rcut/2 bins.
+    Positions and the cell lists come from the seeded host generator; the
+    candidate pairs of the 27 neighbouring cells are filtered with torch on
+    ``device`` (the GPU builds a 65k-atom box in about a second).  Every
+    step is exact or correctly rounded IEEE arithmetic in a fixed order
+    (difference, minimum image, ``(dx^2 + dy^2) + dz^2``), and the edges end
+    sorted by the unique key ``(dst, src)``, so every device yields the same
+    graph bit for bit.
     """
     generator = rng(seed)
     box = (n_atoms / density) ** (1.0 / 3.0)
@@ -108,29 +115,36 @@ def water_graph(n_atoms: int, seed: int, *, rcut: float = 6.0, density: float = 
     counts = np.bincount(cell, minlength=n_cell ** 3)
     starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
     width = int(counts.max())
-    lane = np.arange(width)
-    atoms = np.arange(n_atoms)
-    cutoff2 = rcut * rcut
 
-    srcs, dsts, vecs = [], [], []
-    for shift in itertools.product((-1, 0, 1), repeat=3):
-        nb_xyz = (cell_xyz + np.asarray(shift)) % n_cell
-        nb = (nb_xyz[:, 0] * n_cell + nb_xyz[:, 1]) * n_cell + nb_xyz[:, 2]
-        valid = lane[None, :] < counts[nb][:, None]
-        slot = np.minimum(starts[nb][:, None] + lane[None, :], n_atoms - 1)
-        other = by_cell[slot]
-        delta = positions[other] - positions[:, None, :]
-        delta -= box * np.round(delta / box)
-        keep = valid & ((delta * delta).sum(-1) < cutoff2) & (other != atoms[:, None])
-        rows, cols = np.nonzero(keep)
-        dsts.append(rows.astype(np.int64))
-        srcs.append(other[rows, cols].astype(np.int64))
-        vecs.append(delta[rows, cols])
-    dst = np.concatenate(dsts)
-    src = np.concatenate(srcs)
-    vec = np.concatenate(vecs)
-    order = np.lexsort((src, dst))
-    return WaterGraph(n_atoms, box, positions, types, src[order], dst[order], vec[order])
+    dev = torch.device(device)
+    positions_t = torch.from_numpy(positions).to(dev)
+    cell_xyz_t = torch.from_numpy(cell_xyz).to(dev)
+    counts_t = torch.from_numpy(counts).to(dev)
+    starts_t = torch.from_numpy(starts).to(dev)
+    by_cell_t = torch.from_numpy(by_cell).to(dev)
+    lane = torch.arange(width, device=dev)
+    shifts = torch.tensor(list(itertools.product((-1, 0, 1), repeat=3)), device=dev)
+    cutoff2 = rcut * rcut
+    chunk = max(1024, (1 << 26) // (27 * width * 8))  # about 200 MB of candidate vectors per chunk
+    keys, vectors = [], []
+    for begin in range(0, n_atoms, chunk):
+        atoms = torch.arange(begin, min(n_atoms, begin + chunk), device=dev)
+        neighbour_xyz = (cell_xyz_t[atoms][:, None, :] + shifts[None, :, :]) % n_cell          # [A, 27, 3]
+        neighbour = (neighbour_xyz[..., 0] * n_cell + neighbour_xyz[..., 1]) * n_cell + neighbour_xyz[..., 2]
+        valid = lane < counts_t[neighbour][..., None]                                         # [A, 27, W]
+        other = by_cell_t[torch.clamp(starts_t[neighbour][..., None] + lane, max=n_atoms - 1)]
+        delta = positions_t[other] - positions_t[atoms][:, None, None, :]
+        delta = delta - box * torch.round(delta / box)
+        distance2 = (delta[..., 0] * delta[..., 0] + delta[..., 1] * delta[..., 1]) + delta[..., 2] * delta[..., 2]
+        keep = valid & (distance2 < cutoff2) & (other != atoms[:, None, None])
+        a, s, w = torch.nonzero(keep, as_tuple=True)
+        keys.append(atoms[a] * n_atoms + other[a, s, w])
+        vectors.append(delta[a, s, w])
+    key, order = torch.sort(torch.cat(keys))
+    vector = torch.cat(vectors)[order]
+    dst = (key // n_atoms).cpu().numpy()
+    src = (key % n_atoms).cpu().numpy()
+    return WaterGraph(n_atoms, box, positions, types, src, dst, vector.cpu().numpy())
 
 
 # ---------------------------------------------------------------------------

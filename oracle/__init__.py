@@ -10,7 +10,8 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
 ``bench.py`` may import this package, and only as the checker.  The product
 (``bysj_amd``) never imports it and has no CPU fallback.
 
-Pinning status of each function (see tests/test_oracle_*.py):
+Pinning status of each function (tests/test_oracle_pinning.py; every
+function below has a check of its own, so none is parity unpinned):
 
 =============================  ==============================================
 segment_offsets                known answers of the reference tests, brute force
@@ -25,7 +26,10 @@ force_assembly_reference       reference loop, Newton's third law, exact
                                (math.fsum) fp64 brute force
 zonal_scatter_reference        loop oracle, exact normalise-after-sum known
                                answer, zero row 0, 1-D == 3-D inverse, empty
-zonal_scatter backward         autograd of the chain vs closed form
+zonal_scatter backward         fp64 closed form with exact sums (shared and
+                               unreferenced slots, both inverse shapes), the
+                               golden fixture of the reference's GIE test,
+                               four planted mistakes
 rmsnorm                        closed formula, fp64 brute force, zeros
 rmsnorm backward               autograd of the chain vs closed form
 =============================  ==============================================

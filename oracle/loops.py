@@ -116,6 +116,44 @@ def zonal_scatter_loop(zonal, radial, dst, radial_slot, inv_sqrt_deg):
     return out
 
 
+def zonal_scatter_backward_loop(grad_output, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    """float64 closed-form gradients of the GIE scatter, exactly rounded sums.
+
+    With n = dst[e], g = grad_output and pre[n, r+1, c] = sum_{dst[e]=n} zonal[e, r] radial[e, slot[r], c]:
+      grad_zonal[e, r]     = inv[n] * sum_c g[n, r+1, c] radial[e, slot[r], c]
+      grad_radial[e, s, c] = sum_{r: slot[r] = s} inv[n] g[n, r+1, c] zonal[e, r]   (shared slots summed)
+      grad_inv[n]          = sum_{r, c} g[n, r+1, c] pre[n, r+1, c]                  (row 0 of pre is zero)
+    grad_inv takes the shape of ``inv_sqrt_deg``.
+    """
+    g = _np(grad_output, np.float64)
+    zonal, radial = _np(zonal, np.float64), _np(radial, np.float64)
+    dst, slots = _np(dst, np.int64), _np(radial_slot, np.int64)
+    inv_shape = np.shape(_np(inv_sqrt_deg))
+    inv = _np(inv_sqrt_deg, np.float64).reshape(-1)
+    n_edges, n_rows = zonal.shape
+    n_radial, channels = radial.shape[1], radial.shape[2]
+    grad_zonal = np.zeros((n_edges, n_rows))
+    grad_radial = np.zeros((n_edges, n_radial, channels))
+    for e in range(n_edges):
+        n = dst[e]
+        for r in range(n_rows):
+            grad_zonal[e, r] = inv[n] * math.fsum(g[n, r + 1, c] * radial[e, slots[r], c] for c in range(channels))
+        for s in range(n_radial):
+            rows = [r for r in range(n_rows) if slots[r] == s]
+            for c in range(channels):
+                grad_radial[e, s, c] = math.fsum(inv[n] * g[n, r + 1, c] * zonal[e, r] for r in rows)
+    grad_inv = np.zeros(inv.shape[0])
+    for n in range(inv.shape[0]):
+        edges = np.nonzero(dst == n)[0]
+        terms = []
+        for r in range(n_rows):
+            for c in range(channels):
+                pre = math.fsum(zonal[e, r] * radial[e, slots[r], c] for e in edges)
+                terms.append(g[n, r + 1, c] * pre)
+        grad_inv[n] = math.fsum(terms)
+    return grad_zonal, grad_radial, grad_inv.reshape(inv_shape)
+
+
 def rmsnorm_loop(x, scale=None, eps=1e-6):
     """float64 RMSNorm row by row."""
     x = _np(x, np.float64)

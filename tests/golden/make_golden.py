@@ -203,6 +203,48 @@ def gie_cases() -> list[dict]:
     return cases
 
 
+def gie_backward_cases() -> list[dict]:
+    """Gradients of the test_gie.py fixture (tests/python/test_gie.py:19-30, 135-166).
+
+    The reference checks its backward against autograd of the forward chain
+    with an unseeded upstream of shape [2, 4, 3]; here the upstream is seeded
+    and the expectation is the closed form (``loops.zonal_scatter_backward_loop``),
+    with radial_slot = [0, 0, 1] so slot 0 is shared by rows 0 and 1 and its
+    gradient is a sum over both.  A second case takes the inverse degree as
+    [N, 1, 1] and a wider, irregular graph with an empty node and an
+    unreferenced radial slot (its gradient must be zero).
+    """
+    zonal = np.array([[0.2, -0.1, 0.3], [0.4, 0.5, -0.2], [-0.3, 0.6, 0.1], [0.7, -0.2, 0.4]], dtype=np.float32)
+    radial = (np.arange(24, dtype=np.float32) / np.float32(10)).reshape(4, 2, 3)
+    dst = np.array([1, 0, 1, 1], dtype=np.int64)
+    slots = np.array([0, 0, 1], dtype=np.int64)
+    inverse = np.array([0.7, 0.5], dtype=np.float32)
+    upstream = torch.randn(2, 4, 3, generator=torch.Generator().manual_seed(17)).numpy()
+    gz, gr, gi = loops.zonal_scatter_backward_loop(upstream, zonal, radial, dst, slots, inverse)
+    cases = [{
+        "name": "gie_backward_fixture", "op": "zonal_scatter_backward", "grad_output": _f32(upstream),
+        "zonal": _f32(zonal), "radial": _f32(radial), "dst": _i64(dst), "radial_slot": _i64(slots),
+        "inv_sqrt_deg": _f32(inverse), "grad_zonal_f64": _f64(gz), "grad_radial_f64": _f64(gr),
+        "grad_inv_sqrt_deg_f64": _f64(gi),
+    }]
+    generator = torch.Generator().manual_seed(23)
+    n_nodes, n_edges, n_rows, n_radial, channels = 5, 11, 4, 4, 2
+    dst = torch.randint(0, n_nodes - 1, (n_edges,), generator=generator).numpy()  # node 4 has no edge
+    zonal = torch.randn(n_edges, n_rows, generator=generator).numpy()
+    radial = torch.randn(n_edges, n_radial, channels, generator=generator).numpy()
+    slots = np.array([2, 0, 2, 1], dtype=np.int64)  # slot 2 shared, slot 3 unreferenced
+    inverse = (torch.rand(n_nodes, generator=generator) + 0.25).numpy().reshape(n_nodes, 1, 1)
+    upstream = torch.randn(n_nodes, n_rows + 1, channels, generator=generator).numpy()
+    gz, gr, gi = loops.zonal_scatter_backward_loop(upstream, zonal, radial, dst, slots, inverse)
+    cases.append({
+        "name": "gie_backward_shared_and_unreferenced_slots", "op": "zonal_scatter_backward",
+        "grad_output": _f32(upstream), "zonal": _f32(zonal), "radial": _f32(radial), "dst": _i64(dst),
+        "radial_slot": _i64(slots), "inv_sqrt_deg": _f32(inverse), "grad_zonal_f64": _f64(gz),
+        "grad_radial_f64": _f64(gr), "grad_inv_sqrt_deg_f64": _f64(gi),
+    })
+    return cases
+
+
 def rmsnorm_cases() -> list[dict]:
     """tests/python/test_rmsnorm.py:61-80."""
     generator = torch.Generator().manual_seed(5)
@@ -218,7 +260,7 @@ def rmsnorm_cases() -> list[dict]:
 
 def main() -> None:
     cases = csr_cases() + segment_sum_cases() + segment_softmax_cases() + force_cases() + gie_cases() \
-        + rmsnorm_cases()
+        + gie_backward_cases() + rmsnorm_cases()
     payload = {"source": "lipengfei1409/bysj tests/python known-answer cases; expectations from exact-sum loops",
                "cases": cases}
     lines = ",\n".join(json.dumps(case, separators=(",", ":")) for case in cases)

@@ -39,6 +39,12 @@ def assert_close_scaled(actual, expected, *, rtol=FP32_RTOL, scale=FP32_SCALE, w
         )
 
 
+def assert_gradient(actual, oracle, truth, what="") -> None:
+    """A float32 gradient against the fp32 oracle and the fp64 closed form, each at the fp32 rule."""
+    assert_close_scaled(actual, truth, what=f"{what} vs fp64 truth")
+    assert_close_scaled(actual, oracle, what=f"{what} vs fp32 oracle")
+
+
 def assert_fp64(actual, expected, what="") -> None:
     assert_close_scaled(actual, expected, rtol=FP64_RTOL, scale=FP64_SCALE, what=what)
 

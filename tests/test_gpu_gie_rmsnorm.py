@@ -16,7 +16,8 @@ from oracle import gie as gie_ref
 from oracle import loops
 from oracle.rmsnorm import rmsnorm as reference_rmsnorm
 from oracle.rmsnorm import rmsnorm_backward_reference
-from parity import announce, assert_bitwise, assert_close_scaled
+from closed_forms import gie_rmsnorm_chain_f64, rmsnorm_backward_f64, zonal_scatter_backward_f64
+from parity import announce, assert_bitwise, assert_close_scaled, assert_gradient
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -50,9 +51,10 @@ def test_gie_reference_fixture_forward_and_backward(degree_shape):
     up = torch.randn(2, 4, 3, generator=torch.Generator().manual_seed(0))
     grads = torch.autograd.grad(out, (z, r, inv), up.to(DEV))
     expected_grads = gie_ref.zonal_scatter_backward_reference(up, *inputs)
-    for label, actual, wanted in zip(("zonal", "radial", "inverse"), grads, expected_grads):
-        assert actual.shape == wanted.shape
-        assert_close_scaled(actual, wanted, rtol=2e-5, what=f"grad {label}")
+    truth = zonal_scatter_backward_f64(up, *inputs)
+    for label, actual, wanted, exact in zip(("zonal", "radial", "inverse"), grads, expected_grads, truth):
+        assert actual.shape == wanted.shape == exact.shape
+        assert_gradient(actual, wanted, exact, f"grad {label}")
 
 
 def test_gie_normalise_after_sum_known_answer_and_inverse_gradient():
@@ -106,8 +108,9 @@ def test_gie_water_box(primary, shuffle):
     up = torch.randn(out.shape, generator=torch.Generator().manual_seed(1))
     grads = torch.autograd.grad(out, (z, r, inv), up.to(DEV))
     expected = gie_ref.zonal_scatter_backward_reference(up, *inputs)
-    for label, actual, wanted in zip(("zonal", "radial", "inverse"), grads, expected):
-        assert_close_scaled(actual, wanted, rtol=2e-5, what=f"grad {label}")
+    truth = zonal_scatter_backward_f64(up, *inputs)
+    for label, actual, wanted, exact in zip(("zonal", "radial", "inverse"), grads, expected, truth):
+        assert_gradient(actual, wanted, exact, f"grad {label}")
 
 
 def test_gie_forward_against_fp64_truth():
@@ -158,8 +161,9 @@ def test_rmsnorm_gradients(shape):
     out = kernels.rmsnorm(xd, sd, eps=1e-5)
     grads = torch.autograd.grad(out, (xd, sd), up.to(DEV))
     e_x, e_s = rmsnorm_backward_reference(up, x, scale, eps=1e-5)
-    assert_close_scaled(grads[0], e_x, rtol=3e-5, what="grad_x")
-    assert_close_scaled(grads[1], e_s, rtol=3e-5, what="grad_scale")
+    t_x, t_s = rmsnorm_backward_f64(up, x, scale, eps=1e-5)
+    assert_gradient(grads[0], e_x, t_x, "grad_x")
+    assert_gradient(grads[1], e_s, t_s, "grad_scale")
     again = torch.autograd.grad(kernels.rmsnorm(xd, sd, eps=1e-5), (xd, sd), up.to(DEV))
     assert_bitwise(again[1], grads[1], "grad_scale run-to-run")
 
@@ -184,7 +188,8 @@ def test_rmsnorm_zero_input_no_scale_and_stream():
     grad_x, grad_scale = _C.rmsnorm_backward(torch.ones_like(y), xs.to(DEV), empty, inverse_rms, False)
     assert grad_scale.numel() == 0
     e_x, _ = rmsnorm_backward_reference(torch.ones(9, 131), xs, None, 1e-6)
-    assert_close_scaled(grad_x, e_x, rtol=3e-5, what="grad_x without scale")
+    t_x, _ = rmsnorm_backward_f64(torch.ones(9, 131), xs, None, 1e-6)
+    assert_gradient(grad_x, e_x, t_x, "grad_x without scale")
 
 
 def test_gie_then_rmsnorm_config3_reduced():
@@ -252,35 +257,17 @@ def test_gie_rmsnorm_fused_matches_two_operators(primary, use_scale, shuffle):
     cs = None if scale is None else scale.clone().requires_grad_(True)
     expected_out = _oracle_gie_rmsnorm(cz, cr, inputs[2], inputs[3], cinv, cs, 1e-6)
     expected = torch.autograd.grad(expected_out, (cz, cr, cinv) + (() if cs is None else (cs,)), up)
-    for label, actual, wanted in zip(("zonal", "radial", "inverse", "scale"), grads, expected):
+    truth, terms = gie_rmsnorm_chain_f64(inputs, scale, up, 1e-6)
+    for label, actual, wanted, exact in zip(("zonal", "radial", "inverse", "scale"), grads, expected, truth):
         if label == "inverse":
             continue
-        assert_close_scaled(actual, wanted, rtol=2e-5, scale=2e-5, what=f"grad {label}")
+        assert_gradient(actual, wanted, exact, f"grad {label}")
     # RMSNorm is scale invariant, so d y / d inv_sqrt_deg is a sum of (n_rows + 1) * channels terms
-    # that cancel (exactly, but for eps): fp32 results are rounding noise around a tiny value.  Check
-    # it against the chain in float64, to 2e-5 of the node's sum of absolute terms.
-    truth, terms = _inverse_gradient_fp64(inputs, scale, up, 1e-6)
-    error = (grads[2].double().cpu() - truth).abs()
-    assert bool((error <= 2e-5 * terms + 1e-12).all()), f"grad inverse: worst {float((error / terms).max())}"
-
-
-def _inverse_gradient_fp64(inputs, scale, up, eps):
-    """d(sum up * y)/d inv_sqrt_deg of zonal_scatter -> rmsnorm in float64, and per node the sum
-    of |d(loss)/d x * S| over the row (S the unnormalised scatter), the scale of its terms."""
-    zonal, radial, dst, slots, inverse = (t.double() if t.is_floating_point() else t for t in inputs)
-    n_nodes, n_rows, channels = inverse.shape[0], zonal.shape[1], radial.shape[2]
-    gathered = radial.gather(1, slots.reshape(1, -1, 1).expand(zonal.shape[0], n_rows, channels))
-    summed = torch.zeros((n_nodes, n_rows + 1, channels), dtype=torch.float64)
-    summed[:, 1:, :].index_add_(0, dst, zonal.unsqueeze(-1) * gathered)
-    inv = inverse.reshape(-1).clone().requires_grad_(True)
-    x = (summed * inv.reshape(-1, 1, 1)).reshape(n_nodes, -1)
-    x.retain_grad()
-    y = x * torch.rsqrt(x.pow(2).mean(dim=1, keepdim=True) + eps)
-    if scale is not None:
-        y = y * scale.double()
-    (y * up.double().reshape(n_nodes, -1)).sum().backward()
-    terms = (x.grad * summed.reshape(n_nodes, -1)).abs().sum(dim=1)
-    return inv.grad.detach(), terms.detach()
+    # that cancel (exactly, but for eps): fp32 results are rounding noise around a tiny value, and
+    # max|ref| says nothing about their size.  Check it against the chain in float64, to 1e-5 of
+    # the node's sum of absolute terms (the fp32 rule's relative bar, on the terms that are summed).
+    error = (grads[2].double().cpu() - truth[2]).abs()
+    assert bool((error <= 1e-5 * terms + 1e-12).all()), f"grad inverse: worst {float((error / terms).max())}"
 
 
 def test_gie_rmsnorm_unfused_shapes_and_empty_edges():

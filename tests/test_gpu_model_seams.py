@@ -13,8 +13,8 @@ import pytest
 import torch
 
 from bysj_amd.model import fused_deepmd
-from parity import announce, assert_close_scaled
-from seam_fakes import FakeBlock, FakeModel, softmax_namespace
+from parity import announce, assert_close_scaled, assert_gradient
+from seam_fakes import FakeBlock, FakeModel, softmax_namespace, stock_softmax
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -50,9 +50,14 @@ def test_softmax_seam_on_gfx950(clean):
     fused_deepmd.uninstall()
     expected = space.segment_envelope_gated_softmax(logits, env, dst, 512, bias, 1e-6)
     want = torch.autograd.grad(expected, leaves, upstream)
+    # the stock path once more in float64 on the CPU: the truth both are held to
+    leaves64 = tuple(t.detach().cpu().double().requires_grad_(True) for t in leaves)
+    exact = stock_softmax(leaves64[0], leaves64[1], dst.cpu(), 512, leaves64[2], 1e-6)
+    truth = torch.autograd.grad(exact, leaves64, upstream.cpu().double())
     assert_close_scaled(alpha, expected, what="alpha")
-    for got, ref, name in zip(grads, want, ("grad_logits", "grad_env", "grad_bias")):
-        assert_close_scaled(got, ref, rtol=2e-5, scale=2e-5, what=name)
+    assert_close_scaled(alpha, exact, what="alpha vs fp64 truth")
+    for got, ref, exact_grad, name in zip(grads, want, truth, ("grad_logits", "grad_env", "grad_bias")):
+        assert_gradient(got, ref, exact_grad, name)
 
 
 @pytest.mark.parametrize("gate", [False, True])
@@ -79,6 +84,16 @@ def test_envelope_seam_on_gfx950(clean, gate):
     fused_deepmd.uninstall()
     expected = block.forward_envelope(x, cache, None)
     want = torch.autograd.grad(expected, leaves, upstream)
+    # the stock path once more in float64 on the CPU: the truth both are held to
+    leaves64 = tuple(t.detach().cpu().double().requires_grad_(True) for t in leaves)
+    cache64 = type("EdgeCache", (), {})()
+    cache64.dst = dst.cpu()
+    cache64.edge_env = leaves64[1]
+    cache64.inv_sqrt_deg = cache.inv_sqrt_deg.cpu().double()
+    cache64.edge_src_gate = leaves64[2] if gate else None
+    exact = FakeBlock(leaves64[0]).forward_envelope(x.cpu().double(), cache64, None)
+    truth = torch.autograd.grad(exact, leaves64, upstream.cpu().double())
     assert_close_scaled(out, expected, what="aggregation")
-    for got, ref, name in zip(grads, want, ("grad_message", "grad_edge_env", "grad_gate")):
-        assert_close_scaled(got, ref, rtol=2e-5, scale=2e-5, what=name)
+    assert_close_scaled(out, exact, what="aggregation vs fp64 truth")
+    for got, ref, exact_grad, name in zip(grads, want, truth, ("grad_message", "grad_edge_env", "grad_gate")):
+        assert_gradient(got, ref, exact_grad, name)

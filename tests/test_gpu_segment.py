@@ -18,7 +18,8 @@ from bysj_amd import kernels, workloads
 from oracle import gie as gie_ref
 from oracle import loops
 from oracle import segment as ref
-from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
+from closed_forms import segment_softmax_backward_f64, segment_sum_backward_f64
+from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64, assert_gradient
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -141,6 +142,32 @@ def test_segment_sum_with_order_is_bit_exact(channels):
     assert_bitwise(out, ref.segment_sum_reference(src, dst, offsets, w, s), "segment_sum with order")
 
 
+@pytest.mark.parametrize("channels", [64, 128, 256])
+def test_segment_sum_nan_edge_scale_propagates_with_order(channels):
+    """A NaN in edge_scale reaches the output of its segment, with or without an order, on the
+    small-grid staged path (fewer than 4096 segments, 64-256 channels) as in the oracle's
+    index_add_ chain: the staged kernel's skip flag for bad order entries is not a NaN weight."""
+    announce("segment_sum NaN edge_scale", channels)
+    degrees = workloads.poisson_degrees(211, 12.0, seed=channels)
+    dst_sorted = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    dst, order, offsets = _shuffled(dst_sorted, seed=channels)
+    gen = torch.Generator().manual_seed(channels)
+    src = torch.randn(dst.numel(), channels, generator=gen)
+    w = torch.rand(dst.numel(), generator=gen) + 0.5
+    w[[3, 500, dst.numel() - 1]] = float("nan")
+    s = torch.rand(211, generator=gen) + 0.5
+    expected = ref.segment_sum_reference(src, dst, offsets, w, s)
+    assert bool(torch.isnan(expected).any())
+    with_order = kernels.segment_sum(src.to(DEV), dst.to(DEV), offsets.to(DEV), w.to(DEV), s.to(DEV),
+                                     order=order.to(DEV))
+    assert_bitwise(with_order, expected, "NaN edge_scale with order vs oracle")
+    # the same edges in their grouped (natural) order, without an order argument
+    grouped = order.to(DEV)
+    natural = kernels.segment_sum(src.to(DEV)[grouped].contiguous(), dst_sorted.to(DEV), offsets.to(DEV),
+                                  w.to(DEV)[grouped].contiguous(), s.to(DEV))
+    assert_bitwise(natural, with_order, "order=None on the grouped copy")
+
+
 def test_segment_sum_large_graph_against_fp64_truth():
     announce("segment_sum fp64 truth")
     gen = torch.Generator().manual_seed(11)
@@ -232,9 +259,11 @@ def test_segment_sum_backward_matches_autograd(channels, use_order):
     out = kernels.segment_sum(x, dst.to(DEV), offsets.to(DEV), wd, sd, order=None if order is None else order.to(DEV))
     grads = torch.autograd.grad(out, (x, wd, sd), g.to(DEV))
     e_src, e_w, e_s = ref.segment_sum_backward_reference(g, src, dst, offsets, w, s)
+    t_src, t_w, t_s = segment_sum_backward_f64(g, src, dst, 53, w, s)
     assert_bitwise(grads[0], e_src, "grad_src")
-    assert_close_scaled(grads[1], e_w, what="grad_edge_scale")
-    assert_close_scaled(grads[2], e_s, what="grad_node_scale")
+    assert_close_scaled(grads[0], t_src, what="grad_src vs fp64 truth")
+    assert_gradient(grads[1], e_w, t_w, "grad_edge_scale")
+    assert_gradient(grads[2], e_s, t_s, "grad_node_scale")
 
 
 def test_segment_sum_node_scale_shape_and_empty_edges_backward():
@@ -275,9 +304,10 @@ def test_segment_softmax_reference_case_forward_and_backward():
     assert_close_scaled(alpha, e_alpha, what="alpha")
     assert_close_scaled(null_alpha, e_null, what="null_alpha")
     e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
-    assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
-    assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
-    assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+    t_gl, t_ge, t_gn = segment_softmax_backward_f64(up, logit, env, dst, 4, null_logit, up_null)
+    assert_gradient(grads[0], e_gl, t_gl, "grad_logit")
+    assert_gradient(grads[1], e_ge, t_ge, "grad_env")
+    assert_gradient(grads[2], e_gn, t_gn, "grad_null")
     per_segment = torch.zeros(4, 16).index_add_(0, dst, alpha.detach().cpu())
     assert_close_scaled(per_segment + null_alpha.detach().cpu(), torch.ones(4, 16), what="sum to one")
     assert alpha[1].count_nonzero().item() == 0 and alpha[3].count_nonzero().item() == 0
@@ -328,10 +358,11 @@ def test_segment_softmax_with_hubs(channels, null, use_order):
         outputs, cotangents, inputs = (alpha,), (up.to(DEV),), (x, e)
     grads = torch.autograd.grad(outputs, inputs, cotangents)
     e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
-    assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
-    assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
+    t_gl, t_ge, t_gn = segment_softmax_backward_f64(up, logit, env, dst, 67, null_logit, up_null)
+    assert_gradient(grads[0], e_gl, t_gl, "grad_logit")
+    assert_gradient(grads[1], e_ge, t_ge, "grad_env")
     if null:
-        assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+        assert_gradient(grads[2], e_gn, t_gn, "grad_null")
 
 
 @pytest.mark.parametrize("channels", [1, 3, 8, 16, 64, 256])
@@ -376,9 +407,10 @@ def test_segment_softmax_planned_and_unplanned_paths(channels, use_order):
     for x, y, what in zip(g1, g0, ("grad_logit", "grad_null", "grad_env")):
         assert_bitwise(x, y, f"planned {what}")
     e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
-    assert_close_scaled(g1[0], e_gl, rtol=2e-5, what="grad_logit")
-    assert_close_scaled(g1[1], e_gn, rtol=2e-5, what="grad_null")
-    assert_close_scaled(g1[2], e_ge, rtol=2e-5, what="grad_env")
+    t_gl, t_ge, t_gn = segment_softmax_backward_f64(up, logit, env, dst, n, null_logit, up_null)
+    assert_gradient(g1[0], e_gl, t_gl, "grad_logit")
+    assert_gradient(g1[1], e_gn, t_gn, "grad_null")
+    assert_gradient(g1[2], e_ge, t_ge, "grad_env")
 
 
 def test_segment_softmax_plan_lists_the_long_segments():
@@ -515,11 +547,12 @@ def test_segment_softmax_fully_masked_long_segments(channels):
             outputs, cotangents, inputs = (alpha,), (up.to(DEV),), (x, e)
         grads = torch.autograd.grad(outputs, inputs, cotangents)
         e_gl, e_ge, e_gn = ref.segment_softmax_backward_reference(up, logit, env, dst, offsets, null_logit, up_null)
-        assert_close_scaled(grads[0], e_gl, rtol=2e-5, what="grad_logit")
-        assert_close_scaled(grads[1], e_ge, rtol=2e-5, what="grad_env")
+        t_gl, t_ge, t_gn = segment_softmax_backward_f64(up, logit, env, dst, 6, null_logit, up_null)
+        assert_gradient(grads[0], e_gl, t_gl, "grad_logit")
+        assert_gradient(grads[1], e_ge, t_ge, "grad_env")
         assert grads[1][5:705].count_nonzero().item() == 0 and grads[1][708:5708].count_nonzero().item() == 0
         if null:
-            assert_close_scaled(grads[2], e_gn, rtol=2e-5, what="grad_null")
+            assert_gradient(grads[2], e_gn, t_gn, "grad_null")
 
 
 def test_segment_softmax_config2_full_size_and_determinism():

@@ -21,6 +21,7 @@ import numpy as np
 import pytest
 import torch
 
+import closed_forms
 from golden_cases import load_cases
 from oracle import gie as gie_ref
 from oracle import loops
@@ -102,6 +103,16 @@ def check_gie(zonal_scatter):
             assert_bitwise(out[0, 1], case["exact_f32_row1"], "normalise after the destination sum")
 
 
+def check_gie_backward(backward):
+    for case in load_cases("zonal_scatter_backward"):
+        grad_zonal, grad_radial, grad_inv = backward(case["grad_output"], case["zonal"], case["radial"], case["dst"],
+                                                     case["radial_slot"], case["inv_sqrt_deg"])
+        assert_close_scaled(grad_zonal, case["grad_zonal_f64"], what=case["name"] + " grad_zonal")
+        assert_close_scaled(grad_radial, case["grad_radial_f64"], what=case["name"] + " grad_radial")
+        assert tuple(grad_inv.shape) == tuple(case["inv_sqrt_deg"].shape), case["name"] + " grad_inv shape"
+        assert_close_scaled(grad_inv, case["grad_inv_sqrt_deg_f64"], what=case["name"] + " grad_inv_sqrt_deg")
+
+
 def check_rmsnorm(rmsnorm):
     for case in load_cases("rmsnorm"):
         out = rmsnorm(case["x"], case["scale"], case["eps"])
@@ -139,6 +150,10 @@ def test_force_assembly_known_answers():
 
 def test_gie_known_answers():
     check_gie(gie_ref.zonal_scatter_reference)
+
+
+def test_gie_backward_closed_form():
+    check_gie_backward(gie_ref.zonal_scatter_backward_reference)
 
 
 def test_rmsnorm_known_answers():
@@ -306,6 +321,31 @@ def test_gie_brute_force_and_shapes():
         gie_ref.zonal_scatter_reference(zonal, radial, dst, slots + 3, inverse)
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_gie_backward_brute_force(seed):
+    gen = torch.Generator().manual_seed(40 + seed)
+    nodes, edges, rows, radial_slots, channels = 7, 30, 6, 4, 3
+    dst = torch.randint(0, nodes - 1, (edges,), generator=gen)  # the last node has no edge
+    zonal = torch.randn(edges, rows, generator=gen)
+    radial = torch.randn(edges, radial_slots, channels, generator=gen)
+    slots = torch.randint(0, radial_slots - 1, (rows,), generator=gen)  # shared slots; the last one unreferenced
+    inverse = torch.rand(nodes, generator=gen) + 0.2
+    grad = torch.randn(nodes, rows + 1, channels, generator=gen)
+    for shape in ((nodes,), (nodes, 1, 1)):
+        got = gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, dst, slots, inverse.reshape(shape))
+        expected = loops.zonal_scatter_backward_loop(grad, zonal, radial, dst, slots, inverse.reshape(shape))
+        for actual, truth, label in zip(got, expected, ("grad_zonal", "grad_radial", "grad_inv")):
+            assert tuple(actual.shape) == truth.shape, label
+            assert_close_scaled(actual, truth, what=label)
+        assert int(got[1][:, radial_slots - 1].count_nonzero()) == 0, "unreferenced slot has a gradient"
+        # row 0 of the output is 0 * inv: its cotangent reaches nothing
+        shifted = grad.clone()
+        shifted[:, 0] += 5.0
+        again = gie_ref.zonal_scatter_backward_reference(shifted, zonal, radial, dst, slots, inverse.reshape(shape))
+        for first, second in zip(got, again):
+            torch.testing.assert_close(first, second, rtol=0, atol=0)
+
+
 def test_rmsnorm_brute_force_and_backward_closed_form():
     gen = torch.Generator().manual_seed(9)
     x = torch.randn(4, 3, 33, generator=gen)
@@ -323,6 +363,127 @@ def test_rmsnorm_brute_force_and_backward_closed_form():
     for eps in (0.0, -1.0, float("inf"), float("nan")):
         with pytest.raises(ValueError, match="eps"):
             rms_ref.rmsnorm(x, scale, eps)
+
+
+# ---------------------------------------------------------------------------
+# 2b. the float64 closed forms the GPU gradient tests use as truth
+# ---------------------------------------------------------------------------
+
+def _assert_f64(actual, expected, what):
+    assert_close_scaled(actual, expected, rtol=1e-12, scale=1e-12, what=what)
+
+
+def test_closed_forms_against_golden_cases():
+    for case in load_cases("segment_softmax"):
+        alpha, null_alpha = closed_forms.segment_softmax_f64(case["logit"], case["env"], case["dst"],
+                                                             case["offsets"].numel() - 1, case["null_logit"])
+        _assert_f64(alpha, case["alpha_f64"], case["name"] + " alpha")
+        if case["null_logit"] is not None:
+            _assert_f64(null_alpha, case["null_alpha_f64"], case["name"] + " null_alpha")
+    for case in load_cases("segment_softmax_backward"):
+        gl, ge, gn = closed_forms.segment_softmax_backward_f64(case["grad_alpha"], case["logit"], case["env"],
+                                                               case["dst"], case["offsets"].numel() - 1,
+                                                               case["null_logit"], case["grad_null_alpha"])
+        _assert_f64(gl, case["grad_logit_f64"], "grad_logit")
+        _assert_f64(ge, case["grad_env_f64"], "grad_env")
+        _assert_f64(gn, case["grad_null_logit_f64"], "grad_null")
+    for case in load_cases("segment_sum_backward"):
+        got = closed_forms.segment_sum_backward_f64(case["grad_out"], case["src"], case["dst"],
+                                                    case["offsets"].numel() - 1, case["edge_scale"],
+                                                    case["node_scale"])
+        for actual, key in zip(got, ("grad_src_f64", "grad_edge_scale_f64", "grad_node_scale_f64")):
+            _assert_f64(actual, case[key], key)
+    for case in load_cases("zonal_scatter_backward"):
+        got = closed_forms.zonal_scatter_backward_f64(case["grad_output"], case["zonal"], case["radial"],
+                                                      case["dst"], case["radial_slot"], case["inv_sqrt_deg"])
+        for actual, key in zip(got, ("grad_zonal_f64", "grad_radial_f64", "grad_inv_sqrt_deg_f64")):
+            _assert_f64(actual, case[key], case["name"] + " " + key)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_closed_forms_against_exact_loops_and_autograd(seed):
+    logit, env, dst, offsets, null = _softmax_inputs(seed, masked_fraction=0.25)
+    n_nodes = offsets.numel() - 1
+    for with_null in (False, True):
+        nl = null if with_null else None
+        alpha, null_alpha = closed_forms.segment_softmax_f64(logit, env, dst, n_nodes, nl)
+        e_alpha, e_null = loops.segment_softmax_loop(logit, env, dst, n_nodes, nl)
+        _assert_f64(alpha, e_alpha, "alpha")
+        if with_null:
+            _assert_f64(null_alpha, e_null, "null alpha")
+        # the closed-form backward against autograd of the float64 forward
+        gen = torch.Generator().manual_seed(seed)
+        ga = torch.randn(alpha.shape, generator=gen, dtype=torch.float64)
+        gn = torch.randn((n_nodes, logit.shape[1]), generator=gen, dtype=torch.float64) if with_null else None
+        leaves = [logit.double().requires_grad_(True), env.double().requires_grad_(True)]
+        if with_null:
+            leaves.append(null.double().requires_grad_(True))
+        # the closed forms detach their inputs: autograd runs through a graph-keeping restatement
+        a, na = _softmax_f64_differentiable(leaves[0], leaves[1], dst, n_nodes, leaves[2] if with_null else None)
+        outs, cots = [a], [ga]
+        if with_null:
+            outs.append(na)
+            cots.append(gn)
+        auto = torch.autograd.grad(outs, leaves, cots)
+        gl, ge, gnull = closed_forms.segment_softmax_backward_f64(ga, logit, env, dst, n_nodes, nl, gn)
+        _assert_f64(gl, auto[0], "grad_logit vs autograd")
+        _assert_f64(ge, auto[1], "grad_env vs autograd")
+        if with_null:
+            _assert_f64(gnull, auto[2], "grad_null vs autograd")
+
+    gen = torch.Generator().manual_seed(60 + seed)
+    nodes, edges, rows, radial_slots, channels = 6, 25, 5, 4, 3
+    gdst = torch.randint(0, nodes, (edges,), generator=gen)
+    zonal = torch.randn(edges, rows, generator=gen)
+    radial = torch.randn(edges, radial_slots, channels, generator=gen)
+    slots = torch.randint(0, radial_slots, (rows,), generator=gen)
+    inverse = (torch.rand(nodes, generator=gen) + 0.2).reshape(nodes, 1, 1)
+    grad = torch.randn(nodes, rows + 1, channels, generator=gen)
+    got = closed_forms.zonal_scatter_backward_f64(grad, zonal, radial, gdst, slots, inverse)
+    exact = loops.zonal_scatter_backward_loop(grad, zonal, radial, gdst, slots, inverse)
+    for actual, truth, label in zip(got, exact, ("grad_zonal", "grad_radial", "grad_inv")):
+        assert tuple(actual.shape) == truth.shape
+        _assert_f64(actual, truth, label)
+
+    sdst, soffsets = _random_graph(seed)
+    sn = soffsets.numel() - 1
+    src = torch.randn(sdst.numel(), 4, generator=gen)
+    w = torch.rand(sdst.numel(), generator=gen) + 0.5
+    s = torch.rand(sn, generator=gen) + 0.5
+    g = torch.randn(sn, 4, generator=gen)
+    leaves = [src.double().requires_grad_(True), w.double().requires_grad_(True), s.double().requires_grad_(True)]
+    out = torch.zeros(sn, 4, dtype=torch.float64).index_add_(0, sdst, leaves[0] * leaves[1].reshape(-1, 1))
+    out = out * leaves[2].reshape(-1, 1)
+    auto = torch.autograd.grad(out, leaves, g.double())
+    for actual, truth, label in zip(closed_forms.segment_sum_backward_f64(g, src, sdst, sn, w, s), auto,
+                                    ("grad_src", "grad_w", "grad_s")):
+        _assert_f64(actual, truth, label)
+
+    x = torch.randn(3, 2, 19, generator=gen)
+    scale = torch.rand(19, generator=gen) + 0.5
+    g = torch.randn(x.shape, generator=gen)
+    leaves = [x.double().requires_grad_(True), scale.double().requires_grad_(True)]
+    y = leaves[0] / torch.sqrt(leaves[0].pow(2).mean(-1, keepdim=True) + 1e-6) * leaves[1]
+    auto = torch.autograd.grad(y, leaves, g.double())
+    gx, gs = closed_forms.rmsnorm_backward_f64(g, x, scale, 1e-6)
+    _assert_f64(gx, auto[0], "rmsnorm grad_x")
+    _assert_f64(gs, auto[1], "rmsnorm grad_scale")
+
+
+def _softmax_f64_differentiable(logit, env, dst, n_nodes, null):
+    valid = (env > 0).reshape(-1, 1)
+    effective = torch.where(valid, logit + 2.0 * torch.log(env.clamp_min(1e-30)).reshape(-1, 1),
+                            torch.full_like(logit, float("-inf")))
+    peak = torch.full((n_nodes, logit.shape[1]), float("-inf"), dtype=torch.float64)
+    peak = peak.scatter_reduce(0, dst.reshape(-1, 1).expand_as(logit), effective.detach(), reduce="amax")
+    if null is not None:
+        peak = torch.maximum(peak, null.detach())
+    peak = torch.where(torch.isfinite(peak), peak, torch.zeros_like(peak))
+    weight = torch.where(valid, torch.exp(effective - peak[dst]), torch.zeros_like(effective))
+    null_weight = torch.exp(null - peak) if null is not None else torch.zeros_like(peak)
+    total = torch.zeros_like(peak).index_add(0, dst, weight) + null_weight
+    total = torch.where(total > 0, total, torch.ones_like(total))
+    return weight / total[dst], (null_weight / total if null is not None else None)
 
 
 # ---------------------------------------------------------------------------
@@ -375,6 +536,39 @@ def _gie_wrong_slot(zonal, radial, dst, radial_slot, inv_sqrt_deg):
     return gie_ref.zonal_scatter_reference(zonal, radial, dst, torch.zeros_like(radial_slot), inv_sqrt_deg)
 
 
+def _gie_backward_without_inverse(grad, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    # grad_zonal taken from the unnormalised message: inv[n] dropped
+    grad_zonal, grad_radial, grad_inv = gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, dst,
+                                                                                 radial_slot, inv_sqrt_deg)
+    return grad_zonal / inv_sqrt_deg.reshape(-1)[dst].reshape(-1, 1), grad_radial, grad_inv
+
+
+def _gie_backward_shared_slot_overwritten(grad, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    # a scatter that assigns instead of accumulating: the last row sharing a slot wins
+    grad_zonal, _, grad_inv = gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, dst, radial_slot,
+                                                                       inv_sqrt_deg)
+    inverse = inv_sqrt_deg.reshape(-1)
+    grad_radial = torch.zeros_like(radial)
+    for r in range(zonal.shape[1]):
+        grad_radial[:, int(radial_slot[r])] = (inverse[dst].reshape(-1, 1) * grad[dst, r + 1]
+                                               * zonal[:, r].reshape(-1, 1))
+    return grad_zonal, grad_radial, grad_inv
+
+
+def _gie_backward_inverse_from_output(grad, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    # grad_inv as the dot product with the normalised output instead of the pre-norm sum
+    grad_zonal, grad_radial, _ = gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, dst, radial_slot,
+                                                                          inv_sqrt_deg)
+    out = gie_ref.zonal_scatter_reference(zonal, radial, dst, radial_slot, inv_sqrt_deg)
+    return grad_zonal, grad_radial, (grad * out).sum((1, 2)).reshape(inv_sqrt_deg.shape)
+
+
+def _gie_backward_row_zero(grad, zonal, radial, dst, radial_slot, inv_sqrt_deg):
+    # reading the cotangent of row r instead of row r + 1 (row 0 is the reserved one)
+    shifted = torch.cat([grad[:, 1:], grad[:, :1]], dim=1)
+    return gie_ref.zonal_scatter_backward_reference(shifted, zonal, radial, dst, radial_slot, inv_sqrt_deg)
+
+
 def _rmsnorm_without_eps(x, scale=None, eps=1e-6):
     out = x * torch.rsqrt(x.square().mean(-1, keepdim=True))
     return out if scale is None else out * scale
@@ -407,6 +601,10 @@ PLANTED = [
     ("force: transposed virial", lambda: check_force(_force_transposed_virial)),
     ("gie normalises before the sum", lambda: check_gie(_gie_normalise_first)),
     ("gie ignores radial_slot", lambda: check_gie(_gie_wrong_slot)),
+    ("gie backward drops inv in grad_zonal", lambda: check_gie_backward(_gie_backward_without_inverse)),
+    ("gie backward overwrites a shared slot", lambda: check_gie_backward(_gie_backward_shared_slot_overwritten)),
+    ("gie backward takes grad_inv from the output", lambda: check_gie_backward(_gie_backward_inverse_from_output)),
+    ("gie backward reads the wrong cotangent row", lambda: check_gie_backward(_gie_backward_row_zero)),
     ("rmsnorm without eps", lambda: check_rmsnorm(_rmsnorm_without_eps)),
     ("rmsnorm with sum instead of mean", lambda: check_rmsnorm(_rmsnorm_sum_not_mean)),
 ]
