@@ -12,6 +12,9 @@
 // for its fixed set of rows (two rows loaded per round), the four waves of a
 // workgroup add theirs in LDS, the workgroup partials go to the workspace and
 // one wave per group of columns sums them -- every order fixed.
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 
 namespace dpa4k {
@@ -20,6 +23,18 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 constexpr int kPartialWaves = 3072;   // waves of the grad_scale backward (resident at 3 per SIMD)
+constexpr int64_t kRegisterMaxWidth = 64 * 16 * 4;  // widest row the register kernels hold
+
+// Column partials of dpa4k_rmsnorm_backward_noalloc: one row per workgroup of
+// the grad_scale backward (at most kPartialWaves / kWaves of them) of at most
+// kRegisterMaxWidth floats, the most the register kernels ever write
+// (DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES).  Every device the library runs on
+// holds its own copy until the process ends.  Host code never uses this name
+// as an address: it reaches the array through the per-device pointer that
+// scratch_for_stream() obtains from hipGetSymbolAddress.
+static_assert(int64_t(kPartialWaves / kWaves) * kRegisterMaxWidth * 4 == DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES,
+              "the header's scratch size must match the partial matrix bound");
+__device__ __align__(256) float scratch[DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES / 4];
 
 __device__ __forceinline__ float inverse_rms_of(float sum_squares, int64_t width, float eps) {
   return 1.0f / sqrtf(sum_squares / static_cast<float>(width) + eps);
@@ -315,43 +330,54 @@ unsigned int partial_blocks(int64_t rows) {
   return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > cap ? cap : wanted));
 }
 
-}  // namespace
-}  // namespace dpa4k
-
-using namespace dpa4k;
-
-extern "C" int dpa4k_rmsnorm_forward(const float* x, const float* scale, float* y,
-                                     float* inverse_rms, int64_t rows, int64_t width, float eps,
-                                     dpa4k_stream_t stream_handle) {
-  clear_error();
-  if (rows < 0) return fail(DPA4K_EINVAL, "RMSNorm: negative row count");
-  if (width <= 0) return fail(DPA4K_EINVAL, "RMSNorm feature dimension must be positive");
-  if (!(eps > 0.0f) || !(eps < INFINITY))
-    return fail(DPA4K_EINVAL, "RMSNorm eps must be a finite positive number");
-  if (!grid_fits((rows + kWaves - 1) / kWaves, kBlock))
-    return fail(DPA4K_EINVAL, "RMSNorm row count exceeds the launch limit");
-  if (rows == 0) return DPA4K_OK;
-  if (x == nullptr || y == nullptr || inverse_rms == nullptr)
-    return fail(DPA4K_EINVAL, "RMSNorm: null pointer");
-  hipStream_t stream = as_stream(stream_handle);
-  const bool vec4 = width % 4 == 0 && aligned16(x) && aligned16(y) &&
-                    (scale == nullptr || aligned16(scale));
-  const int64_t chunks = vec4 ? width / 4 : width;
-  const int cpl = per_lane_for(chunks);
-  return vec4 ? launch_forward<4>(cpl, x, scale, y, inverse_rms, rows, width, eps, stream)
-              : launch_forward<1>(cpl, x, scale, y, inverse_rms, rows, width, eps, stream);
+// Device address of `scratch` on the device that runs `stream`, looked up once
+// per device with that device current (the null stream runs on the current
+// device).  Sets `out` or returns an error status.
+int scratch_for_stream(hipStream_t stream, float*& out) {
+  static std::mutex lock;
+  static std::vector<float*> per_device;
+  int current = 0;
+  if (int s = hip_status(hipGetDevice(&current), "hipGetDevice")) return s;
+  int device = current;
+  if (stream != nullptr) {
+    if (int s = hip_status(hipStreamGetDevice(stream, &device), "hipStreamGetDevice")) return s;
+  }
+  std::lock_guard<std::mutex> guard(lock);
+  if (per_device.empty()) {
+    int count = 0;
+    if (int s = hip_status(hipGetDeviceCount(&count), "hipGetDeviceCount")) return s;
+    per_device.assign(static_cast<size_t>(count > 0 ? count : 1), nullptr);
+  }
+  if (device < 0 || static_cast<size_t>(device) >= per_device.size())
+    return fail(DPA4K_EHIP, "RMSNorm backward: stream on unknown device %d", device);
+  if (per_device[device] == nullptr) {
+    if (device != current) {
+      if (int s = hip_status(hipSetDevice(device), "hipSetDevice")) return s;
+    }
+    void* address = nullptr;
+    const hipError_t found = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (device != current) {
+      if (int s = hip_status(hipSetDevice(current), "hipSetDevice")) return s;
+    }
+    if (int s = hip_status(found, "hipGetSymbolAddress(scratch)")) return s;
+    if (address == nullptr) return fail(DPA4K_EHIP, "hipGetSymbolAddress(scratch) returned a null address");
+    per_device[device] = static_cast<float*>(address);
+  }
+  out = per_device[device];
+  return DPA4K_OK;
 }
 
-extern "C" size_t dpa4k_rmsnorm_backward_workspace_size(int64_t rows, int64_t width) {
+size_t backward_workspace_bytes(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return 0;
   return round_up_256(static_cast<size_t>(partial_blocks(rows)) * static_cast<size_t>(width) * 4);
 }
 
-extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const float* scale,
-                                      const float* inverse_rms, float* grad_x, float* grad_scale,
-                                      int64_t rows, int64_t width, void* workspace,
-                                      size_t workspace_bytes, dpa4k_stream_t stream_handle) {
-  clear_error();
+// The backward with its column partials in `workspace` (checked against the size the
+// shape needs; only the register kernels with a scale gradient use it), or, with
+// `static_scratch`, in this device's `scratch` array.
+int rmsnorm_backward(const float* grad, const float* x, const float* scale, const float* inverse_rms,
+                     float* grad_x, float* grad_scale, int64_t rows, int64_t width, void* workspace,
+                     size_t workspace_bytes, bool static_scratch, hipStream_t stream) {
   if (rows < 0) return fail(DPA4K_EINVAL, "RMSNorm: negative row count");
   if (width <= 0) return fail(DPA4K_EINVAL, "RMSNorm feature dimension must be positive");
   if (grad_scale != nullptr && scale == nullptr)
@@ -359,7 +385,6 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
   // the scale gradient takes one thread per column along one grid row
   if (grad_scale != nullptr && width > 4294967295LL / kBlock * kBlock)
     return fail(DPA4K_EINVAL, "RMSNorm scale gradient: feature dimension exceeds the launch limit");
-  hipStream_t stream = as_stream(stream_handle);
   if (rows == 0) {
     if (grad_scale != nullptr) return zero_fill(grad_scale, width * sizeof(float), stream);
     return DPA4K_OK;
@@ -396,7 +421,18 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
                 : launch_backward<1>(cpl, grid, grad, x, scale, inverse_rms, grad_x, nullptr, rows,
                                      width, stream);
   }
-  const size_t needed = dpa4k_rmsnorm_backward_workspace_size(rows, width);
+  const size_t needed = backward_workspace_bytes(rows, width);
+  if (static_scratch) {
+    // every row of partials the register kernels write fits (width <= kRegisterMaxWidth here)
+    if (needed > static_cast<size_t>(DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES))
+      return fail(DPA4K_EINVAL,
+                  "RMSNorm backward (no allocation): %zu bytes of column partials exceed the %d-byte scratch",
+                  needed, DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES);
+    float* address = nullptr;
+    if (int s = scratch_for_stream(stream, address)) return s;
+    workspace = address;
+    workspace_bytes = DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES;
+  }
   if (workspace == nullptr || workspace_bytes < needed)
     return fail(DPA4K_EWORKSPACE, "RMSNorm backward: workspace of %zu bytes is smaller than %zu",
                 workspace_bytes, needed);
@@ -413,4 +449,52 @@ extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const f
   else
     partial_columns_kernel<1><<<blocks_for(width, kWaves), kBlock, 0, stream>>>(partial, grid, width, grad_scale);
   return launched("partial_columns_kernel");
+}
+
+}  // namespace
+}  // namespace dpa4k
+
+using namespace dpa4k;
+
+extern "C" int dpa4k_rmsnorm_forward(const float* x, const float* scale, float* y,
+                                     float* inverse_rms, int64_t rows, int64_t width, float eps,
+                                     dpa4k_stream_t stream_handle) {
+  clear_error();
+  if (rows < 0) return fail(DPA4K_EINVAL, "RMSNorm: negative row count");
+  if (width <= 0) return fail(DPA4K_EINVAL, "RMSNorm feature dimension must be positive");
+  if (!(eps > 0.0f) || !(eps < INFINITY))
+    return fail(DPA4K_EINVAL, "RMSNorm eps must be a finite positive number");
+  if (!grid_fits((rows + kWaves - 1) / kWaves, kBlock))
+    return fail(DPA4K_EINVAL, "RMSNorm row count exceeds the launch limit");
+  if (rows == 0) return DPA4K_OK;
+  if (x == nullptr || y == nullptr || inverse_rms == nullptr)
+    return fail(DPA4K_EINVAL, "RMSNorm: null pointer");
+  hipStream_t stream = as_stream(stream_handle);
+  const bool vec4 = width % 4 == 0 && aligned16(x) && aligned16(y) &&
+                    (scale == nullptr || aligned16(scale));
+  const int64_t chunks = vec4 ? width / 4 : width;
+  const int cpl = per_lane_for(chunks);
+  return vec4 ? launch_forward<4>(cpl, x, scale, y, inverse_rms, rows, width, eps, stream)
+              : launch_forward<1>(cpl, x, scale, y, inverse_rms, rows, width, eps, stream);
+}
+
+extern "C" size_t dpa4k_rmsnorm_backward_workspace_size(int64_t rows, int64_t width) {
+  return backward_workspace_bytes(rows, width);
+}
+
+extern "C" int dpa4k_rmsnorm_backward(const float* grad, const float* x, const float* scale,
+                                      const float* inverse_rms, float* grad_x, float* grad_scale,
+                                      int64_t rows, int64_t width, void* workspace,
+                                      size_t workspace_bytes, dpa4k_stream_t stream_handle) {
+  clear_error();
+  return rmsnorm_backward(grad, x, scale, inverse_rms, grad_x, grad_scale, rows, width, workspace,
+                          workspace_bytes, false, as_stream(stream_handle));
+}
+
+extern "C" int dpa4k_rmsnorm_backward_noalloc(const float* grad, const float* x, const float* scale,
+                                              const float* inverse_rms, float* grad_x, float* grad_scale,
+                                              int64_t rows, int64_t width, dpa4k_stream_t stream_handle) {
+  clear_error();
+  return rmsnorm_backward(grad, x, scale, inverse_rms, grad_x, grad_scale, rows, width, nullptr, 0, true,
+                          as_stream(stream_handle));
 }

@@ -64,6 +64,7 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_rmsnorm_forward": (_INT, [_P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "dpa4k_rmsnorm_backward_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_rmsnorm_backward": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
+    "dpa4k_rmsnorm_backward_noalloc": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "dpa4k_stream_calibrate": (_INT, [_P, _I64, _P, _I64, _P]),
     "dpa4k_set_launch_row_limit": (_INT, [_I64]),
 }

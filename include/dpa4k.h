@@ -332,6 +332,26 @@ int dpa4k_rmsnorm_backward(const float* grad, const float* x,
                            int64_t width, void* workspace,
                            size_t workspace_bytes, dpa4k_stream_t stream);
 
+/* dpa4k_rmsnorm_backward without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * It calls no hipMalloc/hipFree: the column partials of grad_scale live in a
+ * library-owned static device array of DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES
+ * (768 rows of at most 4096 floats, 12 MiB), one per device, held until the
+ * process ends; its address is looked up once per device on the first call.
+ * Same kernels as dpa4k_rmsnorm_backward, so the results are the same bit
+ * for bit.  Every row of partials a call uses is written before it is read:
+ * nothing needs clearing between calls.  Calls that overlap on one device
+ * (concurrent streams or threads) race on the array and must be serialised
+ * by the caller.  Returns DPA4K_EINVAL if a shape would need more partials
+ * than the array holds (no shape the kernels accept does). */
+#define DPA4K_RMSNORM_NOALLOC_SCRATCH_BYTES 12582912
+int dpa4k_rmsnorm_backward_noalloc(const float* grad, const float* x,
+                                   const float* scale, const float* inverse_rms,
+                                   float* grad_x, float* grad_scale,
+                                   int64_t rows, int64_t width,
+                                   dpa4k_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Stream calibration (measurement aid; no reference counterpart)
  * ---------------------------------------------------------------------- */
