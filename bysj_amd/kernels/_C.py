@@ -153,6 +153,40 @@ def group_by_key(keys: torch.Tensor, n_nodes: int) -> tuple[torch.Tensor, torch.
     return order, offsets
 
 
+def group_by_key_async(keys: torch.Tensor, n_nodes: int, *, order=None, offsets=None, status=None,
+                       workspace=None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``group_by_key`` without the host synchronisation: ``(order, offsets, status)``.
+
+    ``status`` (a one-element int32 device tensor) receives bit 1 when a key is
+    out of range (``order`` and ``offsets`` are then unspecified) and bit 2 when
+    the keys were not already sorted; read it before trusting the result.  Any
+    buffer passed in is used as is (``workspace`` of at least
+    ``dpa4k_group_by_key_workspace_size`` bytes), so a caller that passes all of
+    them allocates nothing and may capture the call in a HIP graph.
+    """
+    _i64(keys, "group_by_source keys")
+    _check(keys.dim() == 1, "group_by_source keys must be one-dimensional")
+    n_nodes = int(n_nodes)
+    edges = keys.numel()
+    order = torch.empty(edges, dtype=torch.int64, device=keys.device) if order is None else order
+    offsets = torch.empty(n_nodes + 1, dtype=torch.int64, device=keys.device) if offsets is None else offsets
+    status = torch.empty(1, dtype=torch.int32, device=keys.device) if status is None else status
+    _i64(order, "group_by_source order")
+    _i64(offsets, "group_by_source offsets")
+    _check(order.numel() == edges and offsets.numel() == n_nodes + 1, "group_by_source output buffers have the wrong size")
+    _check(status.is_cuda and status.dtype == torch.int32 and status.numel() >= 1, "status must be a gfx950 int32 tensor")
+    nbytes = _LIB.dpa4k_group_by_key_workspace_size(edges, n_nodes)
+    workspace = _workspace(nbytes, keys.device) if workspace is None else workspace
+    _check(workspace.is_cuda and workspace.numel() * workspace.element_size() >= nbytes, "workspace is too small")
+    with _on(keys.device) as stream:
+        code = _LIB.dpa4k_group_by_key_async(
+            _ptr(keys), edges, n_nodes, _ptr(order), offsets.data_ptr(), status.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), stream,
+        )
+    _lib.check(code)
+    return order, offsets, status
+
+
 # ---------------------------------------------------------------------------
 # segment_sum (csrc/segment_sum.cpp:214, :271)
 # ---------------------------------------------------------------------------

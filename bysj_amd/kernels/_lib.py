@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -31,6 +31,8 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_segment_offsets": (_INT, [_P, _I64, _I64, _P, _P, _SZ, _P]),
     "dpa4k_group_by_key_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_group_by_key": (_INT, [_P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "dpa4k_segment_offsets_async": (_INT, [_P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "dpa4k_group_by_key_async": (_INT, [_P, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "dpa4k_segment_sum_forward": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "dpa4k_segment_sum_backward": (
         _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),

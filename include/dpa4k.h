@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 4
+#define DPA4K_ABI_VERSION 5
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -67,10 +67,12 @@ int dpa4k_abi_version(void);
 
 /* Replaces kernels.segment.segment_offsets (python/kernels/segment.py:46-57).
  * offsets[N+1] = [0, cumsum(bincount(keys, minlength=N))].  Bit-exact.
- * Synchronises: returns DPA4K_EINVAL ("... values must be within the node
- * range") when a key lies outside [0, N), matching the reference's
- * dst.min()/dst.max() check (:54).  N >= 1, E >= 0.
- * workspace >= dpa4k_segment_offsets_workspace_size(E, N) bytes. */
+ * Synchronises once, at the end: returns DPA4K_EINVAL ("... values must be
+ * within the node range") when a key lies outside [0, N), matching the
+ * reference's dst.min()/dst.max() check (:54).  1 <= N <= 2^32,
+ * 0 <= E < 2^32.  workspace >= dpa4k_segment_offsets_workspace_size(E, N)
+ * bytes.  Keys that are already non-decreasing are not sorted; others are
+ * grouped by a stable counting sort on the device. */
 size_t dpa4k_segment_offsets_workspace_size(int64_t n_edges, int64_t n_nodes);
 int dpa4k_segment_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
                           int64_t* offsets, void* workspace,
@@ -78,11 +80,30 @@ int dpa4k_segment_offsets(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
 
 /* Replaces kernels.segment.group_by_source (python/kernels/segment.py:60-71):
  * order[E] = stable argsort(keys), offsets[N+1] as above.  Bit-exact (a
- * stable order is unique).  Synchronises (same range check as above). */
+ * stable order is unique).  Synchronises once (same range check as above). */
 size_t dpa4k_group_by_key_workspace_size(int64_t n_edges, int64_t n_nodes);
 int dpa4k_group_by_key(const int64_t* keys, int64_t n_edges, int64_t n_nodes,
                        int64_t* order, int64_t* offsets, void* workspace,
                        size_t workspace_bytes, dpa4k_stream_t stream);
+
+/* Asynchronous forms of the two builders above (no reference counterpart:
+ * the reference's check synchronises).  They enqueue the whole build on
+ * `stream` and return without waiting, so a caller may capture them in a HIP
+ * graph.  `status` (device int32, cleared by the call) receives the bits
+ *   DPA4K_CSR_OUT_OF_RANGE  a key lies outside [0, N): offsets and order are
+ *                           then unspecified (nothing outside them is written);
+ *   DPA4K_CSR_UNSORTED      the keys were not already non-decreasing.
+ * The caller must read it before trusting the result.  Same workspace. */
+#define DPA4K_CSR_OUT_OF_RANGE 1
+#define DPA4K_CSR_UNSORTED 2
+int dpa4k_segment_offsets_async(const int64_t* keys, int64_t n_edges,
+                                int64_t n_nodes, int64_t* offsets,
+                                int32_t* status, void* workspace,
+                                size_t workspace_bytes, dpa4k_stream_t stream);
+int dpa4k_group_by_key_async(const int64_t* keys, int64_t n_edges,
+                             int64_t n_nodes, int64_t* order, int64_t* offsets,
+                             int32_t* status, void* workspace,
+                             size_t workspace_bytes, dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * segment_sum
@@ -220,11 +241,11 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
 
 /* Grouping step of the GIE operator (no reference counterpart: the
  * reference scatters with atomics on the unsorted dst, csrc/gie.cpp:68-87).
- * Builds the destination CSR of an unsorted dst: offsets[N+1] always,
- * order[E] only when dst is not already non-decreasing.  Also checks
+ * Builds the destination CSR of an unsorted dst: offsets[N+1] and order[E]
+ * (the identity when dst is already non-decreasing).  Also checks
  * 0 <= dst < N and 0 <= radial_slot < S.  Synchronises.
  * host_info (host pointer, may be NULL) receives a bit set:
- *   1 = dst was non-decreasing (order left untouched: use NULL order),
+ *   1 = dst was non-decreasing (the kernels may then take a NULL order),
  *   2 = every radial slot is referenced by at most one row.
  * Out-of-range indices return DPA4K_EINVAL. */
 size_t dpa4k_gie_group_workspace_size(int64_t n_edges, int64_t n_nodes);

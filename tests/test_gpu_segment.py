@@ -60,6 +60,92 @@ def test_segment_offsets_and_grouping_bit_exact(edges, nodes, seed):
     assert_bitwise(src_offsets, e_offsets, "group_by_source offsets")
 
 
+def _check_grouping_against_numpy(keys: np.ndarray, nodes: int, what: str) -> None:
+    """group_by_source and segment_offsets of int64 `keys` against numpy's stable argsort and bincount."""
+    device_keys = torch.from_numpy(keys).to(DEV)
+    expected_offsets = np.concatenate([[0], np.cumsum(np.bincount(keys, minlength=nodes))]).astype(np.int64)
+    expected_order = np.argsort(keys, kind="stable").astype(np.int64)
+    assert_bitwise(kernels.segment_offsets(device_keys, nodes), torch.from_numpy(expected_offsets),
+                   f"{what}: segment_offsets")
+    order, offsets = kernels.group_by_source(device_keys, nodes)
+    assert_bitwise(offsets, torch.from_numpy(expected_offsets), f"{what}: group_by_source offsets")
+    assert_bitwise(order, torch.from_numpy(expected_order), f"{what}: group_by_source order")
+    again, _ = kernels.group_by_source(device_keys, nodes)
+    assert_bitwise(again, order, f"{what}: run to run")
+
+
+@pytest.mark.parametrize("edges,nodes", [
+    (8191, 2), (8192, 513), (8193, 65536), (100000, 1), (250000, 65537), (600000, 2**20),
+    (2_200_000, 2**21),        # (E - 1) << fine_bits passes 32 bits: 64-bit packed entries
+    (300000, 2**21 + 5),       # past 21 key bits: least-significant-digit passes
+    (150000, 2**26), (40000, 2**27 + 3),
+])
+def test_counting_sort_paths_bit_exact(edges, nodes):
+    """Every path of the device counting sort (two-level with 32- and 64-bit packed entries, the LSD
+    passes, partial tiles, one node) against numpy's stable argsort, on unsorted and sorted keys."""
+    announce("counting sort", edges, nodes)
+    keys = workloads.rng(edges % 1000 + nodes % 1000).integers(0, nodes, size=edges).astype(np.int64)
+    _check_grouping_against_numpy(keys, nodes, f"random E={edges} N={nodes}")
+    _check_grouping_against_numpy(np.sort(keys), nodes, f"sorted E={edges} N={nodes}")
+
+
+def test_counting_sort_skewed_and_sparse_keys():
+    """Hubs that fill a bucket many times over (the bucket-local pass runs chunk after chunk), a single
+    key everywhere, and sparse keys over millions of nodes (long runs of empty segments, sorted and not,
+    filled cooperatively instead of by one thread)."""
+    announce("counting sort: skewed and sparse")
+    gen = workloads.rng(77)
+    hubs = np.concatenate([np.full(300000, 4097), np.full(100000, 5), gen.integers(0, 65536, 200000)])
+    gen.shuffle(hubs)
+    _check_grouping_against_numpy(hubs.astype(np.int64), 65536, "hubs")
+    _check_grouping_against_numpy(np.full(70000, 3, dtype=np.int64), 4, "one key")
+    sparse = gen.integers(0, 30_000_000, 50).astype(np.int64)
+    _check_grouping_against_numpy(sparse, 30_000_000, "sparse unsorted")
+    _check_grouping_against_numpy(np.sort(sparse), 30_000_000, "sparse sorted")
+    _check_grouping_against_numpy(np.array([0, 9_999_999], dtype=np.int64), 10_000_000, "two keys, ends")
+
+
+def test_group_by_key_async_status_and_capture():
+    """The asynchronous build reports the status bits on the device, allocates nothing when given its
+    buffers, and replays from a HIP graph with the same result as the synchronous call."""
+    from bysj_amd.kernels import _C, _lib
+
+    announce("group_by_key async")
+    keys = torch.from_numpy(workloads.rng(5).integers(0, 70000, size=90000).astype(np.int64)).to(DEV)
+    order, offsets = kernels.group_by_source(keys, 70000)
+    buffers = dict(order=torch.empty_like(order), offsets=torch.empty_like(offsets),
+                   status=torch.full((1,), 99, dtype=torch.int32, device=DEV),
+                   workspace=torch.empty(_lib.load().dpa4k_group_by_key_workspace_size(90000, 70000),
+                                         dtype=torch.uint8, device=DEV))
+    _C.group_by_key_async(keys, 70000, **buffers)
+    assert int(buffers["status"].item()) == 2  # unsorted, in range
+    assert_bitwise(buffers["order"], order, "async order")
+    assert_bitwise(buffers["offsets"], offsets, "async offsets")
+    graph = torch.cuda.CUDAGraph()
+    fresh = {k: (torch.zeros_like(v) if k != "workspace" else v) for k, v in buffers.items()}
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        _C.group_by_key_async(keys, 70000, **fresh)
+    for replay in range(3):
+        fresh["order"].zero_()
+        fresh["status"].fill_(99)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bitwise(fresh["order"], order, f"replay {replay} order")
+        assert_bitwise(fresh["offsets"], offsets, f"replay {replay} offsets")
+        assert int(fresh["status"].item()) == 2
+    sorted_keys = torch.sort(keys).values
+    _C.group_by_key_async(sorted_keys, 70000, **buffers)
+    assert int(buffers["status"].item()) == 0
+    bad = keys.clone()
+    bad[1234] = 70000
+    _C.group_by_key_async(bad, 70000, **buffers)
+    assert int(buffers["status"].item()) & 1 == 1
+    bad[1234] = -3
+    _C.group_by_key_async(bad, 70000, **buffers)
+    assert int(buffers["status"].item()) & 1 == 1
+
+
 @pytest.mark.parametrize("sort", [False, True])
 def test_destination_grouping(sort):
     """Offsets equal segment_offsets; the order is None exactly when dst is non-decreasing."""
