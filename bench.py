@@ -15,9 +15,13 @@ The `roofline` object prices the same timed region: algorithmic bytes of one
 launch (every input read once, every output written once) over the average
 duration per launch.  `cpu_baseline` times the CPU oracle (the reference's
 ATen chain restated in torch) on the host cores on a bounded sample.  `ops`
-repeats the measurement for the other operators at their configuration sizes.
+repeats the measurement for the other operators at their configuration sizes
+and at the >=10M-edge roofline shapes (1R, 2R, 3R, 4R and 1M RMSNorm rows);
+each large line also carries a same-run plain copy of its own read and write
+bytes (`same_bytes_copy_us`) and its share of that copy.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only] [--no-roofline-shapes]
+       python bench.py --traffic-summary FETCH_CSV WRITE_CSV BENCH_LOG   (see PMC_COMMAND)
 """
 from __future__ import annotations
 
@@ -47,10 +51,14 @@ def parse_args():
     parser.add_argument("--no-backward", action="store_true", help="skip the backward and CSR-build lines")
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
     parser.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
-    parser.add_argument("--roofline-shapes", action="store_true",
-                        help="also run the >=10M-edge shapes (1R, 2R, 4R)")
-    parser.add_argument("--calibrate-copy", action="store_true",
-                        help="launch one plain 256 MiB copy (counter calibration for rocprofv3 --pmc)")
+    parser.add_argument("--no-roofline-shapes", action="store_true",
+                        help="skip the >=10M-edge shapes (1R, 2R, 3R, 4R, 1M RMSNorm rows)")
+    parser.add_argument("--traffic-marks", action="store_true",
+                        help="eager launches with marker kernels around every step and a 256 MiB calibration "
+                             "copy, for two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)")
+    parser.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
+                        help="write profiles/traffic.json and traffic.md from the two passes' counter CSVs and "
+                             "the FETCH pass's bench output, then exit")
     return parser.parse_args()
 
 
@@ -58,11 +66,66 @@ def parse_args():
 # timing harness
 # ---------------------------------------------------------------------------
 
-def time_steps(step, n_sets: int, steps: int, warmup: int, *, graph: bool = True) -> float:
-    """Average milliseconds per step over `steps` steps (step(i) uses input set i % n_sets)."""
+class TrafficMarks:
+    """Marker launches that split a rocprofv3 --pmc dispatch list into bench lines and steps.
+
+    A marker is dpa4k_stream_calibrate's read-only kernel over `blocks` x 4096 floats, which
+    runs exactly `blocks` workgroups: 1 opens a step, 2 closes a line, 3 + k opens line k of
+    `labels`.  Every other launch of that kernel here reads 1 GiB (8,192 workgroups), so a
+    launch of fewer than 256 workgroups is a marker.  traffic_summary() reads them back.
+    """
+
+    STEP, END, FIRST_LABEL = 1, 2, 3
+
+    def __init__(self):
+        import torch
+
+        from bysj_amd.kernels import _lib
+
+        self.labels: list[str] = []
+        self._library = _lib.load()
+        self._source = torch.zeros(4096 * 255, device="cuda")
+        self._sink = torch.zeros(256, device="cuda")
+
+    def _launch(self, blocks: int) -> None:
+        import torch
+
+        from bysj_amd.kernels import _lib
+
+        _lib.check(self._library.dpa4k_stream_calibrate(self._source.data_ptr(), 4096 * blocks, self._sink.data_ptr(),
+                                                        0, torch.cuda.current_stream().cuda_stream))
+
+    def begin(self, label: str) -> None:
+        if label in self.labels or len(self.labels) + self.FIRST_LABEL > 255:
+            raise ValueError(f"traffic mark {label!r} repeated or past the marker range")
+        self.labels.append(label)
+        self._launch(self.FIRST_LABEL + len(self.labels) - 1)
+
+    def step(self) -> None:
+        self._launch(self.STEP)
+
+    def end(self) -> None:
+        self._launch(self.END)
+
+
+MARKS: TrafficMarks | None = None  # set by --traffic-marks
+
+
+def time_steps(step, n_sets: int, steps: int, warmup: int, *, graph: bool = True, label: str | None = None) -> float:
+    """Average milliseconds per step over `steps` steps (step(i) uses input set i % n_sets).
+
+    With --traffic-marks and a `label`, every step is launched eagerly behind a step marker,
+    inside a begin/end pair for the label, so that a counter pass can price each step.
+    """
     import torch
 
+    marks = MARKS if label is not None else None
+    if marks is not None:
+        graph = False
+        marks.begin(label)
     for i in range(warmup):
+        if marks is not None:
+            marks.step()
         step(i % n_sets)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -84,10 +147,14 @@ def time_steps(step, n_sets: int, steps: int, warmup: int, *, graph: bool = True
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         for i in range(steps):
+            if marks is not None:
+                marks.step()
             step(i % n_sets)
         stop.record(stream)
         torch.cuda.synchronize()
         elapsed = start.elapsed_time(stop)
+    if marks is not None:
+        marks.end()
     return elapsed / steps
 
 
@@ -139,7 +206,7 @@ def cpu_time(function, seconds: float) -> tuple[float, int]:
 # workloads
 # ---------------------------------------------------------------------------
 
-def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool, label: str | None = None):
     import torch
 
     from bysj_amd import kernels, workloads
@@ -147,7 +214,8 @@ def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
     base = workloads.segment_softmax_config(n_nodes=n_nodes, seed=0, device="cuda")
     edges, channels = base["logit"].shape
     offsets = base["offsets"]
-    bytes_per_step = 2 * edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + 2 * n_nodes * channels * 4
+    reads = edges * channels * 4 + edges * 4 + (n_nodes + 1) * 8 + n_nodes * channels * 4
+    bytes_per_step = reads + edges * channels * 4 + n_nodes * channels * 4
     n_sets = n_sets_for(bytes_per_step)
     # one graph; every input set draws fresh logits, envelopes and null logits
     sets = [base] + [workloads.segment_softmax_features(edges, n_nodes, channels, seed=s, device="cuda")
@@ -158,12 +226,13 @@ def softmax_job(n_nodes: int, steps: int, warmup: int, graph: bool):
         return kernels.segment_softmax(case["logit"], case["env"], offsets, case["null_logit"])
 
     with torch.no_grad():
-        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph, label=label)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets,
-            "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
+            "ms_per_step": ms, "bytes": bytes_per_step, "reads": reads, "base": base}
 
 
-def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool, scaled_shuffled: bool = False):
+def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool, scaled_shuffled: bool = False,
+                    label: str | None = None):
     """segment_sum forward; `scaled_shuffled` adds edge and node scales ~U(0.5, 1.5) and a shuffled edge order."""
     import torch
 
@@ -190,58 +259,86 @@ def segment_sum_job(n_nodes: int, steps: int, warmup: int, graph: bool, scaled_s
         return kernels.segment_sum(sets[i], dst, base["offsets"], edge_scale, node_scale, order=order)
 
     with torch.no_grad():
-        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph, label=label)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets,
-            "ms_per_step": ms, "bytes": bytes_per_step, "base": base}
+            "ms_per_step": ms, "bytes": bytes_per_step, "reads": bytes_per_step - n_nodes * channels * 4,
+            "base": base}
 
 
-def gie_rmsnorm_jobs(n_atoms: int, steps: int, warmup: int, graph: bool, water=None, gie_steps=None):
+def gie_bytes(case, n_atoms: int, backward: bool = False) -> tuple[int, int]:
+    """(reads, writes) of one GIE zonal-scatter launch over a destination CSR.
+
+    Forward: zonal, every referenced radial slot, offsets, the slot map and the inverse degrees
+    read once; the [N, R + 1, C] output written once.  Backward: the upstream gradient's rows
+    1..R, zonal, the referenced radial slots, offsets, slot map and inverse degrees read; the
+    zonal, radial (every slot: unreferenced ones are written as zeros) and inverse-degree
+    gradients written.
+    """
+    edges, rows = case["zonal"].shape
+    slots, channels = case["radial"].shape[1:]
+    referenced = len(set(case["radial_slot"].tolist()))
+    index = (n_atoms + 1) * 8 + rows * 8 + n_atoms * 4
+    if not backward:
+        return edges * rows * 4 + edges * referenced * channels * 4 + index, n_atoms * (rows + 1) * channels * 4
+    reads = n_atoms * rows * channels * 4 + edges * rows * 4 + edges * referenced * channels * 4 + index
+    return reads, edges * rows * 4 + edges * slots * channels * 4 + n_atoms * 4
+
+
+def gie_forward_jobs(water, case, steps: int, warmup: int, graph: bool, gie_steps=None,
+                     labels: tuple = (None, None, None)):
+    """GIE forward, the fused GIE -> RMSNorm forward and RMSNorm forward on a water box.
+
+    `labels` names the three lines (GIE, fused, RMSNorm); a None label skips that line.  GIE
+    inputs are large enough (>= 1.7 GB of radial features at config 3) to stream from HBM with
+    one input set; RMSNorm rotates through fresh rows.
+    """
     import torch
 
-    from bysj_amd import workloads
     from bysj_amd.kernels import _C
 
-    water = water or workloads.water_graph(n_atoms, seed=0)
-    case = workloads.gie_config(water, seed=0, device="cuda", primary=True)
-    edges = water.n_edges
-    offsets, order, _ = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, 16)
-
-    def gie_step(_):
-        return _C.gie_zonal_scatter_forward_csr(case["zonal"], case["radial"], offsets, order,
-                                                case["radial_slot"], case["inv_sqrt_deg"])
-
-    gie_bytes = edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 + n_atoms * 4 \
-        + n_atoms * 16 * 64 * 4
-    width = 16 * 64
-    fused_bytes = gie_bytes - n_atoms * width * 4 + n_atoms * width * 4 + width * 4 + n_atoms * 4
-
-    def fused_step(_):
-        return _C.gie_rmsnorm_forward_csr(case["zonal"], case["radial"], offsets, order, case["radial_slot"],
-                                          case["inv_sqrt_deg"], case["rms_scale"], 1e-6, False)
-
+    n_atoms = water.n_atoms
+    gie_label, fused_label, rms_label = labels
+    offsets, order, info = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, case["radial"].shape[1])
+    reads, writes = gie_bytes(case, n_atoms)
+    rows = case["zonal"].shape[1]
+    width = (rows + 1) * case["radial"].shape[2]
+    count = gie_steps or max(4, steps // 10)
+    out = {}
     with torch.no_grad():
-        gie_ms = time_steps(gie_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
-        fused_ms = time_steps(fused_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
-        rows = gie_step(0).reshape(n_atoms, 1024)
-    rms_bytes = 2 * n_atoms * 1024 * 4 + 1024 * 4 + n_atoms * 4
-    n_sets = n_sets_for(rms_bytes)
-    generator = torch.Generator(device="cuda")
-    generator.manual_seed(3)
-    row_sets = [rows] + [torch.randn(rows.shape, generator=generator, device="cuda") for _ in range(1, n_sets)]
+        def gie_step(_):
+            return _C.gie_zonal_scatter_forward_csr(case["zonal"], case["radial"], offsets, order,
+                                                    case["radial_slot"], case["inv_sqrt_deg"], info)
 
-    def rms_step(i):
-        return _C.rmsnorm_forward(row_sets[i], case["rms_scale"], 1e-6)
+        def fused_step(_):
+            return _C.gie_rmsnorm_forward_csr(case["zonal"], case["radial"], offsets, order, case["radial_slot"],
+                                              case["inv_sqrt_deg"], case["rms_scale"], 1e-6, False)
 
-    with torch.no_grad():
-        rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
-    gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_bytes, "sets": 1}
-    rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
-    gie["fused_rmsnorm"] = {"edges": edges, "nodes": n_atoms, "ms_per_step": fused_ms, "bytes": fused_bytes,
-                            "sets": 1}
-    return gie, rms, water, case
+        if gie_label is not None:
+            ms = time_steps(gie_step, 1, count, min(warmup, 3), graph=graph, label=gie_label)
+            out["gie"] = {"edges": water.n_edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": reads + writes,
+                          "reads": reads, "sets": 1}
+        if fused_label is not None:
+            # the output is written once, normalised; scale and inverse RMS are the extra bytes
+            fused_reads, fused_writes = reads + width * 4, writes + n_atoms * 4
+            ms = time_steps(fused_step, 1, count, min(warmup, 3), graph=graph, label=fused_label)
+            out["fused"] = {"edges": water.n_edges, "nodes": n_atoms, "ms_per_step": ms,
+                            "bytes": fused_reads + fused_writes, "reads": fused_reads, "sets": 1}
+        if rms_label is not None:
+            x = gie_step(0).reshape(n_atoms, width)
+            rms_reads = n_atoms * width * 4 + width * 4
+            rms_bytes = rms_reads + n_atoms * width * 4 + n_atoms * 4
+            n_sets = n_sets_for(rms_bytes)
+            generator = torch.Generator(device="cuda")
+            generator.manual_seed(3)
+            row_sets = [x] + [torch.randn(x.shape, generator=generator, device="cuda") for _ in range(1, n_sets)]
+            ms = time_steps(lambda i: _C.rmsnorm_forward(row_sets[i], case["rms_scale"], 1e-6), n_sets, steps,
+                            warmup, graph=graph, label=rms_label)
+            out["rms"] = {"rows": n_atoms, "width": width, "ms_per_step": ms, "bytes": rms_bytes,
+                          "reads": rms_reads, "sets": n_sets}
+    return out
 
 
-def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: str, water=None):
+def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: str, water=None, label=None):
     import torch
 
     from bysj_amd import kernels, workloads
@@ -269,12 +366,13 @@ def force_job(n_atoms: int, steps: int, warmup: int, graph: bool, dtype_name: st
                                       base["src_offsets"], base["src_order"])
 
     with torch.no_grad():
-        ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+        ms = time_steps(step, n_sets, steps, warmup, graph=graph, label=label)
     return {"edges": edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": bytes_per_step, "sets": n_sets,
+            "reads": bytes_per_step - n_atoms * 12 * size,
             "dtype": dtype_name}, water, base
 
 
-def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool, label=None):
     """segment_softmax backward (with the null logit) on the config-2 graph.
 
     Every input set holds its own alpha, null alpha (forward outputs of fresh logits), envelope
@@ -309,12 +407,12 @@ def softmax_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
         alpha, null_alpha, env, grad_alpha, grad_null = sets[i]
         return _C.segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha, grad_null, plan=plan)
 
-    ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    ms = time_steps(step, n_sets, steps, warmup, graph=graph, label=label)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
-            "bytes": reads + writes}
+            "bytes": reads + writes, "reads": reads}
 
 
-def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool):
+def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool, label=None):
     """segment_sum backward with edge_scale and node_scale: grad_src, grad_edge_scale, grad_node_scale.
 
     Every input set holds its own src, scales and grad_out, so each step reads them from HBM.
@@ -344,78 +442,73 @@ def segment_sum_backward_job(n_nodes: int, steps: int, warmup: int, graph: bool)
         return _C.segment_sum_backward(grad, src, base["dst"], base["offsets"], edge_scale, node_scale, True, None,
                                        want_edge_scale_grad=True)
 
-    ms = time_steps(step, n_sets, steps, warmup, graph=graph)
+    ms = time_steps(step, n_sets, steps, warmup, graph=graph, label=label)
     return {"edges": int(edges), "nodes": n_nodes, "channels": int(channels), "sets": n_sets, "ms_per_step": ms,
-            "bytes": reads + writes}
+            "bytes": reads + writes, "reads": reads}
 
 
-def gie_rmsnorm_backward_jobs(water, case, steps: int, warmup: int, graph: bool, gie_steps=None):
-    """GIE backward (zonal, radial and inverse-degree gradients) and RMSNorm backward on a water box."""
+def gie_backward_job(water, case, steps: int, warmup: int, graph: bool, gie_steps=None, label=None):
+    """GIE backward (zonal, radial and inverse-degree gradients) on a water box, one input set."""
     import torch
 
     from bysj_amd.kernels import _C
 
-    n_atoms, edges = water.n_atoms, water.n_edges
-    offsets, order, info = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, 16)
+    n_atoms = water.n_atoms
+    rows, channels = case["zonal"].shape[1], case["radial"].shape[2]
+    offsets, order, info = _C.gie_group(case["dst"], case["radial_slot"], n_atoms, case["radial"].shape[1])
     generator = torch.Generator(device="cuda")
     generator.manual_seed(9)
-    grad_out = torch.randn((n_atoms, 16, 64), generator=generator, device="cuda")
+    grad_out = torch.randn((n_atoms, rows + 1, channels), generator=generator, device="cuda")
 
-    def gie_step(_):
+    def step(_):
         return _C.gie_zonal_scatter_backward_csr(grad_out, case["zonal"], case["radial"], offsets, order,
-                                                 case["radial_slot"], case["inv_sqrt_deg"], bool(info & 2))
+                                                 case["radial_slot"], case["inv_sqrt_deg"], info)
 
-    gie_reads = n_atoms * 15 * 64 * 4 + edges * 15 * 4 + edges * 15 * 64 * 4 + (n_atoms + 1) * 8 + 15 * 8 \
-        + n_atoms * 4
-    gie_writes = edges * 15 * 4 + edges * 16 * 64 * 4 + n_atoms * 4
-    gie_ms = time_steps(gie_step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph)
-    del grad_out
-
-    rms_bytes = 3 * n_atoms * 1024 * 4 + 2 * 1024 * 4 + n_atoms * 4
-    n_sets = n_sets_for(rms_bytes)
-    rms_sets = []
-    for _ in range(n_sets):
-        x = torch.randn((n_atoms, 1024), generator=generator, device="cuda")
-        _, inverse_rms = _C.rmsnorm_forward(x, case["rms_scale"], 1e-6)
-        rms_sets.append((torch.randn((n_atoms, 1024), generator=generator, device="cuda"), x, inverse_rms))
-
-    def rms_step(i):
-        grad, x, inverse_rms = rms_sets[i]
-        return _C.rmsnorm_backward(grad, x, case["rms_scale"], inverse_rms, True)
-
-    rms_ms = time_steps(rms_step, n_sets, steps, warmup, graph=graph)
-    gie = {"edges": edges, "nodes": n_atoms, "ms_per_step": gie_ms, "bytes": gie_reads + gie_writes, "sets": 1}
-    rms = {"rows": n_atoms, "width": 1024, "ms_per_step": rms_ms, "bytes": rms_bytes, "sets": n_sets}
-    return gie, rms
+    reads, writes = gie_bytes(case, n_atoms, backward=True)
+    ms = time_steps(step, 1, gie_steps or max(4, steps // 10), min(warmup, 3), graph=graph, label=label)
+    return {"edges": water.n_edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": reads + writes, "reads": reads,
+            "sets": 1, "shared_slots": not bool(info & 2)}
 
 
-def rmsnorm_jobs(rows: int, steps: int, warmup: int, graph: bool):
-    """RMSNorm forward and backward over `rows` random rows of width 1024 (eps 1e-6, scale ~U(0.5, 1.5))."""
+def rmsnorm_jobs(rows: int, steps: int, warmup: int, graph: bool, labels: tuple = (None, None)):
+    """RMSNorm forward and backward over `rows` random rows of width 1024 (eps 1e-6, scale ~U(0.5, 1.5)).
+
+    `labels` names the forward and backward lines; a None label skips that line.
+    """
     import torch
 
     from bysj_amd.kernels import _C
 
+    fwd_label, bwd_label = labels
     generator = torch.Generator(device="cuda")
     generator.manual_seed(13)
     scale = torch.rand(1024, generator=generator, device="cuda") + 0.5
-    fwd_bytes = 2 * rows * 1024 * 4 + 1024 * 4 + rows * 4
-    bwd_bytes = 3 * rows * 1024 * 4 + 2 * 1024 * 4 + rows * 4
+    fwd_reads = rows * 1024 * 4 + 1024 * 4
+    fwd_bytes = fwd_reads + rows * 1024 * 4 + rows * 4
+    bwd_reads = 2 * rows * 1024 * 4 + 1024 * 4 + rows * 4
+    bwd_bytes = bwd_reads + rows * 1024 * 4 + 1024 * 4
     n_sets = n_sets_for(bwd_bytes)
     sets = []
     for _ in range(n_sets):
         x = torch.randn((rows, 1024), generator=generator, device="cuda")
         _, inverse_rms = _C.rmsnorm_forward(x, scale, 1e-6)
         sets.append((x, inverse_rms, torch.randn((rows, 1024), generator=generator, device="cuda")))
-    with torch.no_grad():
-        fwd_ms = time_steps(lambda i: _C.rmsnorm_forward(sets[i][0], scale, 1e-6), n_sets, steps, warmup, graph=graph)
-    bwd_ms = time_steps(lambda i: _C.rmsnorm_backward(sets[i][2], sets[i][0], scale, sets[i][1], True), n_sets,
-                        steps, warmup, graph=graph)
-    fwd = {"rows": rows, "width": 1024, "ms_per_step": fwd_ms, "bytes": fwd_bytes, "sets": n_sets}
-    bwd = {"rows": rows, "width": 1024, "ms_per_step": bwd_ms, "bytes": bwd_bytes, "sets": n_sets}
-    return fwd, bwd
+    out = {}
+    if fwd_label is not None:
+        with torch.no_grad():
+            ms = time_steps(lambda i: _C.rmsnorm_forward(sets[i][0], scale, 1e-6), n_sets, steps, warmup,
+                            graph=graph, label=fwd_label)
+        out["fwd"] = {"rows": rows, "width": 1024, "ms_per_step": ms, "bytes": fwd_bytes, "reads": fwd_reads,
+                      "sets": n_sets}
+    if bwd_label is not None:
+        ms = time_steps(lambda i: _C.rmsnorm_backward(sets[i][2], sets[i][0], scale, sets[i][1], True), n_sets,
+                        steps, warmup, graph=graph, label=bwd_label)
+        out["bwd"] = {"rows": rows, "width": 1024, "ms_per_step": ms, "bytes": bwd_bytes, "reads": bwd_reads,
+                      "sets": n_sets}
+    return out
 
 
-def csr_job(water, steps: int, warmup: int, graph: bool):
+def csr_job(water, steps: int, warmup: int, graph: bool, label=None):
     """Device CSR build of a source list (group_by_source: offsets + stable order) on the config-4 graph.
 
     The step is the asynchronous build (_C.group_by_key_async: every kernel of the counting sort, no
@@ -442,7 +535,7 @@ def csr_job(water, steps: int, warmup: int, graph: bool):
     workspace = torch.empty(_lib.load().dpa4k_group_by_key_workspace_size(edges, n_atoms), dtype=torch.uint8,
                             device="cuda")
     ms = time_steps(lambda i: _C.group_by_key_async(sets[i], n_atoms, workspace=workspace, **buffers[i]), n_sets,
-                    steps, warmup, graph=graph)
+                    steps, warmup, graph=graph, label=label)
     statuses = [int(b["status"].item()) for b in buffers]
     if any(code & 1 for code in statuses):
         raise RuntimeError(f"group_by_key_async reported out-of-range keys: {statuses}")
@@ -450,8 +543,46 @@ def csr_job(water, steps: int, warmup: int, graph: bool):
     torch_ms = time_steps(lambda _: (torch.argsort(src, stable=True),
                                      torch.bincount(src, minlength=n_atoms).cumsum(0)), 1, max(5, steps // 4), 2,
                           graph=False)
-    return {"edges": edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": bytes_per_step, "sets": n_sets,
-            "eager_ms_per_call": eager_ms, "torch_ms_per_call": torch_ms}
+    return {"edges": edges, "nodes": n_atoms, "ms_per_step": ms, "bytes": bytes_per_step, "reads": edges * 8,
+            "sets": n_sets, "eager_ms_per_call": eager_ms, "torch_ms_per_call": torch_ms}
+
+
+def same_bytes_copy_ms(read_bytes: int, write_bytes: int, steps: int, warmup: int) -> tuple[float, int]:
+    """Milliseconds per launch of a plain copy that reads `read_bytes` and writes `write_bytes`.
+
+    The copy (dpa4k_stream_calibrate) streams through enough distinct sources to leave the
+    Infinity Cache, like the operator lines, and is timed the same way.  Returns the time and
+    the bytes the copy moved (the counts rounded up to whole 16-byte chunks; the writes are
+    capped at the reads: every line priced this way reads at least as many bytes as it writes).
+    """
+    import torch
+
+    from bysj_amd.kernels import _lib
+
+    library = _lib.load()
+    torch.cuda.empty_cache()
+    read_floats = (read_bytes // 4 + 3) // 4 * 4
+    write_floats = min(read_floats, (write_bytes // 4 + 3) // 4 * 4)
+    n_sets = n_sets_for(read_bytes + write_bytes)
+    sources = [torch.empty(read_floats, device="cuda") for _ in range(n_sets)]
+    out = torch.empty(max(write_floats, 8192), device="cuda")
+
+    def launch(i):
+        _lib.check(library.dpa4k_stream_calibrate(sources[i].data_ptr(), read_floats, out.data_ptr(), write_floats,
+                                                  torch.cuda.current_stream().cuda_stream))
+
+    ms = time_steps(launch, n_sets, steps, warmup)
+    del sources, out
+    torch.cuda.empty_cache()
+    return ms, (read_floats + write_floats) * 4
+
+
+def copy_share(line: dict, job: dict, steps: int) -> dict:
+    """Add the same-run copy of the line's own read and write bytes, and the line's share of it."""
+    copy_ms, _ = same_bytes_copy_ms(job["reads"], job["bytes"] - job["reads"], steps, 3)
+    line["same_bytes_copy_us"] = round(copy_ms * 1e3, 3)
+    line["share_of_same_bytes_copy"] = round(copy_ms / job["ms_per_step"], 4)
+    return line
 
 
 def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
@@ -479,13 +610,7 @@ def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
     read_ms = time_steps(lambda _: launch(source, floats, sink, 0), 1, 10, 2)
     copy_ms = time_steps(lambda _: launch(source, floats, target, floats), 1, 10, 2)
     del source, target
-    read_floats = (read_bytes // 4 + 3) // 4 * 4
-    write_floats = min(read_floats, (write_bytes // 4 + 3) // 4 * 4)
-    n_sets = n_sets_for(read_bytes + write_bytes)
-    sources = [torch.randn(read_floats, device="cuda") for _ in range(n_sets)]
-    out = torch.empty(max(write_floats, 8192), device="cuda")
-    op_ms = time_steps(lambda i: launch(sources[i], read_floats, out, write_floats), n_sets, steps, 20)
-    moved = (read_floats + write_floats) * 4
+    op_ms, moved = same_bytes_copy_ms(read_bytes, write_bytes, steps, 20)
     return {"read_GBps": round(floats * 4 / (read_ms * 1e-3) / 1e9, 1),
             "copy_GBps": round(2 * floats * 4 / (copy_ms * 1e-3) / 1e9, 1),
             "same_bytes_copy_us": round(op_ms * 1e3, 3),
@@ -534,7 +659,8 @@ def reference_shapes(steps: int) -> dict:
 
     tests/csrc/latency/test_segment_ops_latency.py of the reference: 3,000 atoms, 181,838 edges,
     dst = sorted uniform draws, env ~ U(0.1, 1.1), logits/null logits ~ N(0, 1) at 64 and 256
-    channels, force assembly on uniform random sources.  `eager_ms` follows its `_median_ms`
+    channels, segment_sum with a node scale at 64, 256 and 640 channels (its `_CHANNELS`, :49),
+    force assembly on uniform random sources.  `eager_ms` follows its `_median_ms`
     (10 warmup calls, median of 5 repeats of 20 calls between events, same inputs every call);
     `kernel_ms` is the graph replay of this file.  `dcu_ms` is the reference's published figure
     on its Hygon DCU (docs/task2-hip-fusion-plan.md:229, :272), other hardware.
@@ -590,7 +716,7 @@ def reference_shapes(steps: int) -> dict:
                                      "torch_gpu_ms": round(median_eager(chain), 4), "dcu_ms": 0.182,
                                      "dcu_torch_ms": 1.006, "source": "docs/task2-hip-fusion-plan.md:272"}
         node_scale = torch.rand(atoms, generator=generator, device="cuda") + 0.5
-        for channels in (64, 256):
+        for channels in (64, 256, 640):
             src_rows = torch.randn(edges, channels, generator=generator, device="cuda")
             call = lambda _=None, rows=src_rows: kernels.segment_sum(rows, dst, offsets, None, node_scale)
             chain = lambda _=None, rows=src_rows: _torch_sum_chain(rows, dst, atoms, node_scale)
@@ -687,8 +813,145 @@ def cpu_baselines(softmax_case, seconds: float, extra_ops: dict | None) -> tuple
     return headline, extras
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic per step from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)
+# ---------------------------------------------------------------------------
+
+PMC_COMMAND = ("timeout -s KILL 1100 rocprofv3 --pmc {counter} --output-format csv -d gpurun_out/pmc_{tag} -o run "
+               "-- python3 -u bench.py --no-cpu-baseline --traffic-marks --steps 20 --warmup 5 "
+               "> gpurun_out/pmc_{tag}.log 2>&1")
+SUMMARY_COMMAND = ("python3 bench.py --traffic-summary gpurun_out/pmc_fetch/run_counter_collection.csv "
+                   "gpurun_out/pmc_write/run_counter_collection.csv gpurun_out/pmc_fetch.log")
+CALIBRATION_LABEL = "calibration_copy"
+CALIBRATION_FLOATS = 64 * 2**20  # a 256 MiB read and a 256 MiB write
+
+
+def _kernel_short(name: str) -> str:
+    """A kernel's name without `void`, anonymous namespaces or the parameter list."""
+    name = name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def _counter_dispatches(path: str, counter: str) -> list[tuple[str, int, float]]:
+    """(kernel, workgroups, counter value in KiB) of every dispatch in a rocprofv3 --pmc CSV, in order."""
+    import csv
+
+    with open(path, newline="") as handle:
+        rows = [row for row in csv.DictReader(handle) if row["Counter_Name"] == counter]
+    rows.sort(key=lambda row: int(row["Dispatch_Id"]))
+    return [(_kernel_short(row["Kernel_Name"]), int(row["Grid_Size"]) // max(1, int(row["Workgroup_Size"])),
+             float(row["Counter_Value"])) for row in rows]
+
+
+def _marked_steps(dispatches, labels: list[str]) -> dict:
+    """{label: [[(kernel, workgroups, value), ...] for each step]} from TrafficMarks' markers."""
+    lines, label, steps = {}, None, None
+    for kernel, blocks, value in dispatches:
+        if kernel.endswith("stream_read_kernel") and blocks < 256:
+            if blocks >= TrafficMarks.FIRST_LABEL:
+                label, steps = labels[blocks - TrafficMarks.FIRST_LABEL], []
+            elif blocks == TrafficMarks.STEP and steps is not None:
+                steps.append([])
+            elif blocks == TrafficMarks.END and steps is not None:
+                lines[label] = steps
+                label, steps = None, None
+            continue
+        if steps:
+            steps[-1].append((kernel, blocks, value))
+    return lines
+
+
+def _bench_json(path: str) -> dict:
+    with open(path) as handle:
+        rows = [row for row in handle if row.startswith("{")]
+    if not rows:
+        raise SystemExit(f"no bench JSON line in {path}")
+    return json.loads(rows[-1])
+
+
+def traffic_summary(fetch_csv: str, write_csv: str, bench_log: str, out_dir: Path | None = None) -> int:
+    """Write profiles/traffic.json and profiles/traffic.md from one FETCH_SIZE and one WRITE_SIZE pass.
+
+    Both passes run `bench.py --traffic-marks` under rocprofv3 --pmc (PMC_COMMAND).  Each bench
+    line's steps are the dispatches between its step markers; a step's traffic is the sum over
+    its dispatches of both counters, each scaled by what it reads for the calibration copy
+    (256 MiB read, 256 MiB written by dpa4k_stream_calibrate).  The figure per line is the
+    median over its steps after the first.
+    """
+    import statistics
+
+    line = _bench_json(bench_log)
+    labels = line.get("traffic_marks")
+    if not labels:
+        raise SystemExit(f"{bench_log} was not written by a --traffic-marks run")
+    fetch = _marked_steps(_counter_dispatches(fetch_csv, "FETCH_SIZE"), labels)
+    write = _marked_steps(_counter_dispatches(write_csv, "WRITE_SIZE"), labels)
+    for label, steps in fetch.items():
+        other = write.get(label)
+        same = other is not None and [[d[:2] for d in st] for st in steps] == [[d[:2] for d in st] for st in other]
+        if not same:
+            raise SystemExit(f"the two passes launched different kernels for {label}")
+    copy_bytes = CALIBRATION_FLOATS * 4
+    fetch_scale = copy_bytes / (statistics.median(st[0][2] for st in fetch[CALIBRATION_LABEL]) * 1024)
+    write_scale = copy_bytes / (statistics.median(st[0][2] for st in write[CALIBRATION_LABEL]) * 1024)
+    algorithmic = {line["config"]["workload"]: line["roofline"]["algorithmic_bytes"]}
+    algorithmic.update({key: op["roofline"]["algorithmic_bytes"] for key, op in line.get("ops", {}).items()})
+    table, rows = {}, []
+    for label in labels:
+        if label == CALIBRATION_LABEL or label not in algorithmic or label not in fetch:
+            continue
+        steps_f, steps_w = fetch[label], write[label]
+        counted = range(1, len(steps_f)) if len(steps_f) > 2 else range(len(steps_f))
+        fetched = statistics.median(sum(d[2] for d in steps_f[i]) * 1024 * fetch_scale for i in counted)
+        written = statistics.median(sum(d[2] for d in steps_w[i]) * 1024 * write_scale for i in counted)
+        kernels = list(dict.fromkeys(d[0] for d in steps_f[counted[0]]))
+        table[label] = {"bytes_per_launch": int(fetched + written), "fetch_bytes": int(fetched),
+                        "write_bytes": int(written), "fetch_scale": round(fetch_scale, 4),
+                        "write_scale": round(write_scale, 4), "algorithmic_bytes": int(algorithmic[label]),
+                        "kernels": kernels, "steps": len(counted), "source": "profiles/traffic.md"}
+        rows.append(f"| {label} | {', '.join(f'`{k}`' for k in kernels)} | {len(counted)} | {int(fetched):,} | "
+                    f"{int(written):,} | {int(fetched + written):,} | {int(algorithmic[label]):,} | "
+                    f"{(fetched + written) / algorithmic[label]:.3f} |")
+    out = out_dir or ROOT / "profiles"
+    (out / "traffic.json").write_text(json.dumps(table, indent=1) + "\n")
+    calibration = statistics.median(st[0][2] for st in fetch[CALIBRATION_LABEL])
+    text = [
+        "# HBM traffic per step of every bench line (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+        "Commands (repository root, one MI355X; one counter per pass, eager launches, each step "
+        "bracketed by marker launches):", "", "```",
+        PMC_COMMAND.format(counter="FETCH_SIZE", tag="fetch"),
+        PMC_COMMAND.format(counter="WRITE_SIZE", tag="write"),
+        SUMMARY_COMMAND, "```", "",
+        f"Calibration: a plain copy of {copy_bytes:,} bytes (`dpa4k::stream_copy_kernel`) reads "
+        f"{calibration:,.1f} KiB by FETCH_SIZE (scale {fetch_scale:.4f}) and writes "
+        f"{copy_bytes / 1024 / write_scale:,.1f} KiB by WRITE_SIZE (scale {write_scale:.4f}).  Every figure below is "
+        "scaled by these factors; a step's traffic is the sum over all of its dispatches (library and torch "
+        "kernels alike), the median over its steps after the first.", "",
+        "| Bench line | Kernels of a step | Steps | FETCH bytes | WRITE bytes | Traffic | Algorithmic bytes | "
+        "Traffic / algorithmic |", "| --- | --- | --- | --- | --- | --- | --- | --- |", *rows, ""]
+    (out / "traffic.md").write_text("\n".join(text))
+    print(f"wrote {len(table)} lines to {out / 'traffic.json'} and traffic.md")
+    return 0
+
+
+# ---------------------------------------------------------------------------
+# driver
+# ---------------------------------------------------------------------------
+
 def main() -> int:
     args = parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the operators shard by destination-node ranges; see DESIGN.md)", file=sys.stderr)
@@ -704,10 +967,25 @@ def main() -> int:
     if not kernels.segment_available():
         print("libdpa4k.so is not usable on this device (build it with __graft_entry__.build())", file=sys.stderr)
         return 1
-    graph = not args.eager
-    print(f"[bench] headline: segment_softmax config 2, {args.steps} steps, {args.warmup} warmup", file=sys.stderr,
-          flush=True)
-    head = softmax_job(16384, args.steps, args.warmup, graph)
+    graph = not (args.eager or args.traffic_marks)
+    global MARKS
+    if args.traffic_marks:
+        from bysj_amd.kernels import _lib
+
+        MARKS = TrafficMarks()
+        source = torch.zeros(CALIBRATION_FLOATS, device="cuda")
+        target = torch.empty_like(source)
+        library = _lib.load()
+        time_steps(lambda _: _lib.check(library.dpa4k_stream_calibrate(
+            source.data_ptr(), CALIBRATION_FLOATS, target.data_ptr(), CALIBRATION_FLOATS,
+            torch.cuda.current_stream().cuda_stream)), 1, 3, 1, label=CALIBRATION_LABEL)
+        del source, target
+
+    def progress(what: str) -> None:
+        print(f"[bench] {what}", file=sys.stderr, flush=True)
+
+    progress(f"headline: segment_softmax config 2, {args.steps} steps, {args.warmup} warmup")
+    head = softmax_job(16384, args.steps, args.warmup, graph, label="segment_softmax_fwd_config2")
     value = head["edges"] / (head["ms_per_step"] * 1e-3)
     line = {
         "metric": "segment-op edges/s + % HBM roofline (segment_softmax forward, config 2)",
@@ -728,120 +1006,179 @@ def main() -> int:
                    "parallelism": "single-gpu"},
         "roofline": roofline(head["bytes"], head["ms_per_step"], "segment_softmax_fwd_config2"),
     }
-    print(f"[bench] headline done: {head['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
-    edges, channels, nodes = head["edges"], head["channels"], head["nodes"]
-    head_reads = edges * channels * 4 + edges * 4 + (nodes + 1) * 8 + nodes * channels * 4
-    ceilings = stream_ceilings(head_reads, head["bytes"] - head_reads, args.steps)
-    ceilings["headline_share_of_same_bytes_copy"] = round(ceilings["same_bytes_copy_us"] /
-                                                          (head["ms_per_step"] * 1e3), 4)
-    line["stream_ceilings"] = ceilings
-    print("[bench] stream ceilings done", file=sys.stderr, flush=True)
+    progress(f"headline done: {head['ms_per_step'] * 1e3:.2f} us/step")
+    if not args.traffic_marks:
+        ceilings = stream_ceilings(head["reads"], head["bytes"] - head["reads"], args.steps)
+        ceilings["headline_share_of_same_bytes_copy"] = round(ceilings["same_bytes_copy_us"] /
+                                                              (head["ms_per_step"] * 1e3), 4)
+        line["stream_ceilings"] = ceilings
+        progress("stream ceilings done")
 
     ops = {}
     extra_cpu = {}
     if not args.headline_only:
+        from bysj_amd import workloads
         from oracle import gie as gie_ref
         from oracle import segment as ref
 
         steps = max(10, args.steps // 4)
         warm = max(2, args.warmup // 4)
-        job = segment_sum_job(1024, steps, warm, graph)
-        ops["segment_sum_config1"] = op_line("segment_sum_fwd", job, job["edges"])
+        big = not args.no_roofline_shapes
+        backward = not args.no_backward
+
+        def add(key: str, name: str, job: dict, count: int, unit: str = "edges/s", share: bool = False) -> dict:
+            entry = op_line(name, job, count, unit)
+            if share and MARKS is None:
+                copy_share(entry, job, steps)
+            ops[key] = entry
+            return entry
+
+        # ---- segment_sum forward: config 1, 1R plain and 1R with scales and a shuffled order
+        job = segment_sum_job(1024, steps, warm, graph, label="segment_sum_config1")
+        add("segment_sum_config1", "segment_sum_fwd", job, job["edges"])
         b = {k: (v.cpu() if v is not None else None) for k, v in job["base"].items()}
         extra_cpu["segment_sum_config1"] = (
             lambda b=b: ref.segment_sum_reference(b["src"], b["dst"], b["offsets"]), job["edges"],
             "config 1 full input, oracle zeros->index_add_ chain")
-        print("[bench] segment_sum config 1 done", file=sys.stderr, flush=True)
-        gie, rms, water3, case3 = gie_rmsnorm_jobs(24576, steps, warm, graph)
-        ops["gie_config3"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
-        ops["rmsnorm_config3"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
-        ops["gie_rmsnorm_config3"] = op_line("gie_zonal_scatter_rmsnorm_fwd", gie["fused_rmsnorm"], gie["edges"])
-        ops["gie_rmsnorm_config3"]["unfused_ms_per_step"] = round(gie["ms_per_step"] + rms["ms_per_step"], 5)
+        if big:
+            job = segment_sum_job(262144, steps, warm, graph, label="segment_sum_config1R")
+            add("segment_sum_config1R", "segment_sum_fwd", job, job["edges"], share=True)
+            job = segment_sum_job(262144, steps, warm, graph, scaled_shuffled=True,
+                                  label="segment_sum_config1R_scaled_shuffled")
+            add("segment_sum_config1R_scaled_shuffled", "segment_sum_fwd", job, job["edges"], share=True)
+            del job
+            job = softmax_job(210000, steps, warm, graph, label="segment_softmax_config2R")
+            add("segment_softmax_config2R", "segment_softmax_fwd", job, job["edges"], share=True)
+            del job
+        progress("segment_sum 1/1R and segment_softmax 2R forward done")
+
+        # ---- GIE zonal scatter (primary [E,16,64] and DeepMD-shaped secondary [E,3,64]) -> RMSNorm, config 3
+        water3 = workloads.water_graph(24576, seed=0)
+        case3 = workloads.gie_config(water3, seed=0, device="cuda", primary=True)
+        jobs = gie_forward_jobs(water3, case3, steps, warm, graph,
+                                labels=("gie_config3", "gie_rmsnorm_config3", "rmsnorm_config3"))
+        add("gie_config3", "gie_zonal_scatter_fwd", jobs["gie"], water3.n_edges, share=True)
+        add("rmsnorm_config3", "rmsnorm_fwd", jobs["rms"], jobs["rms"]["rows"], unit="rows/s")
+        fused = add("gie_rmsnorm_config3", "gie_zonal_scatter_rmsnorm_fwd", jobs["fused"], water3.n_edges)
+        fused["unfused_ms_per_step"] = round(jobs["gie"]["ms_per_step"] + jobs["rms"]["ms_per_step"], 5)
         sample_nodes = 2048
         cut = int(water3.offsets()[sample_nodes])
         sample = tuple(t.cpu() for t in (case3["zonal"][:cut], case3["radial"][:cut], case3["dst"][:cut],
                                          case3["radial_slot"], case3["inv_sqrt_deg"][:sample_nodes]))
         extra_cpu["gie_config3"] = (lambda s=sample: gie_ref.zonal_scatter_reference(*s), cut,
                                     f"first {sample_nodes} atoms of config 3 ({cut} edges), oracle chain")
+        if backward:
+            job = gie_backward_job(water3, case3, steps, warm, graph, label="gie_bwd_config3")
+            add("gie_bwd_config3", "gie_zonal_scatter_bwd", job, job["edges"], share=True)
         del case3
-        print("[bench] gie + rmsnorm config 3 done", file=sys.stderr, flush=True)
-        from bysj_amd import workloads
+        case3s = workloads.gie_config(water3, seed=0, device="cuda", primary=False)
+        jobs = gie_forward_jobs(water3, case3s, steps, warm, graph, labels=("gie_config3_secondary", None, None))
+        add("gie_config3_secondary", "gie_zonal_scatter_fwd", jobs["gie"], water3.n_edges, share=True)
+        sample = tuple(t.cpu() for t in (case3s["zonal"][:cut], case3s["radial"][:cut], case3s["dst"][:cut],
+                                         case3s["radial_slot"], case3s["inv_sqrt_deg"][:sample_nodes]))
+        extra_cpu["gie_config3_secondary"] = (lambda s=sample: gie_ref.zonal_scatter_reference(*s), cut,
+                                              f"first {sample_nodes} atoms of config 3 secondary ({cut} edges), "
+                                              "oracle chain")
+        if backward:
+            job = gie_backward_job(water3, case3s, steps, warm, graph, label="gie_bwd_config3_secondary")
+            add("gie_bwd_config3_secondary", "gie_zonal_scatter_bwd", job, job["edges"], share=True)
+            jobs = rmsnorm_jobs(24576, steps, warm, graph, labels=(None, "rmsnorm_bwd_config3"))
+            add("rmsnorm_bwd_config3", "rmsnorm_bwd", jobs["bwd"], 24576, unit="rows/s")
+        del case3s, sample
+        torch.cuda.empty_cache()
+        progress("gie + rmsnorm config 3 (primary, secondary) done")
 
+        # ---- force assembly, config 4 (random and Morton atom numbering) and 4R
         water4 = workloads.water_graph(65536, seed=0)
         for dtype_name in ("f32", "f64"):
-            job, _, base = force_job(65536, steps, warm, graph, dtype_name, water=water4)
-            ops[f"force_assembly_config4_{dtype_name}"] = op_line("force_assembly", job, job["edges"])
+            key = f"force_assembly_config4_{dtype_name}"
+            job, _, base = force_job(65536, steps, warm, graph, dtype_name, water=water4, label=key)
+            add(key, "force_assembly", job, job["edges"])
             bb = {k: v.cpu() for k, v in base.items()}
-            extra_cpu[f"force_assembly_config4_{dtype_name}"] = (
+            extra_cpu[key] = (
                 lambda bb=bb: ref.force_assembly_reference(bb["grad_edge"], bb["edge_vec"], bb["src"], bb["dst"],
                                                            bb["dst_offsets"], bb["src_offsets"]),
                 job["edges"], f"config 4 full input ({dtype_name}), oracle two index_add_ + outer product")
-            print(f"[bench] force config 4 {dtype_name} done", file=sys.stderr, flush=True)
+            del base
         # the same box with atoms numbered in spatial (Morton) order, as MD engines sort them
         water4s = workloads.water_graph(65536, seed=0, spatial_order=True)
         for dtype_name in ("f32", "f64"):
-            job, _, _ = force_job(65536, steps, warm, graph, dtype_name, water=water4s)
-            ops[f"force_assembly_config4_{dtype_name}_spatial"] = op_line("force_assembly", job, job["edges"])
-        print("[bench] force config 4 spatial order done", file=sys.stderr, flush=True)
-        if not args.no_backward:
-            job = softmax_backward_job(16384, steps, warm, graph)
-            ops["segment_softmax_bwd_config2"] = op_line("segment_softmax_bwd", job, job["edges"])
-            job = segment_sum_backward_job(1024, steps, warm, graph)
-            ops["segment_sum_bwd_config1"] = op_line("segment_sum_bwd", job, job["edges"])
-            job = segment_sum_backward_job(262144, max(4, steps // 4), warm, graph)
-            ops["segment_sum_bwd_config1R"] = op_line("segment_sum_bwd", job, job["edges"])
-            case3 = workloads.gie_config(water3, seed=0, device="cuda", primary=True)
-            gie_b, rms_b = gie_rmsnorm_backward_jobs(water3, case3, steps, warm, graph)
-            del case3
-            ops["gie_bwd_config3"] = op_line("gie_zonal_scatter_bwd", gie_b, gie_b["edges"])
-            ops["rmsnorm_bwd_config3"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
-            job = csr_job(water4, steps, warm, graph)
-            line_csr = op_line("group_by_source", job, job["edges"])
-            line_csr["eager_ms_per_call"] = round(job["eager_ms_per_call"], 5)
-            line_csr["torch_argsort_bincount_ms"] = round(job["torch_ms_per_call"], 5)
-            ops["group_by_source_config4"] = line_csr
-            print("[bench] backward kernels and CSR build done", file=sys.stderr, flush=True)
-        if args.roofline_shapes:
-            job = segment_sum_job(262144, steps, warm, graph)
-            ops["segment_sum_config1R"] = op_line("segment_sum_fwd", job, job["edges"])
-            job = segment_sum_job(262144, steps, warm, graph, scaled_shuffled=True)
-            ops["segment_sum_config1R_scaled_shuffled"] = op_line("segment_sum_fwd", job, job["edges"])
-            job = softmax_job(210000, steps, warm, graph)
-            ops["segment_softmax_config2R"] = op_line("segment_softmax_fwd", job, job["edges"])
-            if not args.no_backward:
-                job = softmax_backward_job(210000, steps, warm, graph)
-                ops["segment_softmax_bwd_config2R"] = op_line("segment_softmax_bwd", job, job["edges"])
-            print("[bench] roofline shapes 1R, 2R done", file=sys.stderr, flush=True)
+            key = f"force_assembly_config4_{dtype_name}_spatial"
+            job, _, _ = force_job(65536, steps, warm, graph, dtype_name, water=water4s, label=key)
+            add(key, "force_assembly", job, job["edges"])
+        del water4s
+        if big:
             water4r = workloads.water_graph(131072, seed=0)
             for dtype_name in ("f32", "f64"):
-                job, _, _ = force_job(131072, steps, warm, graph, dtype_name, water=water4r)
-                ops[f"force_assembly_config4R_{dtype_name}"] = op_line("force_assembly", job, job["edges"])
+                key = f"force_assembly_config4R_{dtype_name}"
+                job, _, _ = force_job(131072, steps, warm, graph, dtype_name, water=water4r, label=key)
+                add(key, "force_assembly", job, job["edges"], share=True)
             del water4r
-            print("[bench] roofline shape 4R done", file=sys.stderr, flush=True)
-            # config 3R: 114,688 atoms (E ~ 10.4M; GIE radial [E, 16, 64] is 42.6 GB), two GIE steps
-            water3r = workloads.water_graph(114688, seed=0)
-            gie, rms, _, case3r = gie_rmsnorm_jobs(114688, steps, warm, graph, water=water3r, gie_steps=2)
-            ops["gie_config3R"] = op_line("gie_zonal_scatter_fwd", gie, gie["edges"])
-            ops["rmsnorm_config3R"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
-            ops["gie_rmsnorm_config3R"] = op_line("gie_zonal_scatter_rmsnorm_fwd", gie["fused_rmsnorm"],
-                                                  gie["edges"])
-            ops["gie_rmsnorm_config3R"]["unfused_ms_per_step"] = round(gie["ms_per_step"] + rms["ms_per_step"], 5)
-            if not args.no_backward:
-                gie_b, rms_b = gie_rmsnorm_backward_jobs(water3r, case3r, steps, warm, graph, gie_steps=2)
-                ops["gie_bwd_config3R"] = op_line("gie_zonal_scatter_bwd", gie_b, gie_b["edges"])
-                ops["rmsnorm_bwd_config3R"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
-            del case3r, water3r
+        torch.cuda.empty_cache()
+        progress("force assembly config 4 / 4R done")
+
+        # ---- backward kernels and the CSR build
+        if backward:
+            job = softmax_backward_job(16384, steps, warm, graph, label="segment_softmax_bwd_config2")
+            add("segment_softmax_bwd_config2", "segment_softmax_bwd", job, job["edges"])
+            job = segment_sum_backward_job(1024, steps, warm, graph, label="segment_sum_bwd_config1")
+            add("segment_sum_bwd_config1", "segment_sum_bwd", job, job["edges"])
+            if big:
+                job = softmax_backward_job(210000, steps, warm, graph, label="segment_softmax_bwd_config2R")
+                add("segment_softmax_bwd_config2R", "segment_softmax_bwd", job, job["edges"], share=True)
+                job = segment_sum_backward_job(262144, max(4, steps // 4), warm, graph,
+                                               label="segment_sum_bwd_config1R")
+                add("segment_sum_bwd_config1R", "segment_sum_bwd", job, job["edges"], share=True)
+            job = csr_job(water4, steps, warm, graph, label="group_by_source_config4")
+            entry = add("group_by_source_config4", "group_by_source", job, job["edges"])
+            entry["eager_ms_per_call"] = round(job["eager_ms_per_call"], 5)
+            entry["torch_argsort_bincount_ms"] = round(job["torch_ms_per_call"], 5)
             torch.cuda.empty_cache()
-            print("[bench] roofline shape 3R done", file=sys.stderr, flush=True)
-            rms, rms_b = rmsnorm_jobs(1048576, steps, warm, graph)
-            ops["rmsnorm_rows1M"] = op_line("rmsnorm_fwd", rms, rms["rows"], unit="rows/s")
-            ops["rmsnorm_bwd_rows1M"] = op_line("rmsnorm_bwd", rms_b, rms_b["rows"], unit="rows/s")
-            print("[bench] roofline shapes done", file=sys.stderr, flush=True)
+            progress("backward kernels and CSR build done")
+        del water4
+
+        # ---- config 3R: 114,688 atoms (E ~ 10.4M; the primary radial [E, 16, 64] is 42.6 GB)
+        if big:
+            water3r = workloads.water_graph(114688, seed=0)
+            case = workloads.gie_config(water3r, seed=0, device="cuda", primary=True)
+            jobs = gie_forward_jobs(water3r, case, steps, warm, graph, gie_steps=2,
+                                    labels=("gie_config3R", "gie_rmsnorm_config3R", "rmsnorm_config3R"))
+            add("gie_config3R", "gie_zonal_scatter_fwd", jobs["gie"], water3r.n_edges, share=True)
+            add("rmsnorm_config3R", "rmsnorm_fwd", jobs["rms"], jobs["rms"]["rows"], unit="rows/s", share=True)
+            fused = add("gie_rmsnorm_config3R", "gie_zonal_scatter_rmsnorm_fwd", jobs["fused"], water3r.n_edges,
+                        share=True)
+            fused["unfused_ms_per_step"] = round(jobs["gie"]["ms_per_step"] + jobs["rms"]["ms_per_step"], 5)
+            del jobs
+            if backward:
+                job = gie_backward_job(water3r, case, steps, warm, graph, gie_steps=2, label="gie_bwd_config3R")
+                add("gie_bwd_config3R", "gie_zonal_scatter_bwd", job, job["edges"], share=True)
+            del case
+            torch.cuda.empty_cache()
+            case = workloads.gie_config(water3r, seed=0, device="cuda", primary=False)
+            jobs = gie_forward_jobs(water3r, case, steps, warm, graph, labels=("gie_config3R_secondary", None, None))
+            add("gie_config3R_secondary", "gie_zonal_scatter_fwd", jobs["gie"], water3r.n_edges, share=True)
+            if backward:
+                job = gie_backward_job(water3r, case, steps, warm, graph, label="gie_bwd_config3R_secondary")
+                add("gie_bwd_config3R_secondary", "gie_zonal_scatter_bwd", job, job["edges"], share=True)
+                jobs = rmsnorm_jobs(114688, steps, warm, graph, labels=(None, "rmsnorm_bwd_config3R"))
+                add("rmsnorm_bwd_config3R", "rmsnorm_bwd", jobs["bwd"], 114688, unit="rows/s", share=True)
+            del case, water3r
+            torch.cuda.empty_cache()
+            progress("config 3R (primary, secondary) done")
+            jobs = rmsnorm_jobs(1048576, steps, warm, graph,
+                                labels=("rmsnorm_rows1M", "rmsnorm_bwd_rows1M" if backward else None))
+            add("rmsnorm_rows1M", "rmsnorm_fwd", jobs["fwd"], 1048576, unit="rows/s", share=True)
+            if backward:
+                add("rmsnorm_bwd_rows1M", "rmsnorm_bwd", jobs["bwd"], 1048576, unit="rows/s", share=True)
+            del jobs
+            torch.cuda.empty_cache()
+            progress("rmsnorm 1M rows done")
         for key, op in ops.items():
             op["roofline"]["traffic"] = measured_traffic(key, op["roofline"]["algorithmic_bytes"])
         line["ops"] = ops
-        line["reference_shapes"] = reference_shapes(steps)
-        print("[bench] reference latency shapes done", file=sys.stderr, flush=True)
+        if MARKS is None:
+            line["reference_shapes"] = reference_shapes(steps)
+            progress("reference latency shapes done")
 
     # BASELINE.json config 5 (DPA4Model(fused=True) end to end at 32,768 atoms) needs a DPA4/SeZM
     # model created by DeepMD-kit and DeepMD's own DeepPot; without DeepMD there is nothing to run.
@@ -856,16 +1193,11 @@ def main() -> int:
         line["config5_dpa4_end_to_end"] = {
             "status": "not run", "unit": "atom-steps/s", "value": None,
             "reason": "deepmd-kit is importable, but no frozen DPA4 model is available to this benchmark"}
-
-    if args.calibrate_copy:
-        source = torch.ones(64 * 2**20, dtype=torch.float32, device="cuda")
-        target = torch.empty_like(source)
-        target.copy_(source)
-        torch.cuda.synchronize()
-        line["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4}
+    if MARKS is not None:
+        line["traffic_marks"] = MARKS.labels
 
     if not args.no_cpu_baseline:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        progress("cpu baseline")
         headline_cpu, extras = cpu_baselines(head["base"], args.cpu_seconds, extra_cpu)
         line["cpu_baseline"] = headline_cpu
         for name, result in extras.items():

@@ -57,6 +57,7 @@ constexpr int64_t kShortGap = 64;                      // offsets a thread fills
 constexpr uint32_t kNone = 0xffffffffu;
 
 enum : int32_t { kFlagOutOfRange = 1, kFlagUnsorted = 2, kFlagSlotRange = 4, kFlagSlotShared = 8 };
+constexpr int kSlotRowsShift = 16;  // bits 16..23: most rows reading one radial slot (GIE grouping)
 enum Gate : int { kAlways = 0, kIfSorted = 1, kIfUnsorted = 2 };
 
 static_assert(DPA4K_CSR_OUT_OF_RANGE == kFlagOutOfRange && DPA4K_CSR_UNSORTED == kFlagUnsorted,
@@ -691,16 +692,28 @@ __global__ __launch_bounds__(kThreads) void widen_kernel(const uint32_t* __restr
     order[i] = static_cast<int64_t>(index[i]);
 }
 
-// Range and sharing checks of the GIE radial slots (one small block).
+// Range and sharing checks of the GIE radial slots (one block of 64).  Also
+// ORs the largest number of rows that read one slot, capped at 255, into
+// bits 16..23 of the status word (kSlotRowsShift).
 __global__ __launch_bounds__(64) void slot_check_kernel(const int64_t* __restrict__ radial_slot, int64_t n_rows,
                                                         int64_t n_radial, int32_t* __restrict__ status) {
+  __shared__ int most;
+  if (threadIdx.x == 0) most = 0;
+  __syncthreads();
   int32_t local = 0;
+  int rows_of_slot = 0;
   for (int64_t r = threadIdx.x; r < n_rows; r += blockDim.x) {
     const int64_t slot = radial_slot[r];
     if (static_cast<uint64_t>(slot) >= static_cast<uint64_t>(n_radial)) local |= kFlagSlotRange;
-    for (int64_t other = r + 1; other < n_rows; ++other)
-      if (radial_slot[other] == slot) local |= kFlagSlotShared;
+    int64_t readers = 0;
+    for (int64_t other = 0; other < n_rows; ++other) readers += radial_slot[other] == slot ? 1 : 0;
+    if (readers > 1) local |= kFlagSlotShared;
+    const int capped = readers > 255 ? 255 : static_cast<int>(readers);
+    rows_of_slot = capped > rows_of_slot ? capped : rows_of_slot;
   }
+  atomicMax(&most, rows_of_slot);
+  __syncthreads();
+  if (threadIdx.x == 0) local |= most << kSlotRowsShift;
   if (local != 0) atomicOr(status, local);
 }
 
@@ -1028,6 +1041,7 @@ extern "C" int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot, i
   if (flags & kFlagOutOfRange) return fail(DPA4K_EINVAL, "GIE dst values must be within the node range");
   if (flags & kFlagSlotRange) return fail(DPA4K_EINVAL, "GIE radial_slot values must be within the radial range");
   const bool sorted = !(flags & kFlagUnsorted);
-  if (host_info != nullptr) *host_info = (sorted ? 1 : 0) | ((flags & kFlagSlotShared) ? 0 : 2);
+  if (host_info != nullptr)
+    *host_info = (sorted ? 1 : 0) | ((flags & kFlagSlotShared) ? 0 : 2) | (flags & (0xff << kSlotRowsShift));
   return DPA4K_OK;
 }

@@ -128,6 +128,152 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
   }
 }
 
+// Shared radial slots (several rows read one slot, e.g. one radial channel
+// per degree l).  Each slot's rows are split into groups of at most G rows,
+// G the smallest that lets every group have row_chunks = C / 4 lanes of its
+// own (a slot with k rows takes ceil(k / G) groups); lane pair p = lane + 64 j
+// serves chunk p % row_chunks of group p / row_chunks.  Every radial element
+// is then loaded by one lane per group of its slot instead of once per row,
+// and the lanes' row counts stay within G of each other (DeepMD's 3 / 5 / 7
+// rows at C = 64 become 4 groups of at most 5).  Lane r < R loads zonal[e, r]
+// and the lanes fetch the values of their rows with ds_bpermute.  Per output
+// element the arithmetic is gie_forward_kernel's (edges in CSR order, product
+// rounded, then added, normalised after the sum): the same output bit for
+// bit.  Needs C % 4 == 0, 1 <= R <= 64, S <= 64, S * C / 4 <= 64 * PPL, and
+// at most MAXR rows per slot.
+template <int PPL, int MAXR, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
+    const float* __restrict__ zonal, const float* __restrict__ radial,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ order,
+    const int64_t* __restrict__ radial_slot, const float* __restrict__ inv,
+    float* __restrict__ out, int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+    int64_t channels) {
+  constexpr int U = 4;
+  const int64_t node = block_index() * kWaves + (threadIdx.x >> 6);
+  if (node >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  const int row_chunks = static_cast<int>(channels / 4);
+  const int slots = static_cast<int>(n_radial);
+  const int rows = static_cast<int>(n_rows);
+  const int64_t edge_stride = n_radial * channels;
+
+  // the group plan, the same in every lane: lane t < S counts the rows of slot t
+  int rows_of_lane_slot = 0;
+  for (int r = 0; r < rows; ++r) rows_of_lane_slot += radial_slot[r] == lane ? 1 : 0;
+  const int groups_available = 64 * PPL / row_chunks;
+  int group_rows = MAXR;
+  for (int g = 1; g < MAXR; ++g) {
+    int needed = 0;
+    for (int t = 0; t < slots; ++t) needed += (__builtin_amdgcn_readlane(rows_of_lane_slot, t) + g - 1) / g;
+    if (needed <= groups_available) {
+      group_rows = g;
+      break;
+    }
+  }
+
+  // each pair's slot and its rows (ascending); unused entries point at row 0
+  int row_of[PPL][MAXR];
+  int count[PPL];
+  int64_t radial_col[PPL], chunk_col[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = lane + 64 * j;
+    const int group = p / row_chunks;
+    const int c = p - group * row_chunks;
+    int slot = -1, part = 0, first = 0;
+    for (int t = 0; t < slots; ++t) {
+      const int groups = (__builtin_amdgcn_readlane(rows_of_lane_slot, t) + group_rows - 1) / group_rows;
+      if (group >= first && group < first + groups) {
+        slot = t;
+        part = group - first;
+      }
+      first += groups;
+    }
+    radial_col[j] = slot >= 0 ? static_cast<int64_t>(slot) * channels + c * 4 : 0;
+    chunk_col[j] = c * 4;
+    count[j] = 0;
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k) row_of[j][k] = 0;
+    int seen = 0;
+    for (int r = 0; r < rows; ++r) {
+      const bool reads = slot >= 0 && radial_slot[r] == slot;
+      const int k = seen - part * group_rows;
+      const bool mine = reads && k >= 0 && k < group_rows;
+#pragma unroll
+      for (int kk = 0; kk < MAXR; ++kk)
+        if (mine && k == kk) row_of[j][kk] = r;
+      count[j] += mine ? 1 : 0;
+      seen += reads ? 1 : 0;
+    }
+  }
+
+  fvec<4> acc[PPL][MAXR];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j)
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][k].v[i] = 0.0f;
+
+  const int64_t zonal_row = lane < rows ? lane : rows - 1;
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  for (int64_t slot = begin; slot < end; slot += U) {
+    int64_t edge[U];
+    bool use[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = slot + u < end ? edge_of<kOrdered>(order, slot + u, n_edges) : -1;
+      use[u] = e >= 0;
+      edge[u] = e >= 0 ? e : begin;  // a valid edge to load from when this one is skipped
+    }
+    float zq[U];
+    fvec<4> x[U][PPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      zq[u] = zonal[edge[u] * n_rows + zonal_row];
+#pragma unroll
+      for (int j = 0; j < PPL; ++j) x[u][j] = load_vec<4>(radial + edge[u] * edge_stride + radial_col[j]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!use[u]) continue;  // wave-uniform
+#pragma unroll
+      for (int k = 0; k < MAXR; ++k) {
+        if (k >= group_rows) break;  // wave-uniform
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+          const float z = __int_as_float(__builtin_amdgcn_ds_bpermute(row_of[j][k] << 2, __float_as_int(zq[u])));
+          if (k < count[j])
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[j][k].v[i] = acc[j][k].v[i] + z * x[u][j].v[i];
+        }
+      }
+    }
+  }
+
+  const float scale = inv[node];
+  float* node_out = out + node * (n_rows + 1) * channels;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j)
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k) {
+      if (k >= count[j]) continue;
+      fvec<4> result;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) result.v[i] = acc[j][k].v[i] * scale;
+      store_vec<4>(node_out + (row_of[j][k] + 1) * channels + chunk_col[j], result);
+    }
+  // row 0, and rows whose slot is out of range (no group serves them): 0 * inv
+  fvec<4> zero;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) zero.v[i] = 0.0f * scale;
+  for (int64_t c = lane; c < row_chunks; c += 64) store_vec<4>(node_out + c * 4, zero);
+  for (int64_t r = 0; r < n_rows; ++r)
+    if (static_cast<uint64_t>(radial_slot[r]) >= static_cast<uint64_t>(n_radial))
+      for (int64_t c = lane; c < row_chunks; c += 64) store_vec<4>(node_out + (r + 1) * channels + c * 4, zero);
+}
+
 // Fused GIE -> RMSNorm over each node's flattened row of W = (R + 1) * C
 // floats (no reference counterpart; the reference runs the two operators
 // back to back).  One wave per node, float4 chunks.  Lane l owns the chunks
@@ -348,6 +494,141 @@ __global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
 #pragma unroll
       for (int i = 0; i < V; ++i) total = total + g[j].v[i] * pre[j].v[i];
     total = group_sum<64>(total);
+    if (lane == 0) grad_inv[node] = total;
+  }
+}
+
+// Shared radial slots, backward.  LPE = S * RC lanes serve one edge (RC =
+// C / 8 lanes per slot, 8 channels each) and EPI = 64 / LPE edges are
+// handled side by side: lane (u, s, c) takes edge slot base + u, radial slot
+// s and channels [8 c, 8 c + 8) for every row r that reads s (at most MAXR),
+// with that node's upstream rows g[r + 1, :] held in registers:
+//   grad_zonal[e, r]      = inv * sum_c g[r, c] radial[e, s, c]   (RC-lane butterfly)
+//   grad_radial[e, s, c]  = sum_{r reads s} g[r, c] * (zonal[e, r] * inv)
+//   grad_inv             += zonal[e, r] * sum_c g[r, c] radial[e, s, c]
+// Each radial element is read and each gradient written once.  Every
+// iteration loads UU wave steps' radial and zonal values before any of
+// their arithmetic, which keeps enough bytes in flight per wave.  (Measured
+// on the DeepMD map at C = 64: 8 channels per lane beat 4 (more butterfly
+// steps) and 16 (register-bound occupancy), and the plain loop beat
+// software-pipelined forms, whose loads waited for the previous step's
+// stores: gfx9's vmcnt counts both.)  Fused multiply-adds in a fixed order:
+// reproducible, within fp32 rounding of the oracle's (inv * g) . radial
+// association.  Needs C % 8 == 0 with RC a power of two and S * RC <= 64.
+template <int RC, int MAXR, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_backward_shared_kernel(
+    const float* __restrict__ grad_output, const float* __restrict__ zonal,
+    const float* __restrict__ radial, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ order, const int64_t* __restrict__ radial_slot,
+    const float* __restrict__ inv, float* __restrict__ grad_zonal, float* __restrict__ grad_radial,
+    float* __restrict__ grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+    int64_t n_radial, int64_t channels) {
+  constexpr int V = 8;
+  constexpr int UU = 4;
+  const int64_t node = block_index() * kWaves + (threadIdx.x >> 6);
+  if (node >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  const int lpe = static_cast<int>(n_radial) * RC;
+  const int epi = 64 / lpe;
+  const int u = lane / lpe;
+  const int w = lane - u * lpe;
+  const bool active = u < epi;
+  const int64_t s = active ? w / RC : -1;
+  const int c = w % RC;
+  const int64_t edge_stride = n_radial * channels;
+  const int64_t radial_col = (active ? s : 0) * channels + c * V;
+  const float scale = inv[node];
+
+  // the rows of this lane's slot, ascending; unused entries point at row 0
+  int row_of[MAXR];
+  int count = 0;
+#pragma unroll
+  for (int k = 0; k < MAXR; ++k) row_of[k] = 0;
+  bool stray_rows = false;  // rows whose slot is out of range: their zonal gradient is zero
+  for (int64_t r = 0; r < n_rows; ++r) {
+    const int64_t slot = radial_slot[r];
+    stray_rows = stray_rows || static_cast<uint64_t>(slot) >= static_cast<uint64_t>(n_radial);
+    const bool reads = active && slot == s;
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k)
+      if (reads && count == k) row_of[k] = static_cast<int>(r);
+    count += reads ? 1 : 0;
+  }
+
+  float g[MAXR][V];
+#pragma unroll
+  for (int k = 0; k < MAXR; ++k) {
+    const float* row = grad_output + (node * (n_rows + 1) + row_of[k] + 1) * channels + c * V;
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q) {
+      fvec<4> part;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part.v[i] = 0.0f;
+      if (k < count) part = load_vec<4>(row + 4 * q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) g[k][4 * q + i] = part.v[i];
+    }
+  }
+
+  float inv_partial = 0.0f;
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  for (int64_t base = begin; base < end; base += UU * epi) {
+    int64_t e[UU];
+    float x[UU][V], z[UU][MAXR];
+#pragma unroll
+    for (int uu = 0; uu < UU; ++uu) {
+      const int64_t at = base + uu * epi + u;
+      e[uu] = active && at < end ? edge_of<kOrdered>(order, at, n_edges) : -1;
+      const int64_t edge = e[uu] >= 0 ? e[uu] : begin;  // a valid edge to load from
+#pragma unroll
+      for (int q = 0; q < V / 4; ++q) {
+        const fvec<4> part = load_vec<4>(radial + edge * edge_stride + radial_col + 4 * q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[uu][4 * q + i] = part.v[i];
+      }
+#pragma unroll
+      for (int k = 0; k < MAXR; ++k) z[uu][k] = zonal[edge * n_rows + row_of[k]];
+    }
+#pragma unroll
+    for (int uu = 0; uu < UU; ++uu) {
+      const bool use = e[uu] >= 0;
+      float out[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) out[i] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < MAXR; ++k) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) dot = __builtin_fmaf(g[k][i], x[uu][i], dot);
+        dot = group_sum<RC>(dot);
+        if (use && k < count && c == 0) {
+          if (grad_zonal != nullptr) grad_zonal[e[uu] * n_rows + row_of[k]] = dot * scale;
+          inv_partial = __builtin_fmaf(z[uu][k], dot, inv_partial);
+        }
+        const float weight = k < count ? z[uu][k] * scale : 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) out[i] = __builtin_fmaf(g[k][i], weight, out[i]);
+      }
+      if (use && grad_radial != nullptr)
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          fvec<4> part;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) part.v[i] = out[4 * q + i];
+          store_vec_stream<4>(grad_radial + e[uu] * edge_stride + radial_col + 4 * q, part);
+        }
+    }
+  }
+  if (stray_rows && grad_zonal != nullptr)
+    for (int64_t r = 0; r < n_rows; ++r)
+      if (static_cast<uint64_t>(radial_slot[r]) >= static_cast<uint64_t>(n_radial))
+        for (int64_t at = begin + lane; at < end; at += 64) {
+          const int64_t e = edge_of<kOrdered>(order, at, n_edges);
+          if (e >= 0) grad_zonal[e * n_rows + r] = 0.0f;
+        }
+  if (grad_inv != nullptr) {
+    const float total = group_sum<64>(inv_partial);
     if (lane == 0) grad_inv[node] = total;
   }
 }
@@ -573,6 +854,66 @@ int launch_general(int cpl, size_t lds_bytes, const float* grad_output, const fl
   return launched("gie_backward_general_kernel");
 }
 
+// Bits of dpa4k_gie_group's host_info that pick a kernel: bit 2 = every slot
+// feeds at most one row, bits 16..23 = the most rows that read one slot.
+constexpr int32_t kSlotsDistinct = 2;
+int slot_rows(int32_t slot_info) { return (slot_info >> 16) & 0xff; }
+int rows_template(int rows) { return rows <= 4 ? 4 : 8; }
+
+template <bool kOrdered>
+int launch_forward_shared(int ppl, int maxr, const float* zonal, const float* radial, const int64_t* offsets,
+                          const int64_t* order, const int64_t* radial_slot, const float* inv, float* out,
+                          int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+                          int64_t channels, hipStream_t stream) {
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
+#define DPA4K_GIE_FWD_SHARED(P, M)                                                                  \
+  gie_forward_shared_kernel<P, M, kOrdered><<<grid, kBlock, 0, stream>>>(                           \
+      zonal, radial, offsets, order, radial_slot, inv, out, n_edges, n_nodes, n_rows, n_radial, channels)
+  if (ppl == 1) {
+    if (maxr == 4) DPA4K_GIE_FWD_SHARED(1, 4); else DPA4K_GIE_FWD_SHARED(1, 8);
+  } else {
+    if (maxr == 4) DPA4K_GIE_FWD_SHARED(2, 4); else DPA4K_GIE_FWD_SHARED(2, 8);
+  }
+#undef DPA4K_GIE_FWD_SHARED
+  return launched("gie_forward_shared_kernel");
+}
+
+template <int RC, bool kOrdered>
+int launch_backward_shared(int maxr, const float* grad_output, const float* zonal, const float* radial,
+                           const int64_t* offsets, const int64_t* order, const int64_t* radial_slot,
+                           const float* inv, float* grad_zonal, float* grad_radial, float* grad_inv,
+                           int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
+                           int64_t channels, hipStream_t stream) {
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
+#define DPA4K_GIE_BWD_SHARED(M)                                                                       \
+  gie_backward_shared_kernel<RC, M, kOrdered><<<grid, kBlock, 0, stream>>>(                          \
+      grad_output, zonal, radial, offsets, order, radial_slot, inv, grad_zonal, grad_radial, grad_inv, \
+      n_edges, n_nodes, n_rows, n_radial, channels)
+  if (maxr == 4) DPA4K_GIE_BWD_SHARED(4); else DPA4K_GIE_BWD_SHARED(8);
+#undef DPA4K_GIE_BWD_SHARED
+  return launched("gie_backward_shared_kernel");
+}
+
+template <bool kOrdered>
+int dispatch_backward_shared(int64_t rc, int maxr, const float* grad_output, const float* zonal,
+                             const float* radial, const int64_t* offsets, const int64_t* order,
+                             const int64_t* radial_slot, const float* inv, float* grad_zonal,
+                             float* grad_radial, float* grad_inv, int64_t n_edges, int64_t n_nodes,
+                             int64_t n_rows, int64_t n_radial, int64_t channels, hipStream_t stream) {
+#define DPA4K_GIE_RC_SHARED(RCV)                                                                    \
+  return launch_backward_shared<RCV, kOrdered>(maxr, grad_output, zonal, radial, offsets, order,    \
+                                               radial_slot, inv, grad_zonal, grad_radial, grad_inv, \
+                                               n_edges, n_nodes, n_rows, n_radial, channels, stream)
+  switch (rc) {
+    case 1: DPA4K_GIE_RC_SHARED(1);
+    case 2: DPA4K_GIE_RC_SHARED(2);
+    case 4: DPA4K_GIE_RC_SHARED(4);
+    case 8: DPA4K_GIE_RC_SHARED(8);
+    default: DPA4K_GIE_RC_SHARED(16);
+  }
+#undef DPA4K_GIE_RC_SHARED
+}
+
 int check_shapes(int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
                  int64_t channels, const char* what) {
   if (n_edges < 0 || n_nodes < 0 || n_rows < 0 || n_radial < 0 || channels < 0)
@@ -592,7 +933,7 @@ using namespace dpa4k;
 extern "C" int dpa4k_gie_zonal_scatter_forward_csr(
     const float* zonal, const float* radial, const int64_t* offsets, const int64_t* order,
     const int64_t* radial_slot, const float* inv_sqrt_deg, float* out, int64_t n_edges,
-    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels,
+    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels, int32_t slot_info,
     dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE forward")) return s;
@@ -604,6 +945,19 @@ extern "C" int dpa4k_gie_zonal_scatter_forward_csr(
   hipStream_t stream = as_stream(stream_handle);
   const bool vec4 = channels % 4 == 0 && aligned16(radial) && aligned16(out);
   const int64_t row_chunks = vec4 ? channels / 4 : channels;
+  // Shared slots: one pass over each edge's radial block, rows served per slot.
+  const int most = slot_rows(slot_info);
+  if (vec4 && !(slot_info & kSlotsDistinct) && most >= 2 && most <= 8 && n_rows >= 1 && n_rows <= 64 &&
+      n_radial <= 64 && n_radial * row_chunks <= 128) {
+    const int ppl = n_radial * row_chunks <= 64 ? 1 : 2;
+    return order != nullptr
+               ? launch_forward_shared<true>(ppl, rows_template(most), zonal, radial, offsets, order, radial_slot,
+                                             inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial, channels,
+                                             stream)
+               : launch_forward_shared<false>(ppl, rows_template(most), zonal, radial, offsets, order,
+                                              radial_slot, inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial,
+                                              channels, stream);
+  }
   const int64_t chunks = n_rows * row_chunks;
   const int cpl = per_lane_for(chunks);
   const int64_t window = 64 * static_cast<int64_t>(cpl);
@@ -636,7 +990,7 @@ extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
     const float* grad_output, const float* zonal, const float* radial, const int64_t* offsets,
     const int64_t* order, const int64_t* radial_slot, const float* inv_sqrt_deg,
     float* grad_zonal, float* grad_radial, float* grad_inv_sqrt_deg, int64_t n_edges,
-    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels, int slots_distinct,
+    int64_t n_nodes, int64_t n_rows, int64_t n_radial, int64_t channels, int32_t slot_info,
     dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_shapes(n_edges, n_nodes, n_rows, n_radial, channels, "GIE backward")) return s;
@@ -662,7 +1016,7 @@ extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
   // Register-only path: distinct slots, a power-of-two chunk count per row
   // and the whole radial block of an edge within 8 chunks per lane.
   const bool pow2 = row_chunks <= 64 && (row_chunks & (row_chunks - 1)) == 0;
-  if (slots_distinct && pow2 && n_radial * row_chunks <= 512) {
+  if ((slot_info & kSlotsDistinct) && pow2 && n_radial * row_chunks <= 512) {
     const int cpl = per_lane_for(n_radial * row_chunks);
     if (vec4)
       return order != nullptr
@@ -684,6 +1038,20 @@ extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
                                              grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes,
                                              n_rows, n_radial, channels, stream);
   }
+  // Shared slots with at most 8 rows per slot: registers only, 8 channels per lane.
+  const int most = slot_rows(slot_info);
+  const int64_t rc = channels / 8;
+  if (vec4 && !(slot_info & kSlotsDistinct) && most >= 2 && most <= 8 && channels % 8 == 0 && rc <= 16 &&
+      (rc & (rc - 1)) == 0 && n_radial * rc <= 64)
+    return order != nullptr
+               ? dispatch_backward_shared<true>(rc, rows_template(most), grad_output, zonal, radial, offsets, order,
+                                                radial_slot, inv_sqrt_deg, grad_zonal, grad_radial,
+                                                grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
+                                                stream)
+               : dispatch_backward_shared<false>(rc, rows_template(most), grad_output, zonal, radial, offsets,
+                                                 order, radial_slot, inv_sqrt_deg, grad_zonal, grad_radial,
+                                                 grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
+                                                 stream);
   // General path: split the channels into windows of wc chunks so that both
   // rows x wc and slots x wc fit in 8 chunks per lane.
   const int64_t widest = n_rows > n_radial ? n_rows : n_radial;
@@ -762,7 +1130,7 @@ extern "C" int dpa4k_gie_zonal_scatter_forward(const float* zonal, const float* 
     return s;
   return dpa4k_gie_zonal_scatter_forward_csr(zonal, radial, csr.offsets, csr.order, radial_slot,
                                              inv_sqrt_deg, out, n_edges, n_nodes, n_rows, n_radial,
-                                             channels, stream);
+                                             channels, csr.info, stream);
 }
 
 extern "C" int dpa4k_gie_zonal_scatter_backward(
@@ -779,8 +1147,8 @@ extern "C" int dpa4k_gie_zonal_scatter_backward(
     return s;
   return dpa4k_gie_zonal_scatter_backward_csr(
       grad_output, zonal, radial, csr.offsets, csr.order, radial_slot, inv_sqrt_deg, grad_zonal,
-      grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels,
-      (csr.info & 2) ? 1 : 0, stream);
+      grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows, n_radial, channels, csr.info,
+      stream);
 }
 
 namespace dpa4k {

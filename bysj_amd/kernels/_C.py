@@ -431,8 +431,10 @@ def gie_group(dst, radial_slot, n_nodes: int, n_radial: int):
     """Destination CSR of an unsorted ``dst``: ``(offsets, order or None, info)``.
 
     ``order`` is None when ``dst`` is already non-decreasing; ``info`` bit 2
-    says every radial slot feeds at most one row.  ValueError on out-of-range
-    ``dst`` or ``radial_slot`` values.
+    says every radial slot feeds at most one row and bits 16..23 hold the most
+    rows that read one slot.  The GIE kernels below take ``info`` as
+    ``slot_info`` to pick their layout.  ValueError on out-of-range ``dst`` or
+    ``radial_slot`` values.
     """
     edges, rows = int(dst.numel()), int(radial_slot.numel())
     offsets = torch.empty(n_nodes + 1, dtype=torch.int64, device=dst.device)
@@ -450,7 +452,7 @@ def gie_group(dst, radial_slot, n_nodes: int, n_radial: int):
     return offsets, (None if grouped else order[:edges]), int(info.value)
 
 
-def gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg):
+def gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, slot_info=0):
     edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
     n_radial, channels = int(radial.shape[1]), int(radial.shape[2])
     nodes = int(inv_sqrt_deg.shape[0])
@@ -460,7 +462,7 @@ def gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, in
     with _on(zonal.device) as stream:
         status = _LIB.dpa4k_gie_zonal_scatter_forward_csr(
             _ptr(zonal), _ptr(radial), offsets.data_ptr(), _ptr(order), _ptr(radial_slot),
-            inv_sqrt_deg.data_ptr(), out.data_ptr(), edges, nodes, rows, n_radial, channels, stream,
+            inv_sqrt_deg.data_ptr(), out.data_ptr(), edges, nodes, rows, n_radial, channels, int(slot_info), stream,
         )
     _lib.check(status)
     return out
@@ -503,7 +505,7 @@ def gie_rmsnorm_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt
 
 
 def gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, radial_slot,
-                                   inv_sqrt_deg, slots_distinct, *, need=(True, True, True)):
+                                   inv_sqrt_deg, slot_info, *, need=(True, True, True)):
     edges, rows = int(zonal.shape[0]), int(zonal.shape[1])
     n_radial, channels = int(radial.shape[1]), int(radial.shape[2])
     nodes = int(inv_sqrt_deg.shape[0])
@@ -519,7 +521,7 @@ def gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, r
         status = _LIB.dpa4k_gie_zonal_scatter_backward_csr(
             grad_output.data_ptr(), _ptr(zonal), _ptr(radial), offsets.data_ptr(), _ptr(order),
             _ptr(radial_slot), inv_sqrt_deg.data_ptr(), _ptr(grad_zonal), _ptr(grad_radial),
-            _ptr(grad_inv), edges, nodes, rows, n_radial, channels, int(bool(slots_distinct)), stream,
+            _ptr(grad_inv), edges, nodes, rows, n_radial, channels, int(slot_info), stream,
         )
     _lib.check(status)
     return grad_zonal, grad_radial, grad_inv
@@ -529,8 +531,8 @@ def gie_zonal_scatter_forward(zonal, radial, dst, radial_slot, inv_sqrt_deg):
     edges, rows, n_radial, channels, nodes = _gie_checks(zonal, radial, dst, radial_slot, inv_sqrt_deg)
     if nodes == 0 or edges * rows * channels == 0:
         return torch.zeros((nodes, rows + 1, channels), dtype=torch.float32, device=zonal.device)
-    offsets, order, _ = gie_group(dst, radial_slot, nodes, n_radial)
-    return gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg)
+    offsets, order, info = gie_group(dst, radial_slot, nodes, n_radial)
+    return gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, info)
 
 
 def gie_zonal_scatter_backward(grad_output, zonal, radial, dst, radial_slot, inv_sqrt_deg):
@@ -543,7 +545,7 @@ def gie_zonal_scatter_backward(grad_output, zonal, radial, dst, radial_slot, inv
         return torch.zeros_like(zonal), torch.zeros_like(radial), torch.zeros_like(inv_sqrt_deg)
     offsets, order, info = gie_group(dst, radial_slot, nodes, n_radial)
     return gie_zonal_scatter_backward_csr(grad_output, zonal, radial, offsets, order, radial_slot,
-                                          inv_sqrt_deg, info & 2)
+                                          inv_sqrt_deg, info)
 
 
 # ---------------------------------------------------------------------------

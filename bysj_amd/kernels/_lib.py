@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -52,9 +52,9 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_gie_group": (
         _INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, ctypes.POINTER(ctypes.c_int32), _P, _SZ, _P]),
     "dpa4k_gie_zonal_scatter_forward_csr": (
-        _INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_int32, _P]),
     "dpa4k_gie_zonal_scatter_backward_csr": (
-        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _INT, _P]),
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_int32, _P]),
     "dpa4k_gie_zonal_scatter_forward": (
         _INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "dpa4k_gie_zonal_scatter_backward": (

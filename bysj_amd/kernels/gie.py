@@ -134,8 +134,8 @@ class _GIEZonalScatterFunction(torch.autograd.Function):
             ctx.save_for_backward(zonal, radial, dst, radial_slot, inv_sqrt_deg)
             return torch.zeros((n_nodes, n_rows + 1, channels), dtype=torch.float32, device=zonal.device)
         offsets, order, info = _GROUPINGS.get(native, dst, radial_slot, n_nodes, n_radial)
-        out = native.gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg)
-        ctx.slots_distinct = bool(info & 2)
+        out = native.gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inv_sqrt_deg, info)
+        ctx.slot_info = info
         ctx.has_order = order is not None
         saved = [zonal, radial, radial_slot, inv_sqrt_deg, offsets]
         if order is not None:
@@ -156,7 +156,7 @@ class _GIEZonalScatterFunction(torch.autograd.Function):
             native = _extension("gie_zonal_scatter_backward")
             grads = native.gie_zonal_scatter_backward_csr(
                 grad_output.contiguous(), zonal, radial, offsets, order, radial_slot, inv_sqrt_deg,
-                ctx.slots_distinct, need=need,
+                ctx.slot_info, need=need,
             )
         return (
             grads[0] if need[0] else None,
@@ -194,7 +194,7 @@ class _GIERMSNormFunction(torch.autograd.Function):
         keep_x = any(ctx.needs_input_grad)
         y, x, inverse_rms = native.gie_rmsnorm_forward_csr(zonal, radial, offsets, order, radial_slot,
                                                           inv_sqrt_deg, scale, eps, keep_x)
-        ctx.slots_distinct = bool(info & 2)
+        ctx.slot_info = info
         ctx.has_order = order is not None
         ctx.has_scale = scale.numel() != 0
         saved = [zonal, radial, radial_slot, inv_sqrt_deg, scale, inverse_rms, offsets]
@@ -219,7 +219,7 @@ class _GIERMSNormFunction(torch.autograd.Function):
         if any(need):
             grads = native.gie_zonal_scatter_backward_csr(
                 grad_x.reshape(x.shape), zonal, radial, offsets, order, radial_slot, inv_sqrt_deg,
-                ctx.slots_distinct, need=need,
+                ctx.slot_info, need=need,
             )
         else:
             grads = (None, None, None)

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 5
+#define DPA4K_ABI_VERSION 6
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -246,7 +246,10 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
  * 0 <= dst < N and 0 <= radial_slot < S.  Synchronises.
  * host_info (host pointer, may be NULL) receives a bit set:
  *   1 = dst was non-decreasing (the kernels may then take a NULL order),
- *   2 = every radial slot is referenced by at most one row.
+ *   2 = every radial slot is referenced by at most one row,
+ *   bits 16..23 = the most rows that reference one slot (capped at 255).
+ * The GIE kernels below take this word as `slot_info` to pick their layout;
+ * 0 means "unknown" and selects kernels that assume nothing about the map.
  * Out-of-range indices return DPA4K_EINVAL. */
 size_t dpa4k_gie_group_workspace_size(int64_t n_edges, int64_t n_nodes);
 int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot,
@@ -261,7 +264,11 @@ int dpa4k_gie_group(const int64_t* dst, const int64_t* radial_slot,
  *   out[n, r+1, c] = inv[n] * sum_{slots of n} zonal[e, r] * radial[e, slot[r], c]
  * (normalise after the sum).  zonal[E, R], radial[E, S, C], radial_slot[R],
  * inv_sqrt_deg[N], out[N, R+1, C].  Sequential per-element accumulation:
- * equals the fp32 chain `gather -> mul -> index_add_ -> mul` bit for bit. */
+ * equals the fp32 chain `gather -> mul -> index_add_ -> mul` bit for bit.
+ * slot_info: dpa4k_gie_group's host_info for this radial_slot, or 0.  With
+ * shared slots and at most 8 rows per slot it selects a kernel that reads
+ * each radial element once per edge (same output); it must then describe
+ * radial_slot truthfully. */
 int dpa4k_gie_zonal_scatter_forward_csr(const float* zonal, const float* radial,
                                         const int64_t* offsets,
                                         const int64_t* order,
@@ -269,7 +276,8 @@ int dpa4k_gie_zonal_scatter_forward_csr(const float* zonal, const float* radial,
                                         const float* inv_sqrt_deg, float* out,
                                         int64_t n_edges, int64_t n_nodes,
                                         int64_t n_rows, int64_t n_radial,
-                                        int64_t channels, dpa4k_stream_t stream);
+                                        int64_t channels, int32_t slot_info,
+                                        dpa4k_stream_t stream);
 
 /* Replaces gie_zonal_scatter_backward_hip (csrc/gie.cpp:178), given the CSR:
  *   grad_zonal[e, r]     = sum_c inv[n] grad[n, r+1, c] radial[e, slot[r], c]
@@ -277,14 +285,16 @@ int dpa4k_gie_zonal_scatter_forward_csr(const float* zonal, const float* radial,
  *   grad_inv[n]          = sum_{r, c} grad[n, r+1, c] pre[n, r+1, c]
  * with pre the unnormalised destination sum (recomputed, not saved).  Any
  * of the three outputs may be NULL.  grad_radial is written in full (zeros
- * for unreferenced slots).  `slots_distinct` is bit 2 of dpa4k_gie_group's
- * host_info and selects the register-only kernel. */
+ * for unreferenced slots).  slot_info: dpa4k_gie_group's host_info for this
+ * radial_slot, or 0; bit 2 (distinct slots) or bits 16..23 <= 8 (shared
+ * slots, C % 16 == 0) select register-only kernels, anything else the
+ * general one.  It must describe radial_slot truthfully. */
 int dpa4k_gie_zonal_scatter_backward_csr(
     const float* grad_output, const float* zonal, const float* radial,
     const int64_t* offsets, const int64_t* order, const int64_t* radial_slot,
     const float* inv_sqrt_deg, float* grad_zonal, float* grad_radial,
     float* grad_inv_sqrt_deg, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
-    int64_t n_radial, int64_t channels, int slots_distinct,
+    int64_t n_radial, int64_t channels, int32_t slot_info,
     dpa4k_stream_t stream);
 
 /* One-call forms with the reference's signature (csrc/gie.cpp:148,178):

@@ -94,7 +94,7 @@ def test_invalid_sizes_fail_before_any_device_call():
         (lib.dpa4k_segment_sum_forward, (null,) * 6 + (1, 2**62, 1, null), "segment count too large"),
         (lib.dpa4k_segment_softmax_forward, (null,) * 7 + (1, 2**62, 8, null), "segment count too large"),
         (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (2**62, 4, ctypes.c_float(1e-6), null), "launch limit"),
-        (lib.dpa4k_gie_zonal_scatter_forward_csr, (null,) * 7 + (0, 2**62, 0, 0, 4, null), "launch limit"),
+        (lib.dpa4k_gie_zonal_scatter_forward_csr, (null,) * 7 + (0, 2**62, 0, 0, 4, 0, null), "launch limit"),
         (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 2**62, null), "launch limit"),
     ]
     for function, args, fragment in cases:

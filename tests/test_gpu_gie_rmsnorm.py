@@ -292,3 +292,95 @@ def test_gie_rmsnorm_unfused_shapes_and_empty_edges():
         gie_ops.gie_zonal_scatter_rmsnorm(*_to(inputs), scale=torch.ones(3, device=DEV), eps=1e-6)
     with pytest.raises(ValueError):
         gie_ops.gie_zonal_scatter_rmsnorm(*_to(inputs), eps=0.0)
+
+
+# ---------------------------------------------------------------------------
+# shared radial slots: the per-slot kernels against the oracle and the kernels
+# that assume nothing about the slot map (slot_info = 0)
+# ---------------------------------------------------------------------------
+
+_DEEPMD_SLOTS = [0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2]
+_SHARED_LAYOUTS = [
+    # (radial_slot, n_radial, channels): what each exercises
+    (_DEEPMD_SLOTS, 3, 64),        # DeepMD rows l = 1..3: 7 rows on one slot; backward 8 lanes per slot
+    ([0, 0, 1, 1], 2, 16),         # at most 4 rows per slot; backward 2 lanes per slot
+    ([1, 0, 1, 0, 1], 3, 32),      # slot 2 unreferenced: its gradient is written as zeros
+    ([0] * 8 + [1], 2, 128),       # 8 rows on one slot; backward 16 lanes per slot, 2 edges per wave step
+    ([0] * 9, 1, 64),              # 9 rows on one slot: beyond the per-slot kernels, general kernels
+    (_DEEPMD_SLOTS, 3, 128),       # forward pairs past one per lane (96)
+    (_DEEPMD_SLOTS, 3, 256),       # forward beyond the shared layout; backward general (32 lanes per slot)
+    (_DEEPMD_SLOTS, 3, 8),         # one lane per slot, 21 edges per wave step (backward)
+    (_DEEPMD_SLOTS, 3, 20),        # channels % 8 != 0: forward shared, backward general
+    (_DEEPMD_SLOTS, 3, 6),         # channels % 4 != 0: scalar kernels
+]
+
+
+def _shared_slot_case(slots, n_radial, channels, shuffle, seed=41):
+    generator = torch.Generator().manual_seed(seed)
+    n_nodes = 48
+    degrees = torch.poisson(torch.full((n_nodes,), 6.0), generator=generator).to(torch.int64)
+    degrees[3] = 0
+    degrees[10] = 301  # several wave steps and an uneven tail
+    dst = torch.repeat_interleave(torch.arange(n_nodes), degrees)
+    edges, rows = dst.numel(), len(slots)
+    zonal = torch.randn((edges, rows), generator=generator)
+    radial = torch.randn((edges, n_radial, channels), generator=generator)
+    inverse = torch.rsqrt(degrees.to(torch.float32) + 1.0)
+    if shuffle:
+        perm = torch.randperm(edges, generator=generator)
+        dst, zonal, radial = dst[perm].contiguous(), zonal[perm].contiguous(), radial[perm].contiguous()
+    return zonal, radial, dst, torch.tensor(slots, dtype=torch.int64), inverse
+
+
+@pytest.mark.parametrize("shuffle", [False, True], ids=["sorted", "shuffled"])
+@pytest.mark.parametrize("layout", _SHARED_LAYOUTS, ids=lambda v: f"{max(v[0].count(s) for s in set(v[0]))}rows-S{v[1]}-C{v[2]}")
+def test_gie_shared_slot_layouts(layout, shuffle):
+    slots, n_radial, channels = layout
+    announce("gie shared slots", slots, n_radial, channels, shuffle)
+    inputs = _shared_slot_case(slots, n_radial, channels, shuffle)
+    zonal, radial, dst, radial_slot, inverse = _to(inputs)
+    offsets, order, info = _C.gie_group(dst, radial_slot, inverse.numel(), n_radial)
+    most = max(slots.count(s) for s in set(slots))
+    assert (info >> 16) & 0xFF == most and not info & 2
+
+    # forward: both kernel families equal the sequential oracle bit for bit
+    expected = gie_ref.zonal_scatter_reference(*inputs)
+    out = _C.gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inverse, info)
+    assert_bitwise(out, expected, "forward, slot-aware kernel")
+    plain = _C.gie_zonal_scatter_forward_csr(zonal, radial, offsets, order, radial_slot, inverse, 0)
+    assert_bitwise(plain, expected, "forward, slot-agnostic kernel")
+
+    # backward through the operator, against the oracle's autograd and the fp64 closed form
+    up = torch.randn(expected.shape, generator=torch.Generator().manual_seed(5))
+    z, r = zonal.clone().requires_grad_(True), radial.clone().requires_grad_(True)
+    inv = inverse.clone().requires_grad_(True)
+    out = kernels.zonal_scatter(z, r, dst, radial_slot, inv)
+    assert_bitwise(out, expected, "operator forward")
+    grads = torch.autograd.grad(out, (z, r, inv), up.to(DEV))
+    oracle = gie_ref.zonal_scatter_backward_reference(up, *inputs)
+    truth = zonal_scatter_backward_f64(up, *inputs)
+    for label, actual, wanted, exact in zip(("zonal", "radial", "inverse"), grads, oracle, truth):
+        assert_gradient(actual, wanted, exact, f"grad {label}, slot-aware kernel")
+    plain = _C.gie_zonal_scatter_backward_csr(up.to(DEV), zonal, radial, offsets, order, radial_slot, inverse, 0)
+    for label, actual, wanted, exact in zip(("zonal", "radial", "inverse"), plain, oracle, truth):
+        assert_gradient(actual, wanted, exact, f"grad {label}, slot-agnostic kernel")
+    again = _C.gie_zonal_scatter_backward_csr(up.to(DEV), zonal, radial, offsets, order, radial_slot, inverse, info)
+    for label, first, second in zip(("zonal", "radial", "inverse"), grads, again):
+        assert_bitwise(second, first, f"grad {label} run to run")
+
+
+def test_gie_shared_slot_kernels_skip_absent_outputs():
+    announce("gie shared slots, partial outputs")
+    inputs = _shared_slot_case(_DEEPMD_SLOTS, 3, 64, shuffle=True)
+    zonal, radial, dst, radial_slot, inverse = _to(inputs)
+    offsets, order, info = _C.gie_group(dst, radial_slot, inverse.numel(), 3)
+    up = torch.randn((inverse.numel(), 16, 64), generator=torch.Generator().manual_seed(6)).to(DEV)
+    full = _C.gie_zonal_scatter_backward_csr(up, zonal, radial, offsets, order, radial_slot, inverse, info)
+    for need in ((True, False, False), (False, True, False), (False, False, True)):
+        part = _C.gie_zonal_scatter_backward_csr(up, zonal, radial, offsets, order, radial_slot, inverse, info,
+                                                 need=need)
+        for wanted, got, reference in zip(need, part, full):
+            if wanted:
+                assert_bitwise(got, reference, f"partial outputs {need}")
+            else:
+                assert got is None

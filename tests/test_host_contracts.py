@@ -229,11 +229,11 @@ class _OracleNative:
         order, offsets = ref.group_by_source(dst, n_nodes)
         return offsets, order, 0
 
-    def gie_zonal_scatter_forward_csr(self, zonal, radial, offsets, order, radial_slot, inv):
+    def gie_zonal_scatter_forward_csr(self, zonal, radial, offsets, order, radial_slot, inv, slot_info=0):
         return gie_ref.zonal_scatter_reference(zonal, radial, self._dst(offsets, order, zonal.shape[0]), radial_slot,
                                                inv)
 
-    def gie_zonal_scatter_backward_csr(self, grad, zonal, radial, offsets, order, radial_slot, inv, distinct, *,
+    def gie_zonal_scatter_backward_csr(self, grad, zonal, radial, offsets, order, radial_slot, inv, slot_info, *,
                                        need=(True, True, True)):
         return gie_ref.zonal_scatter_backward_reference(grad, zonal, radial, self._dst(offsets, order, zonal.shape[0]),
                                                         radial_slot, inv)
