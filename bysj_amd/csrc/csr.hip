@@ -45,16 +45,13 @@ constexpr int kThreads = 256;
 constexpr int kGroupWaves = kThreads / 64;
 constexpr int kItems = 32;                             // elements per thread in a tile
 constexpr int kTile = kThreads * kItems;               // 8192 elements per count/scatter tile
-constexpr int kWaveSpan = kTile / kGroupWaves;         // each wave takes 2048 consecutive elements
 constexpr int kDigitBits = 10;                         // at most 1024 buckets per scatter pass
 constexpr int kMaxBuckets = 1 << kDigitBits;
 constexpr int kFineBitsMax = 10;                       // the two-level path: keys of up to 20 bits
 constexpr int kMaxFine = 1 << kFineBitsMax;
 constexpr int kLocalItems = 16;
 constexpr int kLocalChunk = kThreads * kLocalItems;    // 4096 elements per bucket-local round
-constexpr int kLocalWaveSpan = kLocalChunk / kGroupWaves;
 constexpr int64_t kShortGap = 64;                      // offsets a thread fills alone
-constexpr uint32_t kNone = 0xffffffffu;
 
 enum : int32_t { kFlagOutOfRange = 1, kFlagUnsorted = 2, kFlagSlotRange = 4, kFlagSlotShared = 8 };
 constexpr int kSlotRowsShift = 16;  // bits 16..23: most rows reading one radial slot (GIE grouping)

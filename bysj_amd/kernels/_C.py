@@ -375,7 +375,44 @@ def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
 # force_assembly (csrc/force_assembly.cpp:106)
 # ---------------------------------------------------------------------------
 
-def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order):
+class ForcePlan:
+    """Bucket layout of one source grouping for the planned force assembly.
+
+    Built once per graph by :func:`force_assembly_plan`; it holds the row
+    buffer the planned kernels write on every call, so calls that share a
+    plan must not overlap (one stream at a time).
+    """
+
+    __slots__ = ("buffer", "n_edges", "n_nodes", "value_bytes")
+
+    def __init__(self, buffer: torch.Tensor, n_edges: int, n_nodes: int, value_bytes: int):
+        self.buffer, self.n_edges, self.n_nodes, self.value_bytes = buffer, n_edges, n_nodes, value_bytes
+
+
+def force_assembly_plan(src_offsets, src_order, *, value_bytes: int = 8) -> ForcePlan:
+    """Plan of ``(src_offsets, src_order)`` for float32 (value_bytes 4) or both dtypes (8); no host sync."""
+    nodes = _offsets(src_offsets, "force assembly src_offsets")
+    _i64(src_order, "force assembly src_order")
+    _check(src_order.dim() == 1, "force assembly src_order must be one-dimensional")
+    _check(nodes > 0, "force assembly requires at least one atom")
+    _check(value_bytes in (4, 8), "force assembly plan: value_bytes must be 4 or 8")
+    _same_device(src_offsets, src_order)
+    edges = int(src_order.numel())
+    nbytes = int(_LIB.dpa4k_force_assembly_plan_size(edges, nodes, value_bytes))
+    buffer = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=src_order.device)
+    scratch_bytes = int(_LIB.dpa4k_force_assembly_plan_workspace_size(edges, nodes))
+    workspace = _workspace(scratch_bytes, src_order.device)
+    with _on(src_order.device) as stream:
+        status = _LIB.dpa4k_force_assembly_plan(
+            src_offsets.data_ptr(), _ptr(src_order), edges, nodes, value_bytes, buffer.data_ptr(), nbytes,
+            workspace.data_ptr(), scratch_bytes, stream,
+        )
+    _lib.check(status)
+    return ForcePlan(buffer, edges, nodes, value_bytes)
+
+
+def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, *, plan=None):
+    """``(force, virial)``; with a :class:`ForcePlan` of this grouping the bucketed two-pass kernels run."""
     for name, tensor in (("grad_edge", grad_edge), ("edge_vec", edge_vec)):
         _check(isinstance(tensor, torch.Tensor) and tensor.is_cuda and tensor.is_contiguous()
                and tensor.dtype in (torch.float32, torch.float64),
@@ -393,8 +430,19 @@ def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order):
     _same_device(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
     force = torch.empty((nodes, 3), dtype=grad_edge.dtype, device=grad_edge.device)
     virial = torch.empty((nodes, 9), dtype=grad_edge.dtype, device=grad_edge.device)
-    entry = (_LIB.dpa4k_force_assembly_f32 if grad_edge.dtype == torch.float32
-             else _LIB.dpa4k_force_assembly_f64)
+    single = grad_edge.dtype == torch.float32
+    if plan is not None:
+        _check(isinstance(plan, ForcePlan) and plan.n_edges == edges and plan.n_nodes == nodes
+               and plan.buffer.device == grad_edge.device and plan.value_bytes >= grad_edge.element_size(),
+               "force assembly plan was built for another graph, device or dtype")
+        entry = _LIB.dpa4k_force_assembly_f32_planned if single else _LIB.dpa4k_force_assembly_f64_planned
+        with _on(grad_edge.device) as stream:
+            status = entry(_ptr(grad_edge), _ptr(edge_vec), dst_offsets.data_ptr(), src_offsets.data_ptr(),
+                           force.data_ptr(), virial.data_ptr(), edges, nodes, plan.buffer.data_ptr(),
+                           plan.buffer.numel(), stream)
+        _lib.check(status)
+        return force, virial
+    entry = _LIB.dpa4k_force_assembly_f32 if single else _LIB.dpa4k_force_assembly_f64
     with _on(grad_edge.device) as stream:
         status = entry(_ptr(grad_edge), _ptr(edge_vec), dst_offsets.data_ptr(), src_offsets.data_ptr(),
                        _ptr(src_order), force.data_ptr(), virial.data_ptr(), edges, nodes, stream)

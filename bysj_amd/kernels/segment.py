@@ -416,13 +416,66 @@ def segment_softmax(logit, env, offsets, null_logit=None, *, order=None, check_g
     return apply_function(_SegmentSoftmaxNullFunction, logit, env, offsets, null_logit, order)
 
 
+class _ForcePlanCache:
+    """Planned-path layouts of source groupings, kept per ``src_order`` tensor object.
+
+    The planned force assembly (a once-per-graph bucket layout, then two
+    passes per call; same bits as the direct kernel) pays off for float32
+    rows when atom numbering has no spatial locality: the direct kernel's
+    source side is then a random gather of 12-byte rows.  With locality the
+    direct kernel is faster, so the first float32 call on a grouping
+    measures it -- the share of consecutive source slots whose edges lie
+    within LOCAL_SPAN of each other, one host synchronisation -- and builds a
+    plan only below ``LOCAL_SHARE``.  Entries follow ``src_order`` and
+    ``src_offsets`` like the CSR caches: keyed by object identity, dropped
+    when either is written in place or ``src_order`` is freed.  Graphs under
+    ``MIN_EDGES`` edges, inference tensors and calls during HIP graph capture
+    without a cached entry use the direct kernel.
+    """
+
+    LOCAL_SPAN = 4096
+    LOCAL_SHARE = 0.5
+    MIN_EDGES = 1 << 16
+
+    def __init__(self):
+        self._entries: dict[int, tuple] = {}
+
+    def get(self, native, src_offsets: torch.Tensor, src_order: torch.Tensor):
+        edges = int(src_order.numel())
+        if edges < self.MIN_EDGES or not src_order.is_cuda:
+            return None
+        order_stamp, offsets_stamp = version_stamp(src_order), version_stamp(src_offsets)
+        if order_stamp is None or offsets_stamp is None:
+            return None
+        key = id(src_order)
+        entry = self._entries.get(key)
+        stamp = (order_stamp, offsets_stamp, id(src_offsets))
+        if entry is not None and entry[0]() is src_order and entry[1] == stamp:
+            return entry[2]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        local = ((src_order[1:] - src_order[:-1]).abs() < self.LOCAL_SPAN).float().mean().item()
+        plan = native.force_assembly_plan(src_offsets, src_order, value_bytes=4) if local < self.LOCAL_SHARE else None
+        reference = weakref.ref(src_order, lambda _, key=key: self._entries.pop(key, None))
+        self._entries[key] = (reference, stamp, plan)
+        return plan
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+
+_FORCE_PLANS = _ForcePlanCache()
+
+
 def force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None, src_order=None):
     """``(force, virial)`` from per-edge energy gradients (inference only).
 
     ``src_order``/``src_offsets`` group the edges by source; when omitted they
     are derived from ``src`` with :func:`group_by_source` (cache them when this
     runs every step).  float32 in/out as in the reference; float64 inputs give
-    float64 outputs.
+    float64 outputs.  For float32 on a graph whose atom numbering has no
+    spatial locality, the first call builds a bucket layout of the grouping
+    and later calls run the planned kernels (identical results).
     """
     n_nodes = int(dst_offsets.numel()) - 1
     if src_order is None or src_offsets is None:
@@ -432,6 +485,10 @@ def force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None,
     _validate_force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
     require_dcu(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
     native = _extension("force_assembly")
+    if grad_edge.dtype == torch.float32:
+        plan = _FORCE_PLANS.get(native, src_offsets, src_order)
+        if plan is not None:
+            return native.force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, plan=plan)
     return native.force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
 
 

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 6
+#define DPA4K_ABI_VERSION 7
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -234,6 +234,47 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
                              const int64_t* src_order, double* force,
                              double* virial, int64_t n_edges, int64_t n_nodes,
                              dpa4k_stream_t stream);
+
+/* Planned force assembly (no reference counterpart; same outputs as the two
+ * entry points above, bit for bit).  A plan of one source grouping
+ * (src_offsets + src_order) is built once per graph, on `stream` without a
+ * host synchronisation: the atoms fall into <= 256 contiguous buckets and
+ * the edges into tiles of 4096, and the plan records where each edge's row
+ * (g_e, v_e) goes in a row buffer sorted by (tile, source bucket).  A
+ * planned call then streams grad_edge and edge_vec once into that buffer
+ * (each tile's rows land inside the tile's own stretch of it) and gathers
+ * each atom's source rows from it: a bucket's rows lie in one short run per
+ * tile, in place of random 12-byte gathers from the whole inputs.  Pays off
+ * when atom numbering is not spatially ordered and for float32 rows;
+ * measured slower than the direct kernel for spatially ordered atoms and
+ * for float64.  The plan also holds that row buffer: calls sharing a
+ * plan must not overlap.  value_bytes = 4 (float32 only) or 8 (both dtypes).
+ * E < 2^31, N >= 1.  The plan needs dpa4k_force_assembly_plan_size bytes
+ * (about (8 + 6 * value_bytes) * E) and its build a workspace of
+ * dpa4k_force_assembly_plan_workspace_size bytes. */
+size_t dpa4k_force_assembly_plan_size(int64_t n_edges, int64_t n_nodes,
+                                      int64_t value_bytes);
+size_t dpa4k_force_assembly_plan_workspace_size(int64_t n_edges,
+                                                int64_t n_nodes);
+int dpa4k_force_assembly_plan(const int64_t* src_offsets,
+                              const int64_t* src_order, int64_t n_edges,
+                              int64_t n_nodes, int64_t value_bytes, void* plan,
+                              size_t plan_bytes, void* workspace,
+                              size_t workspace_bytes, dpa4k_stream_t stream);
+int dpa4k_force_assembly_f32_planned(const float* grad_edge,
+                                     const float* edge_vec,
+                                     const int64_t* dst_offsets,
+                                     const int64_t* src_offsets, float* force,
+                                     float* virial, int64_t n_edges,
+                                     int64_t n_nodes, void* plan,
+                                     size_t plan_bytes, dpa4k_stream_t stream);
+int dpa4k_force_assembly_f64_planned(const double* grad_edge,
+                                     const double* edge_vec,
+                                     const int64_t* dst_offsets,
+                                     const int64_t* src_offsets, double* force,
+                                     double* virial, int64_t n_edges,
+                                     int64_t n_nodes, void* plan,
+                                     size_t plan_bytes, dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * GIE zonal scatter
