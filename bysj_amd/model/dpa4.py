@@ -1,136 +1,152 @@
-"""``DPA4Model``: a DeepMD ``DeepPot`` facade with the fused seams (python/model/dpa4.py:81-190 of the reference).
+"""``DPA4Model``: DeepMD's ``DeepPot`` with the fused seams (python/model/dpa4.py:81-190 of the reference).
 
 DeepMD-kit owns the DPA4/SeZM graph, checkpoint loading, neighbour lists and
-the energy/force/virial; the facade adds the ``fused=`` switch, which installs
-the seams of :mod:`fused_deepmd`, and a close/context-manager lifecycle that
-uninstalls them before the ``DeepPot`` is closed.
+the energy/force/virial evaluation; this wrapper adds the ``fused=`` switch,
+which installs seams of :mod:`fused_deepmd`, and a lifecycle that removes
+them again before the ``DeepPot`` is closed.
+
+Seams: ``softmax`` and ``envelope`` (the reference's two) and ``force`` (this
+build's third, DeepMD's edge force/virial assembly).  ``fused=True`` selects
+the reference's two; ``force`` is selected by name.
 """
 from __future__ import annotations
 
 import os
+from collections.abc import Iterable, Mapping
 from pathlib import Path
 from typing import Any
 
-SEAMS = ("softmax", "envelope")
-_REMOVED_KEYWORDS = {
+# seam -> selected by fused=True
+_SEAM_TABLE = {"softmax": True, "envelope": True, "force": False}
+SEAMS = tuple(_SEAM_TABLE)
+
+# Keywords of earlier releases: a call site still passing one must fail before
+# anything is loaded, not have the keyword forwarded to DeepPot.
+_RETIRED_KEYWORDS = {
     "tilelang_ops": "drop the argument; TileLang dispatch is not part of this operator slice",
-    "native_ops": "drop the argument and use fused=(\"softmax\", \"envelope\") instead",
+    "native_ops": "drop the argument and select seams with fused=(\"softmax\", \"envelope\")",
 }
+
+# DeepPot methods the wrapper passes through unchanged
+_PASS_THROUGH = ("get_rcut", "get_type_map", "get_ntypes", "get_model_def_script")
+
+
+def _seam_name(name: Any) -> str:
+    key = name.strip().lower() if isinstance(name, str) else None
+    if key not in _SEAM_TABLE:
+        raise ValueError(f"unknown fused seam {name!r}; choose from: {', '.join(SEAMS)}")
+    return key
 
 
 def _normalize_fused(fused: Any) -> dict[str, bool] | None:
-    """Per-seam switches of the ``fused`` argument (None: install nothing).
+    """The per-seam switches of a ``fused`` argument, or None to install nothing.
 
-    ``True`` selects every seam; a seam name or a collection of names selects
-    those; a mapping gives each seam explicitly.  Unknown names raise
-    ``ValueError``, other types ``TypeError``.
+    ``True`` selects the default seams; a name, or a collection of names,
+    selects those; a mapping switches the seams it names.  Unknown names
+    raise ``ValueError``, other argument types ``TypeError``.
     """
-    if not fused:
+    if fused is None or fused is False:
         return None
     if fused is True:
-        return dict.fromkeys(SEAMS, True)
-    if isinstance(fused, str):
-        fused = (fused,)
-    if isinstance(fused, dict):
-        unknown = sorted(map(str, set(fused) - set(SEAMS)))
-        if unknown:
-            raise ValueError(f"unknown fused seams: {', '.join(unknown)}; choose from: {', '.join(SEAMS)}")
-        return {name: bool(fused.get(name, False)) for name in SEAMS}
-    if isinstance(fused, (list, tuple, set, frozenset)):
-        chosen = {}
-        for name in fused:
-            key = name.strip().lower() if isinstance(name, str) else None
-            if key not in SEAMS:
-                raise ValueError(f"unknown fused seam {name!r}; choose from: {', '.join(SEAMS)}")
-            chosen[key] = True
-        return chosen
-    raise TypeError("fused must be a bool, a seam name, a sequence of names or a mapping")
+        return {name: True for name, default in _SEAM_TABLE.items() if default}
+    if isinstance(fused, Mapping):
+        selection = {_seam_name(name): bool(value) for name, value in fused.items()}
+    elif isinstance(fused, str):
+        selection = {_seam_name(fused): True}
+    elif isinstance(fused, Iterable):
+        selection = {_seam_name(name): True for name in fused}
+    else:
+        raise TypeError("fused must be a bool, a seam name, a collection of seam names or a mapping")
+    return selection or None
 
 
 def _create_deep_pot(model_file: str, **kwargs: Any) -> Any:
-    """Load DeepMD lazily: importing the facade must not require DeepMD."""
+    """``deepmd.infer.DeepPot(model_file, **kwargs)``, imported only when a model is opened."""
     try:
         from deepmd.infer import DeepPot
     except ImportError as error:
-        raise RuntimeError("DPA4Model requires an installed DeepMD-kit with the PyTorch inference backend") from error
+        raise RuntimeError("DPA4Model needs DeepMD-kit with its PyTorch inference backend installed") from error
     return DeepPot(model_file, **kwargs)
 
 
 def _backend_name(deep_pot: Any) -> str:
-    """``pt`` / ``pt_expt`` from the module of DeepPot's evaluator, else ``unknown``."""
-    parts = type(getattr(deep_pot, "deep_eval", None)).__module__.split(".")
-    return parts[1] if len(parts) >= 2 and parts[0] == "deepmd" else "unknown"
+    """The DeepMD backend running ``deep_pot`` (``pt``, ``pt_expt``, ...): the package under ``deepmd``."""
+    module = type(getattr(deep_pot, "deep_eval", None)).__module__
+    top, _, rest = module.partition(".")
+    return rest.partition(".")[0] if top == "deepmd" and rest else "unknown"
 
 
-def _fused_module():
+def _seam_module():
     try:
         from . import fused_deepmd
-    except ImportError:  # pragma: no cover
+    except ImportError:  # pragma: no cover -- imported as a top-level package
         import fused_deepmd
     return fused_deepmd
 
 
 class DPA4Model:
-    """``DeepPot`` facade that can bind the gfx950 segment operators.
+    """DeepMD ``DeepPot`` that can bind the gfx950 segment operators.
 
-    ``fused``: ``True`` installs every seam, a name or a sequence of names
-    (``"softmax"``, ``"envelope"``) selects seams, a mapping sets each one,
-    ``None``/``False`` leaves DeepMD untouched.  Other keyword arguments go to
-    ``deepmd.infer.DeepPot``.
+    ``fused``: ``True``, a seam name, a collection of names or a mapping
+    (see :func:`_normalize_fused`); ``None``/``False`` leaves DeepMD as it
+    is.  Remaining keyword arguments go to ``deepmd.infer.DeepPot``.
+    ``fused_ops`` holds the installation's counters, ``fused_seams`` the
+    selection, ``backend`` DeepMD's backend name.
     """
 
     def __init__(self, model_file: str | os.PathLike[str], *, fused: Any = None, **deepmd_kwargs: Any) -> None:
+        retired = [keyword for keyword in _RETIRED_KEYWORDS if keyword in deepmd_kwargs]
+        if retired:
+            keyword = retired[0]
+            raise RuntimeError(f"{keyword} was removed from DPA4Model: {_RETIRED_KEYWORDS[keyword]}")
         self.model_file = str(Path(model_file).expanduser())
-        for keyword, hint in _REMOVED_KEYWORDS.items():
-            if keyword in deepmd_kwargs:
-                raise RuntimeError(f"{keyword} was removed from DPA4Model: {hint}; an old call site should fail "
-                                   "loudly instead of being forwarded to DeepPot")
-        # validate the switch before a possibly large checkpoint is read
-        self.fused_seams = _normalize_fused(fused)
+        self.fused_seams = _normalize_fused(fused)  # before the checkpoint is read
         self._deep_pot = _create_deep_pot(self.model_file, **deepmd_kwargs)
         self.backend = _backend_name(self._deep_pot)
         self.fused_ops: dict[str, Any] = {}
         if self.fused_seams:
-            fused_deepmd = _fused_module()
-            self.fused_ops = dict(fused_deepmd.status(fused_deepmd.deepmd_patch(self._deep_pot, **self.fused_seams)))
+            seams = _seam_module()
+            self.fused_ops = dict(seams.status(seams.deepmd_patch(self._deep_pot, **self.fused_seams)))
 
     def eval(self, coords: Any, cells: Any, atom_types: Any, *, atomic: bool = False, fparam: Any = None,
              aparam: Any = None, **kwargs: Any) -> Any:
-        """Energy, forces and virial through DeepMD's public ``DeepPot.eval``."""
+        """Energies, forces and virials from DeepMD's ``DeepPot.eval`` (every argument forwarded)."""
         return self._deep_pot.eval(coords, cells, atom_types, atomic=atomic, fparam=fparam, aparam=aparam, **kwargs)
 
     predict = eval
     __call__ = eval
 
-    def get_rcut(self) -> float:
-        return self._deep_pot.get_rcut()
-
-    def get_type_map(self) -> list[str]:
-        return self._deep_pot.get_type_map()
-
-    def get_ntypes(self) -> int:
-        return self._deep_pot.get_ntypes()
-
-    def get_model_def_script(self) -> Any:
-        return self._deep_pot.get_model_def_script()
-
     def close(self) -> None:
-        """Uninstall the seams (once), then close the DeepPot."""
+        """Remove the installed seams (the first time only), then close the DeepPot."""
         if self.fused_ops:
-            _fused_module().uninstall(self._deep_pot)
             self.fused_ops = {}
-        closer = getattr(self._deep_pot, "close", None)
-        if callable(closer):
-            closer()
+            _seam_module().uninstall(self._deep_pot)
+        close = getattr(self._deep_pot, "close", None)
+        if callable(close):
+            close()
 
     def __enter__(self) -> "DPA4Model":
         return self
 
-    def __exit__(self, *exc: Any) -> None:
+    def __exit__(self, *exc_info: Any) -> None:
         self.close()
 
     def __repr__(self) -> str:
-        return f"DPA4Model(model_file={self.model_file!r}, backend={self.backend!r}, fused_ops={self.fused_ops!r})"
+        fields = {"model_file": self.model_file, "backend": self.backend, "fused_ops": self.fused_ops}
+        return "DPA4Model(" + ", ".join(f"{key}={value!r}" for key, value in fields.items()) + ")"
 
 
-__all__ = ["DPA4Model"]
+def _pass_through(name: str):
+    def method(self: DPA4Model, *args: Any, **kwargs: Any) -> Any:
+        return getattr(self._deep_pot, name)(*args, **kwargs)
+
+    method.__name__ = method.__qualname__ = name
+    method.__doc__ = f"``DeepPot.{name}`` of the wrapped model."
+    return method
+
+
+for _name in _PASS_THROUGH:
+    setattr(DPA4Model, _name, _pass_through(_name))
+del _name
+
+__all__ = ["DPA4Model", "SEAMS"]

@@ -1,63 +1,88 @@
 """Binds the gfx950 segment operators into a loaded DeepMD DPA4/SeZM model.
 
-Restates the seam layer of the reference (python/model/fused_deepmd.py:103-462
-of lipengfei1409/bysj) over this build's operators.  DeepMD is not edited; two
-of its own dispatch points are rebound and every call keeps a fallback to the
-stock implementation:
+The reference's seam layer (python/model/fused_deepmd.py:103-462 of
+lipengfei1409/bysj) rebinds two of DeepMD's own dispatch points; this module
+offers the same public surface (``deepmd_patch``, ``uninstall``, ``status``,
+``describe_module``, ``FusedStats``) over this build's operators, plus a third
+seam.  DeepMD itself is never edited, and every seam keeps DeepMD's own
+implementation as its fallback:
 
-S1  ``segment_envelope_gated_softmax(logits, edge_env, dst, n_nodes,
-    z_bias_raw, eps, src_weight=None)`` -- the eager softmax that
-    ``SO2Convolution.attention_weights`` calls.  Served by
-    ``kernels.segment_softmax`` with ``null_logit = log(softplus(z_bias) + eps)``
-    and the envelope folded into the logit inside the kernel.
+softmax   ``segment_envelope_gated_softmax(logits, edge_env, dst, n_nodes,
+          z_bias_raw, eps, src_weight=None)``, the eager softmax that
+          ``SO2Convolution.attention_weights`` calls.  Served by
+          ``segment_softmax`` with the null logit ``log(softplus(z_bias) +
+          eps)``; the envelope is folded into the logit inside the kernel.
 
-S2  ``SO2Convolution.forward_envelope(self, x, edge_cache, radial_feat)`` --
-    the attention-free aggregation ``zeros -> index_add_(dst) -> mul_``.
-    Served by one ``kernels.segment_sum`` call with ``edge_scale = edge_env *
-    edge_src_gate`` and ``node_scale = inv_sqrt_deg``.  Unlike the reference,
-    the gradient reaches ``edge_scale`` (DeepMD's envelope depends on the
-    coordinates, so forces need it).
+envelope  ``SO2Convolution.forward_envelope(self, x, edge_cache,
+          radial_feat)``, the attention-free aggregation ``zeros ->
+          index_add_(dst) -> mul_``.  Served by one ``segment_sum`` with
+          ``edge_scale = edge_env * edge_src_gate`` and ``node_scale =
+          inv_sqrt_deg``; the gradient reaches ``edge_scale`` (DeepMD's
+          envelope depends on the coordinates, so forces need it).
 
-Both seams need the destination CSR view of ``dst``.  It is built once per
-neighbour graph on the device (``kernels.group_by_source``: a check pass,
-a stable radix sort when the list is unsorted, a boundary pass) and cached per ``dst`` tensor object; an entry is
-dropped when the tensor is freed or written in place (its version counter
-moves), so a recycled storage address can never return a stale view.
+force     ``edge_force_virial`` (module ``deepmd.pt_expt.kernels.
+          edge_force_virial``; ``transform_output`` imports it as
+          ``fused_edge_force_virial``), the per-atom force and virial from the
+          per-edge energy gradients (call quoted at docs/fused-operators.md:
+          117-130 of the reference, which leaves it unwired).  Served by
+          ``force_assembly`` for one frame with no masked edges and an empty
+          optional tensor; everything else goes to DeepMD's function.  Opt-in:
+          ``deepmd_patch(..., force=True)``.
 
-Counters of hits and fallbacks are kept in :class:`FusedStats`.  A seam falls
-back when its inputs are not what the kernels take (``src_weight`` given,
-non-fp32, not on the GPU, non-contiguous, wrong shapes, training mode) or when
-the operator raises; the first error is reported once as a warning.
+The destination CSR of ``dst`` is built once per neighbour graph on the device
+and cached per ``dst`` tensor object (:class:`_CsrView`).  :class:`FusedStats`
+counts hits and fallbacks; a seam falls back when its inputs are outside what
+the kernels take or when the operator raises, and the first error is reported
+once as a warning.
 """
 from __future__ import annotations
 
+import importlib
 import warnings
 import weakref
-from dataclasses import asdict, dataclass, field
+from dataclasses import asdict, dataclass
 from types import MethodType
-from typing import Any, Iterable
+from typing import Any, Callable, Iterable
 
 import torch
 import torch.nn.functional as F
 
-_CSR_CAPACITY = 4
-# Host tests drive the seams with CPU tensors and a stand-in operator bundle.
-# In a real install the device check below keeps CPU tensors on DeepMD's own
-# path; only a test lifts it.
+# Host tests drive the seams with CPU tensors and a stand-in operator bundle;
+# in a real install CPU tensors stay on DeepMD's path.  Only a test sets this.
 _ACCEPT_ANY_DEVICE = False
+
 _SOFTMAX_NAME = "segment_envelope_gated_softmax"
+_ENVELOPE_NAME = "forward_envelope"
+# Where DeepMD keeps each rebound name (modules imported only on a real install).
+_SOFTMAX_HOMES = (
+    "deepmd.pt.model.descriptor.sezm_nn.attention",
+    "deepmd.pt.model.descriptor.sezm_nn.so2",
+    "deepmd.pt.model.descriptor.sezm_nn",
+)
+_FORCE_HOMES = (
+    ("deepmd.pt_expt.kernels.edge_force_virial", "edge_force_virial"),
+    ("deepmd.pt.model.model.transform_output", "fused_edge_force_virial"),
+)
+# Attributes of a DeepPot's ``deep_eval`` that hold the torch module tree: the
+# legacy ``pt`` backend's ModelWrapper, the ``pt_expt`` backend's
+# deserialized graph, a generic ``model``; ``deep_eval`` itself comes last.
+_TREE_ATTRIBUTES = ("dp", "_dpmodel", "model")
+_CSR_CAPACITY = 4
 
 
 @dataclass
 class FusedStats:
-    """Hit, fallback and error counters of the installed seams."""
+    """Hit, fallback and error counters of one installation."""
 
     softmax_hits: int = 0
     softmax_fallbacks: int = 0
     envelope_hits: int = 0
     envelope_fallbacks: int = 0
+    force_hits: int = 0
+    force_fallbacks: int = 0
     bound_softmax: bool = False
     bound_envelope: bool = False
+    bound_force: bool = False
     blocks: int = 0
     last_error: str | None = None
 
@@ -65,31 +90,45 @@ class FusedStats:
         return asdict(self)
 
 
-def _fp32_operand(value: Any, dtype: torch.dtype = torch.float32) -> bool:
-    """A tensor the kernels accept: right dtype, contiguous, on the GPU."""
-    return (isinstance(value, torch.Tensor) and value.dtype == dtype and value.is_contiguous()
-            and (value.is_cuda or _ACCEPT_ANY_DEVICE))
+# ---------------------------------------------------------------------------
+# operands and operators
+# ---------------------------------------------------------------------------
+
+def _on_device(tensor: torch.Tensor) -> bool:
+    return tensor.is_cuda or _ACCEPT_ANY_DEVICE
+
+
+def _kernel_operand(value: Any, dtypes=(torch.float32,)) -> bool:
+    """A tensor the kernels take: one of ``dtypes``, contiguous, on the GPU."""
+    return (isinstance(value, torch.Tensor) and value.dtype in dtypes and value.is_contiguous()
+            and _on_device(value))
+
+
+def _index_operand(value: Any) -> bool:
+    return _kernel_operand(value, (torch.int64,)) and value.dim() == 1
+
+
+def _kernels_segment():
+    """This build's ``kernels.segment`` module (ImportError when absent)."""
+    try:
+        from ..kernels import segment
+    except ImportError:  # bysj_amd/ on sys.path: this package imported as the reference's `model`
+        from kernels import segment
+    return segment
 
 
 def _segment_operators():
-    """The operator module of this build (``kernels.segment``) or None if it cannot run."""
+    """``kernels.segment`` when it can run on this host, else None."""
     try:
-        from ..kernels import segment
+        segment = _kernels_segment()
     except ImportError:
-        try:
-            from kernels import segment  # imported as the top-level package `model`
-        except ImportError:
-            return None
+        return None
     return segment if segment.segment_available() else None
 
 
-def _group_by_destination(dst: torch.Tensor, n_nodes: int):
-    """``(offsets, order)``, with ``order`` None when ``dst`` is already sorted (natural-order kernels)."""
-    try:
-        from ..kernels.segment import destination_grouping
-    except ImportError:
-        from kernels.segment import destination_grouping
-    return destination_grouping(dst, n_nodes)
+def _destination_grouping(dst: torch.Tensor, n_nodes: int):
+    """``(offsets, order)``; ``order`` is None when ``dst`` is already non-decreasing."""
+    return _kernels_segment().destination_grouping(dst, n_nodes)
 
 
 class _CsrView:
@@ -114,13 +153,13 @@ class _CsrView:
     def get(self, dst: torch.Tensor, n_nodes: int):
         stamp = self._stamp(dst, n_nodes)
         if stamp is None:
-            return _group_by_destination(dst, int(n_nodes))
+            return _destination_grouping(dst, int(n_nodes))
         key = id(dst)
         entry = self._entries.pop(key, None)
         if entry is not None and entry[0]() is dst and entry[1] == stamp:
             self._entries[key] = entry            # most recently used last
             return entry[2], entry[3]
-        offsets, order = _group_by_destination(dst, int(n_nodes))
+        offsets, order = _destination_grouping(dst, int(n_nodes))
         reference = weakref.ref(dst, lambda _, key=key: self._entries.pop(key, None))
         self._entries[key] = (reference, stamp, offsets, order)
         while len(self._entries) > self.capacity:
@@ -131,260 +170,345 @@ class _CsrView:
         return len(self._entries)
 
 
-@dataclass
-class _Session:
-    """One installation: the operators, its counters and the stock softmax."""
-
-    ops: Any
-    stats: FusedStats
-    reference_softmax: Any
-    csr: _CsrView = field(default_factory=_CsrView)
-    warned: bool = False
-
-    def _fall_back(self, error: Exception | None = None) -> None:
-        if error is not None:
-            self.stats.last_error = f"{type(error).__name__}: {error}"
-            if not self.warned:
-                self.warned = True
-                warnings.warn("fused DeepMD dispatch fell back to the stock path: " + self.stats.last_error,
-                              RuntimeWarning, stacklevel=4)
-
-    # -- S1 ------------------------------------------------------------------
-    def softmax(self, logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight=None):
-        stock = self.reference_softmax
-        if src_weight is not None or not self._softmax_inputs_ok(logits, edge_env, dst, n_nodes, z_bias_raw):
-            self.stats.softmax_fallbacks += 1
-            self._fall_back()
-            return stock(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight)
-        n_edges, n_focus, n_head = logits.shape
-        channels = n_focus * n_head
-        try:
-            offsets, order = self.csr.get(dst, n_nodes)
-            bias = z_bias_raw.reshape(-1).to(torch.float32)
-            null_logit = torch.log(F.softplus(bias) + float(eps)).reshape(1, channels).expand(n_nodes, channels)
-            result = self.ops.segment_softmax(logits.reshape(n_edges, channels), edge_env.reshape(n_edges), offsets,
-                                              null_logit.contiguous(), order=order)
-            alpha = result[0] if isinstance(result, tuple) else result
-        except Exception as error:  # noqa: BLE001 -- a seam must never break inference
-            self.stats.softmax_fallbacks += 1
-            self._fall_back(error)
-            return stock(logits, edge_env, dst, n_nodes, z_bias_raw, eps, None)
-        self.stats.softmax_hits += 1
-        return alpha.reshape(n_edges, n_focus, n_head)
-
-    @staticmethod
-    def _softmax_inputs_ok(logits, edge_env, dst, n_nodes, z_bias_raw) -> bool:
-        if not (_fp32_operand(logits) and logits.ndim == 3 and logits.shape[0] > 0 and _fp32_operand(edge_env)):
-            return False
-        if not (isinstance(dst, torch.Tensor) and dst.dtype == torch.int64 and dst.ndim == 1) or n_nodes <= 0:
-            return False
-        n_edges, n_focus, n_head = logits.shape
-        return (isinstance(z_bias_raw, torch.Tensor) and z_bias_raw.numel() == n_focus * n_head
-                and edge_env.numel() == n_edges and dst.numel() == n_edges)
-
-    # -- S2 ------------------------------------------------------------------
-    def envelope(self, original, block, x, edge_cache, radial_feat):
-        """``original`` is the block's stock ``forward_envelope``, already bound."""
-        dst = getattr(edge_cache, "dst", None)
-        edge_env = getattr(edge_cache, "edge_env", None)
-        inverse = getattr(edge_cache, "inv_sqrt_deg", None)
-        gate = getattr(edge_cache, "edge_src_gate", None)
-        if not self._envelope_inputs_ok(block, x, dst, edge_env, inverse, gate):
-            self.stats.envelope_fallbacks += 1
-            self._fall_back()
-            return original(x, edge_cache, radial_feat)
-        n_edges = dst.shape[0]
-        try:
-            message, _ = block.edge_message(x, edge_cache, radial_feat)
-            if not _fp32_operand(message) or message.shape[0] != n_edges:
-                raise ValueError("edge message is not a contiguous fp32 (n_edges, ...) tensor")
-            weight = edge_env.reshape(-1)
-            if gate is not None:
-                weight = weight * gate.reshape(-1).to(torch.float32)
-            offsets, order = self.csr.get(dst, x.shape[0])
-            out = self.ops.segment_sum(message.reshape(n_edges, -1), dst, offsets, weight.contiguous(),
-                                       inverse.reshape(-1).contiguous(), order=order)
-        except Exception as error:  # noqa: BLE001 -- a seam must never break inference
-            self.stats.envelope_fallbacks += 1
-            self._fall_back(error)
-            return original(x, edge_cache, radial_feat)
-        self.stats.envelope_hits += 1
-        return out.reshape(x.shape)
-
-    @staticmethod
-    def _envelope_inputs_ok(block, x, dst, edge_env, inverse, gate) -> bool:
-        if getattr(block, "training", False):
-            return False
-        if not (_fp32_operand(x) and x.ndim == 3 and _fp32_operand(edge_env) and _fp32_operand(inverse)):
-            return False
-        if not (_fp32_operand(dst, torch.int64) and dst.ndim == 1 and dst.numel() > 0):
-            return False
-        if gate is not None and not _fp32_operand(gate):
-            return False
-        return inverse.numel() == x.shape[0] and edge_env.numel() == dst.numel()
-
-
-_SESSION: _Session | None = None
-# What the installation replaced: "<module>.<name>" -> (module, original) for
-# rebound names, "block:<id>" -> (block, instance attribute or None) for
-# patched methods (None: the block used its class's method).
-_SAVED: dict[str, tuple[Any, Any]] = {}
-
-
-def _softmax_namespaces() -> list[Any]:
-    """DeepMD modules that hold the S1 name (imported only when patching a real model)."""
-    import deepmd.pt.model.descriptor.sezm_nn.attention as attention
-    import deepmd.pt.model.descriptor.sezm_nn.so2 as so2
-
-    found = [attention, so2]
-    try:
-        import deepmd.pt.model.descriptor.sezm_nn as package
-    except ImportError:  # pragma: no cover
-        return found
-    return found + [package]
-
-
-def _blocks(root: Any) -> list[Any]:
-    """SO(2) convolution blocks: modules exposing both aggregation seams."""
-    return [m for m in root.modules()
-            if callable(getattr(m, "edge_message", None)) and callable(getattr(m, "forward_envelope", None))
-            and hasattr(m, "_segment_softmax_fn")]
-
+# ---------------------------------------------------------------------------
+# finding the seams
+# ---------------------------------------------------------------------------
 
 def _module_root(model: Any) -> tuple[Any | None, str]:
-    """The ``nn.Module`` tree behind a DeepPot/DeepEval wrapper, and where it was found.
+    """The ``nn.Module`` tree behind ``model`` and the dotted path it was found at.
 
-    A module is its own root.  DeepMD's legacy ``pt`` backend keeps the tree at
-    ``deep_eval.dp``, the ``pt_expt`` backend at ``deep_eval._dpmodel``.
+    ``model`` itself when it is a module tree (path ``"model"``); otherwise
+    the first of ``deep_eval.<attr>`` (see ``_TREE_ATTRIBUTES``) and then
+    ``deep_eval`` that has one; ``(None, "")`` when there is none.
     """
-    if callable(getattr(model, "modules", None)):
+    def is_tree(candidate: Any) -> bool:
+        return candidate is not None and callable(getattr(candidate, "modules", None))
+
+    if is_tree(model):
         return model, "model"
-    deep_eval = getattr(model, "deep_eval", None)
-    if deep_eval is None:
+    evaluator = getattr(model, "deep_eval", None)
+    if evaluator is None:
         return None, ""
-    for name in ("_dpmodel", "dp", "model"):
-        candidate = getattr(deep_eval, name, None)
-        if candidate is not None and callable(getattr(candidate, "modules", None)):
-            return candidate, f"deep_eval.{name}"
-    if callable(getattr(deep_eval, "modules", None)):
-        return deep_eval, "deep_eval"
-    return None, ""
+    paths = [(f"deep_eval.{name}", getattr(evaluator, name, None)) for name in _TREE_ATTRIBUTES]
+    paths.append(("deep_eval", evaluator))
+    return next(((tree, path) for path, tree in paths if is_tree(tree)), (None, ""))
+
+
+def _is_so2_block(module: Any) -> bool:
+    """A SeZM SO(2) convolution: it carries both aggregation seams."""
+    return (hasattr(module, "_segment_softmax_fn") and callable(getattr(module, "edge_message", None))
+            and callable(getattr(module, _ENVELOPE_NAME, None)))
+
+
+def _so2_blocks(root: Any) -> list[Any]:
+    return [] if root is None else [module for module in root.modules() if _is_so2_block(module)]
+
+
+def _importable(names: Iterable[str]) -> list[Any]:
+    """The modules of ``names`` that import here (DeepMD is optional)."""
+    found = []
+    for name in names:
+        try:
+            found.append(importlib.import_module(name))
+        except ImportError:
+            continue
+    return found
 
 
 def describe_module(module: Any, *, max_depth: int = 2, max_rows: int = 40) -> list[str]:
-    """Printable lines: the module tree (to ``max_depth``) and every patch target."""
+    """Printable lines: the module tree down to ``max_depth`` and every patch target."""
     root, path = _module_root(module)
+    kind = type(module).__name__
     if root is None:
-        return [f"module: {type(module).__name__} (no nn.Module tree found -- expected a module, "
-                "or a DeepPot/DeepEval wrapper with deep_eval.dp / deep_eval._dpmodel)",
+        return [f"module: {kind} (no nn.Module tree found -- pass an nn.Module, or a DeepPot/DeepEval "
+                "wrapper holding one at deep_eval.dp or deep_eval._dpmodel)",
                 "patch targets: 0 (nothing can be bound)"]
-    named = list(root.named_modules()) if hasattr(root, "named_modules") else []
-    via = "" if path == "model" else f" -> {path}"
-    lines = [f"module: {type(module).__name__}{via} ({type(root).__name__}, {len(named)} submodules)"]
-    for name, child in named[:max_rows]:
-        depth = name.count(".") + 1 if name else 0
-        if depth <= max_depth:
-            lines.append(f"  {'  ' * depth}{name or '<root>'}  {type(child).__name__}")
-    if len(named) > max_rows:
-        lines.append(f"  ... {len(named) - max_rows} more submodules")
-    targets = _blocks(root)
-    lines.append(f"patch targets: {len(targets)} SO(2) block(s)")
-    for index, block in enumerate(targets):
-        lines.append(f"  [{index}] {type(block).__name__}  n_atten_head={getattr(block, 'n_atten_head', '?')}  "
-                     "seams: forward_envelope -> segment_sum, attention softmax -> segment_softmax")
-    return lines
+    rows = list(root.named_modules()) if hasattr(root, "named_modules") else []
+    shown = [(name, child) for name, child in rows[:max_rows] if (name.count(".") + 1 if name else 0) <= max_depth]
+    suffix = "" if path == "model" else f" -> {path}"
+    report = [f"module: {kind}{suffix} ({type(root).__name__}, {len(rows)} submodules)"]
+    report += [f"  {'  ' * (name.count('.') + 1 if name else 0)}{name or '<root>'}  {type(child).__name__}"
+               for name, child in shown]
+    if len(rows) > max_rows:
+        report.append(f"  ... {len(rows) - max_rows} more submodules")
+    blocks = _so2_blocks(root)
+    report.append(f"patch targets: {len(blocks)} SO(2) block(s)")
+    report += [f"  [{i}] {type(block).__name__}  n_atten_head={getattr(block, 'n_atten_head', '?')}  "
+               "seams: forward_envelope -> segment_sum, attention softmax -> segment_softmax"
+               for i, block in enumerate(blocks)]
+    return report
 
 
-def _say(verbose: bool, text: str) -> None:
-    if verbose:
-        print(f"[deepmd_patch] {text}", flush=True)
+# ---------------------------------------------------------------------------
+# the installation
+# ---------------------------------------------------------------------------
 
+class _Rebinding:
+    """One name rebound on an object, and how to put it back.
 
-def deepmd_patch(module: Any, *, ops: Any = None, softmax: bool = True, envelope: bool = True,
-                 blocks: Iterable[Any] | None = None, namespaces: Iterable[Any] | None = None,
-                 verbose: bool = True) -> FusedStats:
-    """Bind the operators into ``module`` (a DeepPot, DeepEval or ``nn.Module``).
-
-    ``ops`` is a bundle with ``segment_sum`` and ``segment_softmax`` (default:
-    this build's ``kernels.segment``; without a usable gfx950 device the call
-    replaces nothing).  ``blocks`` and ``namespaces`` override where the seams
-    are found (host tests use them instead of importing DeepMD).  Any earlier
-    installation is removed first.  Returns the counters of this installation.
+    For a module attribute the previous value is restored.  For a method
+    patched on an instance, the instance's own attribute is restored when it
+    had one, else removed, so that the class's method shows through again.
     """
-    global _SESSION
-    stats = FusedStats()
-    for line in describe_module(module) if verbose else ():
-        _say(True, line)
-    uninstall(module)
+
+    __slots__ = ("owner", "name", "previous", "on_instance")
+
+    def __init__(self, owner: Any, name: str, value: Any, *, on_instance: bool):
+        self.owner, self.name, self.on_instance = owner, name, on_instance
+        if on_instance:
+            self.previous = vars(owner).get(name)
+            vars(owner)[name] = value
+        else:
+            self.previous = getattr(owner, name)
+            setattr(owner, name, value)
+
+    def undo(self) -> None:
+        if not self.on_instance:
+            setattr(self.owner, self.name, self.previous)
+        elif self.previous is None:
+            vars(self.owner).pop(self.name, None)
+        else:
+            vars(self.owner)[self.name] = self.previous
+
+    def label(self) -> str:
+        where = getattr(self.owner, "__name__", None) or f"{type(self.owner).__name__}@{id(self.owner):x}"
+        return f"{where}.{self.name}"
+
+
+class _Installation:
+    """The operators, counters, CSR cache and rebindings of one ``deepmd_patch``."""
+
+    def __init__(self, ops: Any, stats: FusedStats):
+        self.ops, self.stats = ops, stats
+        self.csr = _CsrView()
+        self.rebindings: list[_Rebinding] = []
+        self.warned = False
+
+    def rebind(self, owner: Any, name: str, value: Any, *, on_instance: bool = False) -> None:
+        self.rebindings.append(_Rebinding(owner, name, value, on_instance=on_instance))
+
+    def undo(self) -> None:
+        while self.rebindings:
+            self.rebindings.pop().undo()
+
+    def fallback(self, seam: str, error: Exception | None = None) -> None:
+        field = f"{seam}_fallbacks"
+        setattr(self.stats, field, getattr(self.stats, field) + 1)
+        if error is None:
+            return
+        self.stats.last_error = f"{type(error).__name__}: {error}"
+        if not self.warned:
+            self.warned = True
+            warnings.warn(f"fused DeepMD dispatch fell back to the stock path: {self.stats.last_error}",
+                          RuntimeWarning, stacklevel=4)
+
+    def hit(self, seam: str) -> None:
+        field = f"{seam}_hits"
+        setattr(self.stats, field, getattr(self.stats, field) + 1)
+
+    # -- softmax ---------------------------------------------------------------
+    def softmax(self, stock, logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight=None):
+        shapes_ok = (src_weight is None and _kernel_operand(logits) and logits.dim() == 3 and logits.shape[0] > 0
+                     and _kernel_operand(edge_env) and edge_env.numel() == logits.shape[0]
+                     and isinstance(dst, torch.Tensor) and dst.dtype == torch.int64 and dst.dim() == 1
+                     and dst.numel() == logits.shape[0] and n_nodes > 0 and isinstance(z_bias_raw, torch.Tensor)
+                     and z_bias_raw.numel() == logits.shape[1] * logits.shape[2])
+        if not shapes_ok:
+            self.fallback("softmax")
+            return stock(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight)
+        edges, focus, heads = logits.shape
+        try:
+            offsets, order = self.csr.get(dst, n_nodes)
+            null = torch.log(F.softplus(z_bias_raw.reshape(1, focus * heads).to(torch.float32)) + float(eps))
+            result = self.ops.segment_softmax(logits.reshape(edges, focus * heads), edge_env.reshape(edges), offsets,
+                                              null.expand(n_nodes, focus * heads).contiguous(), order=order)
+        except Exception as error:  # noqa: BLE001 -- a seam must never break inference
+            self.fallback("softmax", error)
+            return stock(logits, edge_env, dst, n_nodes, z_bias_raw, eps, None)
+        self.hit("softmax")
+        alpha = result[0] if isinstance(result, tuple) else result
+        return alpha.reshape(edges, focus, heads)
+
+    # -- envelope --------------------------------------------------------------
+    def envelope(self, stock, block, x, edge_cache, radial_feat):
+        """``stock`` is the block's own ``forward_envelope``, already bound to it."""
+        dst = getattr(edge_cache, "dst", None)
+        env = getattr(edge_cache, "edge_env", None)
+        inverse = getattr(edge_cache, "inv_sqrt_deg", None)
+        gate = getattr(edge_cache, "edge_src_gate", None)
+        shapes_ok = (not getattr(block, "training", False) and _kernel_operand(x) and x.dim() == 3
+                     and _kernel_operand(env) and _kernel_operand(inverse) and inverse.numel() == x.shape[0]
+                     and _index_operand(dst) and dst.numel() > 0 and env.numel() == dst.numel()
+                     and (gate is None or _kernel_operand(gate)))
+        if not shapes_ok:
+            self.fallback("envelope")
+            return stock(x, edge_cache, radial_feat)
+        try:
+            message, _ = block.edge_message(x, edge_cache, radial_feat)
+            if not _kernel_operand(message) or message.shape[0] != dst.numel():
+                raise ValueError("edge message is not a contiguous fp32 (n_edges, ...) tensor")
+            scale = env.reshape(-1) if gate is None else env.reshape(-1) * gate.reshape(-1).to(torch.float32)
+            offsets, order = self.csr.get(dst, x.shape[0])
+            out = self.ops.segment_sum(message.reshape(dst.numel(), -1), dst, offsets, scale.contiguous(),
+                                       inverse.reshape(-1).contiguous(), order=order)
+        except Exception as error:  # noqa: BLE001 -- a seam must never break inference
+            self.fallback("envelope", error)
+            return stock(x, edge_cache, radial_feat)
+        self.hit("envelope")
+        return out.reshape(x.shape)
+
+    # -- force -----------------------------------------------------------------
+    def force(self, stock, g, edge_vec, edge_scatter_index, edge_mask, dst_order, dst_row_ptr, src_order,
+              src_row_ptr, n_node_per_frame, optional, n_ext, flag):
+        """``(force_flat, atom_virial_flat, frame_virial, None)`` of one frame, or DeepMD's own result.
+
+        Served: one frame (``n_node_per_frame == n_ext``), every edge kept
+        (``edge_mask`` absent or all true), an empty optional tensor, float32
+        or float64 ``[E, 3]`` values and ``[n_ext + 1]`` CSR pointers.  The
+        natural edge order need not be grouped by destination: the values are
+        put in ``dst_order`` first.
+        """
+        args = (g, edge_vec, edge_scatter_index, edge_mask, dst_order, dst_row_ptr, src_order, src_row_ptr,
+                n_node_per_frame, optional, n_ext, flag)
+        dtypes = (torch.float32, torch.float64)
+        try:
+            atoms = int(n_ext)
+            frame_atoms = int(n_node_per_frame) if not isinstance(n_node_per_frame, torch.Tensor) or \
+                n_node_per_frame.numel() == 1 else -1
+            shapes_ok = (atoms > 0 and frame_atoms == atoms and _kernel_operand(g, dtypes) and g.dim() == 2
+                         and g.shape[1] == 3 and _kernel_operand(edge_vec, (g.dtype,)) and edge_vec.shape == g.shape
+                         and all(_index_operand(t) and t.numel() == g.shape[0] for t in (dst_order, src_order))
+                         and all(_index_operand(t) and t.numel() == atoms + 1 for t in (dst_row_ptr, src_row_ptr))
+                         and (optional is None or (isinstance(optional, torch.Tensor) and optional.numel() == 0)))
+            if shapes_ok and edge_mask is not None:
+                shapes_ok = bool(torch.as_tensor(edge_mask).all())
+        except (TypeError, ValueError, RuntimeError):
+            shapes_ok = False
+        if not shapes_ok:
+            self.fallback("force")
+            return stock(*args)
+        try:
+            # rank[e] = the slot of edge e in the destination grouping
+            rank = torch.empty_like(dst_order)
+            rank[dst_order] = torch.arange(dst_order.numel(), device=dst_order.device)
+            grouped_g = g.index_select(0, dst_order).contiguous()
+            grouped_v = edge_vec.detach().index_select(0, dst_order).contiguous()
+            force, virial = self.ops.force_assembly(grouped_g, grouped_v, None, None, dst_row_ptr, src_row_ptr,
+                                                    rank.index_select(0, src_order).contiguous())
+        except Exception as error:  # noqa: BLE001 -- a seam must never break inference
+            self.fallback("force", error)
+            return stock(*args)
+        self.hit("force")
+        return force.reshape(-1), virial.reshape(-1), virial.sum(0, keepdim=True), None
+
+
+_ACTIVE: _Installation | None = None
+
+
+def _dispatcher(seam: str, stock: Callable) -> Callable:
+    """A function that routes calls to the active installation's ``seam``, or to ``stock`` after uninstall."""
+    def dispatch(*args, **kwargs):
+        installation = _ACTIVE
+        if installation is None:
+            return stock(*args, **kwargs)
+        return getattr(installation, seam)(stock, *args, **kwargs)
+
+    dispatch.__name__ = dispatch.__qualname__ = f"fused_{seam}"
+    return dispatch
+
+
+def _envelope_method(block: Any, stock: Callable) -> MethodType:
+    """``forward_envelope`` for ``block``: the active installation's envelope seam, or ``stock`` (already bound)."""
+    def fused_envelope(self, x, edge_cache, radial_feat):
+        installation = _ACTIVE
+        if installation is None:
+            return stock(x, edge_cache, radial_feat)
+        return installation.envelope(stock, self, x, edge_cache, radial_feat)
+
+    return MethodType(fused_envelope, block)
+
+
+def deepmd_patch(module: Any, *, ops: Any = None, softmax: bool = True, envelope: bool = True, force: bool = False,
+                 blocks: Iterable[Any] | None = None, namespaces: Iterable[Any] | None = None,
+                 force_namespaces: Iterable[tuple[Any, str]] | None = None, verbose: bool = True) -> FusedStats:
+    """Bind the operators into ``module`` (a DeepPot, DeepEval or ``nn.Module``); returns its counters.
+
+    ``ops`` bundles ``segment_softmax``, ``segment_sum`` and ``force_assembly``
+    (default: this build's ``kernels.segment``; without a usable gfx950
+    device nothing is replaced).  ``blocks``, ``namespaces`` (modules holding
+    the softmax name) and ``force_namespaces`` (``(module, name)`` pairs)
+    override where the seams are looked up -- host tests use them instead of
+    importing DeepMD.  An earlier installation is removed first.
+    """
+    global _ACTIVE
+
+    def say(text: str) -> None:
+        if verbose:
+            print(f"[deepmd_patch] {text}", flush=True)
+
+    if verbose:
+        for line in describe_module(module):
+            say(line)
+    uninstall()
     root, path = _module_root(module)
-    targets = list(blocks) if blocks is not None else (list(_blocks(root)) if root is not None else [])
-    if root is not None and path != "model":
-        _say(verbose, f"resolved module tree: {path} ({type(root).__name__})")
-    stats.blocks = len(targets)
+    targets = list(blocks) if blocks is not None else _so2_blocks(root)
+    stats = FusedStats(blocks=len(targets))
+    if path not in ("", "model"):
+        say(f"resolved module tree: {path} ({type(root).__name__})")
     ops = _segment_operators() if ops is None else ops
-    _say(verbose, f"operators: {'kernels.segment' if ops is not None else 'unavailable'}; "
-                  f"softmax={softmax} envelope={envelope}")
+    say(f"operators: {'unavailable' if ops is None else 'kernels.segment'}; "
+        f"softmax={softmax} envelope={envelope} force={force}")
     if ops is None:
-        _say(verbose, "no usable gfx950 operator library on this host -> nothing replaced")
+        say("no usable gfx950 operator library on this host -> nothing replaced")
         return stats
-
-    spaces: list[Any] = []
-    stock_softmax = None
-    if softmax:
-        spaces = list(namespaces) if namespaces is not None else _softmax_namespaces()
-        if not spaces:
-            raise ValueError("deepmd_patch needs at least one namespace holding the softmax seam")
-        stock_softmax = getattr(spaces[0], _SOFTMAX_NAME)
-    session = _Session(ops=ops, stats=stats, reference_softmax=stock_softmax)
-    _SESSION = session
+    installation = _Installation(ops, stats)
+    _ACTIVE = installation
 
     if softmax:
-        def bound_softmax(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight=None):
-            active = _SESSION
-            if active is None:  # uninstalled while a reference to this function survived
-                return stock_softmax(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight)
-            return active.softmax(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight)
-
-        for space in spaces:
-            if hasattr(space, _SOFTMAX_NAME):
-                _SAVED[f"{space.__name__}.{_SOFTMAX_NAME}"] = (space, getattr(space, _SOFTMAX_NAME))
-                setattr(space, _SOFTMAX_NAME, bound_softmax)
-                _say(verbose, f"replace {space.__name__}.{_SOFTMAX_NAME} -> fused_deepmd.bound_softmax")
+        homes = [home for home in (namespaces if namespaces is not None else _importable(_SOFTMAX_HOMES))
+                 if hasattr(home, _SOFTMAX_NAME)]
+        if not homes:
+            uninstall()
+            raise ValueError(f"deepmd_patch found no module holding {_SOFTMAX_NAME}")
+        routed = _dispatcher("softmax", getattr(homes[0], _SOFTMAX_NAME))
+        for home in homes:
+            installation.rebind(home, _SOFTMAX_NAME, routed)
+            say(f"replace {home.__name__}.{_SOFTMAX_NAME} -> fused_deepmd.fused_softmax")
         stats.bound_softmax = True
 
     if envelope:
         for block in targets:
-            stock = block.forward_envelope  # bound: called as stock(x, edge_cache, radial_feat)
-            _SAVED[f"block:{id(block)}"] = (block, getattr(block, "__dict__", {}).get("forward_envelope"))
-
-            def patched(self, x, edge_cache, radial_feat, _stock=stock):
-                active = _SESSION
-                if active is None:
-                    return _stock(x, edge_cache, radial_feat)
-                return active.envelope(_stock, self, x, edge_cache, radial_feat)
-
-            block.forward_envelope = MethodType(patched, block)
+            installation.rebind(block, _ENVELOPE_NAME, _envelope_method(block, getattr(block, _ENVELOPE_NAME)),
+                                on_instance=True)
         stats.bound_envelope = bool(targets)
-        _say(verbose, f"replace SO2Convolution.forward_envelope on {len(targets)} block(s) -> fused_deepmd.patched")
-    _say(verbose, f"installed: softmax={stats.bound_softmax} envelope={stats.bound_envelope} blocks={stats.blocks}")
+        say(f"replace SO2Convolution.forward_envelope on {len(targets)} block(s) -> fused_deepmd.fused_envelope")
+
+    if force:
+        pairs = list(force_namespaces) if force_namespaces is not None else [
+            (home, name) for module_name, name in _FORCE_HOMES for home in _importable((module_name,))]
+        for home, name in pairs:
+            if hasattr(home, name):
+                installation.rebind(home, name, _dispatcher("force", getattr(home, name)))
+                say(f"replace {home.__name__}.{name} -> fused_deepmd.fused_force")
+                stats.bound_force = True
+        if not stats.bound_force:
+            say("force seam: DeepMD's edge_force_virial is not importable here -> not bound")
+    say(f"installed: softmax={stats.bound_softmax} envelope={stats.bound_envelope} force={stats.bound_force} "
+        f"blocks={stats.blocks}")
     return stats
 
 
 def uninstall(module: Any = None) -> None:
-    """Restore every rebound name and method; harmless when nothing is installed."""
-    global _SESSION
-    for key, (owner, original) in list(_SAVED.items()):
-        if key.startswith("block:"):
-            # the patch is an instance attribute: put back what was there, or
-            # delete it so that the class method shows through again
-            if original is None:
-                owner.__dict__.pop("forward_envelope", None)
-            else:
-                owner.__dict__["forward_envelope"] = original
-        else:
-            setattr(owner, key.rsplit(".", 1)[1], original)
-    _SAVED.clear()
-    _SESSION = None
+    """Undo the active installation's rebindings (newest first); harmless when none is active."""
+    global _ACTIVE
+    installation, _ACTIVE = _ACTIVE, None
+    if installation is not None:
+        installation.undo()
+
+
+def installed() -> list[str]:
+    """``owner.name`` of every rebinding of the active installation, in the order made."""
+    return [] if _ACTIVE is None else [rebinding.label() for rebinding in _ACTIVE.rebindings]
 
 
 def status(stats: FusedStats | None) -> dict[str, Any]:
@@ -392,4 +516,4 @@ def status(stats: FusedStats | None) -> dict[str, Any]:
     return {} if stats is None else stats.as_dict()
 
 
-__all__ = ["FusedStats", "deepmd_patch", "describe_module", "status", "uninstall"]
+__all__ = ["FusedStats", "deepmd_patch", "describe_module", "installed", "status", "uninstall"]

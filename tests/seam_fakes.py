@@ -10,6 +10,15 @@ lipengfei1409/bysj), the two stock implementations the seams replace:
 * ``FakeBlock.forward_envelope`` -- ``zeros -> index_add_(dst, message *
   edge_env * gate) -> * inv_sqrt_deg``.
 
+* ``stock_edge_force_virial`` -- DeepMD's edge force/virial assembly for one
+  frame, restated from the call the reference quotes
+  (docs/fused-operators.md:111-133): CSR views from ``argsort`` +
+  ``searchsorted``, two ``index_add_`` for the force, the source-side outer
+  product ``-g (x) edge_vec`` scattered into the atom virial.  DeepMD's own
+  ``edge_force_virial`` is not in this container, so the output layout
+  (``force.reshape(-1)``, ``atom_virial.reshape(-1)``, a ``[1, 9]`` frame
+  virial, an unused fourth value) is this stand-in's reading of the quote.
+
 ``OracleOps`` is an operator bundle that answers with the CPU oracle.
 """
 from __future__ import annotations
@@ -51,6 +60,46 @@ class OracleOps:
     def segment_sum(self, src, dst, offsets, edge_scale=None, node_scale=None, *, order=None):
         self.calls.append(("sum", tuple(src.shape)))
         return ref.segment_sum_reference(src, dst_from_csr(offsets, order), offsets, edge_scale, node_scale)
+
+    def force_assembly(self, grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None, src_order=None):
+        """kernels.segment.force_assembly: ``src``/``dst`` may be None when the CSR views are given."""
+        self.calls.append(("force", tuple(grad_edge.shape)))
+        dst = dst_from_csr(dst_offsets, None) if dst is None else dst
+        src = dst_from_csr(src_offsets, src_order) if src is None else src
+        return ref.force_assembly_reference(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets)
+
+
+def edge_force_virial_call(g, edge_vec, dst_ext, src_ext, n_ext, *, edge_mask=None, frames=1, optional=None):
+    """The argument list of DeepMD's call: CSR views from argsort + searchsorted (quoted chain)."""
+    dst_order = torch.argsort(dst_ext)
+    src_order = torch.argsort(src_ext)
+    boundaries = torch.arange(n_ext + 1, device=g.device, dtype=dst_ext.dtype)
+    dst_row_ptr = torch.searchsorted(dst_ext.index_select(0, dst_order), boundaries)
+    src_row_ptr = torch.searchsorted(src_ext.index_select(0, src_order), boundaries)
+    scatter_index = torch.zeros_like(dst_ext)
+    mask = torch.ones(g.shape[0], dtype=torch.bool, device=g.device) if edge_mask is None else edge_mask
+    empty = edge_vec.new_empty(0) if optional is None else optional
+    return (g.contiguous(), edge_vec.contiguous(), scatter_index, mask, dst_order, dst_row_ptr, src_order,
+            src_row_ptr, n_ext // frames, empty, n_ext, True)
+
+
+def stock_edge_force_virial(g, edge_vec, edge_scatter_index, edge_mask, dst_order, dst_row_ptr, src_order,
+                            src_row_ptr, n_node_per_frame, optional, n_ext, flag):
+    """DeepMD's edge force/virial of one frame with torch scatters (masked edges contribute nothing)."""
+    del edge_scatter_index, n_node_per_frame, optional, flag
+    dst = dst_from_csr(dst_row_ptr, dst_order)
+    src = dst_from_csr(src_row_ptr, src_order)
+    kept = torch.where(edge_mask.reshape(-1, 1), g, torch.zeros_like(g))
+    force = g.new_zeros((n_ext, 3)).index_add_(0, dst, kept).index_add_(0, src, -kept)
+    outer = -(kept.unsqueeze(2) * edge_vec.unsqueeze(1)).reshape(-1, 9)
+    atom_virial = g.new_zeros((n_ext, 9)).index_add_(0, src, outer)
+    return force.reshape(-1), atom_virial.reshape(-1), atom_virial.sum(0, keepdim=True), None
+
+
+def force_namespace(name="fake.pt_expt.kernels.edge_force_virial", attribute="edge_force_virial"):
+    module = types.ModuleType(name)
+    setattr(module, attribute, stock_edge_force_virial)
+    return module
 
 
 def stock_softmax(logits, edge_env, dst, n_nodes, z_bias_raw, eps, src_weight=None):

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from bysj_amd.model import fused_deepmd
-from parity import announce, assert_close_scaled, assert_gradient
+from parity import announce, assert_close_scaled, assert_fp64, assert_gradient
 from seam_fakes import FakeBlock, FakeModel, softmax_namespace, stock_softmax
 
 pytestmark = pytest.mark.gpu
@@ -97,3 +97,35 @@ def test_envelope_seam_on_gfx950(clean, gate):
     assert_close_scaled(out, exact, what="aggregation vs fp64 truth")
     for got, ref, exact_grad, name in zip(grads, want, truth, ("grad_message", "grad_edge_env", "grad_gate")):
         assert_gradient(got, ref, exact_grad, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_force_seam_on_gfx950_matches_the_stock_chain(clean, dtype):
+    from seam_fakes import edge_force_virial_call, force_namespace
+
+    announce("force seam", dtype)
+    gen = torch.Generator().manual_seed(9)
+    n_ext, n_edges = 500, 30000
+    dst = torch.randint(0, n_ext, (n_edges,), generator=gen).to(DEV)  # unsorted extended-atom lists
+    src = torch.randint(0, n_ext, (n_edges,), generator=gen).to(DEV)
+    g = torch.randn(n_edges, 3, generator=gen, dtype=torch.float64).to(dtype).to(DEV)
+    vec = torch.randn(n_edges, 3, generator=gen, dtype=torch.float64).to(dtype).to(DEV)
+    space = force_namespace()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), softmax=False, envelope=False, force=True,
+                                      force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    args = edge_force_virial_call(g, vec, dst, src, n_ext)
+    force, atom_virial, frame_virial, _ = space.edge_force_virial(*args)
+    fused_deepmd.uninstall()
+    stock = space.edge_force_virial(*args)
+    assert stats.force_hits == 1 and stats.force_fallbacks == 0
+    # the stock chain scatters with float atomics in the input dtype; the kernel accumulates in double:
+    # both against the fp64 truth of the same sums
+    g64, v64 = g.double().cpu(), vec.double().cpu()
+    truth = force_namespace().edge_force_virial(*edge_force_virial_call(g64, v64, dst.cpu(), src.cpu(), n_ext))
+    for label, got, exact, theirs in zip(("force", "atom virial", "frame virial"), (force, atom_virial, frame_virial),
+                                         truth, stock):
+        if dtype == torch.float64:
+            assert_fp64(got, exact, f"{label} vs fp64 truth")
+        else:
+            assert_close_scaled(got, exact, what=f"{label} vs fp64 truth")
+            assert_close_scaled(got, theirs, what=f"{label} vs the stock chain")

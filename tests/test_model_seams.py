@@ -20,7 +20,8 @@ import torch
 
 from bysj_amd.model import dpa4, fused_deepmd
 from bysj_amd.model.dpa4 import DPA4Model, _normalize_fused
-from seam_fakes import FakeBlock, FakeEdgeCache, FakeModel, OracleOps, grouped_dst, softmax_namespace
+from seam_fakes import (FakeBlock, FakeEdgeCache, FakeModel, OracleOps, edge_force_virial_call, force_namespace,
+                        grouped_dst, softmax_namespace)
 
 
 @pytest.fixture
@@ -193,7 +194,7 @@ def test_installing_twice_keeps_one_patch(any_device):
                                       verbose=False)
     second = fused_deepmd.deepmd_patch(FakeModel([]), ops=OracleOps(), namespaces=[space], envelope=False,
                                        verbose=False)
-    assert [k for k in fused_deepmd._SAVED if k.endswith(".segment_envelope_gated_softmax")] == [
+    assert [k for k in fused_deepmd.installed() if k.endswith(".segment_envelope_gated_softmax")] == [
         "fake.sezm_nn.attention.segment_envelope_gated_softmax"]
     space.segment_envelope_gated_softmax(*_softmax_inputs())
     assert first.softmax_hits == 0 and second.softmax_hits == 1
@@ -382,3 +383,82 @@ def test_facade_rejects_bad_switches_before_loading():
 def test_facade_without_deepmd_says_so():
     with pytest.raises(RuntimeError, match="DeepMD-kit"):
         DPA4Model("water.pt")
+
+
+# ---------------------------------------------------------------------------
+# S3: force seam (opt-in)
+# ---------------------------------------------------------------------------
+
+def _force_case(n_ext=7, n_edges=40, seed=3, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(seed)
+    dst = torch.randint(0, n_ext, (n_edges,), generator=gen)  # unsorted, as DeepMD's extended lists are
+    src = torch.randint(0, n_ext, (n_edges,), generator=gen)
+    g = torch.randn(n_edges, 3, generator=gen, dtype=torch.float64).to(dtype)
+    vec = torch.randn(n_edges, 3, generator=gen, dtype=torch.float64).to(dtype)
+    return g, vec, dst, src, n_ext
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_force_seam_matches_the_stock_chain(any_device, dtype):
+    g, vec, dst, src, n_ext = _force_case(dtype=dtype)
+    space, ops = force_namespace(), OracleOps()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), ops=ops, softmax=False, envelope=False, force=True,
+                                      force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    assert stats.bound_force and fused_deepmd.installed() == ["fake.pt_expt.kernels.edge_force_virial.edge_force_virial"]
+    args = edge_force_virial_call(g, vec, dst, src, n_ext)
+    force, atom_virial, frame_virial, extra = space.edge_force_virial(*args)
+    fused_deepmd.uninstall()
+    assert space.edge_force_virial.__name__ == "stock_edge_force_virial"
+    e_force, e_atom, e_frame, _ = space.edge_force_virial(*args)
+    tolerance = dict(rtol=1e-12, atol=1e-12) if dtype == torch.float64 else dict(rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(force, e_force, **tolerance)
+    torch.testing.assert_close(atom_virial, e_atom, **tolerance)
+    torch.testing.assert_close(frame_virial, e_frame, **tolerance)
+    assert extra is None and force.shape == (3 * n_ext,) and frame_virial.shape == (1, 9)
+    assert stats.force_hits == 1 and stats.force_fallbacks == 0 and ops.calls == [("force", (40, 3))]
+
+
+@pytest.mark.parametrize("case", ["masked_edge", "two_frames", "optional_tensor", "wrong_dtype", "bad_row_ptr"])
+def test_force_seam_falls_back_where_the_quote_is_silent(any_device, case):
+    g, vec, dst, src, n_ext = _force_case(n_ext=8)
+    kwargs = {}
+    if case == "masked_edge":
+        mask = torch.ones(g.shape[0], dtype=torch.bool)
+        mask[5] = False
+        kwargs["edge_mask"] = mask
+    elif case == "two_frames":
+        kwargs["frames"] = 2
+    elif case == "optional_tensor":
+        kwargs["optional"] = torch.ones(3)
+    args = list(edge_force_virial_call(g, vec, dst, src, n_ext, **kwargs))
+    if case == "wrong_dtype":
+        args[0], args[1] = args[0].half(), args[1].half()
+    if case == "bad_row_ptr":
+        args[5] = args[5][:-1]
+    space, ops = force_namespace(), OracleOps()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), ops=ops, softmax=False, envelope=False, force=True,
+                                      force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    if case not in ("wrong_dtype", "bad_row_ptr"):
+        result = space.edge_force_virial(*args)
+        torch.testing.assert_close(result[0], force_namespace().edge_force_virial(*args)[0])
+    else:
+        try:
+            space.edge_force_virial(*args)
+        except (RuntimeError, IndexError):  # the stock chain itself rejects these inputs
+            pass
+    assert stats.force_hits == 0 and stats.force_fallbacks == 1 and ops.calls == []
+
+
+def test_force_seam_is_opt_in_and_reports_missing_homes(any_device):
+    space = force_namespace()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), ops=OracleOps(), softmax=False, envelope=False,
+                                      force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    assert not stats.bound_force and fused_deepmd.installed() == []
+    assert _normalize_fused(True) == {"softmax": True, "envelope": True}
+    assert _normalize_fused(("force",)) == {"force": True}
+    buffer = io.StringIO()
+    with contextlib.redirect_stdout(buffer):
+        stats = fused_deepmd.deepmd_patch(FakeModel([]), ops=OracleOps(), softmax=False, envelope=False,
+                                          force=True, force_namespaces=[])
+    assert not stats.bound_force and "edge_force_virial is not importable here" in buffer.getvalue()
+    fused_deepmd.uninstall()
