@@ -275,14 +275,27 @@ def _null_checks(tensor, nodes, channels, what):
     _check(tensor.numel() == nodes * channels, f"{what} must have shape (n_nodes, channels)")
 
 
+def _offsets_fingerprint(offsets: torch.Tensor):
+    """Storage address, size and version counter of ``offsets`` (no counter for an inference tensor)."""
+    version = None if offsets.is_inference() else offsets._version
+    return (offsets.data_ptr(), offsets.numel(), version)
+
+
 class SoftmaxPlan:
-    """Degree plan of one CSR (the long segments of ``offsets``) for one channel count."""
+    """Degree plan of one CSR (the long segments of ``offsets``) for one channel count.
 
-    __slots__ = ("words", "n_long", "capacity", "n_edges", "channels")
+    ``fingerprint`` identifies the ``offsets`` tensor the plan was built from:
+    a plan only lists that CSR's long segments, and the kernels would leave
+    any other long segment unwritten, so a plan is refused for offsets with
+    another storage, size or version (an in-place write).
+    """
 
-    def __init__(self, words: torch.Tensor, n_long: int, capacity: int, n_edges: int, channels: int):
+    __slots__ = ("words", "n_long", "capacity", "n_edges", "channels", "fingerprint")
+
+    def __init__(self, words: torch.Tensor, n_long: int, capacity: int, n_edges: int, channels: int,
+                 fingerprint=None):
         self.words, self.n_long, self.capacity = words, n_long, capacity
-        self.n_edges, self.channels = n_edges, channels
+        self.n_edges, self.channels, self.fingerprint = n_edges, channels, fingerprint
 
 
 def segment_softmax_plan(offsets, n_edges: int, channels: int) -> SoftmaxPlan:
@@ -298,14 +311,16 @@ def segment_softmax_plan(offsets, n_edges: int, channels: int) -> SoftmaxPlan:
             _lib.ctypes.byref(n_long), _lib.ctypes.byref(capacity), stream,
         )
     _lib.check(status)
-    return SoftmaxPlan(words, int(n_long.value), int(capacity.value), int(n_edges), int(channels))
+    return SoftmaxPlan(words, int(n_long.value), int(capacity.value), int(n_edges), int(channels),
+                       _offsets_fingerprint(offsets))
 
 
 def _plan_args(plan, offsets, edges, channels):
     if plan is None:
         return None
     _check(isinstance(plan, SoftmaxPlan) and plan.words.device == offsets.device
-           and plan.n_edges == edges and plan.channels == channels,
+           and plan.n_edges == edges and plan.channels == channels
+           and plan.fingerprint == _offsets_fingerprint(offsets),
            "segment softmax plan was built for another graph, device or channel count")
     return plan
 

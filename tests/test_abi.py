@@ -138,3 +138,27 @@ def test_launch_row_limit_hook():
         assert "segment count too large" in lib.dpa4k_last_error().decode()
     finally:
         assert lib.dpa4k_set_launch_row_limit(0) == binding.OK
+
+
+def test_softmax_plan_is_refused_for_other_offsets():
+    """A plan lists the long segments of the offsets it was built from; other offsets of the same size are refused."""
+    import torch
+
+    from bysj_amd.kernels import _C
+
+    offsets = torch.tensor([0, 3, 9, 10], dtype=torch.int64)
+    plan = _C.SoftmaxPlan(torch.zeros(4, dtype=torch.int32), 0, 96, 10, 8, _C._offsets_fingerprint(offsets))
+    assert _C._plan_args(plan, offsets, 10, 8) is plan
+    assert _C._plan_args(None, offsets, 10, 8) is None
+    same_values = offsets.clone()  # equal values, other storage
+    with pytest.raises(RuntimeError, match="another graph"):
+        _C._plan_args(plan, same_values, 10, 8)
+    with pytest.raises(RuntimeError, match="another graph"):
+        _C._plan_args(plan, offsets, 10, 4)  # another channel count
+    offsets[1] = 5  # an in-place write bumps the version counter
+    with pytest.raises(RuntimeError, match="another graph"):
+        _C._plan_args(plan, offsets, 10, 8)
+    with torch.inference_mode():
+        frozen = torch.tensor([0, 3, 9, 10], dtype=torch.int64)
+    frozen_plan = _C.SoftmaxPlan(plan.words, 0, 96, 10, 8, _C._offsets_fingerprint(frozen))
+    assert _C._plan_args(frozen_plan, frozen, 10, 8) is frozen_plan
