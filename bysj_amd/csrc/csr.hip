@@ -8,23 +8,29 @@
 //   count     one pass over the int64 keys in tiles of 8192: the range and
 //             sortedness checks (the reference's dst.min()/dst.max() test),
 //             and each tile's histogram of the coarse digit (the key's high
-//             bits, at most 1024 buckets) with LDS atomics;
-//   scan      one wave per bucket scans the bucket's counts over the tiles:
-//             every tile learns where its run of each bucket starts;
-//   scatter   each tile ranks its elements stably within their bucket (a
-//             wave matches equal digits with one ballot per digit bit and
-//             counts the lower lanes with mbcnt, so equal keys keep their
-//             order: wave by wave, round by round, lane by lane), sorts them
-//             in LDS and writes each bucket's run contiguously, packed as
-//             (index << fine_bits | fine digit) in 32 bits when it fits;
-//   finish    one workgroup per bucket: LDS histogram of the fine digit (the
-//             key's low bits) -> the offsets of the bucket's keys, then the
-//             same stable ranking, chunk by chunk -> `order`.  When the keys
-//             were already sorted (DeepMD's layout) the same launch instead
-//             takes the offsets from the boundaries of the sorted list and
-//             writes the identity order, and the count is the only pass.
+//             bits, at most 1024 buckets) with one LDS atomic per run of
+//             equal digits in a wave;
+//   scan      one workgroup per bucket scans the bucket's counts over the
+//             tiles: every tile learns where its run of each bucket starts;
+//   scatter   each wave of a tile's workgroup ranks its contiguous share of
+//             the tile stably by digit (a wave-level multisplit: one ballot
+//             per digit bit finds the lanes with equal digits, mbcnt counts
+//             the lower ones, and the group's leader advances the wave's LDS
+//             counter of the digit); the counts, scanned over the waves and
+//             the digits, place every element in the tile sorted by digit in
+//             LDS, and each bucket's run leaves contiguously, packed as
+//             (index << fine_bits | fine digit) in 32 bits when it fits.
+//             Tiles are dealt to XCDs in contiguous ranges, so the counts of
+//             neighbouring tiles share their L2;
+//   finish    one workgroup per bucket: the same multisplit by the fine digit
+//             (the key's low bits), chunk by chunk, gives the offsets of the
+//             bucket's keys and places its edge indices in `order`.  When
+//             the keys were already sorted (DeepMD's layout) the same launch
+//             instead takes the offsets from the boundaries of the sorted
+//             list and writes the identity order, and the count is the only
+//             pass.
 //
-// Keys of more than 21 bits take least-significant-digit passes of the same
+// Keys of more than 20 bits take least-significant-digit passes of the same
 // count / scan / scatter kernels instead ((key, index) pairs), then offsets
 // from the sorted keys.  The count pass records in the status word whether
 // the keys were sorted, and every later kernel reads it on the device, so the
@@ -41,16 +47,16 @@
 namespace dpa4k {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kGroupWaves = kThreads / 64;
-constexpr int kItems = 32;                             // elements per thread in a tile
+constexpr int kItems = 16;                             // elements per thread in a tile
 constexpr int kTile = kThreads * kItems;               // 8192 elements per count/scatter tile
 constexpr int kDigitBits = 10;                         // at most 1024 buckets per scatter pass
 constexpr int kMaxBuckets = 1 << kDigitBits;
 constexpr int kFineBitsMax = 10;                       // the two-level path: keys of up to 20 bits
 constexpr int kMaxFine = 1 << kFineBitsMax;
 constexpr int kLocalItems = 16;
-constexpr int kLocalChunk = kThreads * kLocalItems;    // 4096 elements per bucket-local round
+constexpr int kLocalChunk = kThreads * kLocalItems;    // 8192 elements per bucket-local round
 constexpr int64_t kShortGap = 64;                      // offsets a thread fills alone
 
 enum : int32_t { kFlagOutOfRange = 1, kFlagUnsorted = 2, kFlagSlotRange = 4, kFlagSlotShared = 8 };
@@ -137,81 +143,69 @@ __device__ __forceinline__ int64_t element_limit(int64_t n, const uint32_t* coun
 }
 
 // ---------------------------------------------------------------------------
-// block-local stable counting sort in LDS
+// wave-level multisplit
 // ---------------------------------------------------------------------------
 //
-// Elements live in LDS at padded positions (one spare word per 32, so that a
-// thread reading its 32 consecutive elements, or its 32 consecutive counters,
-// touches 32 different banks).  Each pass sorts them stably by kSubBits of the
-// digit: thread t owns the consecutive positions [t K, t K + K), counts them
-// in its own column of a [digit][thread] counter array (no other thread
-// touches the column), the array is scanned in digit-major order, and every
-// element moves to (its digit's count before this thread) + (its rank among
-// this thread's equal digits).  Least-significant sub-digit first, so after
-// the last pass the elements are ordered by the whole digit and, within a
-// digit, by their position before the sort.
-constexpr int kSubBits = 5;
-constexpr int kSubDigits = 1 << kSubBits;
-constexpr int kCounterWords = kSubDigits * kThreads + kSubDigits * kThreads / 32;
+// A wave ranks its 64 elements stably by a digit of up to kDigitBits bits.
+// One ballot per digit bit leaves every lane the mask of the active lanes
+// that share its digit; its rank among them is the number of lower lanes
+// (mbcnt), and the lowest of them, the group's leader, adds the group's size
+// to the wave's own LDS counter of the digit.  Only the leader touches a
+// digit's counter in a round and each wave has counters of its own, so the
+// value the leader reads back is the number of equal digits the wave met in
+// its earlier rounds: a lane's rank among the equal digits of the wave's
+// whole range is that value plus its rank in the round.
 
-__device__ __forceinline__ int padded(int position) { return position + (position >> 5); }
-
-template <typename E>
-__device__ __forceinline__ uint32_t digit_of(E element, int shift, uint32_t mask) {
-  return static_cast<uint32_t>(element >> shift) & mask;
+template <int kBits>
+__device__ __forceinline__ uint64_t lanes_with_digit(uint32_t digit, bool active) {
+  uint64_t same = __ballot(active);
+#pragma unroll
+  for (int i = 0; i < kBits; ++i) {
+    const bool set = ((digit >> i) & 1u) != 0u;
+    const uint64_t with = __ballot(set);
+    same &= set ? with : ~with;
+  }
+  return active ? same : 0ull;
 }
 
-template <typename E, int K>
-__device__ void block_stable_sort(E* buffer, int n, int shift, int bits, uint32_t* counters, uint32_t* wave_totals) {
-  const int t = threadIdx.x;
-  for (int done = 0; done < bits; done += kSubBits) {
-    const int pass_bits = bits - done < kSubBits ? bits - done : kSubBits;
-    const int pass_shift = shift + done;
-    const int digits = 1 << pass_bits;
-    const uint32_t mask = static_cast<uint32_t>(digits - 1);
-    E element[K];
-    uint32_t rank[K / 4];  // ranks below K <= 32: four per word
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// rank[r] = the rank of this lane's round-r element among the equal digits
+// the wave meets before it (its earlier rounds, then the lower lanes of round
+// r); digit(r) has at most kBits bits, `valid` has bit r for an element in
+// round r, and `counter` is the wave's [digit] array, advanced by the call.
+// Every lane of the wave must call it.
+template <int kBits, int kRounds, typename DigitOf>
+__device__ __forceinline__ void wave_split_ranks(DigitOf digit, uint32_t valid, uint32_t* counter,
+                                                 uint32_t (&rank)[kRounds]) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < K; ++i) {
-      const int position = t * K + i;
-      element[i] = position < n ? buffer[padded(position)] : E(0);
-    }
-    for (int d = 0; d < digits; ++d) counters[padded(d * kThreads + t)] = 0u;
+  for (int r = 0; r < kRounds; ++r) {
+    const bool active = ((valid >> r) & 1u) != 0u;
+    const uint64_t same = lanes_with_digit<kBits>(digit(r), active);
+    const uint32_t below = lanes_below(same);
+    uint32_t before = 0u;
+    if (active && below == 0u) before = atomicAdd(&counter[digit(r)], static_cast<uint32_t>(__popcll(same)));
+    const int leader = active ? __builtin_ctzll(same) : lane;
+    rank[r] = static_cast<uint32_t>(__shfl(static_cast<int>(before), leader, 64)) + below;
+  }
+}
+
+// In place over digits [0, digits): the per-wave counts become the counts of
+// the earlier waves, and `total[d]` gets the digit's count over all waves.
+__device__ __forceinline__ void wave_prefix(uint32_t* wave_count, int stride, int digits, uint32_t* total) {
+  for (int d = threadIdx.x; d < digits; d += kThreads) {
+    uint32_t running = 0u;
 #pragma unroll
-    for (int i = 0; i < K / 4; ++i) rank[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if (t * K + i < n) {
-        const int slot = padded(static_cast<int>(digit_of(element[i], pass_shift, mask)) * kThreads + t);
-        const uint32_t count = counters[slot];
-        rank[i / 4] |= count << (8 * (i % 4));
-        counters[slot] = count + 1u;
-      }
+    for (int w = 0; w < kGroupWaves; ++w) {
+      const uint32_t count = wave_count[w * stride + d];
+      wave_count[w * stride + d] = running;
+      running += count;
     }
-    __syncthreads();
-    // exclusive scan of counters[digit][thread] in flat order; thread t scans
-    // the flat range [t * digits, (t + 1) * digits)
-    const int first = t * digits;
-    uint32_t sum = 0;
-    for (int j = 0; j < digits; ++j) sum += counters[padded(first + j)];
-    uint32_t total;
-    uint32_t running = block_exclusive_scan(sum, wave_totals, total);
-    for (int j = 0; j < digits; ++j) {
-      const int slot = padded(first + j);
-      const uint32_t value = counters[slot];
-      counters[slot] = running;
-      running += value;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if (t * K + i < n) {
-        const uint32_t digit = digit_of(element[i], pass_shift, mask);
-        const uint32_t own = (rank[i / 4] >> (8 * (i % 4))) & 0xffu;
-        buffer[padded(static_cast<int>(counters[padded(static_cast<int>(digit) * kThreads + t)] + own))] = element[i];
-      }
-    }
-    __syncthreads();
+    total[d] = running;
   }
 }
 
@@ -223,8 +217,8 @@ __global__ __launch_bounds__(64) void clear_word_kernel(int32_t* __restrict__ wo
   if (threadIdx.x == 0) *word = 0;
 }
 
-// Tile `blockIdx.x` of the keys (the caller's int64 keys, or the uint32 keys
-// of an earlier pass): element q of the tile is q = 256 r + thread for
+// A tile of the keys (the caller's int64 keys, or the uint32 keys of an
+// earlier pass): element q of the tile is q = kThreads r + thread for
 // r < kItems, so each wave's loads cover 64 consecutive elements.
 struct TileKeys {
   uint32_t key[kItems];
@@ -325,7 +319,10 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(const int64_t* __r
   if (gate_closed(status, gate)) return;
   const int64_t limit = element_limit(n, count_limit);
   for (int b = threadIdx.x; b < buckets; b += kThreads) histogram[b] = 0u;
-  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kTile;
+  // tiles dealt to XCDs in contiguous ranges: a line of a bucket's counts
+  // (consecutive tiles) is written, and later read, within one L2
+  const unsigned int tile_index = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t tile_base = static_cast<int64_t>(tile_index) * kTile;
   const uint32_t digit_mask = (1u << bits) - 1u;
   TileKeys tile;
   int32_t local = 0;
@@ -334,10 +331,22 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(const int64_t* __r
   else
     load_keys64<kCheck>(keys64, tile_base, limit, n_nodes, tile, local, first_of_wave, first_ok);
   __syncthreads();
-  // plain LDS atomics: a histogram needs no ranks
+  // LDS atomics, one per run of equal digits among a round's 64 consecutive
+  // elements (sorted or clustered keys would otherwise queue on one counter)
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int r = 0; r < kItems; ++r)
-    if ((tile.ok >> r) & 1u) atomicAdd(&histogram[(tile.key[r] >> shift) & digit_mask], 1u);
+  for (int r = 0; r < kItems; ++r) {
+    const bool valid = ((tile.ok >> r) & 1u) != 0u;
+    const uint32_t digit = (tile.key[r] >> shift) & digit_mask;
+    const uint32_t previous = static_cast<uint32_t>(__shfl_up(static_cast<int>(digit), 1, 64));
+    const bool previous_valid = __shfl_up(valid ? 1 : 0, 1, 64) != 0;
+    const bool head = valid && (lane == 0 || !previous_valid || previous != digit);
+    // a run ends at the next head or invalid element
+    const uint64_t stops = __ballot(head || !valid);
+    const uint64_t after = stops & ~((2ull << lane) - 1ull);
+    const int next = after == 0ull ? 64 : __builtin_ctzll(after);
+    if (head) atomicAdd(&histogram[digit], static_cast<uint32_t>(next - lane));
+  }
   if constexpr (kCheck) {
     const int32_t found = (__syncthreads_or(local & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
                           (__syncthreads_or(local & kFlagUnsorted) ? kFlagUnsorted : 0);
@@ -347,7 +356,7 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(const int64_t* __r
   }
   __syncthreads();
   for (int b = threadIdx.x; b < buckets; b += kThreads)
-    counts[static_cast<int64_t>(b) * tiles + blockIdx.x] = histogram[b];
+    counts[static_cast<int64_t>(b) * tiles + tile_index] = histogram[b];
 }
 
 // counts[b][t] -> the number of bucket-b elements in tiles before t, and
@@ -370,18 +379,15 @@ __global__ __launch_bounds__(kThreads) void row_scan_kernel(uint32_t* __restrict
   if (threadIdx.x == 0) bucket_total[blockIdx.x] = running;
 }
 
-// Elements of the scatter's LDS sort.  32-bit: key in bits [0, 19), position
-// in the tile in [19, 32) (keys of at most 19 bits); 64-bit: key in the high
-// word, the position (or, for pairs, the edge index) in the low word.
-// Elements that are out of range take the largest key, which sorts them
-// after every in-range element of the tile's last bucket.
+// Elements of the scatter's sorted tile in LDS.  32-bit: key in bits
+// [0, 19), position in the tile in [19, 32) (keys of at most 19 bits);
+// 64-bit: key in the high word, the position (or, for pairs, the edge index)
+// in the low word.
 template <typename E>
 struct ElementCodec;
 
 template <>
 struct ElementCodec<uint32_t> {
-  static constexpr int kKeyShift = 0;
-  static constexpr uint32_t kBadKey = (1u << 19) - 1u;
   __device__ static uint32_t make(uint32_t key, uint32_t low) { return key | (low << 19); }
   __device__ static uint32_t key(uint32_t e) { return e & ((1u << 19) - 1u); }
   __device__ static uint32_t low(uint32_t e) { return e >> 19; }
@@ -389,8 +395,6 @@ struct ElementCodec<uint32_t> {
 
 template <>
 struct ElementCodec<uint64_t> {
-  static constexpr int kKeyShift = 32;
-  static constexpr uint32_t kBadKey = 0xffffffffu;
   __device__ static uint64_t make(uint32_t key, uint32_t low) { return (static_cast<uint64_t>(key) << 32) | low; }
   __device__ static uint32_t key(uint64_t e) { return static_cast<uint32_t>(e >> 32); }
   __device__ static uint32_t low(uint64_t e) { return static_cast<uint32_t>(e); }
@@ -416,82 +420,91 @@ struct PairsOut {
   }
 };
 
+constexpr int kScatterSpan = kTile / kGroupWaves;  // elements of a tile per wave
+constexpr int kScatterRounds = kScatterSpan / 64;
+
 // Stable scatter of one tile by digit: each element goes to
 //   bucket_start[b] + (elements of b in earlier tiles) + (its rank within b in this tile).
-// The tile is loaded (coalesced) into LDS, sorted there stably by the digit
-// (block_stable_sort), and each bucket's run leaves as one contiguous write.
+// Wave w takes the tile's elements [w S, (w + 1) S) (S = kScatterSpan), 64
+// consecutive ones a round, and ranks them with the wave-level multisplit.
+// The per-wave digit counts, scanned over the waves and then over the
+// digits, give every element its place in the tile sorted stably by digit;
+// it takes that place in LDS, and the sorted tile leaves in order, each
+// bucket's run as one contiguous write.  Out-of-range keys take no place.
 // Every block scans the bucket totals for itself; block 0 also publishes the
 // bucket starts (and the count of in-range elements) for the next launch.
 template <typename E, bool kPairs, typename Out>
-__global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
+__global__ __launch_bounds__(kThreads, 4) void tile_scatter_kernel(
     const int64_t* __restrict__ keys64, const uint32_t* __restrict__ keys32, const uint32_t* __restrict__ index32,
     int64_t n, const uint32_t* count_limit, uint64_t n_nodes, int shift, int bits, int buckets, int64_t tiles,
     const uint32_t* __restrict__ counts, const uint32_t* __restrict__ bucket_total,
     uint32_t* __restrict__ bucket_start, uint32_t* __restrict__ valid_count, int64_t* __restrict__ offsets_last,
     Out out, const int32_t* __restrict__ status, int gate) {
   using Codec = ElementCodec<E>;
-  __shared__ E elements[kTile + kTile / 32];
-  __shared__ uint32_t counters[kCounterWords];
+  static_assert(kGroupWaves * kMaxBuckets * 4 <= kTile * sizeof(E), "the wave counters fit the tile's space");
+  // the wave counters, then (once every place is known) the sorted tile
+  __shared__ E sorted[kTile];
+  uint32_t* wave_count = reinterpret_cast<uint32_t*>(sorted);
   __shared__ uint32_t tile_start[kMaxBuckets];
   __shared__ uint32_t shift_to_target[kMaxBuckets];
   __shared__ uint32_t wave_totals[kGroupWaves];
   if (gate_closed(status, gate)) return;
   const int64_t limit = element_limit(n, count_limit);
   const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
   const uint32_t digit_mask = (1u << bits) - 1u;
-  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kTile;
+  const unsigned int tile_index = xcd_block(blockIdx.x, gridDim.x);  // as in the count pass
+  const int64_t tile_base = static_cast<int64_t>(tile_index) * kTile;
   const int n_tile = tile_elements(tile_base, limit);
-  for (int b = t; b < buckets; b += kThreads) tile_start[b] = 0u;
+  for (int i = t; i < kGroupWaves * kMaxBuckets; i += kThreads) wave_count[i] = 0u;
+  const int first = wave * kScatterSpan + lane;  // the lane's element of round 0
+  // the tile's column of counts and the bucket totals, loaded early (used after the ranking)
+  constexpr int kPerThread = kMaxBuckets / kThreads;
+  uint32_t earlier[kPerThread], total[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int b = t + j * kThreads;
+    earlier[j] = b < buckets ? counts[static_cast<int64_t>(b) * tiles + tile_index] : 0u;
+    total[j] = b < buckets ? bucket_total[b] : 0u;
+  }
 
-  // the tile into LDS, in order; out-of-range keys become the largest key
+  uint32_t key[kScatterRounds];
+  uint32_t low[kPairs ? kScatterRounds : 1];
+  uint32_t ok = 0u;  // bit r: the round-r element exists and is in range
   if constexpr (kPairs) {
     const BufferView key_view = buffer_view(keys32 + (n_tile > 0 ? tile_base : 0), static_cast<int64_t>(n_tile) * 4);
     const BufferView index_view = buffer_view(index32 + (n_tile > 0 ? tile_base : 0), static_cast<int64_t>(n_tile) * 4);
-    __syncthreads();  // tile_start is zero
-    for (int half = 0; half < 2; ++half) {
-      constexpr int kHalf = kItems / 2;
-      uint32_t key[kHalf], index[kHalf];
 #pragma unroll
-      for (int r = 0; r < kHalf; ++r) {
-        const uint32_t q = static_cast<uint32_t>((half * kHalf + r) * kThreads + t);
-        key[r] = load_u32(key_view, q * 4u);
-        index[r] = load_u32(index_view, q * 4u);
-      }
-#pragma unroll
-      for (int r = 0; r < kHalf; ++r) {
-        const int q = (half * kHalf + r) * kThreads + t;
-        if (q < n_tile) {
-          elements[padded(q)] = Codec::make(key[r], index[r]);
-          atomicAdd(&tile_start[(key[r] >> shift) & digit_mask], 1u);
-        }
-      }
+    for (int r = 0; r < kScatterRounds; ++r) {
+      const int q = first + 64 * r;
+      key[r] = load_u32(key_view, static_cast<uint32_t>(q) * 4u);
+      low[r] = load_u32(index_view, static_cast<uint32_t>(q) * 4u);
+      ok |= q < n_tile ? (1u << r) : 0u;
     }
   } else {
     const BufferView view = buffer_view(keys64 + (n_tile > 0 ? tile_base : 0), static_cast<int64_t>(n_tile) * 8);
-    __syncthreads();  // tile_start is zero
-    for (int half = 0; half < 2; ++half) {
-      constexpr int kHalf = kItems / 2;
-      int64_t raw[kHalf];
 #pragma unroll
-      for (int r = 0; r < kHalf; ++r)
-        raw[r] = load_i64(view, static_cast<uint32_t>((half * kHalf + r) * kThreads + t) * 8u);
-#pragma unroll
-      for (int r = 0; r < kHalf; ++r) {
-        const int q = (half * kHalf + r) * kThreads + t;
-        if (q < n_tile) {
-          const bool in = static_cast<uint64_t>(raw[r]) < n_nodes;
-          const uint32_t key = in ? static_cast<uint32_t>(raw[r]) : Codec::kBadKey;
-          elements[padded(q)] = Codec::make(key, static_cast<uint32_t>(q));
-          if (in) atomicAdd(&tile_start[(key >> shift) & digit_mask], 1u);
-        }
-      }
+    for (int r = 0; r < kScatterRounds; ++r) {
+      const int q = first + 64 * r;
+      const int64_t raw = load_i64(view, static_cast<uint32_t>(q) * 8u);
+      key[r] = static_cast<uint32_t>(raw);
+      ok |= q < n_tile && static_cast<uint64_t>(raw) < n_nodes ? (1u << r) : 0u;
     }
   }
+  __syncthreads();  // the wave counters are zero
+
+  const auto digit = [&](int r) { return (key[r] >> shift) & digit_mask; };
+  uint32_t rank[kScatterRounds];
+  uint32_t* counter = wave_count + wave * kMaxBuckets;
+  wave_split_ranks<kDigitBits>(digit, ok, counter, rank);
   __syncthreads();
-  block_stable_sort<E, kItems>(elements, n_tile, Codec::kKeyShift + shift, bits, counters, wave_totals);
+  wave_prefix(wave_count, kMaxBuckets, buckets, tile_start);
 
   // bucket starts: every block scans the bucket totals (block 0 publishes them)
-  for (int b = t; b < buckets; b += kThreads) shift_to_target[b] = bucket_total[b];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j)
+    if (t + j * kThreads < buckets) shift_to_target[t + j * kThreads] = total[j];
   __syncthreads();
   const uint32_t in_range_total = lds_exclusive_scan(shift_to_target, buckets, 0u, wave_totals);
   if (blockIdx.x == 0) {
@@ -503,17 +516,34 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     }
   }
   const uint32_t in_tile = lds_exclusive_scan(tile_start, buckets, 0u, wave_totals);
-  for (int b = t; b < buckets; b += kThreads)
-    shift_to_target[b] += counts[static_cast<int64_t>(b) * tiles + blockIdx.x] - tile_start[b];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int b = t + j * kThreads;
+    if (b < buckets) shift_to_target[b] += earlier[j] - tile_start[b];
+  }
+  // places in the sorted tile, then (the counters read) the elements move there
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r)
+    rank[r] += ((ok >> r) & 1u) ? tile_start[digit(r)] + counter[digit(r)] : 0u;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r) {
+    if ((ok >> r) & 1u) {
+      if constexpr (kPairs)
+        sorted[rank[r]] = Codec::make(key[r], low[r]);
+      else
+        sorted[rank[r]] = Codec::make(key[r], static_cast<uint32_t>(first + 64 * r));
+    }
+  }
   __syncthreads();
   // each bucket's run: sorted position p goes to shift_to_target[b] + p
   for (int p = t; p < static_cast<int>(in_tile); p += kThreads) {
-    const E e = elements[padded(p)];
-    const uint32_t key = Codec::key(e);
-    const uint32_t target = shift_to_target[(key >> shift) & digit_mask] + static_cast<uint32_t>(p);
+    const E e = sorted[p];
+    const uint32_t k = Codec::key(e);
+    const uint32_t target = shift_to_target[(k >> shift) & digit_mask] + static_cast<uint32_t>(p);
     const uint32_t index = kPairs ? Codec::low(e) : static_cast<uint32_t>(tile_base) + Codec::low(e);
     // unreachable past the element count: the count pass saw the same elements
-    if (static_cast<int64_t>(target) < limit) out.store(target, key, index);
+    if (static_cast<int64_t>(target) < limit) out.store(target, k, index);
   }
 }
 
@@ -577,21 +607,28 @@ __global__ __launch_bounds__(kThreads) void offsets_from_sorted_kernel(const K* 
 }
 
 // Last launch of the two-level path.  Unsorted keys: one workgroup per bucket
-// of 2^fine_bits keys; the fine-digit histogram gives the offsets of the
-// bucket's keys, and each chunk of the bucket, sorted stably by the fine
-// digit in LDS, places its edge indices in `order`.  Sorted keys: every
-// workgroup strides over the keys themselves for the offsets and the identity
-// order.
-template <typename P>
-__global__ __launch_bounds__(kThreads) void finish_kernel(const P* __restrict__ packed,
+// of 2^fine_bits keys.  The fine-digit histogram gives the offsets of the
+// bucket's keys, and each chunk of the bucket, ranked by the fine digit with
+// the wave-level multisplit (wave w takes the chunk's elements
+// [w S, (w + 1) S), S = kLocalChunk / 4) and sorted stably in LDS, places its
+// edge indices in `order`.  A bucket of one chunk takes its histogram from the
+// ranking's counts; a longer one counts first in a pass of its own.  Sorted
+// keys: every workgroup strides over the keys themselves for the offsets and
+// the identity order.
+template <typename P, int kFineMatch>
+__global__ __launch_bounds__(kThreads, sizeof(P) == 4 ? 4 : 2) void finish_kernel(const P* __restrict__ packed,
                                                           const uint32_t* __restrict__ bucket_start, int buckets,
                                                           int fine_bits, const int64_t* __restrict__ keys,
                                                           int64_t n_edges, int64_t n_nodes,
                                                           int64_t* __restrict__ order,
                                                           int64_t* __restrict__ offsets,
                                                           const int32_t* __restrict__ status) {
-  __shared__ P elements[kLocalChunk + kLocalChunk / 32];
-  __shared__ uint32_t counters[kCounterWords];
+  constexpr int kSpan = kLocalChunk / kGroupWaves;
+  constexpr int kRounds = kSpan / 64;
+  static_assert(kGroupWaves * kMaxFine * 4 <= kLocalChunk * sizeof(P), "the wave counters fit the chunk's space");
+  // the wave counters, then (once every place is known) the sorted chunk
+  __shared__ P sorted[kLocalChunk];
+  uint32_t* wave_count = reinterpret_cast<uint32_t*>(sorted);
   __shared__ uint32_t fine_base[kMaxFine];
   __shared__ uint32_t chunk_start[kMaxFine];
   __shared__ uint32_t wave_totals[kGroupWaves];
@@ -603,78 +640,98 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const P* __restrict__ 
   const int b = blockIdx.x;
   if (b >= buckets) return;
   const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
   const int64_t start = bucket_start[b];
   const int64_t end = bucket_start[b + 1];
   const int64_t count = end - start;
   const int fines = 1 << fine_bits;
   const P fine_mask = static_cast<P>(fines - 1);
-
-  // the bucket's fine-digit histogram -> offsets of its keys
+  const bool one_chunk = count <= kLocalChunk;
+  for (int i = t; i < kGroupWaves * kMaxFine; i += kThreads) wave_count[i] = 0u;
   for (int f = t; f < fines; f += kThreads) fine_base[f] = 0u;
   __syncthreads();
-  for (int64_t first = 0; first < count; first += kLocalChunk) {
-    // a view per chunk keeps every offset small, however long the bucket
-    const int in_chunk = static_cast<int>(count - first < kLocalChunk ? count - first : kLocalChunk);
-    const BufferView view = buffer_view(packed + start + first, static_cast<int64_t>(in_chunk) * sizeof(P));
-    P values[kLocalItems];
-#pragma unroll
-    for (int r = 0; r < kLocalItems; ++r) {
-      const uint32_t offset = static_cast<uint32_t>(r * kThreads + t) * sizeof(P);
-      if constexpr (sizeof(P) == 8)
-        values[r] = static_cast<P>(load_i64(view, offset));
-      else
-        values[r] = load_u32(view, offset);
-    }
-#pragma unroll
-    for (int r = 0; r < kLocalItems; ++r)
-      if (r * kThreads + t < in_chunk) atomicAdd(&fine_base[static_cast<uint32_t>(values[r] & fine_mask)], 1u);
-  }
-  __syncthreads();
-  lds_exclusive_scan(fine_base, fines, static_cast<uint32_t>(start), wave_totals);
-  for (int f = t; f < fines; f += kThreads) {
-    const int64_t key = (static_cast<int64_t>(b) << fine_bits) + f;
-    if (key < n_nodes) offsets[key] = fine_base[f];
-  }
-  if (order == nullptr) return;
 
-  for (int64_t first = 0; first < count; first += kLocalChunk) {
-    const int in_chunk = static_cast<int>(count - first < kLocalChunk ? count - first : kLocalChunk);
+  const auto load_chunk = [&](int64_t first, int in_chunk, P (&values)[kRounds]) {
+    // a view per chunk keeps every offset small, however long the bucket
     const BufferView view = buffer_view(packed + start + first, static_cast<int64_t>(in_chunk) * sizeof(P));
-    for (int f = t; f < fines; f += kThreads) chunk_start[f] = 0u;
-    P values[kLocalItems];
 #pragma unroll
-    for (int r = 0; r < kLocalItems; ++r) {
-      const uint32_t offset = static_cast<uint32_t>(r * kThreads + t) * sizeof(P);
+    for (int r = 0; r < kRounds; ++r) {
+      const uint32_t offset = static_cast<uint32_t>(wave * kSpan + 64 * r + lane) * sizeof(P);
       if constexpr (sizeof(P) == 8)
         values[r] = static_cast<P>(load_i64(view, offset));
       else
         values[r] = load_u32(view, offset);
     }
-    __syncthreads();
+  };
+  const auto write_offsets = [&]() {
+    for (int f = t; f < fines; f += kThreads) {
+      const int64_t key = (static_cast<int64_t>(b) << fine_bits) + f;
+      if (key < n_nodes) offsets[key] = fine_base[f];
+    }
+  };
+
+  if (!one_chunk) {
+    // the bucket's fine-digit histogram -> offsets of its keys
+    for (int64_t first = 0; first < count; first += kLocalChunk) {
+      const int in_chunk = static_cast<int>(count - first < kLocalChunk ? count - first : kLocalChunk);
+      P values[kRounds];
+      load_chunk(first, in_chunk, values);
 #pragma unroll
-    for (int r = 0; r < kLocalItems; ++r) {
-      const int q = r * kThreads + t;
-      if (q < in_chunk) {
-        elements[padded(q)] = values[r];
-        atomicAdd(&chunk_start[static_cast<uint32_t>(values[r] & fine_mask)], 1u);
-      }
+      for (int r = 0; r < kRounds; ++r)
+        if (wave * kSpan + 64 * r + lane < in_chunk)
+          atomicAdd(&fine_base[static_cast<uint32_t>(values[r] & fine_mask)], 1u);
     }
     __syncthreads();
-    block_stable_sort<P, kLocalItems>(elements, in_chunk, 0, fine_bits, counters, wave_totals);
+    lds_exclusive_scan(fine_base, fines, static_cast<uint32_t>(start), wave_totals);
+    write_offsets();
+    if (order == nullptr) return;
+  }
+
+  // an empty bucket takes one (empty) round too: it still writes its keys' offsets
+  for (int64_t first = 0; first < count || first == 0; first += kLocalChunk) {
+    const int in_chunk = static_cast<int>(count - first < kLocalChunk ? count - first : kLocalChunk);
+    P values[kRounds];
+    uint32_t rank[kRounds];
+    load_chunk(first, in_chunk, values);
+    const auto fine = [&](int r) { return static_cast<uint32_t>(values[r] & fine_mask); };
+    uint32_t valid = 0u;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) valid |= wave * kSpan + 64 * r + lane < in_chunk ? (1u << r) : 0u;
+    uint32_t* counter = wave_count + wave * kMaxFine;
+    wave_split_ranks<kFineMatch>(fine, valid, counter, rank);
+    __syncthreads();
+    wave_prefix(wave_count, kMaxFine, fines, chunk_start);
+    __syncthreads();
     lds_exclusive_scan(chunk_start, fines, 0u, wave_totals);
+    if (one_chunk) {
+      // the chunk is the bucket: its digit counts are the histogram
+      for (int f = t; f < fines; f += kThreads) fine_base[f] = static_cast<uint32_t>(start) + chunk_start[f];
+      __syncthreads();
+      write_offsets();
+      if (order == nullptr) return;
+    }
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) rank[r] += ((valid >> r) & 1u) ? chunk_start[fine(r)] + counter[fine(r)] : 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      if ((valid >> r) & 1u) sorted[rank[r]] = values[r];
+    __syncthreads();
     for (int p = t; p < in_chunk; p += kThreads) {
-      const P e = elements[padded(p)];
+      const P e = sorted[p];
       const uint32_t f = static_cast<uint32_t>(e & fine_mask);
       const int64_t target = static_cast<int64_t>(fine_base[f]) + (p - static_cast<int64_t>(chunk_start[f]));
       // unreachable outside the bucket: its fine digits were counted from the same elements
       if (target >= start && target < end) order[target] = static_cast<int64_t>(e >> fine_bits);
     }
     __syncthreads();
-    // the next chunk's elements of digit f follow this chunk's
+    // the next chunk's elements of digit f follow this chunk's; the wave counters restart
     for (int f = t; f < fines; f += kThreads) {
       const uint32_t next = f + 1 < fines ? chunk_start[f + 1] : static_cast<uint32_t>(in_chunk);
       fine_base[f] += next - chunk_start[f];
     }
+    for (int i = t; i < kGroupWaves * kMaxFine; i += kThreads) wave_count[i] = 0u;
     __syncthreads();
   }
 }
@@ -853,20 +910,28 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
           s.bucket_total, s.bucket_start, nullptr, offsets + plan.n_nodes, out, status, kIfUnsorted);
       return launched("tile_scatter_kernel");
     };
+    // the fine digits are matched over 6 bits when they fit, else over all kFineBitsMax
+    const auto finish = [&](auto element) {
+      using P = decltype(element);
+      const P* packed = static_cast<const P*>(s.packed);
+      if (plan.fine_bits <= 6)
+        finish_kernel<P, 6><<<finish_blocks, kThreads, 0, stream>>>(packed, s.bucket_start, buckets, plan.fine_bits,
+                                                                    keys, plan.n_edges, plan.n_nodes, order, offsets,
+                                                                    status);
+      else
+        finish_kernel<P, kFineBitsMax><<<finish_blocks, kThreads, 0, stream>>>(
+            packed, s.bucket_start, buckets, plan.fine_bits, keys, plan.n_edges, plan.n_nodes, order, offsets,
+            status);
+      return launched("finish_kernel");
+    };
     if (plan.wide) {
       const PackedOut<uint64_t> packed{static_cast<uint64_t*>(s.packed), plan.fine_bits};
       if (int code = plan.narrow_elements ? scatter(packed, uint32_t(0)) : scatter(packed, uint64_t(0))) return code;
-      finish_kernel<uint64_t><<<finish_blocks, kThreads, 0, stream>>>(
-          static_cast<const uint64_t*>(s.packed), s.bucket_start, buckets, plan.fine_bits, keys, plan.n_edges,
-          plan.n_nodes, order, offsets, status);
-    } else {
-      const PackedOut<uint32_t> packed{static_cast<uint32_t*>(s.packed), plan.fine_bits};
-      if (int code = plan.narrow_elements ? scatter(packed, uint32_t(0)) : scatter(packed, uint64_t(0))) return code;
-      finish_kernel<uint32_t><<<finish_blocks, kThreads, 0, stream>>>(
-          static_cast<const uint32_t*>(s.packed), s.bucket_start, buckets, plan.fine_bits, keys, plan.n_edges,
-          plan.n_nodes, order, offsets, status);
+      return finish(uint64_t(0));
     }
-    return launched("finish_kernel");
+    const PackedOut<uint32_t> packed{static_cast<uint32_t*>(s.packed), plan.fine_bits};
+    if (int code = plan.narrow_elements ? scatter(packed, uint32_t(0)) : scatter(packed, uint64_t(0))) return code;
+    return finish(uint32_t(0));
   }
 
   // least significant digit first; pass 0 reads the caller's keys and checks them
