@@ -11,7 +11,8 @@
 // float atomic per (row, column); here each wave keeps per-column partials
 // for its fixed set of rows (two rows loaded per round), the four waves of a
 // workgroup add theirs in LDS, the workgroup partials go to the workspace and
-// one wave per group of columns sums them -- every order fixed.
+// a workgroup per 64 columns sums them (its waves split the rows, each load
+// reading 256 contiguous bytes) -- every order fixed.
 #include <mutex>
 #include <vector>
 
@@ -206,26 +207,45 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_backward_kernel(
   }
 }
 
-// grad_scale[w] = sum over the workgroup partial rows, one wave per group of
-// V columns: lane l adds rows l, l + 64, ... in order, then a fixed butterfly.
-template <int V>
-__global__ __launch_bounds__(kBlock) void partial_columns_kernel(const float* __restrict__ partial, int64_t n,
-                                                                 int64_t width, float* __restrict__ grad_scale) {
-  const int64_t group = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (group * V >= width) return;
+// grad_scale[w] = sum over the workgroup partial rows [n, W]: one workgroup
+// of kColumnWaves waves per 64 columns, lane l on column 64 b + l.  Wave k
+// adds, in order, the rows of its share [k p, (k + 1) p) (p = n / kColumnWaves
+// rounded up), so each of its loads reads 256 consecutive bytes of one row;
+// the waves' sums are then added in wave order.
+constexpr int kColumnWaves = 16;
+
+__global__ __launch_bounds__(kColumnWaves * 64) void partial_columns_kernel(const float* __restrict__ partial,
+                                                                            int64_t n, int64_t width,
+                                                                            float* __restrict__ grad_scale) {
+  __shared__ float wave_sum[kColumnWaves][64];
   const int lane = threadIdx.x & 63;
-  const int64_t column = group * V;
-  fvec<V> sum;
+  const int wave = threadIdx.x >> 6;
+  const int64_t column = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const int64_t per = (n + kColumnWaves - 1) / kColumnWaves;
+  const int64_t first = wave * per;
+  const int64_t last = first + per < n ? first + per : n;
+  float sum = 0.0f;
+  if (column < width) {
+    const float* source = partial + column;
+    int64_t r = first;
+    // eight loads in flight, added in row order
+    for (; r + 8 <= last; r += 8) {
+      float value[8];
 #pragma unroll
-  for (int i = 0; i < V; ++i) sum.v[i] = 0.0f;
-  for (int64_t r = lane; r < n; r += 64) {
-    const fvec<V> value = load_vec<V>(partial + r * width + column);
+      for (int i = 0; i < 8; ++i) value[i] = source[(r + i) * width];
 #pragma unroll
-    for (int i = 0; i < V; ++i) sum.v[i] = sum.v[i] + value.v[i];
+      for (int i = 0; i < 8; ++i) sum = sum + value[i];
+    }
+    for (; r < last; ++r) sum = sum + source[r * width];
   }
+  wave_sum[wave][lane] = sum;
+  __syncthreads();
+  if (wave == 0 && column < width) {
+    float total = 0.0f;
 #pragma unroll
-  for (int i = 0; i < V; ++i) sum.v[i] = group_sum<64>(sum.v[i]);
-  if (lane == 0) store_vec<V>(grad_scale + column, sum);
+    for (int k = 0; k < kColumnWaves; ++k) total = total + wave_sum[k][lane];
+    grad_scale[column] = total;
+  }
 }
 
 // Streaming grad_x for wide rows: two passes over the row.
@@ -443,11 +463,8 @@ int rmsnorm_backward(const float* grad, const float* x, const float* scale, cons
                : launch_backward<1>(cpl, grid, grad, x, scale, inverse_rms, grad_x, partial, rows,
                                     width, stream);
   if (s) return s;
-  const int64_t groups = vec4 ? width / 4 : width;
-  if (vec4 && aligned16(grad_scale))
-    partial_columns_kernel<4><<<blocks_for(groups, kWaves), kBlock, 0, stream>>>(partial, grid, width, grad_scale);
-  else
-    partial_columns_kernel<1><<<blocks_for(width, kWaves), kBlock, 0, stream>>>(partial, grid, width, grad_scale);
+  partial_columns_kernel<<<static_cast<unsigned int>((width + 63) / 64), kColumnWaves * 64, 0, stream>>>(
+      partial, grid, width, grad_scale);
   return launched("partial_columns_kernel");
 }
 
