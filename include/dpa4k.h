@@ -327,9 +327,10 @@ int dpa4k_gie_zonal_scatter_forward_csr(const float* zonal, const float* radial,
  * with pre the unnormalised destination sum (recomputed, not saved).  Any
  * of the three outputs may be NULL.  grad_radial is written in full (zeros
  * for unreferenced slots).  slot_info: dpa4k_gie_group's host_info for this
- * radial_slot, or 0; bit 2 (distinct slots) or bits 16..23 <= 8 (shared
- * slots, C % 16 == 0) select register-only kernels, anything else the
- * general one.  It must describe radial_slot truthfully. */
+ * radial_slot, or 0; bit 2 (distinct slots) or bits 16..23 in [2, 8]
+ * (shared slots, C = 8 * k with k a power of two, k <= 16 and S * k <= 64)
+ * select register-only kernels, anything else the general one.  It must
+ * describe radial_slot truthfully. */
 int dpa4k_gie_zonal_scatter_backward_csr(
     const float* grad_output, const float* zonal, const float* radial,
     const int64_t* offsets, const int64_t* order, const int64_t* radial_slot,
