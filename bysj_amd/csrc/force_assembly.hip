@@ -352,7 +352,7 @@ unsigned int grid_stride_blocks(int64_t items) {
   return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > 8192 ? 8192 : wanted));
 }
 
-constexpr int64_t kPlanTile = 4096;   // edges per pass-1 tile
+constexpr int64_t kPlanTile = 8192;   // edges per pass-1 tile
 constexpr int64_t kPlanBuckets = 256;  // most source-atom buckets
 
 // Tiles and buckets of a graph: `bucket_atoms` consecutive atoms per bucket.

@@ -239,7 +239,7 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
  * entry points above, bit for bit).  A plan of one source grouping
  * (src_offsets + src_order) is built once per graph, on `stream` without a
  * host synchronisation: the atoms fall into <= 256 contiguous buckets and
- * the edges into tiles of 4096, and the plan records where each edge's row
+ * the edges into tiles of 8192, and the plan records where each edge's row
  * (g_e, v_e) goes in a row buffer sorted by (tile, source bucket).  A
  * planned call then streams grad_edge and edge_vec once into that buffer
  * (each tile's rows land inside the tile's own stretch of it) and gathers

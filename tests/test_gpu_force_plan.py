@@ -5,7 +5,7 @@ accumulates in the direct kernel's order, so the two must agree bit for bit;
 the direct kernel is itself checked against the oracle and an fp64 truth in
 test_gpu_segment.py, and one case here repeats that check.  The plan's layout
 is checked exactly against a NumPy restatement: the edges sorted stably by
-(tile of 4096 edges, source bucket), and each source slot's row in that order.
+(tile of 8192 edges, source bucket), and each source slot's row in that order.
 """
 from __future__ import annotations
 
@@ -21,7 +21,7 @@ from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
-TILE, MOST_BUCKETS = 4096, 256
+TILE, MOST_BUCKETS = 8192, 256
 
 
 def _random_graph(atoms, edges, seed, hubs=()):
@@ -60,7 +60,7 @@ def _decode_plan(plan: _C.ForcePlan, edges: int):
 
 
 def _expected_slots(case, atoms):
-    """Edges sorted stably by (tile of 4096 edges, bucket of their source atom)."""
+    """Edges sorted stably by (tile of 8192 edges, bucket of their source atom)."""
     edges = case["src_order"].numel()
     wanted = min(atoms, MOST_BUCKETS)
     bucket_atoms = -(-atoms // wanted)
