@@ -508,6 +508,46 @@ def rmsnorm_jobs(rows: int, steps: int, warmup: int, graph: bool, labels: tuple 
     return out
 
 
+def edge_stream_job(n_edges: int, steps: int, warmup: int, graph: bool, label=None):
+    """Fused edge-stream chain over [E, 10, 64]: out = silu(x + a * s + b), s one value per (edge, row).
+
+    The shape and the chain are the reference's typical elementwise triple over [1, E, 10, 64]
+    (docs/task2-hip-fusion-plan.md:282-284: residual add, per-row gate, accumulate) with the
+    activation its design adds (:289).  `torch_chain_ms` times the eager chain the fused kernel
+    replaces (t = a * s; t += x; t += b; silu(t): four passes, ten [E, 10, 64] streams against the
+    fused kernel's four) on the same tensors.  One input set: each of the three inputs is larger
+    than the Infinity Cache.
+    """
+    import torch
+
+    from bysj_amd.kernels import _C
+
+    shape = (n_edges, 10, 64)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(23)
+    x, a, b = (torch.randn(shape, generator=generator, device="cuda") for _ in range(3))
+    s = torch.randn((n_edges, 10, 1), generator=generator, device="cuda")
+    out = torch.empty(shape, device="cuda")
+    full = n_edges * 640 * 4
+    reads = 3 * full + n_edges * 10 * 4
+    terms = [(1.0, x, None), (1.0, a, s), (1.0, b, None)]
+
+    def chain(_):
+        t = a * s
+        t += x
+        t += b
+        return torch.nn.functional.silu(t)
+
+    with torch.no_grad():
+        ms = time_steps(lambda _: _C.edge_stream_combine(terms, shape, "silu", None, None, out), 1, steps, warmup,
+                        graph=graph, label=label)
+        torch_ms = time_steps(chain, 1, max(5, steps // 4), 2, graph=graph)
+    del x, a, b, s, out, terms
+    torch.cuda.empty_cache()
+    return {"edges": n_edges, "rows": 10, "channels": 64, "ms_per_step": ms, "bytes": reads + full, "reads": reads,
+            "sets": 1, "torch_chain_ms": torch_ms}
+
+
 def csr_job(water, steps: int, warmup: int, graph: bool, label=None):
     """Device CSR build of a source list (group_by_source: offsets + stable order) on the config-4 graph.
 
@@ -1162,9 +1202,17 @@ def main() -> int:
                 add("gie_bwd_config3R_secondary", "gie_zonal_scatter_bwd", job, job["edges"], share=True)
                 jobs = rmsnorm_jobs(114688, steps, warm, graph, labels=(None, "rmsnorm_bwd_config3R"))
                 add("rmsnorm_bwd_config3R", "rmsnorm_bwd", jobs["bwd"], 114688, unit="rows/s", share=True)
+            edges_3r = water3r.n_edges
             del case, water3r
             torch.cuda.empty_cache()
             progress("config 3R (primary, secondary) done")
+            # ---- fused edge-stream chain over [E, 10, 64] at config 3R's edge count
+            job = edge_stream_job(edges_3r, steps, warm, graph, label="edge_stream_combine_config3R")
+            entry = add("edge_stream_combine_config3R", "edge_stream_combine", job, job["edges"], share=True)
+            entry["torch_chain_ms_per_step"] = round(job["torch_chain_ms"], 5)
+            del job
+            torch.cuda.empty_cache()
+            progress("edge stream chain done")
             jobs = rmsnorm_jobs(1048576, steps, warm, graph,
                                 labels=("rmsnorm_rows1M", "rmsnorm_bwd_rows1M" if backward else None))
             add("rmsnorm_rows1M", "rmsnorm_fwd", jobs["fwd"], 1048576, unit="rows/s", share=True)

@@ -16,10 +16,12 @@ inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
 ``*_csr`` GIE entry points expose the device-side CSR construction;
 ``segment_softmax_plan`` builds the degree plan that
 ``segment_softmax_forward/backward(..., plan=...)`` accept;
-``gie_rmsnorm_forward_csr`` is the fused GIE -> RMSNorm forward.
+``gie_rmsnorm_forward_csr`` is the fused GIE -> RMSNorm forward;
+``edge_stream_combine`` is the fused edge-stream elementwise chain.
 """
 from __future__ import annotations
 
+import ctypes
 
 import torch
 
@@ -665,6 +667,107 @@ def rmsnorm_backward(grad_output, x, scale, inverse_rms, compute_scale_grad):
         )
     _lib.check(status)
     return grad_x, grad_scale
+
+
+# ---------------------------------------------------------------------------
+# edge-stream elementwise chain (no reference implementation: the fusion the
+# reference designs as candidate C4, docs/task2-hip-fusion-plan.md:280-300)
+# ---------------------------------------------------------------------------
+
+EDGE_STREAM_ACTIVATIONS = {"none": 0, "silu": 1, "gate": 2}
+EDGE_STREAM_MAX_TERMS = 4
+EDGE_STREAM_MAX_GATE_ROWS = 64
+
+
+def _edge_view(tensor, shape, what: str) -> torch.Tensor:
+    """`tensor` broadcast to `shape` (zero strides on broadcast axes), checked as a gfx950 float32 operand."""
+    _check(isinstance(tensor, torch.Tensor) and tensor.is_cuda and tensor.dtype == torch.float32,
+           f"{what}: expected a gfx950 float32 tensor")
+    try:
+        return tensor.expand(shape)
+    except RuntimeError as error:
+        raise RuntimeError(f"{what} of shape {tuple(tensor.shape)} does not broadcast to {tuple(shape)}") from error
+
+
+def _edge_operand(view: torch.Tensor) -> "_lib.EdgeOperand":
+    return _lib.EdgeOperand(view.data_ptr(), (ctypes.c_int64 * 3)(*view.stride()))
+
+
+def _byte_span(view: torch.Tensor) -> tuple[int, int]:
+    """[first, last) bytes a view addresses (empty views address nothing)."""
+    if view.numel() == 0:
+        return view.data_ptr(), view.data_ptr()
+    extent = 1 + sum((size - 1) * stride for size, stride in zip(view.shape, view.stride()))
+    return view.data_ptr(), view.data_ptr() + 4 * extent
+
+
+def edge_stream_combine(terms, shape, activation: str = "none", gate=None, gate_rows=None, out=None):
+    """``act(sum_k (a_k * b_k) * coef_k)`` over (edge, row, channel) ``shape`` in one pass.
+
+    ``terms``: 1 to 4 ``(coef, a, b)`` with ``b`` None for a factor of 1;
+    ``a``, ``b`` and ``gate`` are float32 tensors that broadcast to ``shape``
+    (``gate`` to ``(E, G, C)``).  ``activation``: "none", "silu" or "gate"
+    (``gate_rows``: R ints, negative for the silu rows).  ``out`` may be
+    given (contiguous, ``shape``) and may be the same memory as a contiguous
+    full-shape operand; it must not overlap any other operand.
+    """
+    _check(isinstance(shape, (tuple, list, torch.Size)) and len(shape) == 3 and all(int(d) >= 0 for d in shape),
+           "edge_stream_combine: shape must be (n_edges, n_rows, channels)")
+    shape = tuple(int(d) for d in shape)
+    edges, rows, channels = shape
+    _check(1 <= len(terms) <= EDGE_STREAM_MAX_TERMS,
+           f"edge_stream_combine takes 1 to {EDGE_STREAM_MAX_TERMS} terms, got {len(terms)}")
+    _check(activation in EDGE_STREAM_ACTIVATIONS, f"edge_stream_combine: unknown activation {activation!r}")
+    views = []
+    for k, (coef, a, b) in enumerate(terms):
+        views.append((float(coef), _edge_view(a, shape, f"edge_stream_combine term {k} a"),
+                      None if b is None else _edge_view(b, shape, f"edge_stream_combine term {k} b")))
+    device = views[0][1].device
+    _same_device(views[0][1], *[v for _, a, b in views for v in (a, b)])
+    gate_view, rows_array = None, None
+    if activation == "gate":
+        _check(gate_rows is not None and len(gate_rows) == rows,
+               "edge_stream_combine: the gate activation needs one gate row per row")
+        _check(rows <= EDGE_STREAM_MAX_GATE_ROWS,
+               f"edge_stream_combine: the gate activation takes at most {EDGE_STREAM_MAX_GATE_ROWS} rows")
+        rows_list = [int(g) for g in gate_rows]
+        _check(all(g < EDGE_STREAM_MAX_GATE_ROWS for g in rows_list), "edge_stream_combine: gate row out of range")
+        gates = max([g + 1 for g in rows_list if g >= 0], default=0)
+        if gates > 0:
+            _check(gate is not None, "edge_stream_combine: gated rows need a gate tensor")
+            gate_view = _edge_view(gate, (edges, gates, channels), "edge_stream_combine gate")
+            _same_device(views[0][1], gate_view)
+        rows_array = (ctypes.c_int32 * max(rows, 1))(*rows_list)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=device)
+    else:
+        _f32(out, "edge_stream_combine out")
+        _check(tuple(out.shape) == shape, f"edge_stream_combine: out must have shape {shape}")
+        _same_device(views[0][1], out)
+        out_span = _byte_span(out)
+        operands = [v for _, a, b in views for v in (a, b) if v is not None] + ([gate_view] if gate_view is not None else [])
+        for view in operands:
+            if view.data_ptr() == out.data_ptr() and view.stride() == out.stride():
+                continue  # the same elements: each is read before it is written, by the same thread
+            first, last = _byte_span(view)
+            _check(last <= out_span[0] or first >= out_span[1] or out.numel() == 0,
+                   "edge_stream_combine: out overlaps an operand other than a full-shape alias")
+    if out.numel() == 0:
+        return out
+    count = len(views)
+    a_array = (_lib.EdgeOperand * count)(*[_edge_operand(a) for _, a, _ in views])
+    b_array = (_lib.EdgeOperand * count)(*[_edge_operand(b) if b is not None else _lib.EdgeOperand()
+                                           for _, _, b in views])
+    coefs = (ctypes.c_float * count)(*[coef for coef, _, _ in views])
+    gate_operand = _edge_operand(gate_view) if gate_view is not None else None
+    with _on(device) as stream:
+        status = _LIB.dpa4k_edge_stream_combine(
+            a_array, b_array, coefs, count, EDGE_STREAM_ACTIVATIONS[activation],
+            ctypes.byref(gate_operand) if gate_operand is not None else None, rows_array, out.data_ptr(),
+            edges, rows, channels, stream,
+        )
+    _lib.check(status)
+    return out
 
 
 __all__ = [

@@ -15,13 +15,23 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _SZ = ctypes.c_size_t
 _F32 = ctypes.c_float
 _INT = ctypes.c_int
+
+
+
+class EdgeOperand(ctypes.Structure):
+    """``dpa4k_edge_operand``: an fp32 view over (edge, row, channel) with element strides."""
+
+    _fields_ = [("data", ctypes.c_void_p), ("stride", ctypes.c_int64 * 3)]
+
+
+_OPERANDS = ctypes.POINTER(EdgeOperand)
 
 # name -> (restype, argtypes); mirrors include/dpa4k.h one to one.
 PROTOTYPES: dict[str, tuple[object, list[object]]] = {
@@ -72,6 +82,9 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_rmsnorm_backward_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_rmsnorm_backward": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
     "dpa4k_rmsnorm_backward_noalloc": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
+    "dpa4k_edge_stream_combine": (
+        _INT, [_OPERANDS, _OPERANDS, ctypes.POINTER(_F32), _INT, _INT, _OPERANDS, ctypes.POINTER(ctypes.c_int32), _P,
+               _I64, _I64, _I64, _P]),
     "dpa4k_stream_calibrate": (_INT, [_P, _I64, _P, _I64, _P]),
     "dpa4k_set_launch_row_limit": (_INT, [_I64]),
 }

@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 7
+#define DPA4K_ABI_VERSION 8
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -275,6 +275,49 @@ int dpa4k_force_assembly_f64_planned(const double* grad_edge,
                                      double* virial, int64_t n_edges,
                                      int64_t n_nodes, void* plan,
                                      size_t plan_bytes, dpa4k_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Edge-stream elementwise chain
+ * ---------------------------------------------------------------------- */
+
+/* No reference implementation: the reference designs this fusion as its
+ * candidate C4 (docs/task2-hip-fusion-plan.md:280-300, "designed, not
+ * implemented"), to replace chains of add_/mul/copy_ passes over [E, R, C]
+ * edge tensors in DeepMD's SeZM blocks.  One pass computes
+ *   acc[e, r, c] = sum_{k < n_terms, left to right} (a_k * b_k) * coef_k
+ *   out[e, r, c] = act(acc[e, r, c])
+ * over E edges, R rows and C channels; out is a contiguous [E, R, C] fp32
+ * array.  Each operand is an fp32 view: element (e, r, c) sits at
+ * data + e * stride[0] + r * stride[1] + c * stride[2], strides >= 0, and a
+ * zero stride broadcasts it along that axis (a per-edge scalar, a per-row
+ * gate, a per-channel weight).  The caller guarantees that every element the
+ * strides address lies in the operand's allocation.  b may be NULL, or b[k]
+ * have data NULL: factor 1.  Every product is rounded before the next
+ * operation, so with DPA4K_ACT_NONE the result equals the eager fp32 chain
+ * t = a * b; t = t * coef; acc = t_0 + t_1 + ... bit for bit.  Activations:
+ *   DPA4K_ACT_SILU  x * sigmoid(x);
+ *   DPA4K_ACT_GATE  SeZM's gated activation: gate_row (host array of R
+ *                   ints, R <= DPA4K_EDGE_STREAM_MAX_GATE_ROWS) maps each row
+ *                   to a gate index; rows with gate_row[r] < 0 take silu, the
+ *                   others x * sigmoid(gate[e, gate_row[r], c]), gate being
+ *                   an operand view over (edge, gate index, channel).
+ * out may be the same array as a contiguous [E, R, C] operand (in-place
+ * accumulation); it must not overlap any other operand.  1 <= n_terms <=
+ * DPA4K_EDGE_STREAM_MAX_TERMS.  Enqueued on `stream`, no allocation. */
+#define DPA4K_EDGE_STREAM_MAX_TERMS 4
+#define DPA4K_EDGE_STREAM_MAX_GATE_ROWS 64
+enum { DPA4K_ACT_NONE = 0, DPA4K_ACT_SILU = 1, DPA4K_ACT_GATE = 2 };
+typedef struct dpa4k_edge_operand {
+  const float* data;
+  int64_t stride[3]; /* element strides over (edge, row, channel) */
+} dpa4k_edge_operand;
+int dpa4k_edge_stream_combine(const dpa4k_edge_operand* a,
+                              const dpa4k_edge_operand* b, const float* coef,
+                              int n_terms, int activation,
+                              const dpa4k_edge_operand* gate,
+                              const int32_t* gate_row, float* out,
+                              int64_t n_edges, int64_t n_rows,
+                              int64_t channels, dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * GIE zonal scatter

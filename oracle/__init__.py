@@ -32,9 +32,12 @@ zonal_scatter backward         fp64 closed form with exact sums (shared and
                                four planted mistakes
 rmsnorm                        closed formula, fp64 brute force, zeros
 rmsnorm backward               autograd of the chain vs closed form
+edge_stream_combine_reference  float64 element loop, closed values, the
+                               float32 rounding order, planted mistakes
 =============================  ==============================================
 """
 
+from .edge_stream import edge_stream_combine_reference
 from .gie import gie_zonal_scatter_reference, zonal_scatter_backward_reference, zonal_scatter_reference
 from .rmsnorm import rmsnorm, rmsnorm_backward_reference
 from .segment import (
@@ -48,6 +51,7 @@ from .segment import (
 )
 
 __all__ = [
+    "edge_stream_combine_reference",
     "force_assembly_reference",
     "gie_zonal_scatter_reference",
     "group_by_source",

@@ -96,6 +96,10 @@ def test_invalid_sizes_fail_before_any_device_call():
         (lib.dpa4k_rmsnorm_forward, (null,) * 4 + (2**62, 4, ctypes.c_float(1e-6), null), "launch limit"),
         (lib.dpa4k_gie_zonal_scatter_forward_csr, (null,) * 7 + (0, 2**62, 0, 0, 4, 0, null), "launch limit"),
         (lib.dpa4k_force_assembly_f32, (null,) * 7 + (0, 2**62, null), "launch limit"),
+        (lib.dpa4k_edge_stream_combine, (null,) * 3 + (0, 0) + (null,) * 3 + (1, 1, 1, null), "1 to 4 terms"),
+        (lib.dpa4k_edge_stream_combine, (null,) * 3 + (1, 7) + (null,) * 3 + (1, 1, 1, null), "unknown activation"),
+        (lib.dpa4k_edge_stream_combine, (null,) * 3 + (1, 0) + (null,) * 3 + (2**40, 2**20, 2**10, null),
+         "overflows 64 bits"),
     ]
     for function, args, fragment in cases:
         status = function(*args)

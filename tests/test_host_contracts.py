@@ -152,6 +152,46 @@ def test_invalid_inputs_fail_before_the_device_gate():
             kernels.rmsnorm(torch.ones(2, 4), eps=eps)
 
 
+def test_edge_stream_validation_precedes_the_device_gate():
+    from bysj_amd.kernels import edge_stream
+
+    x = torch.randn(6, 4, 8)
+    with pytest.raises(RuntimeError, match=GATE):
+        edge_stream.edge_stream_combine([(1.0, x), (0.5, x, torch.rand(6, 4, 1))], activation="silu")
+    with pytest.raises(TypeError, match="sequence"):
+        edge_stream.edge_stream_combine(x)
+    with pytest.raises(ValueError, match="1 to 4 terms"):
+        edge_stream.edge_stream_combine([])
+    with pytest.raises(TypeError, match=r"\(coef, a\)"):
+        edge_stream.edge_stream_combine([(1.0,)])
+    with pytest.raises(TypeError, match="coefficient must be a real number"):
+        edge_stream.edge_stream_combine([("2", x)])
+    with pytest.raises(ValueError, match="finite"):
+        edge_stream.edge_stream_combine([(float("nan"), x)])
+    with pytest.raises(TypeError, match="b must be a tensor"):
+        edge_stream.edge_stream_combine([(1.0, x, 3.0)])
+    with pytest.raises(TypeError, match="float32"):
+        edge_stream.edge_stream_combine([(1.0, x.half())])
+    with pytest.raises(ValueError, match="more than three"):
+        edge_stream.edge_stream_combine([(1.0, x[None])])
+    with pytest.raises(ValueError, match=r"\(edges, rows, channels\)"):
+        edge_stream.edge_stream_combine([(1.0, torch.randn(4, 8))])
+    with pytest.raises(ValueError, match="do not broadcast"):
+        edge_stream.edge_stream_combine([(1.0, x), (1.0, torch.randn(6, 3, 8))])
+    with pytest.raises(ValueError, match="activation"):
+        edge_stream.edge_stream_combine([(1.0, x)], activation="relu")
+    with pytest.raises(ValueError, match="gate_rows"):
+        edge_stream.edge_stream_combine([(1.0, x)], activation="gate", gate=x, gate_rows=[0])
+    with pytest.raises(TypeError, match="gate tensor"):
+        edge_stream.edge_stream_combine([(1.0, x)], activation="gate", gate_rows=[-1, 0, 0, 1])
+    with pytest.raises(ValueError, match="belong to the gate activation"):
+        edge_stream.edge_stream_combine([(1.0, x)], gate=x)
+    with pytest.raises(ValueError, match="contiguous tensor of shape"):
+        edge_stream.edge_stream_combine([(1.0, x)], out=torch.empty(6, 4, 9))
+    with pytest.raises(RuntimeError, match="inference-only"):
+        edge_stream.edge_stream_combine([(1.0, x.clone().requires_grad_())])
+
+
 def test_native_loader_requires_the_entry_point():
     extension = SimpleNamespace(rmsnorm_forward=object())
     with patch.object(native_mod, "_require_hip_runtime"), patch.object(native_mod, "_LOADED", None), \

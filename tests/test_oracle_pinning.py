@@ -16,6 +16,7 @@ Three kinds of checks, all on the CPU:
 from __future__ import annotations
 
 import importlib
+import math
 
 import numpy as np
 import pytest
@@ -23,6 +24,7 @@ import torch
 
 import closed_forms
 from golden_cases import load_cases
+from oracle import edge_stream as es_ref
 from oracle import gie as gie_ref
 from oracle import loops
 from oracle import segment as ref
@@ -118,6 +120,59 @@ def check_rmsnorm(rmsnorm):
         out = rmsnorm(case["x"], case["scale"], case["eps"])
         assert_close_scaled(out, case["out_f64"], what=case["name"])
         assert bool(torch.isfinite(out).all())
+
+
+def _edge_stream_case(seed):
+    """Operands of every broadcast shape the fused chain takes, over (E, R, C) = (3, 4, 5)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(3, 4, 5, generator=g)
+    a = torch.randn(3, 4, 5, generator=g)
+    s = torch.randn(3, 4, 1, generator=g)      # per (edge, row), broadcast over channels
+    w = torch.randn(5, generator=g)            # per channel, broadcast over edges and rows
+    e = torch.randn(3, 1, 1, generator=g)      # per edge
+    terms = [(1.0, x), (-0.75, a, s), (1.5, w, e), (0.3, a)]
+    q = torch.randn(3, 2, 5, generator=g)      # two gates per edge and channel
+    gate_rows = [-1, 0, 1, 1]
+    return terms, q, gate_rows
+
+
+def _edge_stream_loops(terms, activation, gate, gate_rows, shape, exact_f32):
+    """Element by element: float32 scalar arithmetic in the chain's order (exact_f32), else float64."""
+    cast = np.float32 if exact_f32 else float
+    out = np.zeros(shape, dtype=np.float32 if exact_f32 else np.float64)
+    views = []
+    for term in terms:
+        b = term[2] if len(term) == 3 else None
+        views.append((cast(term[0]), term[1].expand(shape).numpy(), None if b is None else b.expand(shape).numpy()))
+    for e, r, c in np.ndindex(*shape):
+        acc = None
+        for coef, a, b in views:
+            t = cast(a[e, r, c]) if b is None else cast(a[e, r, c]) * cast(b[e, r, c])
+            t = t * coef
+            acc = t if acc is None else acc + t
+        if activation == "silu" or (activation == "gate" and gate_rows[r] < 0):
+            acc = acc / (1.0 + math.exp(-float(acc)))
+        elif activation == "gate":
+            acc = acc / (1.0 + math.exp(-float(gate[e, gate_rows[r], c])))
+        out[e, r, c] = acc
+    return torch.from_numpy(out)
+
+
+def check_edge_stream(combine):
+    for seed in (0, 1):
+        terms, q, gate_rows = _edge_stream_case(seed)
+        shape = (3, 4, 5)
+        plain = combine(terms)
+        assert_bitwise(plain, _edge_stream_loops(terms, None, None, None, shape, True), "edge stream float32 order")
+        for activation in ("silu", "gate"):
+            got = combine(terms, activation, q, gate_rows)
+            want = _edge_stream_loops(terms, activation, q, gate_rows, shape, False)
+            assert_close_scaled(got, want, what=f"edge stream {activation}")
+        # closed values: sigmoid(0) = 1/2 on the gated rows, silu(0) = 0
+        zero_gate = combine(terms, "gate", torch.zeros_like(q), gate_rows)
+        assert_bitwise(zero_gate[:, 1:], plain[:, 1:] * 0.5, "edge stream gate at sigmoid(0)")
+        zeros = combine([(1.0, torch.zeros(3, 4, 5))], "silu")
+        assert int(zeros.count_nonzero()) == 0
 
 
 # ---------------------------------------------------------------------------
@@ -569,6 +624,21 @@ def _gie_backward_row_zero(grad, zonal, radial, dst, radial_slot, inv_sqrt_deg):
     return gie_ref.zonal_scatter_backward_reference(shifted, zonal, radial, dst, radial_slot, inv_sqrt_deg)
 
 
+def _edge_stream_coef_first(terms, activation=None, gate=None, gate_rows=None):
+    moved = [(1.0, term[1] * float(term[0])) + tuple(term[2:]) for term in terms]
+    return es_ref.edge_stream_combine_reference(moved, activation, gate, gate_rows)
+
+
+def _edge_stream_gate_by_row(terms, activation=None, gate=None, gate_rows=None):
+    if activation == "gate":
+        gate_rows = [-1 if g < 0 else min(r, gate.shape[1] - 1) for r, g in enumerate(gate_rows)]
+    return es_ref.edge_stream_combine_reference(terms, activation, gate, gate_rows)
+
+
+def _edge_stream_silu_everywhere(terms, activation=None, gate=None, gate_rows=None):
+    return es_ref.edge_stream_combine_reference(terms, "silu" if activation == "gate" else activation, gate, gate_rows)
+
+
 def _rmsnorm_without_eps(x, scale=None, eps=1e-6):
     out = x * torch.rsqrt(x.square().mean(-1, keepdim=True))
     return out if scale is None else out * scale
@@ -607,7 +677,14 @@ PLANTED = [
     ("gie backward reads the wrong cotangent row", lambda: check_gie_backward(_gie_backward_row_zero)),
     ("rmsnorm without eps", lambda: check_rmsnorm(_rmsnorm_without_eps)),
     ("rmsnorm with sum instead of mean", lambda: check_rmsnorm(_rmsnorm_sum_not_mean)),
+    ("edge stream applies the coefficient before the product", lambda: check_edge_stream(_edge_stream_coef_first)),
+    ("edge stream gates by row instead of gate_rows", lambda: check_edge_stream(_edge_stream_gate_by_row)),
+    ("edge stream takes silu on the gated rows", lambda: check_edge_stream(_edge_stream_silu_everywhere)),
 ]
+
+
+def test_edge_stream_oracle_pinned():
+    check_edge_stream(es_ref.edge_stream_combine_reference)
 
 
 @pytest.mark.parametrize("label,run", PLANTED, ids=[label for label, _ in PLANTED])
