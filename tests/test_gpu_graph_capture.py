@@ -155,3 +155,26 @@ def test_force_assembly_capture(dtype):
         return kernels.force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets, src_order)
 
     _check_replays(step, (grad_edge, edge_vec), seed=5)
+
+
+@pytest.mark.parametrize("activation", [None, "gate"])
+def test_edge_stream_capture(activation):
+    from bysj_amd.kernels import edge_stream
+
+    announce("capture edge_stream", activation)
+    x = torch.rand(2000, 9, 64, device=DEV)
+    a = torch.rand(2000, 9, 64, device=DEV)
+    s = torch.rand(2000, 9, 1, device=DEV)
+    q = torch.rand(2000, 2, 64, device=DEV)
+    rows = [-1, 0, 0, 0, 1, 1, 1, 1, 1]
+    acc = torch.empty(2000, 9, 64, device=DEV)
+
+    def step():
+        with torch.no_grad():
+            out = edge_stream.edge_stream_combine([(1.0, x), (0.5, a, s)], activation=activation,
+                                                  gate=q if activation else None,
+                                                  gate_rows=rows if activation else None)
+            edge_stream.edge_stream_combine([(1.0, out), (-2.0, a)], out=acc)
+        return (out, acc.clone())
+
+    _check_replays(step, [x, a, s, q], seed=19)

@@ -210,3 +210,25 @@ def test_force_assembly_rows(limit, dtype):
 
     expected, actual = _run_both(limit, compute)
     _assert_all(expected, actual, "force_assembly")
+
+
+@pytest.mark.parametrize("limit", LIMITS)
+@pytest.mark.parametrize("channels", [64, 6])
+def test_edge_stream_rows(limit, channels):
+    from bysj_amd.kernels import edge_stream
+
+    announce("rows edge stream", limit, channels)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(31)
+    shape = (3001, 9, channels)
+    x, a = (torch.randn(*shape, generator=gen, device=DEV) for _ in range(2))
+    s = torch.randn(shape[0], shape[1], 1, generator=gen, device=DEV)
+    q = torch.randn(shape[0], 2, channels, generator=gen, device=DEV)
+    rows = [-1, 0, 0, 0, 1, 1, 1, 1, 1]
+
+    def compute():
+        return (edge_stream.edge_stream_combine([(1.0, x), (0.5, a, s)]),
+                edge_stream.edge_stream_combine([(1.0, x), (-1.0, a)], activation="gate", gate=q, gate_rows=rows))
+
+    expected, actual = _run_both(limit, compute)
+    _assert_all(expected, actual, "edge_stream")
