@@ -149,22 +149,32 @@ __device__ __forceinline__ int64_t element_limit(int64_t n, const uint32_t* coun
 // A wave ranks its 64 elements stably by a digit of up to kDigitBits bits.
 // One ballot per digit bit leaves every lane the mask of the active lanes
 // that share its digit; its rank among them is the number of lower lanes
-// (mbcnt), and the lowest of them, the group's leader, adds the group's size
-// to the wave's own LDS counter of the digit.  Only the leader touches a
-// digit's counter in a round and each wave has counters of its own, so the
-// value the leader reads back is the number of equal digits the wave met in
-// its earlier rounds: a lane's rank among the equal digits of the wave's
-// whole range is that value plus its rank in the round.
+// (mbcnt).  The wave's own LDS counter of the digit holds the number of equal
+// digits the wave met in its earlier rounds; the lowest lane of the group,
+// its leader, advances it by the group's size.  Either every lane reads the
+// counter and the leader then stores it (each wave has counters of its own
+// and a wave's LDS operations take effect in program order, so no atomic is
+// needed), or the leader advances it atomically and broadcasts the old value.
+// A lane's rank among the equal digits of the wave's whole range is that
+// value plus its rank in the round.
 
+// Per digit bit: m = the bit spread over the word (v_bfe_i32: all ones or
+// zero), its ballot (v_cmp of m itself), and per half `differ |= ballot ^ m`
+// (the lanes whose bit differs from this lane's) as one v_bitop3: four VALU
+// operations a bit.
 template <int kBits>
 __device__ __forceinline__ uint64_t lanes_with_digit(uint32_t digit, bool active) {
-  uint64_t same = __ballot(active);
+  constexpr uint32_t kOrOfXor = 0xF6;  // v_bitop3 table of a | (b ^ c)
+  constexpr int kNotEqual = 33;        // the integer predicate "ne" of the compare builtin
+  uint32_t differ_lo = 0u, differ_hi = 0u;
 #pragma unroll
   for (int i = 0; i < kBits; ++i) {
-    const bool set = ((digit >> i) & 1u) != 0u;
-    const uint64_t with = __ballot(set);
-    same &= set ? with : ~with;
+    const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int>(digit), i, 1));
+    const uint64_t with = __builtin_amdgcn_uicmp(m, 0u, kNotEqual);
+    differ_lo = __builtin_amdgcn_bitop3_b32(differ_lo, static_cast<uint32_t>(with), m, kOrOfXor);
+    differ_hi = __builtin_amdgcn_bitop3_b32(differ_hi, static_cast<uint32_t>(with >> 32), m, kOrOfXor);
   }
+  const uint64_t same = ~((static_cast<uint64_t>(differ_hi) << 32) | differ_lo) & __ballot(active);
   return active ? same : 0ull;
 }
 
@@ -178,7 +188,10 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // r); digit(r) has at most kBits bits, `valid` has bit r for an element in
 // round r, and `counter` is the wave's [digit] array, advanced by the call.
 // Every lane of the wave must call it.
-template <int kBits, int kRounds, typename DigitOf>
+// kLeaderStores: every lane reads the counter and the leader stores it
+// advanced; otherwise the leader advances it with an atomic and broadcasts
+// the old value (fewer live registers where a kernel is close to spilling).
+template <int kBits, int kRounds, bool kLeaderStores, typename DigitOf>
 __device__ __forceinline__ void wave_split_ranks(DigitOf digit, uint32_t valid, uint32_t* counter,
                                                  uint32_t (&rank)[kRounds]) {
   const int lane = threadIdx.x & 63;
@@ -187,10 +200,19 @@ __device__ __forceinline__ void wave_split_ranks(DigitOf digit, uint32_t valid, 
     const bool active = ((valid >> r) & 1u) != 0u;
     const uint64_t same = lanes_with_digit<kBits>(digit(r), active);
     const uint32_t below = lanes_below(same);
-    uint32_t before = 0u;
-    if (active && below == 0u) before = atomicAdd(&counter[digit(r)], static_cast<uint32_t>(__popcll(same)));
-    const int leader = active ? __builtin_ctzll(same) : lane;
-    rank[r] = static_cast<uint32_t>(__shfl(static_cast<int>(before), leader, 64)) + below;
+    const uint32_t size = static_cast<uint32_t>(__popcll(same));
+    if constexpr (kLeaderStores) {
+      // digits are masked, so every lane's read is in range; the leader's
+      // store follows the wave's read in LDS order
+      const uint32_t before = counter[digit(r)];
+      if (active && below == 0u) counter[digit(r)] = before + size;
+      rank[r] = before + below;
+    } else {
+      uint32_t before = 0u;
+      if (active && below == 0u) before = atomicAdd(&counter[digit(r)], size);
+      const int leader = active ? __builtin_ctzll(same) : lane;
+      rank[r] = static_cast<uint32_t>(__shfl(static_cast<int>(before), leader, 64)) + below;
+    }
   }
 }
 
@@ -497,7 +519,7 @@ __global__ __launch_bounds__(kThreads, 4) void tile_scatter_kernel(
   const auto digit = [&](int r) { return (key[r] >> shift) & digit_mask; };
   uint32_t rank[kScatterRounds];
   uint32_t* counter = wave_count + wave * kMaxBuckets;
-  wave_split_ranks<kDigitBits>(digit, ok, counter, rank);
+  wave_split_ranks<kDigitBits, kScatterRounds, sizeof(E) == 4>(digit, ok, counter, rank);
   __syncthreads();
   wave_prefix(wave_count, kMaxBuckets, buckets, tile_start);
 
@@ -699,7 +721,7 @@ __global__ __launch_bounds__(kThreads, sizeof(P) == 4 ? 4 : 2) void finish_kerne
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) valid |= wave * kSpan + 64 * r + lane < in_chunk ? (1u << r) : 0u;
     uint32_t* counter = wave_count + wave * kMaxFine;
-    wave_split_ranks<kFineMatch>(fine, valid, counter, rank);
+    wave_split_ranks<kFineMatch, kRounds, false>(fine, valid, counter, rank);
     __syncthreads();
     wave_prefix(wave_count, kMaxFine, fines, chunk_start);
     __syncthreads();
