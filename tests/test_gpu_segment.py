@@ -324,6 +324,30 @@ def test_segment_sum_workgroup_path_long_segments(channels, use_order):
     assert_close_scaled(grads_big[1][:nodes], grads[2], what="padded grid vs small grid grad_node_scale")
 
 
+@pytest.mark.parametrize("channels", [3, 5, 8, 32, 64, 128])
+@pytest.mark.parametrize("scales", [False, True])
+def test_segment_sum_large_grid_natural_order_rounds(channels, scales):
+    """Grids past the small-grid limit (N * lanes per segment / 64 >= 2048 waves) read rows in natural
+    order 32 slots a round: segments shorter than a round, of exactly one, and of several rounds plus a
+    tail, at widths of one float per lane (C = 3, 5) to one float4 per lane (C = 128)."""
+    announce("segment_sum large grid rounds", channels, scales)
+    nodes = 70000  # past the limit for every width here (C = 8: 2 lanes per segment)
+    gen = np.random.default_rng(channels)
+    degrees = gen.poisson(3.0, nodes).astype(np.int64)
+    degrees[::997] = 32
+    degrees[5::1009] = 100
+    degrees[7::4001] = 0
+    case_dst = torch.from_numpy(workloads.dst_from_degrees(degrees))
+    offsets = ref.segment_offsets(case_dst, nodes)
+    g = torch.Generator().manual_seed(channels)
+    src = torch.randn(case_dst.numel(), channels, generator=g)
+    w = torch.rand(case_dst.numel(), generator=g) + 0.5 if scales else None
+    s = torch.rand(nodes, generator=g) + 0.5 if scales else None
+    out = kernels.segment_sum(src.to(DEV), case_dst.to(DEV), offsets.to(DEV),
+                              None if w is None else w.to(DEV), None if s is None else s.to(DEV))
+    assert_bitwise(out, ref.segment_sum_reference(src, case_dst, offsets, w, s), "large grid vs sequential oracle")
+
+
 @pytest.mark.parametrize("channels", [3, 8, 64, 128, 256, 640])
 @pytest.mark.parametrize("use_order", [False, True])
 def test_segment_sum_backward_matches_autograd(channels, use_order):
