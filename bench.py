@@ -994,7 +994,8 @@ def main() -> int:
         return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(the operators shard by destination-node ranges; see DESIGN.md)", file=sys.stderr)
+              "(the operators would shard by contiguous destination-node ranges, one range per GPU, "
+              "with the ghost rows' partial sums exchanged; no multi-GPU path is built)", file=sys.stderr)
         return 2
     import torch
 
