@@ -26,22 +26,8 @@
 // locality: each 12-byte row then costs a whole cache line, which bounds the
 // kernel well below the HBM roofline of its algorithmic bytes.
 //
-// The planned path (dpa4k_force_assembly_plan, once per graph) removes that
-// gather from HBM.  The plan partitions the atoms into <= 256 contiguous
-// buckets and the edges into tiles of kPlanTile, and sorts the edges stably
-// by (tile, source bucket) with the library's counting sort.  Each call then
-//   pass 1  streams the rows (g_e, v_e) in edge order into a buffer in that
-//           sorted order: the reads are one contiguous stream, and the
-//           writes of a tile stay inside its own kPlanTile rows of the
-//           buffer, which the tile's blocks (one XCD) complete in their L2;
-//   pass 2  is the kernel above with its source rows read from that buffer
-//           through 32-bit positions: one 24- or 48-byte row per edge.  The
-//           rows one bucket's atoms need lie in one short run per tile, so
-//           the blocks of a bucket (one XCD: blocks are dealt to XCDs in
-//           contiguous atom ranges) gather from a few hundred KB that their
-//           L2 holds instead of from the whole input.
-// The accumulation order is the unplanned kernel's, so both give the same
-// bits.
+// The planned path (dpa4k_force_assembly_plan, once per graph; below) replaces
+// that gather with a blocked two-level reduction over spatial blobs of edges.
 #include "common.h"
 
 namespace dpa4k {
@@ -124,47 +110,15 @@ __device__ __forceinline__ void add_source(double (&acc)[12], const Row3<T>& g, 
   acc[11] -= g2 * v2;
 }
 
-// Row (g_e, v_e) of the planned path's bucketed buffer ([E, 6] of T); offset
-// kNoRow reads zeros.  Three 8-byte loads (f32) or three 16-byte loads (f64).
-// The f32 halves are split from a 64-bit integer: with per-element access to
-// the builtin's two-dword vector this toolchain emits a single-dword load and
-// the high halves read garbage.
-template <typename T>
-__device__ __forceinline__ void view_pair(BufferView view, uint32_t offset, Row3<T>& g, Row3<T>& v) {
-  if constexpr (sizeof(T) == 4) {
-    auto pair = [&](uint32_t at, float& low, float& high) {
-      const uint64_t bits = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(view, static_cast<int>(at), 0, 0));
-      low = __builtin_bit_cast(float, static_cast<uint32_t>(bits));
-      high = __builtin_bit_cast(float, static_cast<uint32_t>(bits >> 32));
-    };
-    pair(offset, g.x, g.y);
-    pair(offset == kNoRow ? kNoRow : offset + 8u, g.z, v.x);
-    pair(offset == kNoRow ? kNoRow : offset + 16u, v.y, v.z);
-  } else {
-    typedef double f64x2 __attribute__((ext_vector_type(2)));
-    const f64x2 a = __builtin_bit_cast(f64x2, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(offset), 0, 0));
-    const f64x2 b = __builtin_bit_cast(
-        f64x2, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(offset == kNoRow ? kNoRow : offset + 16u), 0, 0));
-    const f64x2 c = __builtin_bit_cast(
-        f64x2, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(offset == kNoRow ? kNoRow : offset + 32u), 0, 0));
-    g = Row3<T>{a.x, a.y, b.x};
-    v = Row3<T>{b.y, c.x, c.y};
-  }
-}
-
 // kRowViews: the gathered rows' array is under 2^31 bytes, so they are
 // addressed through 32-bit offsets into a view of the whole array (one
 // register per address, zeros for a lane without a row); otherwise through
 // pointers at a clamped id, with the rows of invalid slots zeroed afterwards.
-// kPlanned: the source slots hold int32 positions (src_pos) into the bucketed
-// buffer `rows` ([E, 6]: g_e then v_e) instead of int64 edge ids (src_order)
-// into grad_edge and edge_vec.
-template <typename T, bool kRowViews, bool kPlanned>
+template <typename T, bool kRowViews>
 __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
     const T* __restrict__ grad_edge, const T* __restrict__ edge_vec,
     const int64_t* __restrict__ dst_offsets, const int64_t* __restrict__ src_offsets,
-    const int64_t* __restrict__ src_order, const int32_t* __restrict__ src_pos, const T* __restrict__ rows,
-    T* __restrict__ force, T* __restrict__ virial, int64_t n_edges, int64_t n_nodes) {
+    const int64_t* __restrict__ src_order, T* __restrict__ force, T* __restrict__ virial, int64_t n_edges, int64_t n_nodes) {
   constexpr int kPer = 16 / sizeof(T);          // T per 16-byte chunk
   constexpr int kDstChunks = kDstBytes / 16;     // chunks per lane
   // Neighbouring atoms gather rows from the same destination segments when
@@ -200,23 +154,19 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
   // name are requested.
   constexpr int64_t kWindowBytes = 4096;  // covers both windows of a lane
   const int64_t wave_dst = uniform_i64(dst_begin), wave_src = uniform_i64(src_begin);
-  constexpr int64_t kSlotBytes = kPlanned ? 4 : 8;
+  constexpr int64_t kSlotBytes = 8;
   const int64_t dst_base = (dst_begin - wave_dst) * 3 * static_cast<int64_t>(sizeof(T));
   const int64_t src_base = (src_begin - wave_src) * kSlotBytes;
   const bool dst_window = dst_base >= 0 && dst_base < int64_t(kNoRow) - kWindowBytes;
   const bool src_window = src_base >= 0 && src_base < int64_t(kNoRow) - kWindowBytes;
 
-  const BufferView slots = kPlanned ? buffer_view(src_pos + wave_src, (n_edges - wave_src) * 4)
-                                    : buffer_view(src_order + wave_src, (n_edges - wave_src) * 8);
-  int64_t edge[kSrcRounds];  // edge ids, or positions in `rows` when planned
+  const BufferView slots = buffer_view(src_order + wave_src, (n_edges - wave_src) * 8);
+  int64_t edge[kSrcRounds];
 #pragma unroll
   for (int r = 0; r < kSrcRounds; ++r) {
     const uint32_t offset =
         src_window ? static_cast<uint32_t>(src_base) + static_cast<uint32_t>(r * kGroup + lane) * kSlotBytes : kNoRow;
-    if constexpr (kPlanned)
-      edge[r] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(slots, static_cast<int>(offset), 0, 0));
-    else
-      edge[r] = view_i64(slots, offset);
+    edge[r] = view_i64(slots, offset);
   }
   const BufferView dst_view =
       buffer_view(grad_edge + 3 * wave_dst, 3 * (n_edges - wave_dst) * static_cast<int64_t>(sizeof(T)));
@@ -236,27 +186,7 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
     edge[r] = valid ? edge[r] : -1;
   }
   Row3<T> g[kSrcRounds], v[kSrcRounds];
-  if constexpr (kPlanned && kRowViews) {
-    const BufferView row_view = buffer_view(rows, 6 * n_edges * static_cast<int64_t>(sizeof(T)));
-#pragma unroll
-    for (int r = 0; r < kSrcRounds; ++r) {
-      const uint32_t offset = edge[r] >= 0 ? static_cast<uint32_t>(edge[r]) * (6u * sizeof(T)) : kNoRow;
-      view_pair<T>(row_view, offset, g[r], v[r]);
-    }
-  } else if constexpr (kPlanned) {
-#pragma unroll
-    for (int r = 0; r < kSrcRounds; ++r) {
-      const int64_t e = edge[r] >= 0 ? edge[r] : 0;
-      g[r] = load_row(rows, 2 * e);
-      v[r] = load_row(rows, 2 * e + 1);
-    }
-#pragma unroll
-    for (int r = 0; r < kSrcRounds; ++r) {
-      const bool valid = edge[r] >= 0;
-      g[r] = Row3<T>{valid ? g[r].x : T(0), valid ? g[r].y : T(0), valid ? g[r].z : T(0)};
-      v[r] = Row3<T>{valid ? v[r].x : T(0), valid ? v[r].y : T(0), valid ? v[r].z : T(0)};
-    }
-  } else if constexpr (kRowViews) {
+  if constexpr (kRowViews) {
     const int64_t bytes = 3 * n_edges * static_cast<int64_t>(sizeof(T));
     const BufferView g_view = buffer_view(grad_edge, bytes), v_view = buffer_view(edge_vec, bytes);
 #pragma unroll
@@ -297,15 +227,9 @@ __global__ __launch_bounds__(kBlock) void force_assembly_kernel(
 #pragma unroll
   for (int r = 0; r < kSrcRounds; ++r) add_source(acc, g[r], v[r]);
   for (int64_t slot = src_begin + (src_window ? kSrcRounds * kGroup : 0) + lane; slot < src_end; slot += kGroup) {
-    if constexpr (kPlanned) {
-      const int64_t at = src_pos[slot];
-      if (static_cast<uint64_t>(at) >= static_cast<uint64_t>(n_edges)) continue;
-      add_source(acc, load_row(rows, 2 * at), load_row(rows, 2 * at + 1));
-    } else {
-      const int64_t e = edge_of<true>(src_order, slot, n_edges);
-      if (e < 0) continue;
-      add_source(acc, load_row(grad_edge, e), load_row(edge_vec, e));
-    }
+    const int64_t e = edge_of<true>(src_order, slot, n_edges);
+    if (e < 0) continue;
+    add_source(acc, load_row(grad_edge, e), load_row(edge_vec, e));
   }
 
 #pragma unroll
@@ -335,194 +259,975 @@ int run(const T* grad_edge, const T* edge_vec, const int64_t* dst_offsets,
   hipStream_t stream = as_stream(stream_handle);
   const dim3 grid = launch_grid((n_nodes + kAtoms - 1) / kAtoms, kBlock);
   if (3 * n_edges * static_cast<int64_t>(sizeof(T)) < (int64_t(1) << 31))
-    force_assembly_kernel<T, true, false><<<grid, kBlock, 0, stream>>>(
-        grad_edge, edge_vec, dst_offsets, src_offsets, src_order, nullptr, nullptr, force, virial, n_edges, n_nodes);
+    force_assembly_kernel<T, true><<<grid, kBlock, 0, stream>>>(grad_edge, edge_vec, dst_offsets, src_offsets,
+                                                                 src_order, force, virial, n_edges, n_nodes);
   else
-    force_assembly_kernel<T, false, false><<<grid, kBlock, 0, stream>>>(
-        grad_edge, edge_vec, dst_offsets, src_offsets, src_order, nullptr, nullptr, force, virial, n_edges, n_nodes);
+    force_assembly_kernel<T, false><<<grid, kBlock, 0, stream>>>(grad_edge, edge_vec, dst_offsets, src_offsets,
+                                                                  src_order, force, virial, n_edges, n_nodes);
   return launched("force_assembly_kernel");
 }
 
 // ---------------------------------------------------------------------------
-// planned path
+// planned path: spatial blobs of edges, partial sums per (blob, source atom)
 // ---------------------------------------------------------------------------
+//
+// Plan (once per graph).  The atoms are put in a spatial order: positions are
+// recovered from the edge vectors along a breadth-first tree of the graph
+// (r_k = r_s - v_e for the edge e = (dst k, src s) that first reaches k), and
+// the atoms are sorted by the Morton code of those positions.  Concatenating
+// the destination segments in that order and cutting the result into windows
+// of kBlobRows rows gives the blobs: each holds the incoming edges of a few
+// dozen atoms that lie close together, so the sources of its edges repeat
+// (about 6.5 edges per source at the config-4 shape).  A segment that crosses
+// a window boundary is split into pieces, one per window.  Within each blob
+// the edges are grouped by source atom (the stable order of src_order): a
+// run of equal sources is a record.
+//
+// Pass 1 (force_blob_kernel, one workgroup per blob) reads the blob's rows
+// (g_e, v_e) into LDS (the rows of a piece are contiguous in the inputs), sums
+// each piece's g_e (the destination side, in double), and sums each record's
+// -g_e and -(g_e outer v_e) from LDS: 12 values per record, rounded once to
+// the value type.  Pass 2 (force_records_kernel) adds, per atom, its pieces
+// and its records in a fixed order (blob order) and writes force and virial.
+// Every sum has a fixed order: results are reproducible run to run.  They
+// differ from the direct kernel's in the last bits (other association).
+//
+// HBM bytes per call (f32, config 4: E = 5.9M, 916k records): the rows once
+// (24 B per edge), the plan's row and entry indices (6 B per edge), the
+// records written and read (2 x 48 B each), against the direct kernel's 12-byte
+// random gathers that cost a line each.
 
-unsigned int grid_stride_blocks(int64_t items) {
-  const int64_t wanted = (items + 255) / 256;
-  return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > 8192 ? 8192 : wanted));
+constexpr int kBlobThreads = 512;
+constexpr int64_t kBlobBytes = 67584;  // LDS rows of one blob: two workgroups per CU
+constexpr int kRecordLanes = 16;       // pass 2: lanes per atom
+constexpr int kScanBlock = 1024;       // elements per block of the plan's scans
+constexpr int32_t kUnreached = 0x7fffffff;
+constexpr int kMaxLevels = 4096;       // breadth-first levels before the rest count as unreached
+constexpr int kBoxBlocks = 256;
+
+template <typename T>
+constexpr int64_t blob_rows_of() { return kBlobBytes / (6 * static_cast<int64_t>(sizeof(T))); }
+
+int64_t blob_rows(int64_t value_bytes) { return kBlobBytes / (6 * value_bytes); }  // 2816 (f32), 1408 (f64)
+
+int64_t blob_count(int64_t n_edges, int64_t value_bytes) {
+  const int64_t rows = blob_rows(value_bytes);
+  return (n_edges + rows - 1) / rows;
 }
 
-constexpr int64_t kPlanTile = 8192;   // edges per pass-1 tile
-constexpr int64_t kPlanBuckets = 256;  // most source-atom buckets
-
-// Tiles and buckets of a graph: `bucket_atoms` consecutive atoms per bucket.
-struct PlanShape {
-  int64_t tiles, buckets, bucket_atoms;
-};
-
-PlanShape plan_shape(int64_t n_edges, int64_t n_nodes) {
-  PlanShape shape;
-  shape.tiles = (n_edges + kPlanTile - 1) / kPlanTile;
-  const int64_t wanted = n_nodes < kPlanBuckets ? n_nodes : kPlanBuckets;
-  shape.bucket_atoms = (n_nodes + wanted - 1) / wanted;
-  shape.buckets = (n_nodes + shape.bucket_atoms - 1) / shape.bucket_atoms;
-  return shape;
+// Morton bits per axis: about one cell per atom.
+int morton_bits(int64_t n_nodes) {
+  int bits = 1;
+  while (bits < 10 && (int64_t(1) << (3 * (bits + 1))) <= n_nodes) ++bits;
+  return bits;
 }
 
-// The plan's arrays, carved in this order from the caller's buffer.
-struct PlanArrays {
-  int32_t* edge_row;   // [E] row of each edge in the (tile, bucket)-sorted buffer
-  int32_t* src_pos;    // [E] row of each source-CSR slot (-1: invalid src_order entry)
-  void* rows;          // [E, 6] of the value type
+struct BlobPlan {
+  int32_t* perm;          // [N] atoms in spatial order ("positions" below index perm)
+  int32_t* piece_first;   // [N+1] first piece of each position; [N] = pieces
+  int32_t* piece_t;       // [N+B+1] first concatenated row of each piece; [pieces] = E
+  int32_t* blob_piece;    // [B+1] first piece of each blob; [B] = pieces
+  int32_t* blob_rec;      // [B+1] first record of each blob; [B] = records
+  int32_t* blob_entry;    // [B+1] first entry of each blob; [B] = valid entries
+  int32_t* row_edge;      // [E] edge of each concatenated row
+  uint16_t* entry_row;    // [E] blob row of each entry (entries: valid src slots sorted by blob, source, slot)
+  int32_t* rec_entry;     // [E+1] first entry of each record; [records] = valid entries
+  int32_t* pos_records;   // [E] record ids grouped by the position of their source atom, in blob order
+  int32_t* pos_rec;       // [N+1] records of position i: pos_records[pos_rec[i] .. pos_rec[i+1])
 };
 
-bool carve_plan(void* plan, size_t plan_bytes, int64_t n_edges, int64_t value_bytes, PlanArrays& out) {
+bool carve_blob_plan(void* plan, size_t plan_bytes, int64_t n_edges, int64_t n_nodes, int64_t value_bytes,
+                     BlobPlan& out) {
   Carver carver{static_cast<char*>(plan), plan_bytes};
-  const size_t count = static_cast<size_t>(n_edges > 0 ? n_edges : 1);
-  out.edge_row = carver.take<int32_t>(count);
-  out.src_pos = carver.take<int32_t>(count);
-  out.rows = value_bytes == 8 ? static_cast<void*>(carver.take<double>(6 * count))
-                              : static_cast<void*>(carver.take<float>(6 * count));
-  return out.edge_row && out.src_pos && out.rows;
+  const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
+  const size_t b = static_cast<size_t>(blob_count(n_edges, value_bytes));
+  out.perm = carver.take<int32_t>(n);
+  out.piece_first = carver.take<int32_t>(n + 1);
+  out.piece_t = carver.take<int32_t>(n + b + 1);
+  out.blob_piece = carver.take<int32_t>(b + 1);
+  out.blob_rec = carver.take<int32_t>(b + 1);
+  out.blob_entry = carver.take<int32_t>(b + 1);
+  out.row_edge = carver.take<int32_t>(e);
+  out.entry_row = carver.take<uint16_t>(e);
+  out.rec_entry = carver.take<int32_t>(e + 1);
+  out.pos_records = carver.take<int32_t>(e);
+  out.pos_rec = carver.take<int32_t>(n + 1);
+  return out.perm && out.piece_first && out.piece_t && out.blob_piece && out.blob_rec && out.blob_entry &&
+         out.row_edge && out.entry_row && out.rec_entry && out.pos_records && out.pos_rec;
 }
 
-struct PlanScratch {
-  int64_t *key, *order, *tile_offsets;
-  int32_t* status;
+size_t blob_plan_bytes(int64_t n_edges, int64_t n_nodes, int64_t value_bytes) {
+  const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
+  const size_t b = static_cast<size_t>(blob_count(n_edges, value_bytes));
+  return round_up_256(n * 4) + round_up_256((n + 1) * 4) + round_up_256((n + b + 1) * 4) +
+         3 * round_up_256((b + 1) * 4) + round_up_256(e * 4) + round_up_256(e * 2) + round_up_256((e + 1) * 4) +
+         round_up_256(e * 4) + round_up_256((n + 1) * 4);
+}
+
+// Records buffer of a plan: the pieces' destination sums (3 doubles each), then the records (12 values each).
+size_t records_bytes_for(int64_t n_records, int64_t n_pieces, int64_t value_bytes) {
+  return round_up_256(static_cast<size_t>(n_pieces > 0 ? n_pieces : 1) * 3 * 8) +
+         round_up_256(static_cast<size_t>(n_records > 0 ? n_records : 1) * 12 * static_cast<size_t>(value_bytes));
+}
+
+struct BuildScratch {
+  int32_t *edge_src, *slot_atom, *tpos, *level, *rank, *cum, *flags, *counts, *scanned, *scan_blocks, *lengths,
+      *rec_old;
+  uint16_t* entry_old;
+  float *pos, *box_part, *box;
+  int64_t *key, *order, *key_offsets, *key2;
+  int32_t* sort_status;
   void* sort;
   size_t sort_bytes;
 };
 
-size_t plan_sort_bytes(int64_t n_edges, const PlanShape& shape) {
-  return dpa4k_group_by_key_workspace_size(n_edges, shape.tiles * shape.buckets);
+int64_t morton_keys_of(int64_t n_nodes) { return (int64_t(1) << (3 * morton_bits(n_nodes))) + 1; }
+
+// Records of a blob are ordered by descending length (entries, capped at kLengthKeys - 1), so
+// that the 64 records a wave takes are of similar length.
+constexpr int64_t kLengthKeys = 64;
+
+size_t sort_keys_of(int64_t n_edges, int64_t n_nodes) {
+  const size_t blobs = static_cast<size_t>(blob_count(n_edges, 4) > blob_count(n_edges, 8) ? blob_count(n_edges, 4)
+                                                                                            : blob_count(n_edges, 8));
+  size_t keys = blobs * kLengthKeys + 1;
+  keys = static_cast<size_t>(n_nodes) > keys ? static_cast<size_t>(n_nodes) : keys;
+  const size_t cells = static_cast<size_t>(morton_keys_of(n_nodes));
+  return cells > keys ? cells : keys;
 }
 
-bool carve_scratch(void* workspace, size_t bytes, int64_t n_edges, const PlanShape& shape, PlanScratch& out) {
+size_t build_sort_bytes(int64_t n_edges, int64_t n_nodes) {
+  const int64_t blobs = blob_count(n_edges, 4) > blob_count(n_edges, 8) ? blob_count(n_edges, 4)
+                                                                         : blob_count(n_edges, 8);
+  size_t most = dpa4k_group_by_key_workspace_size(n_nodes, morton_keys_of(n_nodes));
+  const size_t slots = dpa4k_group_by_key_workspace_size(n_edges, blobs + 1);
+  const size_t records = dpa4k_group_by_key_workspace_size(n_edges, n_nodes);
+  const size_t lengths = dpa4k_group_by_key_workspace_size(n_edges, blobs * kLengthKeys);
+  most = slots > most ? slots : most;
+  most = lengths > most ? lengths : most;
+  return records > most ? records : most;
+}
+
+bool carve_build(void* workspace, size_t bytes, int64_t n_edges, int64_t n_nodes, BuildScratch& out) {
   Carver carver{static_cast<char*>(workspace), bytes};
-  const size_t count = static_cast<size_t>(n_edges > 0 ? n_edges : 1);
-  const size_t cells = static_cast<size_t>(shape.tiles * shape.buckets);
-  out.key = carver.take<int64_t>(count);
-  out.order = carver.take<int64_t>(count);
-  out.tile_offsets = carver.take<int64_t>(cells + 1);
-  out.status = carver.take<int32_t>(1);
-  out.sort_bytes = plan_sort_bytes(n_edges, shape);
+  const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
+  const size_t m = e > n ? e : n;
+  const size_t keys = sort_keys_of(n_edges, n_nodes);
+  out.edge_src = carver.take<int32_t>(e);
+  out.slot_atom = carver.take<int32_t>(e);
+  out.tpos = carver.take<int32_t>(e);
+  out.level = carver.take<int32_t>(n);
+  out.rank = carver.take<int32_t>(n);
+  out.cum = carver.take<int32_t>(n + 1);
+  out.flags = carver.take<int32_t>(kMaxLevels + 8);
+  out.counts = carver.take<int32_t>(m + 1);
+  out.scanned = carver.take<int32_t>(m + 1);
+  out.scan_blocks = carver.take<int32_t>((m + 1) / kScanBlock + 2);
+  out.lengths = carver.take<int32_t>(m + 1);
+  out.rec_old = carver.take<int32_t>(m + 1);
+  out.entry_old = carver.take<uint16_t>(m);
+  out.key2 = carver.take<int64_t>(m);
+  out.pos = carver.take<float>(3 * n);
+  out.box_part = carver.take<float>(kBoxBlocks * 6);
+  out.box = carver.take<float>(8);
+  out.key = carver.take<int64_t>(m);
+  out.order = carver.take<int64_t>(m);
+  out.key_offsets = carver.take<int64_t>(keys + 2);
+  out.sort_status = carver.take<int32_t>(1);
+  out.sort_bytes = build_sort_bytes(n_edges, n_nodes);
   out.sort = carver.take<char>(out.sort_bytes);
-  return out.key && out.order && out.tile_offsets && out.status && out.sort;
+  return out.edge_src && out.slot_atom && out.tpos && out.level && out.rank && out.cum && out.flags &&
+         out.counts && out.scanned && out.scan_blocks && out.lengths && out.rec_old && out.entry_old && out.key2 &&
+         out.pos && out.box_part && out.box && out.key && out.order && out.key_offsets && out.sort_status && out.sort;
 }
 
-// key[q] = tile(e) * buckets + bucket(src of e) for the edge e = src_order[q]
-// of every source slot q; the atom of slot q is found by a binary search of
-// src_offsets.  Edges no valid slot names keep key tile(e) * buckets.
-__global__ __launch_bounds__(256) void plan_default_keys_kernel(int64_t* __restrict__ key, int64_t n_edges,
-                                                                int64_t buckets) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n_edges; e += stride)
-    key[e] = (e / kPlanTile) * buckets;
+size_t build_workspace_bytes(int64_t n_edges, int64_t n_nodes) {
+  const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
+  const size_t m = e > n ? e : n;
+  const size_t keys = sort_keys_of(n_edges, n_nodes);
+  return 3 * round_up_256(e * 4) + 2 * round_up_256(n * 4) + round_up_256((n + 1) * 4) +
+         round_up_256((kMaxLevels + 8) * 4) + 2 * round_up_256((m + 1) * 4) +
+         round_up_256(((m + 1) / kScanBlock + 2) * 4) + 2 * round_up_256((m + 1) * 4) + round_up_256(m * 2) +
+         round_up_256(m * 8) + round_up_256(3 * n * 4) + round_up_256(kBoxBlocks * 6 * 4) +
+         round_up_256(8 * 4) + 2 * round_up_256(m * 8) + round_up_256((keys + 2) * 8) + round_up_256(4) +
+         round_up_256(build_sort_bytes(n_edges, n_nodes));
 }
 
-__global__ __launch_bounds__(256) void plan_source_keys_kernel(const int64_t* __restrict__ src_offsets,
-                                                               const int64_t* __restrict__ src_order,
-                                                               int64_t* __restrict__ key, int64_t n_edges,
-                                                               int64_t n_nodes, int64_t buckets,
-                                                               int64_t bucket_atoms) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n_edges; q += stride) {
+unsigned int stride_blocks(int64_t items) {
+  const int64_t wanted = (items + 255) / 256;
+  return static_cast<unsigned int>(wanted < 1 ? 1 : (wanted > 8192 ? 8192 : wanted));
+}
+
+#define DPA4K_GRID_STRIDE(i, n) \
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < (n); \
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+
+// ---- exclusive scan of int32 counts: out[0..n], out[n] = total ----
+
+// Exclusive prefix of `value` over a 256-thread block; `total` gets the block's sum.
+__device__ __forceinline__ int32_t block_exclusive_256(int32_t value, int32_t* wave_sums, int32_t& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int32_t inclusive = value;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t other = __shfl_up(inclusive, d, 64);
+    inclusive += lane >= d ? other : 0;
+  }
+  if (lane == 63) wave_sums[wave] = inclusive;
+  __syncthreads();
+  int32_t before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int32_t s = wave_sums[w];
+    before += w < wave ? s : 0;
+    sum += s;
+  }
+  __syncthreads();
+  total = sum;
+  return before + inclusive - value;
+}
+
+__global__ __launch_bounds__(256) void scan_reduce_kernel(const int32_t* __restrict__ in, int64_t n,
+                                                          int32_t* __restrict__ block_sums) {
+  __shared__ int32_t wave_sums[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanBlock + threadIdx.x * 4;
+  int32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sum += base + i < n ? in[base + i] : 0;
+  int32_t total;
+  block_exclusive_256(sum, wave_sums, total);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+}
+
+// One block: exclusive scan of the block sums in place, chunk by chunk.
+__global__ __launch_bounds__(256) void scan_blocks_kernel(int32_t* __restrict__ block_sums, int64_t blocks) {
+  __shared__ int32_t wave_sums[4];
+  int32_t carry = 0;
+  for (int64_t base = 0; base < blocks; base += 256) {
+    const int64_t i = base + threadIdx.x;
+    const int32_t value = i < blocks ? block_sums[i] : 0;
+    int32_t total;
+    const int32_t before = block_exclusive_256(value, wave_sums, total);
+    if (i < blocks) block_sums[i] = carry + before;
+    carry += total;
+  }
+  if (threadIdx.x == 0) block_sums[blocks] = carry;
+}
+
+__global__ __launch_bounds__(256) void scan_apply_kernel(const int32_t* __restrict__ in, int64_t n,
+                                                         const int32_t* __restrict__ block_sums,
+                                                         int32_t* __restrict__ out, int64_t blocks) {
+  __shared__ int32_t wave_sums[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanBlock + threadIdx.x * 4;
+  int32_t v[4], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = base + i < n ? in[base + i] : 0;
+    sum += v[i];
+  }
+  int32_t total;
+  int32_t running = block_sums[blockIdx.x] + block_exclusive_256(sum, wave_sums, total);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (base + i < n) out[base + i] = running;
+    running += v[i];
+  }
+  if (blockIdx.x == blocks - 1 && threadIdx.x == 0) out[n] = block_sums[blocks];
+}
+
+int scan_exclusive(const int32_t* in, int32_t* out, int64_t n, int32_t* block_sums, hipStream_t stream) {
+  const int64_t blocks = (n + kScanBlock - 1) / kScanBlock > 0 ? (n + kScanBlock - 1) / kScanBlock : 1;
+  scan_reduce_kernel<<<static_cast<unsigned int>(blocks), 256, 0, stream>>>(in, n, block_sums);
+  if (int s = launched("scan_reduce_kernel")) return s;
+  scan_blocks_kernel<<<1, 256, 0, stream>>>(block_sums, blocks);
+  if (int s = launched("scan_blocks_kernel")) return s;
+  scan_apply_kernel<<<static_cast<unsigned int>(blocks), 256, 0, stream>>>(in, n, block_sums, out, blocks);
+  return launched("scan_apply_kernel");
+}
+
+// ---- plan kernels ----
+
+// flags[0] |= 1 when an offsets array is not a CSR of n_edges slots; flags[1] = the first atom with incoming edges.
+__global__ __launch_bounds__(256) void plan_check_kernel(const int64_t* __restrict__ dst_offsets,
+                                                         const int64_t* __restrict__ src_offsets, int64_t n_edges,
+                                                         int64_t n_nodes, int32_t* __restrict__ flags) {
+  DPA4K_GRID_STRIDE(k, n_nodes + 1) {
+    bool bad = false;
+    for (int side = 0; side < 2; ++side) {
+      const int64_t* offsets = side == 0 ? dst_offsets : src_offsets;
+      const int64_t here = offsets[k];
+      if (k == 0) bad |= here != 0;
+      if (k == n_nodes) bad |= here != n_edges;
+      if (k < n_nodes) bad |= offsets[k + 1] < here;
+    }
+    if (bad) flags[0] = 1;
+    if (k < n_nodes && dst_offsets[k] == 0 && dst_offsets[k + 1] > 0) flags[1] = static_cast<int32_t>(k);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ out, int64_t n, int32_t value) {
+  DPA4K_GRID_STRIDE(i, n) out[i] = value;
+}
+
+// Atom of every source slot, and the source atom of every edge a slot names
+// (the largest such atom when src_order names an edge twice).
+__global__ __launch_bounds__(256) void plan_slot_atoms_kernel(const int64_t* __restrict__ src_offsets,
+                                                              const int64_t* __restrict__ src_order,
+                                                              int32_t* __restrict__ slot_atom,
+                                                              int32_t* __restrict__ edge_src, int64_t n_edges,
+                                                              int64_t n_nodes) {
+  DPA4K_GRID_STRIDE(q, n_edges) {
     int64_t low = 0, high = n_nodes;  // the last atom k with src_offsets[k] <= q
     while (high - low > 1) {
       const int64_t mid = (low + high) / 2;
       if (src_offsets[mid] <= q) low = mid; else high = mid;
     }
+    slot_atom[q] = static_cast<int32_t>(low);
     const int64_t e = src_order[q];
-    if (static_cast<uint64_t>(e) < static_cast<uint64_t>(n_edges))
-      key[e] = (e / kPlanTile) * buckets + low / bucket_atoms;
+    if (static_cast<uint64_t>(e) < static_cast<uint64_t>(n_edges)) atomicMax(&edge_src[e], static_cast<int32_t>(low));
   }
 }
 
-// Sorted slot p (tile-major, then bucket, then edge) is row p of the
-// buffer: record that row for its edge.
-__global__ __launch_bounds__(256) void plan_rows_kernel(const int64_t* __restrict__ order,
-                                                        int32_t* __restrict__ edge_row, int64_t n_edges) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < n_edges; p += stride)
-    edge_row[order[p]] = static_cast<int32_t>(p);
-}
-
-__global__ __launch_bounds__(256) void plan_source_positions_kernel(const int64_t* __restrict__ src_order,
-                                                                    const int32_t* __restrict__ position,
-                                                                    int32_t* __restrict__ src_pos, int64_t n_edges) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < n_edges; q += stride) {
-    const int64_t e = src_order[q];
-    src_pos[q] = static_cast<uint64_t>(e) < static_cast<uint64_t>(n_edges) ? position[e] : -1;
+__global__ __launch_bounds__(256) void plan_bfs_init_kernel(int32_t* __restrict__ level, float* __restrict__ pos,
+                                                            const int32_t* __restrict__ flags, int64_t n_nodes) {
+  const int32_t root = flags[1];
+  DPA4K_GRID_STRIDE(k, n_nodes) {
+    level[k] = k == root ? 0 : kUnreached;
+    pos[3 * k] = pos[3 * k + 1] = pos[3 * k + 2] = 0.0f;
   }
 }
 
-// Pass 1: edge e's row (g_e, v_e) to row edge_row[e] of the buffer, one
-// edge per thread.  The reads are one contiguous stream; the writes of a
-// tile stay inside the tile's own kPlanTile rows, and the blocks of a tile
-// (consecutive logical blocks) run on one XCD, so its L2 assembles whole
-// lines before they are written back.  (Measured against the transposed
-// form, contiguous writes of rows gathered inside the tile: slightly
-// slower.)
+// Level `depth` of the breadth-first tree: every unreached atom takes as its
+// parent the source of its first incoming edge whose source sits at `depth`,
+// and its position from that edge's vector.  Reads only levels set by earlier
+// launches, so the tree does not depend on the order threads run in.
 template <typename T>
-__global__ __launch_bounds__(256) void force_place_rows_kernel(const T* __restrict__ grad_edge,
-                                                               const T* __restrict__ edge_vec,
-                                                               const int32_t* __restrict__ edge_row,
-                                                               T* __restrict__ rows, int64_t n_edges) {
-  const int64_t block = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
-  const int64_t e = block * 256 + threadIdx.x;
-  if (e >= n_edges) return;
-  const int64_t to = edge_row[e];
-  const Row3<T> g = load_row(grad_edge, e);
-  const Row3<T> v = load_row(edge_vec, e);
-  *reinterpret_cast<Row3<T>*>(rows + 6 * to) = g;
-  *reinterpret_cast<Row3<T>*>(rows + 6 * to + 3) = v;
+__global__ __launch_bounds__(256) void plan_bfs_level_kernel(const int64_t* __restrict__ dst_offsets,
+                                                             const int32_t* __restrict__ edge_src,
+                                                             const T* __restrict__ edge_vec,
+                                                             int32_t* __restrict__ level, float* __restrict__ pos,
+                                                             int32_t* __restrict__ flags, int32_t depth,
+                                                             int64_t n_nodes) {
+  int32_t* progress = flags + 8;  // progress[d]: some atom joined level d + 1
+  if (depth > 0 && progress[depth - 1] == 0) return;
+  DPA4K_GRID_STRIDE(k, n_nodes) {
+    if (level[k] != kUnreached) continue;
+    for (int64_t e = dst_offsets[k]; e < dst_offsets[k + 1]; ++e) {
+      const int32_t s = edge_src[e];
+      if (s < 0 || level[s] != depth) continue;
+      pos[3 * k] = pos[3 * s] - static_cast<float>(edge_vec[3 * e]);
+      pos[3 * k + 1] = pos[3 * s + 1] - static_cast<float>(edge_vec[3 * e + 1]);
+      pos[3 * k + 2] = pos[3 * s + 2] - static_cast<float>(edge_vec[3 * e + 2]);
+      level[k] = depth + 1;
+      progress[depth] = 1;
+      break;
+    }
+  }
 }
 
-size_t plan_bytes_for(int64_t n_edges, int64_t value_bytes) {
-  const size_t count = static_cast<size_t>(n_edges > 0 ? n_edges : 1);
-  return 2 * round_up_256(count * 4) + round_up_256(count * 6 * static_cast<size_t>(value_bytes));
+__device__ __forceinline__ void box_reduce(float (&box)[6], float* lds) {
+  // lds: [6][256]
+#pragma unroll
+  for (int i = 0; i < 6; ++i) lds[i * 256 + threadIdx.x] = box[i];
+  __syncthreads();
+  for (int width = 128; width > 0; width >>= 1) {
+    if (threadIdx.x < width) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        lds[i * 256 + threadIdx.x] = fminf(lds[i * 256 + threadIdx.x], lds[i * 256 + threadIdx.x + width]);
+        lds[(i + 3) * 256 + threadIdx.x] =
+            fmaxf(lds[(i + 3) * 256 + threadIdx.x], lds[(i + 3) * 256 + threadIdx.x + width]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 6; ++i) box[i] = lds[i * 256];
+}
+
+__global__ __launch_bounds__(256) void plan_box_kernel(const float* __restrict__ pos,
+                                                       const int32_t* __restrict__ level, int64_t n_nodes,
+                                                       float* __restrict__ box_part) {
+  __shared__ float lds[6 * 256];
+  float box[6] = {INFINITY, INFINITY, INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  DPA4K_GRID_STRIDE(k, n_nodes) {
+    if (level[k] == kUnreached) continue;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      box[i] = fminf(box[i], pos[3 * k + i]);
+      box[i + 3] = fmaxf(box[i + 3], pos[3 * k + i]);
+    }
+  }
+  box_reduce(box, lds);
+  if (threadIdx.x < 6) box_part[blockIdx.x * 6 + threadIdx.x] = box[threadIdx.x];
+}
+
+__global__ __launch_bounds__(256) void plan_box_final_kernel(const float* __restrict__ box_part, int parts,
+                                                             float* __restrict__ box_out) {
+  __shared__ float lds[6 * 256];
+  float box[6] = {INFINITY, INFINITY, INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int p = threadIdx.x; p < parts; p += 256) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      box[i] = fminf(box[i], box_part[p * 6 + i]);
+      box[i + 3] = fmaxf(box[i + 3], box_part[p * 6 + i + 3]);
+    }
+  }
+  box_reduce(box, lds);
+  if (threadIdx.x < 6) box_out[threadIdx.x] = box[threadIdx.x];
+}
+
+// Morton key of each reached atom's cell; unreached atoms after every cell.
+__global__ __launch_bounds__(256) void plan_morton_kernel(const float* __restrict__ pos,
+                                                          const int32_t* __restrict__ level,
+                                                          const float* __restrict__ box, int64_t n_nodes, int bits,
+                                                          int64_t* __restrict__ key) {
+  const float extent = fmaxf(fmaxf(box[3] - box[0], box[4] - box[1]), box[5] - box[2]);
+  const float cells = static_cast<float>(1 << bits);
+  const float scale = extent > 0.0f && extent < INFINITY ? cells / extent : 0.0f;
+  DPA4K_GRID_STRIDE(k, n_nodes) {
+    if (level[k] == kUnreached) {
+      key[k] = int64_t(1) << (3 * bits);
+      continue;
+    }
+    uint32_t q[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      q[i] = static_cast<uint32_t>(fminf(fmaxf((pos[3 * k + i] - box[i]) * scale, 0.0f), cells - 1.0f));
+    int64_t code = 0;
+    for (int b = 0; b < bits; ++b)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) code |= static_cast<int64_t>((q[i] >> b) & 1u) << (3 * b + (2 - i));
+    key[k] = code;
+  }
+}
+
+// perm, rank and the clamped in-degree of each position of perm.
+__global__ __launch_bounds__(256) void plan_perm_kernel(const int64_t* __restrict__ order,
+                                                        const int64_t* __restrict__ dst_offsets,
+                                                        int32_t* __restrict__ perm, int32_t* __restrict__ rank,
+                                                        int32_t* __restrict__ degree, int64_t n_nodes) {
+  DPA4K_GRID_STRIDE(i, n_nodes) {
+    const int64_t a = order[i];
+    perm[i] = static_cast<int32_t>(a);
+    rank[a] = static_cast<int32_t>(i);
+    degree[i] = static_cast<int32_t>(dst_offsets[a + 1] - dst_offsets[a]);
+  }
+}
+
+// Pieces of position i of perm: one per window of `rows` concatenated rows its segment meets.
+__global__ __launch_bounds__(256) void plan_piece_counts_kernel(const int32_t* __restrict__ cum,
+                                                                int32_t* __restrict__ count, int64_t n_nodes,
+                                                                int64_t rows) {
+  DPA4K_GRID_STRIDE(i, n_nodes) {
+    const int64_t begin = cum[i], end = cum[i + 1];
+    count[i] = end > begin ? static_cast<int32_t>((end - 1) / rows - begin / rows + 1) : 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_pieces_kernel(const int32_t* __restrict__ cum,
+                                                          const int32_t* __restrict__ piece_first,
+                                                          int32_t* __restrict__ piece_t,
+                                                          int32_t* __restrict__ blob_piece, int64_t n_nodes,
+                                                          int64_t rows, int64_t n_edges, int64_t blobs) {
+  DPA4K_GRID_STRIDE(i, n_nodes) {
+    const int64_t begin = cum[i], end = cum[i + 1];
+    if (end <= begin) continue;
+    const int64_t w0 = begin / rows;
+    for (int64_t w = w0; w <= (end - 1) / rows; ++w) {
+      const int64_t id = piece_first[i] + (w - w0);
+      const int64_t start = begin > w * rows ? begin : w * rows;
+      piece_t[id] = static_cast<int32_t>(start);
+      if (start == w * rows) blob_piece[w] = static_cast<int32_t>(id);
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int32_t pieces = piece_first[n_nodes];
+    piece_t[pieces] = static_cast<int32_t>(n_edges);
+    blob_piece[blobs] = pieces;
+  }
+}
+
+// Concatenated row of every edge, and the edge of every row.
+__global__ __launch_bounds__(256) void plan_rows_kernel(const int64_t* __restrict__ dst_offsets,
+                                                        const int32_t* __restrict__ rank,
+                                                        const int32_t* __restrict__ cum, int32_t* __restrict__ tpos,
+                                                        int32_t* __restrict__ row_edge, int64_t n_edges,
+                                                        int64_t n_nodes) {
+  DPA4K_GRID_STRIDE(e, n_edges) {
+    int64_t low = 0, high = n_nodes;  // the last atom k with dst_offsets[k] <= e
+    while (high - low > 1) {
+      const int64_t mid = (low + high) / 2;
+      if (dst_offsets[mid] <= e) low = mid; else high = mid;
+    }
+    const int64_t t = cum[rank[low]] + (e - dst_offsets[low]);
+    tpos[e] = static_cast<int32_t>(t);
+    row_edge[t] = static_cast<int32_t>(e);
+  }
+}
+
+// Blob of every source slot's edge; `blobs` for a slot whose src_order entry is out of range.
+__global__ __launch_bounds__(256) void plan_slot_keys_kernel(const int64_t* __restrict__ src_order,
+                                                             const int32_t* __restrict__ tpos,
+                                                             int64_t* __restrict__ key, int64_t n_edges, int64_t rows,
+                                                             int64_t blobs) {
+  DPA4K_GRID_STRIDE(q, n_edges) {
+    const int64_t e = src_order[q];
+    key[q] = static_cast<uint64_t>(e) < static_cast<uint64_t>(n_edges) ? tpos[e] / rows : blobs;
+  }
+}
+
+// Entries (slots sorted by blob, source atom, slot): their blob rows, and a
+// 1 where a record starts (a new blob or a new source atom).
+__global__ __launch_bounds__(256) void plan_entries_kernel(const int64_t* __restrict__ order,
+                                                           const int64_t* __restrict__ key,
+                                                           const int64_t* __restrict__ src_order,
+                                                           const int32_t* __restrict__ slot_atom,
+                                                           const int32_t* __restrict__ tpos,
+                                                           uint16_t* __restrict__ entry_row,
+                                                           int32_t* __restrict__ starts, int64_t n_edges, int64_t rows,
+                                                           int64_t blobs) {
+  DPA4K_GRID_STRIDE(j, n_edges) {
+    const int64_t q = order[j];
+    const int64_t blob = key[q];
+    const bool valid = blob < blobs;
+    entry_row[j] = valid ? static_cast<uint16_t>(tpos[src_order[q]] - blob * rows) : uint16_t(0);
+    bool start = valid;
+    if (valid && j > 0) {
+      const int64_t previous = order[j - 1];
+      start = key[previous] != blob || slot_atom[previous] != slot_atom[q];
+    }
+    starts[j] = start ? 1 : 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_records_kernel(const int32_t* __restrict__ starts,
+                                                           const int32_t* __restrict__ record_of,
+                                                           const int64_t* __restrict__ key_offsets,
+                                                           int32_t* __restrict__ rec_entry,
+                                                           int32_t* __restrict__ blob_rec,
+                                                           int32_t* __restrict__ blob_entry, int64_t n_edges,
+                                                           int64_t blobs) {
+  DPA4K_GRID_STRIDE(j, n_edges) {
+    if (starts[j]) rec_entry[record_of[j]] = static_cast<int32_t>(j);
+  }
+  DPA4K_GRID_STRIDE(b, blobs + 1) {
+    blob_rec[b] = record_of[key_offsets[b]];
+    blob_entry[b] = static_cast<int32_t>(key_offsets[b]);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) rec_entry[record_of[n_edges]] = static_cast<int32_t>(key_offsets[blobs]);
+}
+
+// Key of each record (in source order within its blob): its blob, then its
+// length descending; the record's length and source atom on the side.
+__global__ __launch_bounds__(256) void plan_length_keys_kernel(const int32_t* __restrict__ rec_old,
+                                                               const int64_t* __restrict__ order,
+                                                               const int64_t* __restrict__ slot_key,
+                                                               const int32_t* __restrict__ slot_atom,
+                                                               int64_t* __restrict__ key, int32_t* __restrict__ length,
+                                                               int32_t* __restrict__ rec_atom, int64_t records) {
+  DPA4K_GRID_STRIDE(r, records) {
+    const int32_t n = rec_old[r + 1] - rec_old[r];
+    const int64_t slot = order[rec_old[r]];
+    key[r] = slot_key[slot] * kLengthKeys + (kLengthKeys - 1 - (n < kLengthKeys - 1 ? n : kLengthKeys - 1));
+    length[r] = n;
+    rec_atom[r] = slot_atom[slot];
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_gather_i32_kernel(const int64_t* __restrict__ order,
+                                                              const int32_t* __restrict__ in,
+                                                              int32_t* __restrict__ out, int64_t n) {
+  DPA4K_GRID_STRIDE(k, n) out[k] = in[order[k]];
+}
+
+// Record k of the balanced order is old record order[k]: its entries move to
+// [first[k], first[k + 1]); the key of its source atom's position goes to key[k].
+__global__ __launch_bounds__(256) void plan_move_entries_kernel(const int64_t* __restrict__ order,
+                                                                const int32_t* __restrict__ rec_old,
+                                                                const uint16_t* __restrict__ entry_old,
+                                                                const int32_t* __restrict__ first,
+                                                                const int32_t* __restrict__ rec_atom,
+                                                                const int32_t* __restrict__ rank,
+                                                                uint16_t* __restrict__ entry_row,
+                                                                int32_t* __restrict__ rec_entry,
+                                                                int64_t* __restrict__ key, int64_t records) {
+  DPA4K_GRID_STRIDE(k, records) {
+    const int64_t old = order[k];
+    const int32_t from = rec_old[old], count = rec_old[old + 1] - from, to = first[k];
+    for (int32_t i = 0; i < count; ++i) entry_row[to + i] = entry_old[from + i];
+    rec_entry[k] = to;
+    key[k] = rank[rec_atom[old]];
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) rec_entry[records] = first[records];
+}
+
+// Records sorted stably by position.
+__global__ __launch_bounds__(256) void plan_record_slots_kernel(const int64_t* __restrict__ order,
+                                                                const int64_t* __restrict__ key_offsets,
+                                                                int32_t* __restrict__ pos_records,
+                                                                int32_t* __restrict__ pos_rec, int64_t records,
+                                                                int64_t n_nodes) {
+  DPA4K_GRID_STRIDE(k, records) pos_records[k] = static_cast<int32_t>(order[k]);
+  DPA4K_GRID_STRIDE(i, n_nodes + 1) pos_rec[i] = static_cast<int32_t>(key_offsets[i]);
+}
+
+// ---- the two passes of a planned call ----
+
+struct BlobView {
+  const int32_t *perm, *piece_first, *piece_t, *blob_piece, *blob_rec, *blob_entry, *row_edge, *rec_entry,
+      *pos_records, *pos_rec;
+  const uint16_t* entry_row;
+};
+
+template <typename T>
+__device__ __forceinline__ void store_record(T* __restrict__ out, const double (&acc)[12]) {
+  if constexpr (sizeof(T) == 4) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4* v = reinterpret_cast<f32x4*>(out);  // 48-byte records: 16-byte aligned
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      v[i] = f32x4{static_cast<float>(acc[4 * i]), static_cast<float>(acc[4 * i + 1]),
+                   static_cast<float>(acc[4 * i + 2]), static_cast<float>(acc[4 * i + 3])};
+  } else {
+    typedef double f64x2 __attribute__((ext_vector_type(2)));
+    f64x2* v = reinterpret_cast<f64x2*>(out);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) v[i] = f64x2{acc[2 * i], acc[2 * i + 1]};
+  }
+}
+
+// Destination sums of pieces [0, count) of a blob, kPieceLanes lanes per
+// piece: piece p covers the blob's LDS rows [bound(p) - t0, bound(p + 1) -
+// t0); lane l sums rows l, l + kPieceLanes, ... in order, then a fixed
+// butterfly adds the lanes.
+constexpr int kPieceLanes = 8;
+
+template <typename T, typename Bound>
+__device__ __forceinline__ void blob_pieces(const T* rows, int32_t count, int64_t t0, int32_t piece0, Bound bound,
+                                            double* __restrict__ dst_rec) {
+  const int group = threadIdx.x / kPieceLanes, sub = threadIdx.x % kPieceLanes;
+  for (int32_t p = group; p < count; p += kBlobThreads / kPieceLanes) {
+    const int32_t begin = static_cast<int32_t>(bound(p) - t0), end = static_cast<int32_t>(bound(p + 1) - t0);
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0;
+    for (int32_t row = begin + sub; row < end; row += kPieceLanes) {
+      s0 += static_cast<double>(rows[row * 6]);
+      s1 += static_cast<double>(rows[row * 6 + 1]);
+      s2 += static_cast<double>(rows[row * 6 + 2]);
+    }
+    s0 = group_sum<kPieceLanes>(s0);
+    s1 = group_sum<kPieceLanes>(s1);
+    s2 = group_sum<kPieceLanes>(s2);
+    if (sub < 3) dst_rec[static_cast<int64_t>(piece0 + p) * 3 + sub] = sub == 0 ? s0 : (sub == 1 ? s1 : s2);
+  }
+}
+
+// Twelve source sums of one record: entries [from, to), their blob rows from `row_of`.
+template <typename T, typename RowOf>
+__device__ __forceinline__ void blob_record(const T* rows, int32_t from, int32_t to, RowOf row_of,
+                                            T* __restrict__ out) {
+  double acc[12];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) acc[i] = 0.0;
+  int32_t j = from;
+  for (; j + 2 <= to; j += 2) {  // two entries' reads in flight; the sums stay in entry order
+    const T* a = rows + row_of(j) * 6;
+    const T* b = rows + row_of(j + 1) * 6;
+    const Row3<T> ga{a[0], a[1], a[2]}, va{a[3], a[4], a[5]}, gb{b[0], b[1], b[2]}, vb{b[3], b[4], b[5]};
+    add_source(acc, ga, va);
+    add_source(acc, gb, vb);
+  }
+  if (j < to) {
+    const T* a = rows + row_of(j) * 6;
+    add_source(acc, Row3<T>{a[0], a[1], a[2]}, Row3<T>{a[3], a[4], a[5]});
+  }
+  store_record(out, acc);
+}
+
+// Pass 1: one workgroup per blob.  Every global load of the blob is issued
+// before any LDS work: the rows' edge ids, the blob's entries and piece
+// bounds (contiguous in the plan), each thread's record bounds and slots,
+// then the rows (g_e, v_e) themselves (consecutive threads read consecutive
+// rows of a piece).  After one barrier eight lanes sum each piece's g and
+// each thread a record's twelve products (the records of a blob come
+// longest first, so a wave's records are of similar length), from LDS only,
+// and the record is stored at its id (a blob's records are contiguous).  A blob with more entries than rows
+// (src_order naming an edge twice) or more pieces than threads reads those
+// from the plan instead: a branch uniform over the workgroup, so the common
+// case's loops hold no global load.
+template <typename T>
+__global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __restrict__ grad_edge,
+                                                                  const T* __restrict__ edge_vec, BlobView plan,
+                                                                  double* __restrict__ dst_rec,
+                                                                  T* __restrict__ src_rec, int64_t n_edges,
+                                                                  int64_t blobs) {
+  constexpr int64_t kRows = blob_rows_of<T>();
+  constexpr int kRounds = static_cast<int>((kRows + kBlobThreads - 1) / kBlobThreads);
+  __shared__ T rows[kRows * 6];
+  __shared__ uint16_t entries[kRows];
+  __shared__ int32_t bounds[kBlobThreads];
+  // each XCD takes a contiguous range of blobs (so of atom positions): pass 2 on
+  // that XCD then reads the records its L2 received
+  const int64_t blob = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
+  if (blob >= blobs) return;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int64_t t0 = blob * kRows;
+  const int64_t count = n_edges - t0 < kRows ? n_edges - t0 : kRows;
+  const int32_t entry0 = plan.blob_entry[blob], entry_count = plan.blob_entry[blob + 1] - entry0;
+  const int32_t piece0 = plan.blob_piece[blob], piece_count = plan.blob_piece[blob + 1] - piece0;
+  const int32_t rec0 = plan.blob_rec[blob], rec1 = plan.blob_rec[blob + 1];
+  const bool staged_entries = entry_count <= kRows;
+  const bool staged_pieces = piece_count < kBlobThreads;
+
+  int32_t edge[kRounds], entry[kRounds], first[kRounds], last[kRounds];
+  const int32_t bound = plan.piece_t[piece0 + (tid <= piece_count ? tid : 0)];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int32_t i = r * kBlobThreads + tid;
+    edge[r] = plan.row_edge[t0 + (i < count ? i : count - 1)];
+    entry[r] = plan.entry_row[entry0 + (i < entry_count ? i : 0)];
+    const int32_t rec = rec0 + i < rec1 ? rec0 + i : rec0;
+    first[r] = plan.rec_entry[rec];
+    last[r] = plan.rec_entry[rec + 1];
+  }
+  Row3<T> g[kRounds], v[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    g[r] = load_row(grad_edge, edge[r]);
+    v[r] = load_row(edge_vec, edge[r]);
+  }
+  if (tid <= piece_count && staged_pieces) bounds[tid] = bound;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int32_t i = r * kBlobThreads + tid;
+    if (i < entry_count && staged_entries) entries[i] = static_cast<uint16_t>(entry[r]);
+    if (i < count) {
+      T* at = rows + i * 6;
+      at[0] = g[r].x; at[1] = g[r].y; at[2] = g[r].z;
+      at[3] = v[r].x; at[4] = v[r].y; at[5] = v[r].z;
+    }
+  }
+  __syncthreads();
+
+  if (staged_pieces)
+    blob_pieces(rows, piece_count, t0, piece0, [&](int32_t p) { return bounds[p]; }, dst_rec);
+  else
+    blob_pieces(rows, piece_count, t0, piece0, [&](int32_t p) { return plan.piece_t[piece0 + p]; }, dst_rec);
+
+  if (staged_entries) {
+    auto row_of = [&](int32_t j) { return static_cast<int32_t>(entries[j - entry0]); };
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      if (rec0 + r * kBlobThreads + tid < rec1)
+        blob_record(rows, first[r], last[r], row_of, src_rec + static_cast<int64_t>(rec0 + r * kBlobThreads + tid) * 12);
+    for (int32_t rec = rec0 + kRounds * kBlobThreads + tid; rec < rec1; rec += kBlobThreads)
+      blob_record(rows, plan.rec_entry[rec], plan.rec_entry[rec + 1], row_of, src_rec + static_cast<int64_t>(rec) * 12);
+  } else {
+    auto row_of = [&](int32_t j) { return static_cast<int32_t>(plan.entry_row[j]); };
+    for (int32_t rec = rec0 + tid; rec < rec1; rec += kBlobThreads)
+      blob_record(rows, plan.rec_entry[rec], plan.rec_entry[rec + 1], row_of, src_rec + static_cast<int64_t>(rec) * 12);
+  }
+}
+
+// Pass 2: kRecordLanes lanes per position of perm; lane c < 12 adds
+// component c of the position's pieces (c < 3) and of its records, in blob
+// order, and writes it for the atom.  The group loads up to kRecordLanes
+// record ids at once (one per lane) and then every record's 48 bytes.
+template <typename T>
+__global__ __launch_bounds__(256) void force_records_kernel(BlobView plan, const double* __restrict__ dst_rec,
+                                                            const T* __restrict__ src_rec, T* __restrict__ force,
+                                                            T* __restrict__ virial, int64_t n_nodes) {
+  const int64_t block = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
+  const int64_t i = block * (256 / kRecordLanes) + threadIdx.x / kRecordLanes;
+  if (i >= n_nodes) return;
+  const int c = threadIdx.x & (kRecordLanes - 1);
+  const int32_t atom = plan.perm[i];
+  const int32_t piece0 = plan.piece_first[i], piece1 = plan.piece_first[i + 1];
+  const int32_t rec0 = plan.pos_rec[i], rec1 = plan.pos_rec[i + 1];
+  const int cc = c < 12 ? c : 0;
+  double acc = 0.0;
+  for (int32_t p = piece0; p < piece1; ++p) acc += c < 3 ? dst_rec[static_cast<int64_t>(p) * 3 + c] : 0.0;
+  for (int32_t base = rec0; base < rec1; base += kRecordLanes) {
+    const int32_t here = rec1 - base < kRecordLanes ? rec1 - base : kRecordLanes;
+    const int32_t mine = plan.pos_records[base + (c < here ? c : 0)];
+    T part[kRecordLanes];
+#pragma unroll
+    for (int k = 0; k < kRecordLanes; ++k) {
+      const int32_t record = __shfl(mine, k < here ? k : 0, kRecordLanes);
+      part[k] = src_rec[static_cast<int64_t>(record) * 12 + cc];
+    }
+#pragma unroll
+    for (int k = 0; k < kRecordLanes; ++k) acc += k < here && c < 12 ? static_cast<double>(part[k]) : 0.0;
+  }
+  if (c < 3)
+    force[static_cast<int64_t>(atom) * 3 + c] = static_cast<T>(acc);
+  else if (c < 12)
+    virial[static_cast<int64_t>(atom) * 9 + (c - 3)] = static_cast<T>(acc);
 }
 
 int check_plan_shapes(int64_t n_edges, int64_t n_nodes, const char* what) {
   if (n_edges < 0) return fail(DPA4K_EINVAL, "%s: negative edge count", what);
   if (n_nodes <= 0) return fail(DPA4K_EINVAL, "%s requires at least one atom", what);
-  if (n_edges > int64_t(0x7fffffff)) return fail(DPA4K_EINVAL, "%s: more than 2^31 - 1 edges", what);
+  if (n_edges > int64_t(0x7fffffff) - 1) return fail(DPA4K_EINVAL, "%s: at least 2^31 - 1 edges", what);
+  if (n_nodes > int64_t(0x7fffffff) - 1) return fail(DPA4K_EINVAL, "%s: at least 2^31 - 1 atoms", what);
   return DPA4K_OK;
 }
 
+BlobView view_of(const BlobPlan& p) {
+  return BlobView{p.perm,     p.piece_first, p.piece_t,  p.blob_piece, p.blob_rec, p.blob_entry,
+                  p.row_edge, p.rec_entry,   p.pos_records, p.pos_rec, p.entry_row};
+}
+
 template <typename T>
-int run_planned(const T* grad_edge, const T* edge_vec, const int64_t* dst_offsets, const int64_t* src_offsets,
-                T* force, T* virial, int64_t n_edges, int64_t n_nodes, void* plan, size_t plan_bytes,
-                dpa4k_stream_t stream_handle) {
+int run_planned(const T* grad_edge, const T* edge_vec, T* force, T* virial, int64_t n_edges, int64_t n_nodes,
+                const void* plan, size_t plan_bytes, void* records, size_t records_bytes, int64_t n_records,
+                int64_t n_pieces, dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_plan_shapes(n_edges, n_nodes, "planned force assembly")) return s;
-  if (!grid_fits((n_nodes + kAtoms - 1) / kAtoms, kBlock))
-    return fail(DPA4K_EINVAL, "force assembly atom count exceeds the launch limit");
-  if (dst_offsets == nullptr || src_offsets == nullptr || force == nullptr || virial == nullptr || plan == nullptr ||
+  if (force == nullptr || virial == nullptr || plan == nullptr || records == nullptr ||
       (n_edges > 0 && (grad_edge == nullptr || edge_vec == nullptr)))
     return fail(DPA4K_EINVAL, "planned force assembly: null pointer");
-  if (plan_bytes < plan_bytes_for(n_edges, sizeof(T)))
-    return fail(DPA4K_EINVAL, "planned force assembly: plan of %zu bytes is smaller than %zu", plan_bytes,
-                plan_bytes_for(n_edges, sizeof(T)));
-  PlanArrays arrays;
-  if (!carve_plan(plan, plan_bytes, n_edges, sizeof(T), arrays))
+  const size_t needed = blob_plan_bytes(n_edges, n_nodes, sizeof(T));
+  if (plan_bytes < needed)
+    return fail(DPA4K_EINVAL, "planned force assembly: plan of %zu bytes is smaller than %zu", plan_bytes, needed);
+  if (n_records < 0 || n_records > n_edges || n_pieces < 0 || n_pieces > n_nodes + blob_count(n_edges, sizeof(T)))
+    return fail(DPA4K_EINVAL, "planned force assembly: record or piece count out of range");
+  const size_t records_needed = records_bytes_for(n_records, n_pieces, sizeof(T));
+  if (records_bytes < records_needed)
+    return fail(DPA4K_EINVAL, "planned force assembly: records buffer of %zu bytes is smaller than %zu",
+                records_bytes, records_needed);
+  BlobPlan arrays;
+  if (!carve_blob_plan(const_cast<void*>(plan), plan_bytes, n_edges, n_nodes, sizeof(T), arrays))
     return fail(DPA4K_EINVAL, "planned force assembly: plan too small");
   hipStream_t stream = as_stream(stream_handle);
-  T* rows = static_cast<T*>(arrays.rows);
-  if (n_edges > 0) {
-    force_place_rows_kernel<T><<<launch_grid((n_edges + 255) / 256, 256), 256, 0, stream>>>(
-        grad_edge, edge_vec, arrays.edge_row, rows, n_edges);
-    if (int s = launched("force_place_rows_kernel")) return s;
+  if (n_edges == 0) {
+    if (int s = zero_fill(force, static_cast<size_t>(n_nodes) * 3 * sizeof(T), stream)) return s;
+    return zero_fill(virial, static_cast<size_t>(n_nodes) * 9 * sizeof(T), stream);
   }
-  const dim3 grid = launch_grid((n_nodes + kAtoms - 1) / kAtoms, kBlock);
-  if (6 * n_edges * static_cast<int64_t>(sizeof(T)) < (int64_t(1) << 31))
-    force_assembly_kernel<T, true, true><<<grid, kBlock, 0, stream>>>(
-        grad_edge, edge_vec, dst_offsets, src_offsets, nullptr, arrays.src_pos, rows, force, virial, n_edges, n_nodes);
-  else
-    force_assembly_kernel<T, false, true><<<grid, kBlock, 0, stream>>>(
-        grad_edge, edge_vec, dst_offsets, src_offsets, nullptr, arrays.src_pos, rows, force, virial, n_edges, n_nodes);
-  return launched("force_assembly_kernel");
+  Carver carver{static_cast<char*>(records), records_bytes};
+  double* dst_rec = carver.take<double>(static_cast<size_t>(n_pieces > 0 ? n_pieces : 1) * 3);
+  T* src_rec = carver.take<T>(static_cast<size_t>(n_records > 0 ? n_records : 1) * 12);
+  const BlobView view = view_of(arrays);
+  const int64_t blobs = blob_count(n_edges, sizeof(T));
+  force_blob_kernel<T><<<launch_grid(blobs, kBlobThreads), kBlobThreads, 0, stream>>>(
+      grad_edge, edge_vec, view, dst_rec, src_rec, n_edges, blobs);
+  if (int s = launched("force_blob_kernel")) return s;
+  const int64_t groups = (n_nodes + (256 / kRecordLanes) - 1) / (256 / kRecordLanes);
+  force_records_kernel<T><<<launch_grid(groups, 256), 256, 0, stream>>>(view, dst_rec, src_rec, force, virial,
+                                                                          n_nodes);
+  return launched("force_records_kernel");
+}
+
+int read_back(const int32_t* device, int32_t* host, size_t count, hipStream_t stream) {
+  if (int s = hip_status(hipMemcpyAsync(host, device, count * 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync"))
+    return s;
+  return hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize");
+}
+
+template <typename T>
+int build_plan(const int64_t* dst_offsets, const int64_t* src_offsets, const int64_t* src_order, const T* edge_vec,
+               int64_t n_edges, int64_t n_nodes, const BlobPlan& plan, const BuildScratch& w, int64_t* counts_out,
+               hipStream_t stream) {
+  const int64_t rows = blob_rows_of<T>();
+  const int64_t blobs = blob_count(n_edges, sizeof(T));
+  const unsigned int node_blocks = stride_blocks(n_nodes + 1), edge_blocks = stride_blocks(n_edges);
+  // validity of both CSRs, and the breadth-first root
+  fill_i32_kernel<<<1, 256, 0, stream>>>(w.flags, kMaxLevels + 8, 0);
+  if (int s = launched("fill_i32_kernel")) return s;
+  plan_check_kernel<<<node_blocks, 256, 0, stream>>>(dst_offsets, src_offsets, n_edges, n_nodes, w.flags);
+  if (int s = launched("plan_check_kernel")) return s;
+  int32_t head[2];
+  if (int s = read_back(w.flags, head, 2, stream)) return s;
+  if (head[0] != 0) return fail(DPA4K_EINVAL, "force assembly plan: the offsets are not a CSR of n_edges slots");
+
+  fill_i32_kernel<<<edge_blocks, 256, 0, stream>>>(w.edge_src, n_edges, -1);
+  if (int s = launched("fill_i32_kernel")) return s;
+  plan_slot_atoms_kernel<<<edge_blocks, 256, 0, stream>>>(src_offsets, src_order, w.slot_atom, w.edge_src, n_edges,
+                                                          n_nodes);
+  if (int s = launched("plan_slot_atoms_kernel")) return s;
+
+  // positions along a breadth-first tree (edge_vec given), then Morton keys
+  plan_bfs_init_kernel<<<node_blocks, 256, 0, stream>>>(w.level, w.pos, w.flags, n_nodes);
+  if (int s = launched("plan_bfs_init_kernel")) return s;
+  if (edge_vec != nullptr) {
+    for (int depth = 0; depth < kMaxLevels; ++depth) {
+      plan_bfs_level_kernel<T><<<node_blocks, 256, 0, stream>>>(dst_offsets, w.edge_src, edge_vec, w.level, w.pos,
+                                                                w.flags, depth, n_nodes);
+      if (int s = launched("plan_bfs_level_kernel")) return s;
+      if (depth % 8 == 7) {
+        int32_t progress;
+        if (int s = read_back(w.flags + 8 + depth, &progress, 1, stream)) return s;
+        if (progress == 0) break;
+      }
+    }
+  }
+  plan_box_kernel<<<kBoxBlocks, 256, 0, stream>>>(w.pos, w.level, n_nodes, w.box_part);
+  if (int s = launched("plan_box_kernel")) return s;
+  plan_box_final_kernel<<<1, 256, 0, stream>>>(w.box_part, kBoxBlocks, w.box);
+  if (int s = launched("plan_box_final_kernel")) return s;
+  const int bits = morton_bits(n_nodes);
+  plan_morton_kernel<<<node_blocks, 256, 0, stream>>>(w.pos, w.level, w.box, n_nodes, bits, w.key);
+  if (int s = launched("plan_morton_kernel")) return s;
+  if (int s = dpa4k_group_by_key_async(w.key, n_nodes, (int64_t(1) << (3 * bits)) + 1, w.order, w.key_offsets,
+                                       w.sort_status, w.sort, w.sort_bytes, stream))
+    return s;
+  plan_perm_kernel<<<node_blocks, 256, 0, stream>>>(w.order, dst_offsets, plan.perm, w.rank, w.counts, n_nodes);
+  if (int s = launched("plan_perm_kernel")) return s;
+  if (int s = scan_exclusive(w.counts, w.cum, n_nodes, w.scan_blocks, stream)) return s;
+
+  // pieces and rows
+  plan_piece_counts_kernel<<<node_blocks, 256, 0, stream>>>(w.cum, w.counts, n_nodes, rows);
+  if (int s = launched("plan_piece_counts_kernel")) return s;
+  if (int s = scan_exclusive(w.counts, plan.piece_first, n_nodes, w.scan_blocks, stream)) return s;
+  plan_pieces_kernel<<<node_blocks, 256, 0, stream>>>(w.cum, plan.piece_first, plan.piece_t, plan.blob_piece, n_nodes,
+                                                      rows, n_edges, blobs);
+  if (int s = launched("plan_pieces_kernel")) return s;
+  plan_rows_kernel<<<edge_blocks, 256, 0, stream>>>(dst_offsets, w.rank, w.cum, w.tpos, plan.row_edge, n_edges,
+                                                    n_nodes);
+  if (int s = launched("plan_rows_kernel")) return s;
+
+  // entries and records
+  plan_slot_keys_kernel<<<edge_blocks, 256, 0, stream>>>(src_order, w.tpos, w.key, n_edges, rows, blobs);
+  if (int s = launched("plan_slot_keys_kernel")) return s;
+  if (int s = dpa4k_group_by_key_async(w.key, n_edges, blobs + 1, w.order, w.key_offsets, w.sort_status, w.sort,
+                                       w.sort_bytes, stream))
+    return s;
+  plan_entries_kernel<<<edge_blocks, 256, 0, stream>>>(w.order, w.key, src_order, w.slot_atom, w.tpos,
+                                                       w.entry_old, w.counts, n_edges, rows, blobs);
+  if (int s = launched("plan_entries_kernel")) return s;
+  if (int s = scan_exclusive(w.counts, w.scanned, n_edges, w.scan_blocks, stream)) return s;
+  plan_records_kernel<<<edge_blocks, 256, 0, stream>>>(w.counts, w.scanned, w.key_offsets, w.rec_old,
+                                                       plan.blob_rec, plan.blob_entry, n_edges, blobs);
+  if (int s = launched("plan_records_kernel")) return s;
+  int32_t records, pieces;
+  if (int s = read_back(w.scanned + n_edges, &records, 1, stream)) return s;
+  if (int s = read_back(plan.piece_first + n_nodes, &pieces, 1, stream)) return s;
+
+  // each blob's records by descending length (stable), their entries moved to match
+  const unsigned int record_blocks = stride_blocks(records);
+  plan_length_keys_kernel<<<record_blocks, 256, 0, stream>>>(w.rec_old, w.order, w.key, w.slot_atom, w.key2,
+                                                             w.lengths, w.tpos, records);
+  if (int s = launched("plan_length_keys_kernel")) return s;
+  if (int s = dpa4k_group_by_key_async(w.key2, records, blobs * kLengthKeys, w.order, w.key_offsets, w.sort_status,
+                                       w.sort, w.sort_bytes, stream))
+    return s;
+  plan_gather_i32_kernel<<<record_blocks, 256, 0, stream>>>(w.order, w.lengths, w.counts, records);
+  if (int s = launched("plan_gather_i32_kernel")) return s;
+  if (int s = scan_exclusive(w.counts, w.scanned, records, w.scan_blocks, stream)) return s;
+  plan_move_entries_kernel<<<record_blocks, 256, 0, stream>>>(w.order, w.rec_old, w.entry_old, w.scanned, w.tpos,
+                                                              w.rank, plan.entry_row, plan.rec_entry, w.key, records);
+  if (int s = launched("plan_move_entries_kernel")) return s;
+
+  // record ids grouped by position (stable: blob order within a position)
+  if (int s = dpa4k_group_by_key_async(w.key, records, n_nodes, w.order, w.key_offsets, w.sort_status, w.sort,
+                                       w.sort_bytes, stream))
+    return s;
+  plan_record_slots_kernel<<<stride_blocks(records > n_nodes + 1 ? records : n_nodes + 1), 256, 0, stream>>>(
+      w.order, w.key_offsets, plan.pos_records, plan.pos_rec, records, n_nodes);
+  if (int s = launched("plan_record_slots_kernel")) return s;
+  counts_out[0] = records;
+  counts_out[1] = pieces;
+  return hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
 
 }  // namespace
@@ -547,74 +1252,66 @@ extern "C" int dpa4k_force_assembly_f64(const double* grad_edge, const double* e
 }
 
 extern "C" size_t dpa4k_force_assembly_plan_size(int64_t n_edges, int64_t n_nodes, int64_t value_bytes) {
-  (void)n_nodes;
-  if (n_edges < 0 || (value_bytes != 4 && value_bytes != 8)) return 0;
-  return dpa4k::plan_bytes_for(n_edges, value_bytes);
+  if (n_edges < 0 || n_nodes <= 0 || (value_bytes != 4 && value_bytes != 8)) return 0;
+  return dpa4k::blob_plan_bytes(n_edges, n_nodes, value_bytes);
 }
 
 extern "C" size_t dpa4k_force_assembly_plan_workspace_size(int64_t n_edges, int64_t n_nodes) {
-  using namespace dpa4k;
   if (n_edges < 0 || n_nodes <= 0) return 0;
-  const PlanShape shape = plan_shape(n_edges, n_nodes);
-  const size_t count = static_cast<size_t>(n_edges > 0 ? n_edges : 1);
-  const size_t cells = static_cast<size_t>(shape.tiles * shape.buckets);
-  return 2 * round_up_256(count * 8) + round_up_256((cells + 1) * 8) + round_up_256(4) +
-         round_up_256(plan_sort_bytes(n_edges, shape));
+  return dpa4k::build_workspace_bytes(n_edges, n_nodes);
 }
 
-extern "C" int dpa4k_force_assembly_plan(const int64_t* src_offsets, const int64_t* src_order, int64_t n_edges,
+extern "C" size_t dpa4k_force_assembly_records_size(int64_t n_records, int64_t n_pieces, int64_t value_bytes) {
+  if (n_records < 0 || n_pieces < 0 || (value_bytes != 4 && value_bytes != 8)) return 0;
+  return dpa4k::records_bytes_for(n_records, n_pieces, value_bytes);
+}
+
+extern "C" int dpa4k_force_assembly_plan(const int64_t* dst_offsets, const int64_t* src_offsets,
+                                         const int64_t* src_order, const void* edge_vec, int64_t n_edges,
                                          int64_t n_nodes, int64_t value_bytes, void* plan, size_t plan_bytes,
-                                         void* workspace, size_t workspace_bytes, dpa4k_stream_t stream_handle) {
+                                         void* workspace, size_t workspace_bytes, int64_t* counts,
+                                         dpa4k_stream_t stream_handle) {
   using namespace dpa4k;
   clear_error();
   if (int s = check_plan_shapes(n_edges, n_nodes, "force assembly plan")) return s;
   if (value_bytes != 4 && value_bytes != 8) return fail(DPA4K_EINVAL, "force assembly plan: values of 4 or 8 bytes");
-  if (src_offsets == nullptr || plan == nullptr || (n_edges > 0 && src_order == nullptr))
+  if (dst_offsets == nullptr || src_offsets == nullptr || plan == nullptr || counts == nullptr ||
+      (n_edges > 0 && src_order == nullptr))
     return fail(DPA4K_EINVAL, "force assembly plan: null pointer");
-  const size_t needed = dpa4k_force_assembly_plan_size(n_edges, n_nodes, value_bytes);
+  const size_t needed = blob_plan_bytes(n_edges, n_nodes, value_bytes);
   if (plan_bytes < needed)
     return fail(DPA4K_EINVAL, "force assembly plan: buffer of %zu bytes is smaller than %zu", plan_bytes, needed);
-  const size_t scratch_needed = dpa4k_force_assembly_plan_workspace_size(n_edges, n_nodes);
+  const size_t scratch_needed = build_workspace_bytes(n_edges, n_nodes);
   if (workspace == nullptr || workspace_bytes < scratch_needed)
     return fail(DPA4K_EWORKSPACE, "force assembly plan: workspace of %zu bytes is smaller than %zu", workspace_bytes,
                 scratch_needed);
+  counts[0] = counts[1] = 0;
   if (n_edges == 0) return DPA4K_OK;
-  const PlanShape shape = plan_shape(n_edges, n_nodes);
-  PlanArrays arrays;
-  PlanScratch scratch;
-  if (!carve_plan(plan, plan_bytes, n_edges, value_bytes, arrays) ||
-      !carve_scratch(workspace, workspace_bytes, n_edges, shape, scratch))
+  BlobPlan arrays;
+  BuildScratch scratch;
+  if (!carve_blob_plan(plan, plan_bytes, n_edges, n_nodes, value_bytes, arrays) ||
+      !carve_build(workspace, workspace_bytes, n_edges, n_nodes, scratch))
     return fail(DPA4K_EINVAL, "force assembly plan: buffers too small");
   hipStream_t stream = as_stream(stream_handle);
-  const unsigned int blocks = grid_stride_blocks(n_edges);
-  plan_default_keys_kernel<<<blocks, 256, 0, stream>>>(scratch.key, n_edges, shape.buckets);
-  if (int s = launched("plan_default_keys_kernel")) return s;
-  plan_source_keys_kernel<<<blocks, 256, 0, stream>>>(src_offsets, src_order, scratch.key, n_edges, n_nodes,
-                                                      shape.buckets, shape.bucket_atoms);
-  if (int s = launched("plan_source_keys_kernel")) return s;
-  // keys lie in [0, tiles * buckets) by construction: the status word is not read
-  if (int s = dpa4k_group_by_key_async(scratch.key, n_edges, shape.tiles * shape.buckets, scratch.order,
-                                       scratch.tile_offsets, scratch.status, scratch.sort, scratch.sort_bytes,
-                                       stream_handle))
-    return s;
-  plan_rows_kernel<<<blocks, 256, 0, stream>>>(scratch.order, arrays.edge_row, n_edges);
-  if (int s = launched("plan_rows_kernel")) return s;
-  plan_source_positions_kernel<<<blocks, 256, 0, stream>>>(src_order, arrays.edge_row, arrays.src_pos, n_edges);
-  return launched("plan_source_positions_kernel");
+  if (value_bytes == 4)
+    return build_plan<float>(dst_offsets, src_offsets, src_order, static_cast<const float*>(edge_vec), n_edges,
+                             n_nodes, arrays, scratch, counts, stream);
+  return build_plan<double>(dst_offsets, src_offsets, src_order, static_cast<const double*>(edge_vec), n_edges,
+                            n_nodes, arrays, scratch, counts, stream);
 }
 
-extern "C" int dpa4k_force_assembly_f32_planned(const float* grad_edge, const float* edge_vec,
-                                                const int64_t* dst_offsets, const int64_t* src_offsets,
-                                                float* force, float* virial, int64_t n_edges, int64_t n_nodes,
-                                                void* plan, size_t plan_bytes, dpa4k_stream_t stream) {
-  return dpa4k::run_planned<float>(grad_edge, edge_vec, dst_offsets, src_offsets, force, virial, n_edges, n_nodes,
-                                   plan, plan_bytes, stream);
+extern "C" int dpa4k_force_assembly_f32_planned(const float* grad_edge, const float* edge_vec, float* force,
+                                                float* virial, int64_t n_edges, int64_t n_nodes, const void* plan,
+                                                size_t plan_bytes, void* records, size_t records_bytes,
+                                                int64_t n_records, int64_t n_pieces, dpa4k_stream_t stream) {
+  return dpa4k::run_planned<float>(grad_edge, edge_vec, force, virial, n_edges, n_nodes, plan, plan_bytes, records,
+                                   records_bytes, n_records, n_pieces, stream);
 }
 
-extern "C" int dpa4k_force_assembly_f64_planned(const double* grad_edge, const double* edge_vec,
-                                                const int64_t* dst_offsets, const int64_t* src_offsets,
-                                                double* force, double* virial, int64_t n_edges, int64_t n_nodes,
-                                                void* plan, size_t plan_bytes, dpa4k_stream_t stream) {
-  return dpa4k::run_planned<double>(grad_edge, edge_vec, dst_offsets, src_offsets, force, virial, n_edges, n_nodes,
-                                    plan, plan_bytes, stream);
+extern "C" int dpa4k_force_assembly_f64_planned(const double* grad_edge, const double* edge_vec, double* force,
+                                                double* virial, int64_t n_edges, int64_t n_nodes, const void* plan,
+                                                size_t plan_bytes, void* records, size_t records_bytes,
+                                                int64_t n_records, int64_t n_pieces, dpa4k_stream_t stream) {
+  return dpa4k::run_planned<double>(grad_edge, edge_vec, force, virial, n_edges, n_nodes, plan, plan_bytes, records,
+                                    records_bytes, n_records, n_pieces, stream);
 }

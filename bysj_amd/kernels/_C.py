@@ -393,43 +393,73 @@ def segment_softmax_backward(alpha, grad_alpha, env, offsets, null_alpha=None,
 # ---------------------------------------------------------------------------
 
 class ForcePlan:
-    """Bucket layout of one source grouping for the planned force assembly.
+    """Blob layout of one graph for the planned force assembly.
 
-    Built once per graph by :func:`force_assembly_plan`; it holds the row
-    buffer the planned kernels write on every call, so calls that share a
-    plan must not overlap (one stream at a time).
+    Built once per graph by :func:`force_assembly_plan`.  ``records`` is the
+    buffer the planned kernels write on every call (per-piece destination
+    sums and per-record source sums), so calls that share a plan must not
+    overlap (one stream at a time).  ``fingerprint`` identifies the offsets
+    and ``src_order`` tensors the plan describes; a plan is refused for any
+    other (another storage, size or in-place version).
     """
 
-    __slots__ = ("buffer", "n_edges", "n_nodes", "value_bytes")
+    __slots__ = ("plan", "records", "n_edges", "n_nodes", "value_bytes", "n_records", "n_pieces", "fingerprint")
 
-    def __init__(self, buffer: torch.Tensor, n_edges: int, n_nodes: int, value_bytes: int):
-        self.buffer, self.n_edges, self.n_nodes, self.value_bytes = buffer, n_edges, n_nodes, value_bytes
+    def __init__(self, plan: torch.Tensor, records: torch.Tensor, n_edges: int, n_nodes: int, value_bytes: int,
+                 n_records: int, n_pieces: int, fingerprint):
+        self.plan, self.records = plan, records
+        self.n_edges, self.n_nodes, self.value_bytes = n_edges, n_nodes, value_bytes
+        self.n_records, self.n_pieces, self.fingerprint = n_records, n_pieces, fingerprint
 
 
-def force_assembly_plan(src_offsets, src_order, *, value_bytes: int = 8) -> ForcePlan:
-    """Plan of ``(src_offsets, src_order)`` for float32 (value_bytes 4) or both dtypes (8); no host sync."""
-    nodes = _offsets(src_offsets, "force assembly src_offsets")
+def _force_fingerprint(dst_offsets, src_offsets, src_order):
+    return tuple(_offsets_fingerprint(t) for t in (dst_offsets, src_offsets, src_order))
+
+
+def force_assembly_plan(dst_offsets, src_offsets, src_order, edge_vec=None, *, value_bytes: int = 4) -> ForcePlan:
+    """Blob plan of a graph for float32 (value_bytes 4) or float64 (8) values; synchronises the device.
+
+    ``edge_vec`` is a geometry hint: atom positions are recovered from it
+    along a breadth-first tree to order the atoms in space (``None`` keeps
+    the natural order).  Results do not depend on it, only the speed does.
+    """
+    nodes = _offsets(dst_offsets, "force assembly dst_offsets")
+    _check(_offsets(src_offsets, "force assembly src_offsets") == nodes,
+           "force assembly offsets must describe the same atom count")
     _i64(src_order, "force assembly src_order")
     _check(src_order.dim() == 1, "force assembly src_order must be one-dimensional")
     _check(nodes > 0, "force assembly requires at least one atom")
     _check(value_bytes in (4, 8), "force assembly plan: value_bytes must be 4 or 8")
-    _same_device(src_offsets, src_order)
+    _same_device(dst_offsets, src_offsets, src_order)
     edges = int(src_order.numel())
+    hint = 0
+    if edge_vec is not None:
+        _check(isinstance(edge_vec, torch.Tensor) and edge_vec.is_contiguous() and edge_vec.dim() == 2
+               and tuple(edge_vec.shape) == (edges, 3) and edge_vec.element_size() == value_bytes
+               and edge_vec.dtype in (torch.float32, torch.float64),
+               "force assembly plan: edge_vec must be a contiguous (n_edges, 3) tensor of the plan's dtype")
+        _same_device(src_order, edge_vec)
+        hint = edge_vec.data_ptr()
     nbytes = int(_LIB.dpa4k_force_assembly_plan_size(edges, nodes, value_bytes))
-    buffer = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=src_order.device)
+    plan = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=src_order.device)
     scratch_bytes = int(_LIB.dpa4k_force_assembly_plan_workspace_size(edges, nodes))
     workspace = _workspace(scratch_bytes, src_order.device)
+    counts = (_lib.ctypes.c_int64 * 2)()
     with _on(src_order.device) as stream:
         status = _LIB.dpa4k_force_assembly_plan(
-            src_offsets.data_ptr(), _ptr(src_order), edges, nodes, value_bytes, buffer.data_ptr(), nbytes,
-            workspace.data_ptr(), scratch_bytes, stream,
+            dst_offsets.data_ptr(), src_offsets.data_ptr(), _ptr(src_order), hint, edges, nodes, value_bytes,
+            plan.data_ptr(), nbytes, workspace.data_ptr(), scratch_bytes, counts, stream,
         )
-    _lib.check(status)
-    return ForcePlan(buffer, edges, nodes, value_bytes)
+    _lib.check(status, index_error=True)  # offsets that are not CSRs of the edge list: ValueError
+    n_records, n_pieces = int(counts[0]), int(counts[1])
+    records_bytes = int(_LIB.dpa4k_force_assembly_records_size(n_records, n_pieces, value_bytes))
+    records = torch.empty(max(records_bytes, 1), dtype=torch.uint8, device=src_order.device)
+    return ForcePlan(plan, records, edges, nodes, value_bytes, n_records, n_pieces,
+                     _force_fingerprint(dst_offsets, src_offsets, src_order))
 
 
 def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, *, plan=None):
-    """``(force, virial)``; with a :class:`ForcePlan` of this grouping the bucketed two-pass kernels run."""
+    """``(force, virial)``; with a :class:`ForcePlan` of this graph the blob kernels run."""
     for name, tensor in (("grad_edge", grad_edge), ("edge_vec", edge_vec)):
         _check(isinstance(tensor, torch.Tensor) and tensor.is_cuda and tensor.is_contiguous()
                and tensor.dtype in (torch.float32, torch.float64),
@@ -450,13 +480,14 @@ def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, *, 
     single = grad_edge.dtype == torch.float32
     if plan is not None:
         _check(isinstance(plan, ForcePlan) and plan.n_edges == edges and plan.n_nodes == nodes
-               and plan.buffer.device == grad_edge.device and plan.value_bytes >= grad_edge.element_size(),
+               and plan.plan.device == grad_edge.device and plan.value_bytes == grad_edge.element_size()
+               and plan.fingerprint == _force_fingerprint(dst_offsets, src_offsets, src_order),
                "force assembly plan was built for another graph, device or dtype")
         entry = _LIB.dpa4k_force_assembly_f32_planned if single else _LIB.dpa4k_force_assembly_f64_planned
         with _on(grad_edge.device) as stream:
-            status = entry(_ptr(grad_edge), _ptr(edge_vec), dst_offsets.data_ptr(), src_offsets.data_ptr(),
-                           force.data_ptr(), virial.data_ptr(), edges, nodes, plan.buffer.data_ptr(),
-                           plan.buffer.numel(), stream)
+            status = entry(_ptr(grad_edge), _ptr(edge_vec), force.data_ptr(), virial.data_ptr(), edges, nodes,
+                           plan.plan.data_ptr(), plan.plan.numel(), plan.records.data_ptr(), plan.records.numel(),
+                           plan.n_records, plan.n_pieces, stream)
         _lib.check(status)
         return force, virial
     entry = _LIB.dpa4k_force_assembly_f32 if single else _LIB.dpa4k_force_assembly_f64

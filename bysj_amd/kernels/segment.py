@@ -417,45 +417,51 @@ def segment_softmax(logit, env, offsets, null_logit=None, *, order=None, check_g
 
 
 class _ForcePlanCache:
-    """Planned-path layouts of source groupings, kept per ``src_order`` tensor object.
+    """Blob plans of force graphs, kept per ``src_order`` tensor object and dtype.
 
-    The planned force assembly (a once-per-graph bucket layout, then two
-    passes per call; same bits as the direct kernel) pays off for float32
-    rows when atom numbering has no spatial locality: the direct kernel's
-    source side is then a random gather of 12-byte rows.  With locality the
-    direct kernel is faster, so the first float32 call on a grouping
-    measures it -- the share of consecutive source slots whose edges lie
-    within LOCAL_SPAN of each other, one host synchronisation -- and builds a
-    plan only below ``LOCAL_SHARE``.  Entries follow ``src_order`` and
-    ``src_offsets`` like the CSR caches: keyed by object identity, dropped
-    when either is written in place or ``src_order`` is freed.  Graphs under
-    ``MIN_EDGES`` edges, inference tensors and calls during HIP graph capture
-    without a cached entry use the direct kernel.
+    The planned force assembly (a once-per-graph blob layout, then two
+    streaming passes per call) replaces the direct kernel's gathers of
+    12- or 24-byte source rows, which cost a cache line each when atom
+    numbering has no spatial locality and still bound the kernel by its load
+    latency when it has.  The first call on a graph builds the plan, using
+    that call's ``edge_vec`` to order the atoms in space (one build: a few
+    host synchronisations), and keeps it when the blobs are compact: at
+    least ``MIN_EDGES_PER_RECORD`` edges per record on average (the records
+    are what the planned path writes and reads back).  Otherwise, and for
+    graphs under ``MIN_EDGES`` edges, inference tensors and calls during HIP
+    graph capture without a cached entry, the direct kernel runs.  Entries
+    follow the three graph tensors like the CSR caches: keyed by object
+    identity, dropped when one is written in place or ``src_order`` is freed.
     """
 
-    LOCAL_SPAN = 4096
-    LOCAL_SHARE = 0.5
     MIN_EDGES = 1 << 16
+    MIN_EDGES_PER_RECORD = 3.0
 
     def __init__(self):
-        self._entries: dict[int, tuple] = {}
+        self._entries: dict[tuple, tuple] = {}
 
-    def get(self, native, src_offsets: torch.Tensor, src_order: torch.Tensor):
+    def get(self, native, dst_offsets: torch.Tensor, src_offsets: torch.Tensor, src_order: torch.Tensor,
+            edge_vec: torch.Tensor):
         edges = int(src_order.numel())
         if edges < self.MIN_EDGES or not src_order.is_cuda:
             return None
-        order_stamp, offsets_stamp = version_stamp(src_order), version_stamp(src_offsets)
-        if order_stamp is None or offsets_stamp is None:
+        stamps = tuple(version_stamp(t) for t in (src_order, src_offsets, dst_offsets))
+        if any(stamp is None for stamp in stamps):
             return None
-        key = id(src_order)
+        key = (id(src_order), edge_vec.dtype)
         entry = self._entries.get(key)
-        stamp = (order_stamp, offsets_stamp, id(src_offsets))
+        stamp = stamps + (id(src_offsets), id(dst_offsets))
         if entry is not None and entry[0]() is src_order and entry[1] == stamp:
             return entry[2]
         if torch.cuda.is_current_stream_capturing():
             return None
-        local = ((src_order[1:] - src_order[:-1]).abs() < self.LOCAL_SPAN).float().mean().item()
-        plan = native.force_assembly_plan(src_offsets, src_order, value_bytes=4) if local < self.LOCAL_SHARE else None
+        try:
+            plan = native.force_assembly_plan(dst_offsets, src_offsets, src_order, edge_vec,
+                                              value_bytes=edge_vec.element_size())
+        except ValueError:  # not a pair of CSRs of the edge list: the direct kernel clamps such offsets
+            plan = None
+        if plan is not None and edges < self.MIN_EDGES_PER_RECORD * max(plan.n_records, 1):
+            plan = None
         reference = weakref.ref(src_order, lambda _, key=key: self._entries.pop(key, None))
         self._entries[key] = (reference, stamp, plan)
         return plan
@@ -473,9 +479,10 @@ def force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None,
     ``src_order``/``src_offsets`` group the edges by source; when omitted they
     are derived from ``src`` with :func:`group_by_source` (cache them when this
     runs every step).  float32 in/out as in the reference; float64 inputs give
-    float64 outputs.  For float32 on a graph whose atom numbering has no
-    spatial locality, the first call builds a bucket layout of the grouping
-    and later calls run the planned kernels (identical results).
+    float64 outputs.  On a graph of at least 65,536 edges the first call
+    builds a blob plan of the graph (ordered in space with that call's
+    ``edge_vec``) and later calls run the planned kernels: the same sums in
+    another fixed order, reproducible run to run.
     """
     n_nodes = int(dst_offsets.numel()) - 1
     if src_order is None or src_offsets is None:
@@ -485,10 +492,9 @@ def force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None,
     _validate_force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
     require_dcu(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
     native = _extension("force_assembly")
-    if grad_edge.dtype == torch.float32:
-        plan = _FORCE_PLANS.get(native, src_offsets, src_order)
-        if plan is not None:
-            return native.force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, plan=plan)
+    plan = _FORCE_PLANS.get(native, dst_offsets, src_offsets, src_order, edge_vec)
+    if plan is not None:
+        return native.force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, plan=plan)
     return native.force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order)
 
 

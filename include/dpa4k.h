@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 8
+#define DPA4K_ABI_VERSION 9
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -235,46 +235,57 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
                              double* virial, int64_t n_edges, int64_t n_nodes,
                              dpa4k_stream_t stream);
 
-/* Planned force assembly (no reference counterpart; same outputs as the two
- * entry points above, bit for bit).  A plan of one source grouping
- * (src_offsets + src_order) is built once per graph, on `stream` without a
- * host synchronisation: the atoms fall into <= 256 contiguous buckets and
- * the edges into tiles of 8192, and the plan records where each edge's row
- * (g_e, v_e) goes in a row buffer sorted by (tile, source bucket).  A
- * planned call then streams grad_edge and edge_vec once into that buffer
- * (each tile's rows land inside the tile's own stretch of it) and gathers
- * each atom's source rows from it: a bucket's rows lie in one short run per
- * tile, in place of random 12-byte gathers from the whole inputs.  Pays off
- * when atom numbering is not spatially ordered and for float32 rows;
- * measured slower than the direct kernel for spatially ordered atoms and
- * for float64.  The plan also holds that row buffer: calls sharing a
- * plan must not overlap.  value_bytes = 4 (float32 only) or 8 (both dtypes).
- * E < 2^31, N >= 1.  The plan needs dpa4k_force_assembly_plan_size bytes
- * (about (8 + 6 * value_bytes) * E) and its build a workspace of
- * dpa4k_force_assembly_plan_workspace_size bytes. */
+/* Planned force assembly (no reference counterpart; same sums as the two
+ * entry points above, in another fixed order: equal to them within rounding,
+ * and reproducible run to run).  A plan of one graph (both CSRs and
+ * src_order) is built once:
+ *   - atom positions are recovered from `edge_vec` (a hint: r_dst = r_src -
+ *     v_e along a breadth-first tree; NULL keeps the natural atom order) and
+ *     the atoms are sorted by their Morton cell;
+ *   - the destination segments, concatenated in that order, are cut into
+ *     blobs of 2816 (float32) or 1408 (float64) rows; a segment crossing a
+ *     blob boundary becomes one piece per blob;
+ *   - within a blob, the edges of one source atom form a record.
+ * A planned call stages each blob's rows (g_e, v_e) in LDS, writes one
+ * destination sum per piece and twelve source sums per record, then adds
+ * each atom's pieces and records in blob order.  The build synchronises
+ * `stream` (it reads the record and piece counts back, returned in
+ * counts[0] and counts[1]) and fails with DPA4K_EINVAL unless both offsets
+ * arrays are CSRs of n_edges slots.  Slots of src_order out of [0, E) are
+ * skipped, as in the direct kernels.  The calls write the caller's records
+ * buffer (dpa4k_force_assembly_records_size bytes): calls sharing one must
+ * not overlap.  value_bytes = 4 (float32) or 8 (float64); a plan serves the
+ * dtype it was built for.  E < 2^31 - 1, N >= 1.  The plan needs
+ * dpa4k_force_assembly_plan_size bytes (about 14 * E) and its build a
+ * workspace of dpa4k_force_assembly_plan_workspace_size bytes. */
 size_t dpa4k_force_assembly_plan_size(int64_t n_edges, int64_t n_nodes,
                                       int64_t value_bytes);
 size_t dpa4k_force_assembly_plan_workspace_size(int64_t n_edges,
                                                 int64_t n_nodes);
-int dpa4k_force_assembly_plan(const int64_t* src_offsets,
-                              const int64_t* src_order, int64_t n_edges,
-                              int64_t n_nodes, int64_t value_bytes, void* plan,
+size_t dpa4k_force_assembly_records_size(int64_t n_records, int64_t n_pieces,
+                                         int64_t value_bytes);
+int dpa4k_force_assembly_plan(const int64_t* dst_offsets,
+                              const int64_t* src_offsets,
+                              const int64_t* src_order, const void* edge_vec,
+                              int64_t n_edges, int64_t n_nodes,
+                              int64_t value_bytes, void* plan,
                               size_t plan_bytes, void* workspace,
-                              size_t workspace_bytes, dpa4k_stream_t stream);
+                              size_t workspace_bytes, int64_t* counts,
+                              dpa4k_stream_t stream);
 int dpa4k_force_assembly_f32_planned(const float* grad_edge,
-                                     const float* edge_vec,
-                                     const int64_t* dst_offsets,
-                                     const int64_t* src_offsets, float* force,
+                                     const float* edge_vec, float* force,
                                      float* virial, int64_t n_edges,
-                                     int64_t n_nodes, void* plan,
-                                     size_t plan_bytes, dpa4k_stream_t stream);
+                                     int64_t n_nodes, const void* plan,
+                                     size_t plan_bytes, void* records,
+                                     size_t records_bytes, int64_t n_records,
+                                     int64_t n_pieces, dpa4k_stream_t stream);
 int dpa4k_force_assembly_f64_planned(const double* grad_edge,
-                                     const double* edge_vec,
-                                     const int64_t* dst_offsets,
-                                     const int64_t* src_offsets, double* force,
+                                     const double* edge_vec, double* force,
                                      double* virial, int64_t n_edges,
-                                     int64_t n_nodes, void* plan,
-                                     size_t plan_bytes, dpa4k_stream_t stream);
+                                     int64_t n_nodes, const void* plan,
+                                     size_t plan_bytes, void* records,
+                                     size_t records_bytes, int64_t n_records,
+                                     int64_t n_pieces, dpa4k_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Edge-stream elementwise chain

@@ -1,11 +1,13 @@
-"""The planned (bucketed two-pass) force assembly against the direct gather kernel.
+"""The planned (blob) force assembly against the direct kernel, the oracle and an exact plan restatement.
 
 The planned path (dpa4k_force_assembly_plan + dpa4k_force_assembly_f*_planned)
-accumulates in the direct kernel's order, so the two must agree bit for bit;
-the direct kernel is itself checked against the oracle and an fp64 truth in
-test_gpu_segment.py, and one case here repeats that check.  The plan's layout
-is checked exactly against a NumPy restatement: the edges sorted stably by
-(tile of 8192 edges, source bucket), and each source slot's row in that order.
+adds the same terms as the direct gather kernel in another fixed order: the
+destination sums of each piece, then each record's source sums, in blob
+order.  The two paths therefore agree within rounding, and the planned one
+is reproducible run to run.  Its layout is checked exactly against a NumPy
+restatement of the plan's definition: positions along the breadth-first tree
+(float32 arithmetic, as the kernels do it), Morton cells, blobs of
+2816 / 1408 concatenated rows, pieces, entries and records.
 """
 from __future__ import annotations
 
@@ -21,16 +23,18 @@ from parity import announce, assert_bitwise, assert_close_scaled, assert_fp64
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
-TILE, MOST_BUCKETS = 8192, 256
+ROWS = {4: 2816, 8: 1408}  # blob rows per value size (67,584 bytes of LDS)
 
 
-def _random_graph(atoms, edges, seed, hubs=()):
+def _random_graph(atoms, edges, seed, src_hubs=(), dst_hubs=()):
     gen = torch.Generator().manual_seed(seed)
-    dst = torch.sort(torch.randint(0, atoms, (edges,), generator=gen)).values
+    dst = torch.randint(0, atoms, (edges,), generator=gen)
+    for hub, count in dst_hubs:  # atoms with many incoming edges: segments split over blobs
+        dst[torch.randperm(edges, generator=gen)[:count]] = hub
+    dst = torch.sort(dst).values
     src = torch.randint(0, atoms, (edges,), generator=gen)
-    for hub, count in hubs:  # atoms that are the source of many edges
-        picks = torch.randperm(edges, generator=gen)[:count]
-        src[picks] = hub
+    for hub, count in src_hubs:  # atoms that are the source of many edges
+        src[torch.randperm(edges, generator=gen)[:count]] = hub
     g = torch.randn(edges, 3, generator=gen, dtype=torch.float64)
     v = torch.randn(edges, 3, generator=gen, dtype=torch.float64)
     order, src_offsets = ref.group_by_source(src, atoms)
@@ -46,76 +50,193 @@ def _water(atoms, seed, spatial):
 CASES = {
     "water_random_numbering": lambda: _water(4096, 5, False),
     "water_morton_numbering": lambda: _water(4096, 5, True),
-    "source_hubs": lambda: _random_graph(700, 20000, 11, hubs=((3, 600), (650, 250))),
+    "source_hubs": lambda: _random_graph(700, 20000, 11, src_hubs=((3, 600), (650, 250))),
+    "destination_hubs_split_over_blobs": lambda: _random_graph(900, 30000, 29, dst_hubs=((5, 7000), (400, 3000))),
     "three_atoms": lambda: _random_graph(3, 5, 12),
-    "one_tile_and_one_edge": lambda: _random_graph(300, TILE * 2 + 1, 13),
+    "two_blobs_and_one_edge": lambda: _random_graph(300, 2 * 2816 + 1, 13),
 }
 
 
-def _decode_plan(plan: _C.ForcePlan, edges: int):
-    """edge_row and src_pos from the plan buffer (two int32 arrays, 256-byte aligned)."""
-    stride = -(-4 * max(edges, 1) // 256) * 256
-    raw = plan.buffer.cpu().numpy()
-    return [raw[i * stride:i * stride + 4 * edges].view(np.int32) for i in range(2)]
+# ---------------------------------------------------------------------------
+# the plan, restated
+# ---------------------------------------------------------------------------
+
+def _morton_bits(atoms):
+    bits = 1
+    while bits < 10 and (1 << (3 * (bits + 1))) <= atoms:
+        bits += 1
+    return bits
 
 
-def _expected_slots(case, atoms):
-    """Edges sorted stably by (tile of 8192 edges, bucket of their source atom)."""
-    edges = case["src_order"].numel()
-    wanted = min(atoms, MOST_BUCKETS)
-    bucket_atoms = -(-atoms // wanted)
-    buckets = -(-atoms // bucket_atoms)
-    src_of = np.zeros(edges, dtype=np.int64)  # edges no valid slot names keep bucket 0
-    offsets, order = case["src_offsets"].numpy(), case["src_order"].numpy()
-    for atom in range(atoms):
-        slots = order[offsets[atom]:offsets[atom + 1]]
-        valid = slots[(slots >= 0) & (slots < edges)]
-        src_of[valid] = atom
-    key = (np.arange(edges) // TILE) * buckets + src_of // bucket_atoms
-    return np.argsort(key, kind="stable")
-
-
-def _check_plan_layout(plan, case, atoms):
-    edges = case["src_order"].numel()
-    edge_row, src_pos = _decode_plan(plan, edges)
-    position = np.empty(edges, dtype=np.int64)
-    position[_expected_slots(case, atoms)] = np.arange(edges)
-    np.testing.assert_array_equal(edge_row, position, err_msg="plan: row of each edge")
+def _plan_restated(case, value_bytes, hint=True):
+    """Every array of the plan from its definition (see dpa4k_force_assembly_plan)."""
+    dst_off = case["dst_offsets"].numpy()
+    src_off = case["src_offsets"].numpy()
     order = case["src_order"].numpy()
+    atoms, edges = dst_off.size - 1, order.size
+    rows = ROWS[value_bytes]
+    blobs = -(-edges // rows)
+    slot_atom = np.repeat(np.arange(atoms), np.diff(src_off))
     valid = (order >= 0) & (order < edges)
-    expected = np.where(valid, position[np.clip(order, 0, max(edges - 1, 0))], -1)
-    np.testing.assert_array_equal(src_pos, expected, err_msg="plan: source positions")
+    edge_src = np.full(edges, -1, dtype=np.int64)
+    np.maximum.at(edge_src, order[valid], slot_atom[valid])
+    dst_of = np.repeat(np.arange(atoms), np.diff(dst_off))
+
+    # breadth-first positions: an unreached atom joins level d + 1 through its first incoming
+    # edge whose source is at level d; r_k = r_s - v_e in float32
+    unreached = np.iinfo(np.int32).max
+    level = np.full(atoms, unreached, dtype=np.int64)
+    pos = np.zeros((atoms, 3), dtype=np.float32)
+    vec = case["edge_vec"].numpy().astype(np.float64 if value_bytes == 8 else np.float32).astype(np.float32)
+    level[int(dst_of[0])] = 0
+    depth = 0
+    while hint:
+        before = level.copy()
+        moved = False
+        for k in np.nonzero(before == unreached)[0]:
+            for e in range(dst_off[k], dst_off[k + 1]):
+                s = edge_src[e]
+                if s >= 0 and before[s] == depth:
+                    pos[k] = pos[s] - vec[e]
+                    level[k] = depth + 1
+                    moved = True
+                    break
+        if not moved:
+            break
+        depth += 1
+    reached = level != unreached
+    bits = _morton_bits(atoms)
+    cells = np.float32(1 << bits)
+    lo = pos[reached].min(0)
+    hi = pos[reached].max(0)
+    extent = np.float32(max(hi[0] - lo[0], hi[1] - lo[1], hi[2] - lo[2]))
+    scale = cells / extent if 0 < extent < np.inf else np.float32(0)
+    q = np.minimum(np.maximum((pos - lo) * np.float32(scale), np.float32(0)), cells - np.float32(1)).astype(np.int64)
+    key = np.zeros(atoms, dtype=np.int64)
+    for b in range(bits):
+        for i in range(3):
+            key |= ((q[:, i] >> b) & 1) << (3 * b + (2 - i))
+    key[~reached] = 1 << (3 * bits)
+    perm = np.argsort(key, kind="stable")
+    rank = np.empty(atoms, dtype=np.int64)
+    rank[perm] = np.arange(atoms)
+    degree = np.diff(dst_off)[perm]
+    cum = np.concatenate([[0], np.cumsum(degree)])
+
+    piece_t, piece_count, blob_piece = [], [], np.zeros(blobs + 1, dtype=np.int64)
+    for i in range(atoms):
+        begin, end = cum[i], cum[i + 1]
+        piece_count.append(0 if end <= begin else (end - 1) // rows - begin // rows + 1)
+        if end > begin:
+            for w in range(begin // rows, (end - 1) // rows + 1):
+                start = max(begin, w * rows)
+                if start == w * rows:
+                    blob_piece[w] = len(piece_t)
+                piece_t.append(start)
+    pieces = len(piece_t)
+    blob_piece[blobs] = pieces
+    piece_first = np.concatenate([[0], np.cumsum(piece_count)])
+    tpos = cum[rank[dst_of]] + (np.arange(edges) - dst_off[dst_of])
+    row_edge = np.empty(edges, dtype=np.int64)
+    row_edge[tpos] = np.arange(edges)
+
+    slots = np.nonzero(valid)[0]
+    slot_blob = tpos[order[slots]] // rows
+    sorted_slots = slots[np.argsort(slot_blob, kind="stable")]
+    entry_blob = tpos[order[sorted_slots]] // rows
+    entry_row = tpos[order[sorted_slots]] - entry_blob * rows
+    entry_atom = slot_atom[sorted_slots]
+    start = np.ones(sorted_slots.size, dtype=bool)
+    start[1:] = (entry_blob[1:] != entry_blob[:-1]) | (entry_atom[1:] != entry_atom[:-1])
+    rec_first = np.concatenate([np.nonzero(start)[0], [sorted_slots.size]])
+    records = rec_first.size - 1
+    rec_blob = entry_blob[rec_first[:-1]]
+    blob_rec = np.searchsorted(rec_blob, np.arange(blobs + 1), side="left")
+    blob_entry = np.searchsorted(entry_blob, np.arange(blobs + 1), side="left")
+    # each blob's records by descending length (capped at 63), stable; their entries follow
+    length = np.diff(rec_first)
+    balanced = np.argsort(rec_blob * 64 + (63 - np.minimum(length, 63)), kind="stable")
+    entry_row = np.concatenate([entry_row[rec_first[r]:rec_first[r + 1]] for r in balanced] + [entry_row[:0]])
+    rec_entry = np.concatenate([[0], np.cumsum(length[balanced])])
+    rec_position = rank[entry_atom[rec_first[:-1]]][balanced]
+    pos_records = np.argsort(rec_position, kind="stable")  # record ids grouped by position, in blob order
+    pos_rec = np.concatenate([[0], np.cumsum(np.bincount(rec_position, minlength=atoms))])
+    return {"perm": perm, "piece_first": piece_first, "piece_t": np.append(piece_t, edges), "blob_piece": blob_piece,
+            "blob_rec": blob_rec, "blob_entry": blob_entry, "row_edge": row_edge, "entry_row": entry_row,
+            "rec_entry": rec_entry, "pos_records": pos_records, "pos_rec": pos_rec, "records": records, "pieces": pieces}
 
 
-def _run(case, dtype, plan=None):
-    d = {k: v.to(DEV) for k, v in case.items()}
+def _decode_plan(plan: _C.ForcePlan):
+    """The plan buffer's arrays (carved in order, each 256-byte aligned)."""
+    atoms, edges = plan.n_nodes, plan.n_edges
+    blobs = -(-edges // ROWS[plan.value_bytes])
+    e = max(edges, 1)
+    layout = [("perm", atoms, np.int32), ("piece_first", atoms + 1, np.int32),
+              ("piece_t", atoms + blobs + 1, np.int32), ("blob_piece", blobs + 1, np.int32),
+              ("blob_rec", blobs + 1, np.int32), ("blob_entry", blobs + 1, np.int32), ("row_edge", e, np.int32),
+              ("entry_row", e, np.uint16), ("rec_entry", e + 1, np.int32), ("pos_records", e, np.int32),
+              ("pos_rec", atoms + 1, np.int32)]
+    raw = plan.plan.cpu().numpy()
+    out, at = {}, 0
+    for name, count, dtype in layout:
+        size = count * np.dtype(dtype).itemsize
+        out[name] = raw[at:at + size].view(dtype)
+        at += -(-size // 256) * 256
+    return out
+
+
+def _check_plan_layout(plan, case):
+    expected = _plan_restated(case, plan.value_bytes)
+    got = _decode_plan(plan)
+    assert plan.n_records == expected["records"] and plan.n_pieces == expected["pieces"]
+    lengths = {"piece_t": expected["pieces"] + 1, "rec_entry": expected["records"] + 1,
+               "pos_records": expected["records"], "entry_row": expected["rec_entry"][-1]}
+    for name in ("perm", "piece_first", "piece_t", "blob_piece", "blob_rec", "blob_entry", "row_edge", "entry_row",
+                 "rec_entry", "pos_records", "pos_rec"):
+        n = lengths.get(name, expected[name].size)
+        np.testing.assert_array_equal(got[name][:n], expected[name][:n], err_msg=f"plan: {name}")
+
+
+def _on_device(case):
+    return {k: v.to(DEV) for k, v in case.items()}
+
+
+def _run(d, dtype, plan=None):
+    """Force and virial of a case already on the device (a plan is tied to those very offsets tensors)."""
     return _C.force_assembly(d["grad_edge"].to(dtype), d["edge_vec"].to(dtype), d["dst_offsets"], d["src_offsets"],
                              d["src_order"], plan=plan)
 
 
+def _plan(d, dtype):
+    return _C.force_assembly_plan(d["dst_offsets"], d["src_offsets"], d["src_order"], d["edge_vec"].to(dtype),
+                                  value_bytes=torch.empty((), dtype=dtype).element_size())
+
+
 @pytest.mark.parametrize("name", list(CASES))
-def test_planned_force_matches_the_direct_kernel_bit_for_bit(name):
+def test_planned_force_matches_the_direct_kernel_and_its_restated_plan(name):
     case = CASES[name]()
     atoms = case["dst_offsets"].numel() - 1
     announce("force plan", name, atoms, case["src_order"].numel())
-    plan8 = _C.force_assembly_plan(case["src_offsets"].to(DEV), case["src_order"].to(DEV), value_bytes=8)
-    plan4 = _C.force_assembly_plan(case["src_offsets"].to(DEV), case["src_order"].to(DEV), value_bytes=4)
-    _check_plan_layout(plan8, case, atoms)
-    for dtype, plans in ((torch.float32, (plan8, plan4)), (torch.float64, (plan8,))):
-        direct = _run(case, dtype)
-        for plan in plans:
-            planned = _run(case, dtype, plan)
-            again = _run(case, dtype, plan)
-            for label, a, b, c in zip(("force", "virial"), direct, planned, again):
-                assert_bitwise(b, a, f"{name} {dtype} {label}: planned vs direct (plan of {plan.value_bytes} bytes)")
-                assert_bitwise(c, b, f"{name} {dtype} {label}: planned run to run")
+    d = _on_device(case)
+    for dtype in (torch.float32, torch.float64):
+        plan = _plan(d, dtype)
+        _check_plan_layout(plan, case)
+        direct = _run(d, dtype)
+        planned = _run(d, dtype, plan)
+        again = _run(d, dtype, plan)
+        for label, a, b, c in zip(("force", "virial"), direct, planned, again):
+            if dtype == torch.float32:
+                assert_close_scaled(b, a, what=f"{name} {label}: planned vs direct")
+            else:
+                assert_fp64(b, a, f"{name} {label}: planned vs direct")
+            assert_bitwise(c, b, f"{name} {dtype} {label}: planned run to run")
 
 
 def test_planned_force_against_the_oracle_and_truth():
-    case = _random_graph(500, 30000, 17, hubs=((7, 400),))
+    case = _random_graph(500, 30000, 17, src_hubs=((7, 400),), dst_hubs=((9, 4000),))
     announce("force plan vs oracle")
-    plan = _C.force_assembly_plan(case["src_offsets"].to(DEV), case["src_order"].to(DEV))
-    force, virial = _run(case, torch.float32, plan)
+    d = _on_device(case)
+    force, virial = _run(d, torch.float32, _plan(d, torch.float32))
     g, v = case["grad_edge"].float(), case["edge_vec"].float()
     e_force, e_virial = ref.force_assembly_reference(g, v, case["src"], case["dst"], case["dst_offsets"],
                                                      case["src_offsets"])
@@ -124,23 +245,50 @@ def test_planned_force_against_the_oracle_and_truth():
     assert_close_scaled(virial, e_virial, what="fp32 virial vs oracle")
     assert_close_scaled(force, t_force, what="fp32 force vs truth")
     assert_close_scaled(virial, t_virial, what="fp32 virial vs truth")
-    force64, virial64 = _run(case, torch.float64, plan)
+    force64, virial64 = _run(d, torch.float64, _plan(d, torch.float64))
     t_force, t_virial = loops.force_assembly_loop(case["grad_edge"], case["edge_vec"], case["src"], case["dst"], 500)
     assert_fp64(force64, t_force, "fp64 force vs truth")
     assert_fp64(virial64, t_virial, "fp64 virial vs truth")
 
 
-def test_planned_force_skips_invalid_source_slots_like_the_direct_kernel():
+def _invalid_slots():
     case = _random_graph(200, 9000, 19)
     order = case["src_order"].clone()
     order[5], order[700], order[-1] = -1, order.numel() + 7, -3
-    case["src_order"] = order
-    announce("force plan, invalid slots")
-    plan = _C.force_assembly_plan(case["src_offsets"].to(DEV), order.to(DEV))
-    _check_plan_layout(plan, case, 200)
+    return dict(case, src_order=order)
+
+
+def _one_edge_named_by_every_slot():
+    """src_order names edge 0 from every slot: one blob holds every entry (more than it stages in LDS)
+    and more records than its threads take in their first rounds."""
+    case = _random_graph(4000, 12000, 37)
+    return dict(case, src_order=torch.zeros_like(case["src_order"]))
+
+
+@pytest.mark.parametrize("make", [_invalid_slots, _one_edge_named_by_every_slot],
+                         ids=["out_of_range_slots", "one_edge_named_by_every_slot"])
+def test_planned_force_takes_source_slots_like_the_direct_kernel(make):
+    case = make()
+    announce("force plan, unusual src_order", make.__name__)
+    d = _on_device(case)
     for dtype in (torch.float32, torch.float64):
-        for label, a, b in zip(("force", "virial"), _run(case, dtype), _run(case, dtype, plan)):
-            assert_bitwise(b, a, f"{dtype} {label} with invalid slots")
+        plan = _plan(d, dtype)
+        _check_plan_layout(plan, case)
+        for label, a, b in zip(("force", "virial"), _run(d, dtype), _run(d, dtype, plan)):
+            if dtype == torch.float32:
+                assert_close_scaled(b, a, what=f"{label}: planned vs direct")
+            else:
+                assert_fp64(b, a, f"{label}: planned vs direct")
+
+
+def test_planned_force_without_a_geometry_hint_keeps_the_natural_order():
+    case = _water(2048, 3, False)
+    announce("force plan without a hint")
+    d = _on_device(case)
+    plan = _C.force_assembly_plan(d["dst_offsets"], d["src_offsets"], d["src_order"], None, value_bytes=4)
+    np.testing.assert_array_equal(_decode_plan(plan)["perm"], np.arange(2048), err_msg="identity order")
+    for label, a, b in zip(("force", "virial"), _run(d, torch.float32), _run(d, torch.float32, plan)):
+        assert_close_scaled(b, a, what=f"{label} without a hint")
 
 
 def test_planned_force_without_edges_and_plan_checks():
@@ -148,51 +296,62 @@ def test_planned_force_without_edges_and_plan_checks():
     offsets = torch.zeros(5, dtype=torch.int64, device=DEV)
     order = torch.empty(0, dtype=torch.int64, device=DEV)
     empty = torch.empty((0, 3), device=DEV)
-    plan = _C.force_assembly_plan(offsets, order, value_bytes=4)
+    plan = _C.force_assembly_plan(offsets, offsets, order, empty, value_bytes=4)
     force, virial = _C.force_assembly(empty, empty, offsets, offsets, order, plan=plan)
     assert force.shape == (4, 3) and virial.shape == (4, 9)
     assert force.count_nonzero().item() == 0 and virial.count_nonzero().item() == 0
-    case = _random_graph(50, 800, 23)
-    plan = _C.force_assembly_plan(case["src_offsets"].to(DEV), case["src_order"].to(DEV), value_bytes=4)
+    d = _on_device(_random_graph(50, 800, 23))
+    plan = _plan(d, torch.float32)
     with pytest.raises(RuntimeError, match="another graph, device or dtype"):
-        _run(case, torch.float64, plan)  # a float32 plan cannot hold float64 rows
-    other = _random_graph(50, 801, 23)
+        _run(d, torch.float64, plan)  # a float32 plan does not serve float64 rows
     with pytest.raises(RuntimeError, match="another graph"):
-        _run(other, torch.float32, plan)
+        _run(_on_device(_random_graph(50, 801, 23)), torch.float32, plan)
+    copy = dict(d, dst_offsets=d["dst_offsets"].clone())  # the same values in another tensor
+    with pytest.raises(RuntimeError, match="another graph"):
+        _run(copy, torch.float32, plan)
+    bad = {k: v.clone() for k, v in d.items()}
+    bad["dst_offsets"][10] = 10 ** 6  # not a CSR of the edge list
+    with pytest.raises(ValueError, match="not a CSR"):
+        _C.force_assembly_plan(bad["dst_offsets"], bad["src_offsets"], bad["src_order"], bad["edge_vec"].float())
 
 
-def test_operator_plans_float32_on_scattered_numbering_only():
-    """kernels.force_assembly builds a plan for float32 on a graph without spatial locality, and for no other."""
+def test_operator_plans_compact_graphs_only():
+    """kernels.force_assembly keeps a plan for water graphs in either numbering and dtype, and not for a
+    graph whose edge vectors carry no geometry (records about as many as edges)."""
     from bysj_amd import kernels
     from bysj_amd.kernels import segment as segment_ops
 
     announce("force plan policy")
     segment_ops._FORCE_PLANS.clear()
-    results = {}
+    kept = {}
     for spatial in (False, True):
-        # 16,384 atoms (1.5M edges): with random numbering an atom's source edges lie ~16K edges apart
         case = _water(16384, 6, spatial)
         assert case["src_order"].numel() >= segment_ops._ForcePlanCache.MIN_EDGES
         d = {k: v.to(DEV) for k, v in case.items()}
-        args = (d["grad_edge"].float(), d["edge_vec"].float(), d["src"], d["dst"], d["dst_offsets"],
-                d["src_offsets"], d["src_order"])
-        force, virial = kernels.force_assembly(*args)
-        entry = segment_ops._FORCE_PLANS._entries[id(d["src_order"])]
-        assert (entry[2] is not None) == (not spatial), "a plan exactly for the scattered numbering"
-        direct = _C.force_assembly(args[0], args[1], d["dst_offsets"], d["src_offsets"], d["src_order"])
-        assert_bitwise(force, direct[0], f"operator force (spatial={spatial})")
-        assert_bitwise(virial, direct[1], f"operator virial (spatial={spatial})")
-        # float64 calls never build or use a plan
-        force64, _ = kernels.force_assembly(d["grad_edge"], d["edge_vec"], d["src"], d["dst"], d["dst_offsets"],
-                                            d["src_offsets"], d["src_order"])
-        assert force64.dtype == torch.float64
-        results[spatial] = d
-    # an in-place write to src_order drops the cached plan; the next call measures and plans again
-    d = results[False]
-    before = segment_ops._FORCE_PLANS._entries[id(d["src_order"])][2]
+        for dtype in (torch.float32, torch.float64):
+            args = (d["grad_edge"].to(dtype), d["edge_vec"].to(dtype), d["src"], d["dst"], d["dst_offsets"],
+                    d["src_offsets"], d["src_order"])
+            force, virial = kernels.force_assembly(*args)
+            plan = segment_ops._FORCE_PLANS._entries[(id(d["src_order"]), dtype)][2]
+            assert plan is not None, f"a plan for the water graph (spatial={spatial}, {dtype})"
+            assert plan.n_records * segment_ops._ForcePlanCache.MIN_EDGES_PER_RECORD <= plan.n_edges
+            direct = _C.force_assembly(args[0], args[1], d["dst_offsets"], d["src_offsets"], d["src_order"])
+            check = assert_close_scaled if dtype == torch.float32 else assert_fp64
+            check(force, direct[0], what=f"operator force (spatial={spatial}, {dtype})")
+            check(virial, direct[1], what=f"operator virial (spatial={spatial}, {dtype})")
+        kept[spatial] = d
+    scattered = {k: v.to(DEV) for k, v in _random_graph(4096, 1 << 17, 31).items()}
+    args = (scattered["grad_edge"].float(), scattered["edge_vec"].float(), scattered["src"], scattered["dst"],
+            scattered["dst_offsets"], scattered["src_offsets"], scattered["src_order"])
+    force, _ = kernels.force_assembly(*args)
+    assert segment_ops._FORCE_PLANS._entries[(id(scattered["src_order"]), torch.float32)][2] is None
+    assert_bitwise(force, _C.force_assembly(args[0], args[1], args[4], args[5], args[6])[0], "unplanned operator")
+    # an in-place write to src_order drops the cached plan; the next call plans again
+    d = kept[False]
+    before = segment_ops._FORCE_PLANS._entries[(id(d["src_order"]), torch.float32)][2]
     d["src_order"].add_(0)
     kernels.force_assembly(d["grad_edge"].float(), d["edge_vec"].float(), d["src"], d["dst"], d["dst_offsets"],
                            d["src_offsets"], d["src_order"])
-    after = segment_ops._FORCE_PLANS._entries[id(d["src_order"])][2]
+    after = segment_ops._FORCE_PLANS._entries[(id(d["src_order"]), torch.float32)][2]
     assert after is not None and after is not before
     segment_ops._FORCE_PLANS.clear()
