@@ -427,15 +427,22 @@ class _ForcePlanCache:
     that call's ``edge_vec`` to order the atoms in space (one build: a few
     host synchronisations), and keeps it when the blobs are compact: at
     least ``MIN_EDGES_PER_RECORD`` edges per record on average (the records
-    are what the planned path writes and reads back).  Otherwise, and for
-    graphs under ``MIN_EDGES`` edges, inference tensors and calls during HIP
-    graph capture without a cached entry, the direct kernel runs.  Entries
-    follow the three graph tensors like the CSR caches: keyed by object
-    identity, dropped when one is written in place or ``src_order`` is freed.
+    are what the planned path writes and reads back).  float64 rows make
+    records twice as large, and there the direct kernel stays faster when
+    the numbering already follows space: a float64 graph is planned only
+    when fewer than ``LOCAL_SHARE`` of its consecutive source slots name
+    edges within ``LOCAL_SPAN`` of each other (one host synchronisation).
+    Otherwise, and for graphs under ``MIN_EDGES`` edges, inference tensors
+    and calls during HIP graph capture without a cached entry, the direct
+    kernel runs.  Entries follow the three graph tensors like the CSR
+    caches: keyed by object identity, dropped when one is written in place
+    or ``src_order`` is freed.
     """
 
     MIN_EDGES = 1 << 16
     MIN_EDGES_PER_RECORD = 3.0
+    LOCAL_SPAN = 4096
+    LOCAL_SHARE = 0.5
 
     def __init__(self):
         self._entries: dict[tuple, tuple] = {}
@@ -455,11 +462,16 @@ class _ForcePlanCache:
             return entry[2]
         if torch.cuda.is_current_stream_capturing():
             return None
-        try:
-            plan = native.force_assembly_plan(dst_offsets, src_offsets, src_order, edge_vec,
-                                              value_bytes=edge_vec.element_size())
-        except ValueError:  # not a pair of CSRs of the edge list: the direct kernel clamps such offsets
-            plan = None
+        plan = None
+        local = 0.0
+        if edge_vec.dtype == torch.float64:
+            local = ((src_order[1:] - src_order[:-1]).abs() < self.LOCAL_SPAN).float().mean().item()
+        if local < self.LOCAL_SHARE:
+            try:
+                plan = native.force_assembly_plan(dst_offsets, src_offsets, src_order, edge_vec,
+                                                  value_bytes=edge_vec.element_size())
+            except ValueError:  # not a pair of CSRs of the edge list: the direct kernel clamps such offsets
+                plan = None
         if plan is not None and edges < self.MIN_EDGES_PER_RECORD * max(plan.n_records, 1):
             plan = None
         reference = weakref.ref(src_order, lambda _, key=key: self._entries.pop(key, None))

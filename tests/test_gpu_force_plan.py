@@ -316,8 +316,9 @@ def test_planned_force_without_edges_and_plan_checks():
 
 
 def test_operator_plans_compact_graphs_only():
-    """kernels.force_assembly keeps a plan for water graphs in either numbering and dtype, and not for a
-    graph whose edge vectors carry no geometry (records about as many as edges)."""
+    """kernels.force_assembly keeps a plan for water graphs in float32 (either numbering) and in float64 with
+    random numbering, and none for float64 with Morton numbering or for a graph whose edge vectors carry no
+    geometry (records about as many as edges)."""
     from bysj_amd import kernels
     from bysj_amd.kernels import segment as segment_ops
 
@@ -333,9 +334,13 @@ def test_operator_plans_compact_graphs_only():
                     d["src_offsets"], d["src_order"])
             force, virial = kernels.force_assembly(*args)
             plan = segment_ops._FORCE_PLANS._entries[(id(d["src_order"]), dtype)][2]
+            direct = _C.force_assembly(args[0], args[1], d["dst_offsets"], d["src_offsets"], d["src_order"])
+            if dtype == torch.float64 and spatial:
+                assert plan is None, "float64 with Morton numbering keeps the direct kernel"
+                assert_bitwise(force, direct[0], "operator force, direct")
+                continue
             assert plan is not None, f"a plan for the water graph (spatial={spatial}, {dtype})"
             assert plan.n_records * segment_ops._ForcePlanCache.MIN_EDGES_PER_RECORD <= plan.n_edges
-            direct = _C.force_assembly(args[0], args[1], d["dst_offsets"], d["src_offsets"], d["src_order"])
             check = assert_close_scaled if dtype == torch.float32 else assert_fp64
             check(force, direct[0], what=f"operator force (spatial={spatial}, {dtype})")
             check(virial, direct[1], what=f"operator virial (spatial={spatial}, {dtype})")
