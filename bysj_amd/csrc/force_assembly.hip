@@ -979,16 +979,19 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
   const bool staged_entries = entry_count <= kRows;
   const bool staged_pieces = piece_count < kBlobThreads;
 
-  int32_t edge[kRounds], entry[kRounds], first[kRounds], last[kRounds];
+  // thread t takes record t of the blob (records come longest first, so the
+  // lanes of a wave take records of similar length); any records past the
+  // first kBlobThreads are taken in the loop below
+  const int32_t my_record = rec0 + tid;
+  int32_t edge[kRounds], entry[kRounds];
   const int32_t bound = plan.piece_t[piece0 + (tid <= piece_count ? tid : 0)];
+  const int32_t first = plan.rec_entry[my_record < rec1 ? my_record : rec0];
+  const int32_t last = plan.rec_entry[(my_record < rec1 ? my_record : rec0) + 1];
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int32_t i = r * kBlobThreads + tid;
     edge[r] = plan.row_edge[t0 + (i < count ? i : count - 1)];
     entry[r] = plan.entry_row[entry0 + (i < entry_count ? i : 0)];
-    const int32_t rec = rec0 + i < rec1 ? rec0 + i : rec0;
-    first[r] = plan.rec_entry[rec];
-    last[r] = plan.rec_entry[rec + 1];
   }
   Row3<T> g[kRounds], v[kRounds];
 #pragma unroll
@@ -1016,11 +1019,8 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
 
   if (staged_entries) {
     auto row_of = [&](int32_t j) { return static_cast<int32_t>(entries[j - entry0]); };
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r)
-      if (rec0 + r * kBlobThreads + tid < rec1)
-        blob_record(rows, first[r], last[r], row_of, src_rec + static_cast<int64_t>(rec0 + r * kBlobThreads + tid) * 12);
-    for (int32_t rec = rec0 + kRounds * kBlobThreads + tid; rec < rec1; rec += kBlobThreads)
+    if (my_record < rec1) blob_record(rows, first, last, row_of, src_rec + static_cast<int64_t>(my_record) * 12);
+    for (int32_t rec = rec0 + kBlobThreads + tid; rec < rec1; rec += kBlobThreads)
       blob_record(rows, plan.rec_entry[rec], plan.rec_entry[rec + 1], row_of, src_rec + static_cast<int64_t>(rec) * 12);
   } else {
     auto row_of = [&](int32_t j) { return static_cast<int32_t>(plan.entry_row[j]); };
