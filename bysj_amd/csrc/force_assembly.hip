@@ -286,11 +286,13 @@ int run(const T* grad_edge, const T* edge_vec, const int64_t* dst_offsets,
 // Pass 1 (force_blob_kernel, one workgroup per blob) reads the blob's rows
 // (g_e, v_e) into LDS (the rows of a piece are contiguous in the inputs), sums
 // each piece's g_e (the destination side, in double), and sums each record's
-// -g_e and -(g_e outer v_e) from LDS: 12 values per record, rounded once to
-// the value type.  Pass 2 (force_records_kernel) adds, per atom, its pieces
-// and its records in a fixed order (blob order) and writes force and virial.
-// Every sum has a fixed order: results are reproducible run to run.  They
-// differ from the direct kernel's in the last bits (other association).
+// -g_e and -(g_e outer v_e) from LDS: 12 values per record, in the value
+// type (float32 records with fused products, float64 records in double).
+// Pass 2 (force_records_kernel) adds, per atom, its pieces and its records in
+// double in a fixed order (blob order) and writes force and virial.  Every
+// sum has a fixed order: results are reproducible run to run.  They differ
+// from the direct kernel's in the last bits (other association; float32
+// records round each of their few terms).
 //
 // HBM bytes per call (f32, config 4: E = 5.9M, 916k records): the rows once
 // (24 B per edge), the plan's row and entry indices (6 B per edge), the
@@ -881,14 +883,12 @@ struct BlobView {
 };
 
 template <typename T>
-__device__ __forceinline__ void store_record(T* __restrict__ out, const double (&acc)[12]) {
+__device__ __forceinline__ void store_record(T* __restrict__ out, const T (&acc)[12]) {
   if constexpr (sizeof(T) == 4) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     f32x4* v = reinterpret_cast<f32x4*>(out);  // 48-byte records: 16-byte aligned
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-      v[i] = f32x4{static_cast<float>(acc[4 * i]), static_cast<float>(acc[4 * i + 1]),
-                   static_cast<float>(acc[4 * i + 2]), static_cast<float>(acc[4 * i + 3])};
+    for (int i = 0; i < 3; ++i) v[i] = f32x4{acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
   } else {
     typedef double f64x2 __attribute__((ext_vector_type(2)));
     f64x2* v = reinterpret_cast<f64x2*>(out);
@@ -923,24 +923,60 @@ __device__ __forceinline__ void blob_pieces(const T* rows, int32_t count, int64_
 }
 
 // Twelve source sums of one record: entries [from, to), their blob rows from `row_of`.
+// acc -= the twelve source products of one row, in the accumulator's precision.
+template <typename A, typename T>
+__device__ __forceinline__ void sub_source(A (&acc)[12], const T* r6) {
+  const A g0 = r6[0], g1 = r6[1], g2 = r6[2], v0 = r6[3], v1 = r6[4], v2 = r6[5];
+  acc[0] -= g0;
+  acc[1] -= g1;
+  acc[2] -= g2;
+  if constexpr (sizeof(A) == 4) {  // float32 records: one rounding per product and sum (fused)
+    acc[3] = __builtin_fmaf(-g0, v0, acc[3]);
+    acc[4] = __builtin_fmaf(-g0, v1, acc[4]);
+    acc[5] = __builtin_fmaf(-g0, v2, acc[5]);
+    acc[6] = __builtin_fmaf(-g1, v0, acc[6]);
+    acc[7] = __builtin_fmaf(-g1, v1, acc[7]);
+    acc[8] = __builtin_fmaf(-g1, v2, acc[8]);
+    acc[9] = __builtin_fmaf(-g2, v0, acc[9]);
+    acc[10] = __builtin_fmaf(-g2, v1, acc[10]);
+    acc[11] = __builtin_fmaf(-g2, v2, acc[11]);
+  } else {
+    acc[3] -= g0 * v0;
+    acc[4] -= g0 * v1;
+    acc[5] -= g0 * v2;
+    acc[6] -= g1 * v0;
+    acc[7] -= g1 * v1;
+    acc[8] -= g1 * v2;
+    acc[9] -= g2 * v0;
+    acc[10] -= g2 * v1;
+    acc[11] -= g2 * v2;
+  }
+}
+
+// Twelve source sums of one record: entries [from, to), their blob rows from
+// `row_of`.  A record holds a few edges (6.5 on average at config 4) and is
+// stored in the value type, so float32 records accumulate in float32 with
+// fused products; float64 records in double.
 template <typename T, typename RowOf>
 __device__ __forceinline__ void blob_record(const T* rows, int32_t from, int32_t to, RowOf row_of,
                                             T* __restrict__ out) {
-  double acc[12];
+  T acc[12];
 #pragma unroll
-  for (int i = 0; i < 12; ++i) acc[i] = 0.0;
+  for (int i = 0; i < 12; ++i) acc[i] = T(0);
   int32_t j = from;
   for (; j + 2 <= to; j += 2) {  // two entries' reads in flight; the sums stay in entry order
     const T* a = rows + row_of(j) * 6;
     const T* b = rows + row_of(j + 1) * 6;
-    const Row3<T> ga{a[0], a[1], a[2]}, va{a[3], a[4], a[5]}, gb{b[0], b[1], b[2]}, vb{b[3], b[4], b[5]};
-    add_source(acc, ga, va);
-    add_source(acc, gb, vb);
+    T ra[6], rb[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      ra[i] = a[i];
+      rb[i] = b[i];
+    }
+    sub_source(acc, ra);
+    sub_source(acc, rb);
   }
-  if (j < to) {
-    const T* a = rows + row_of(j) * 6;
-    add_source(acc, Row3<T>{a[0], a[1], a[2]}, Row3<T>{a[3], a[4], a[5]});
-  }
+  if (j < to) sub_source(acc, rows + row_of(j) * 6);
   store_record(out, acc);
 }
 
