@@ -42,6 +42,28 @@ def _random_graph(atoms, edges, seed, src_hubs=(), dst_hubs=()):
             "src_offsets": src_offsets, "src_order": order}
 
 
+def _chain(atoms, seed, components=1):
+    """Atoms on lines, each bonded to its neighbours both ways: a breadth-first tree as deep as a
+    component is long; with several components the later ones are never reached from the root."""
+    gen = torch.Generator().manual_seed(seed)
+    per = atoms // components
+    dst, src = [], []
+    for k in range(atoms):
+        start = (k // per) * per
+        for other in (k - 1, k + 1):
+            if start <= other < min(start + per, atoms):
+                dst.append(k)
+                src.append(other)
+    dst, src = torch.tensor(dst), torch.tensor(src)
+    edges = dst.numel()
+    position = torch.arange(atoms, dtype=torch.float64)[:, None] * torch.tensor([1.0, 0.3, -0.2], dtype=torch.float64)
+    v = position[src] - position[dst]
+    g = torch.randn(edges, 3, generator=gen, dtype=torch.float64)
+    order, src_offsets = ref.group_by_source(src, atoms)
+    return {"grad_edge": g, "edge_vec": v, "src": src, "dst": dst, "dst_offsets": ref.segment_offsets(dst, atoms),
+            "src_offsets": src_offsets, "src_order": order}
+
+
 def _water(atoms, seed, spatial):
     graph = workloads.water_graph(atoms, seed=seed, spatial_order=spatial)
     return workloads.force_config(graph, seed=seed, device="cpu", dtype=torch.float64)
@@ -54,6 +76,8 @@ CASES = {
     "destination_hubs_split_over_blobs": lambda: _random_graph(900, 30000, 29, dst_hubs=((5, 7000), (400, 3000))),
     "three_atoms": lambda: _random_graph(3, 5, 12),
     "two_blobs_and_one_edge": lambda: _random_graph(300, 2 * 2816 + 1, 13),
+    "chain_of_3000_atoms": lambda: _chain(3000, 41),
+    "three_chains_two_unreached": lambda: _chain(3000, 43, components=3),
 }
 
 
