@@ -758,6 +758,166 @@ __global__ __launch_bounds__(kThreads, sizeof(P) == 4 ? 4 : 2) void finish_kerne
   }
 }
 
+// Last launch of the two-level path for fine digits of at most 6 bits and
+// 32-bit packed elements (index << fine_bits | fine digit): the same outputs
+// as finish_kernel, ranked without ballots.  Thread t takes a contiguous run
+// of kPrivateItems elements of the chunk and counts its digits in its own
+// row of LDS counters (no other thread touches the row).  Lane d of each
+// wave then turns column d of its wave's 64 rows into exclusive prefixes,
+// the waves' digit totals are scanned over the waves and the digits, and
+// every thread walks its run again in order, placing each element at the
+// next position of its digit: a stable rank (run order within a thread,
+// thread order within a wave, wave order within the chunk); the chunk is
+// then sorted in LDS and written out in order.  Longer buckets take a
+// histogram pass first, then chunk after chunk as above.
+constexpr int kPrivateItems = kLocalChunk / kThreads;  // 16 elements per thread and chunk
+constexpr int kPrivateDigits = 64;
+constexpr int kPrivateRow = kPrivateDigits + 2;         // padded row: lanes of one digit fall in 32 banks
+static_assert(sizeof(uint16_t) * kThreads * kPrivateRow >= kLocalChunk * sizeof(uint32_t),
+              "a sorted chunk fits over the counters");
+
+__global__ __launch_bounds__(kThreads, 2) void finish_private_kernel(
+    const uint32_t* __restrict__ packed, const uint32_t* __restrict__ bucket_start, int buckets, int fine_bits,
+    const int64_t* __restrict__ keys, int64_t n_edges, int64_t n_nodes, int64_t* __restrict__ order,
+    int64_t* __restrict__ offsets, const int32_t* __restrict__ status) {
+  constexpr size_t kRankBytes = sizeof(uint16_t) * kThreads * kPrivateRow;
+  constexpr size_t kShared = kRankBytes > sizeof(GapList) ? kRankBytes : sizeof(GapList);
+  __shared__ __align__(16) unsigned char shared[kShared];
+  __shared__ uint32_t wave_digit[kGroupWaves][kPrivateDigits];
+  __shared__ uint32_t fine_base[kPrivateDigits];
+  __shared__ uint32_t chunk_base[kPrivateDigits];
+  __shared__ uint32_t wave_totals[kGroupWaves];
+  if (!(status_of(status) & kFlagUnsorted)) {
+    boundary_offsets(keys, n_edges, n_nodes, offsets, order, blockIdx.x, gridDim.x,
+                     *reinterpret_cast<GapList*>(shared));
+    return;
+  }
+  const int b = blockIdx.x;
+  if (b >= buckets) return;
+  uint16_t* rank = reinterpret_cast<uint16_t*>(shared);
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int64_t start = bucket_start[b];
+  const int64_t end = bucket_start[b + 1];
+  const int64_t count = end - start;
+  const int fines = 1 << fine_bits;
+  const uint32_t fine_mask = static_cast<uint32_t>(fines - 1);
+  uint16_t* mine = rank + t * kPrivateRow;
+
+  const auto write_offsets = [&]() {
+    for (int f = t; f < fines; f += kThreads) {
+      const int64_t key = (static_cast<int64_t>(b) << fine_bits) + f;
+      if (key < n_nodes) offsets[key] = fine_base[f];
+    }
+  };
+  if (count > kLocalChunk) {
+    // the bucket's fine-digit histogram -> offsets of its keys
+    for (int f = t; f < kPrivateDigits; f += kThreads) fine_base[f] = 0u;
+    __syncthreads();
+    for (int64_t i = t; i < count; i += kThreads) atomicAdd(&fine_base[packed[start + i] & fine_mask], 1u);
+    __syncthreads();
+    lds_exclusive_scan(fine_base, fines, static_cast<uint32_t>(start), wave_totals);
+    write_offsets();
+    if (order == nullptr) return;
+  }
+
+  // an empty bucket takes one (empty) round too: it still writes its keys' offsets
+  for (int64_t first = 0; first < count || first == 0; first += kLocalChunk) {
+    const int in_chunk = static_cast<int>(count - first < kLocalChunk ? count - first : kLocalChunk);
+    // this thread's run: elements [t * kPrivateItems, (t + 1) * kPrivateItems) of the chunk
+    const BufferView view = buffer_view(packed + start + first, static_cast<int64_t>(in_chunk) * 4);
+    uint32_t value[kPrivateItems];
+#pragma unroll
+    for (int q = 0; q < kPrivateItems / 4; ++q) {  // 16-byte loads (zeros past the chunk, dword by dword)
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 four = __builtin_amdgcn_raw_buffer_load_b128(
+          view, static_cast<int>((t * kPrivateItems + 4 * q) * 4), 0, 0);
+      value[4 * q] = four.x;
+      value[4 * q + 1] = four.y;
+      value[4 * q + 2] = four.z;
+      value[4 * q + 3] = four.w;
+    }
+    const int here = in_chunk - t * kPrivateItems;  // elements of the run inside the chunk (may be <= 0)
+#pragma unroll
+    for (int d = 0; d < kPrivateDigits; ++d) mine[d] = 0;
+#pragma unroll
+    for (int i = 0; i < kPrivateItems; ++i)
+      if (i < here) ++mine[value[i] & fine_mask];
+    __syncthreads();
+    // column `lane` of this wave's rows -> exclusive prefixes over the wave's lanes
+    if (lane < fines) {
+      uint32_t running = 0;
+      uint16_t* column = rank + (wave * 64) * kPrivateRow + lane;
+      for (int l0 = 0; l0 < 64; l0 += 16) {  // sixteen rows' reads in flight
+        uint32_t c[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) c[l] = column[(l0 + l) * kPrivateRow];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+          column[(l0 + l) * kPrivateRow] = static_cast<uint16_t>(running);
+          running += c[l];
+        }
+      }
+      wave_digit[wave][lane] = running;
+    }
+    __syncthreads();
+    // digit totals of the chunk -> chunk_base (exclusive over digits); each wave's
+    // base per digit = chunk_base + the digit's elements in earlier waves
+    if (t < kPrivateDigits) {
+      uint32_t total = 0;
+      for (int w = 0; w < kGroupWaves; ++w) total += t < fines ? wave_digit[w][t] : 0u;
+      chunk_base[t] = total;
+    }
+    __syncthreads();
+    lds_exclusive_scan(chunk_base, kPrivateDigits, 0u, wave_totals);
+    if (t < fines) {
+      uint32_t running = chunk_base[t];
+      for (int w = 0; w < kGroupWaves; ++w) {
+        const uint32_t c = wave_digit[w][t];
+        wave_digit[w][t] = running;
+        running += c;
+      }
+    }
+    if (count <= kLocalChunk) {
+      // the chunk is the bucket: its digit starts are the offsets of its keys
+      for (int f = t; f < fines; f += kThreads) fine_base[f] = static_cast<uint32_t>(start) + chunk_base[f];
+      __syncthreads();
+      write_offsets();
+      if (order == nullptr) return;
+    }
+    __syncthreads();
+    uint32_t place[kPrivateItems];
+#pragma unroll
+    for (int i = 0; i < kPrivateItems; ++i) {
+      const uint32_t d = value[i] & fine_mask;
+      place[i] = wave_digit[wave][d] + mine[d];
+      if (i < here) mine[d] = static_cast<uint16_t>(mine[d] + 1);
+    }
+    __syncthreads();
+    // the chunk sorted by digit in LDS (over the counters), then written out in order
+    uint32_t* sorted = reinterpret_cast<uint32_t*>(shared);
+#pragma unroll
+    for (int i = 0; i < kPrivateItems; ++i)
+      if (i < here) sorted[place[i]] = value[i];
+    __syncthreads();
+    for (int p = t; p < in_chunk; p += kThreads) {
+      const uint32_t e = sorted[p];
+      const uint32_t d = e & fine_mask;
+      const int64_t target = static_cast<int64_t>(fine_base[d]) + (p - static_cast<int64_t>(chunk_base[d]));
+      // unreachable outside the bucket: its digits were counted from the same elements
+      if (target >= start && target < end) order[target] = static_cast<int64_t>(e >> fine_bits);
+    }
+    __syncthreads();
+    // the next chunk's elements of digit d follow this chunk's
+    for (int f = t; f < fines; f += kThreads) {
+      const uint32_t next = f + 1 < fines ? chunk_base[f + 1] : static_cast<uint32_t>(in_chunk);
+      fine_base[f] += next - chunk_base[f];
+    }
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void widen_kernel(const uint32_t* __restrict__ index, int64_t n,
                                                          const uint32_t* count_limit, int64_t* __restrict__ order,
                                                          const int32_t* __restrict__ status, int gate) {
@@ -936,6 +1096,14 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
     const auto finish = [&](auto element) {
       using P = decltype(element);
       const P* packed = static_cast<const P*>(s.packed);
+      if constexpr (sizeof(P) == 4) {
+        if (plan.fine_bits <= 6) {
+          finish_private_kernel<<<finish_blocks, kThreads, 0, stream>>>(
+              packed, s.bucket_start, buckets, plan.fine_bits, keys, plan.n_edges, plan.n_nodes, order, offsets,
+              status);
+          return launched("finish_private_kernel");
+        }
+      }
       if (plan.fine_bits <= 6)
         finish_kernel<P, 6><<<finish_blocks, kThreads, 0, stream>>>(packed, s.bucket_start, buckets, plan.fine_bits,
                                                                     keys, plan.n_edges, plan.n_nodes, order, offsets,
