@@ -1266,6 +1266,8 @@ int build_plan(const int64_t* dst_offsets, const int64_t* src_offsets, const int
   return hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
 
+#undef DPA4K_GRID_STRIDE
+
 }  // namespace
 }  // namespace dpa4k
 
