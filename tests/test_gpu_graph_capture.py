@@ -157,6 +157,27 @@ def test_force_assembly_capture(dtype):
     _check_replays(step, (grad_edge, edge_vec), seed=5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_force_assembly_planned_capture(dtype):
+    """A water graph keeps its blob plan (built by the first eager call), so the planned passes are
+    what the graph records.  16,384 atoms: with random numbering an atom's source edges lie far apart
+    (about 16K edges), so float64 is planned too."""
+    from bysj_amd.kernels import segment as segment_ops
+
+    announce("capture planned force_assembly", dtype)
+    graph = workloads.water_graph(16384, seed=7, device=DEV)
+    case = workloads.force_config(graph, seed=7, device=DEV, dtype=dtype)
+    grad_edge, edge_vec = case["grad_edge"], case["edge_vec"]
+
+    def step():
+        return kernels.force_assembly(grad_edge, edge_vec, case["src"], case["dst"], case["dst_offsets"],
+                                      case["src_offsets"], case["src_order"])
+
+    step()  # builds the plan outside the capture
+    assert segment_ops._FORCE_PLANS._entries[(id(case["src_order"]), dtype)][2] is not None
+    _check_replays(step, (grad_edge,), seed=7)
+
+
 @pytest.mark.parametrize("activation", [None, "gate"])
 def test_edge_stream_capture(activation):
     from bysj_amd.kernels import edge_stream
