@@ -324,7 +324,14 @@ int morton_bits(int64_t n_nodes) {
   return bits;
 }
 
+// A plan starts with a header naming what it was built for; the planned
+// kernels do nothing with a plan whose header does not match their call
+// (every index inside a plan is consistent with its own graph size).
+constexpr int64_t kPlanMagic = 0x4e4c5046'34415044LL;  // "DPA4FPLN"
+constexpr int kHeaderWords = 4;                         // magic, n_edges, n_nodes, value_bytes
+
 struct BlobPlan {
+  int64_t* header;        // [kHeaderWords]
   int32_t* perm;          // [N] atoms in spatial order ("positions" below index perm)
   int32_t* piece_first;   // [N+1] first piece of each position; [N] = pieces
   int32_t* piece_t;       // [N+B+1] first concatenated row of each piece; [pieces] = E
@@ -343,6 +350,7 @@ bool carve_blob_plan(void* plan, size_t plan_bytes, int64_t n_edges, int64_t n_n
   Carver carver{static_cast<char*>(plan), plan_bytes};
   const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
   const size_t b = static_cast<size_t>(blob_count(n_edges, value_bytes));
+  out.header = carver.take<int64_t>(kHeaderWords);
   out.perm = carver.take<int32_t>(n);
   out.piece_first = carver.take<int32_t>(n + 1);
   out.piece_t = carver.take<int32_t>(n + b + 1);
@@ -354,15 +362,15 @@ bool carve_blob_plan(void* plan, size_t plan_bytes, int64_t n_edges, int64_t n_n
   out.rec_entry = carver.take<int32_t>(e + 1);
   out.pos_records = carver.take<int32_t>(e);
   out.pos_rec = carver.take<int32_t>(n + 1);
-  return out.perm && out.piece_first && out.piece_t && out.blob_piece && out.blob_rec && out.blob_entry &&
+  return out.header && out.perm && out.piece_first && out.piece_t && out.blob_piece && out.blob_rec && out.blob_entry &&
          out.row_edge && out.entry_row && out.rec_entry && out.pos_records && out.pos_rec;
 }
 
 size_t blob_plan_bytes(int64_t n_edges, int64_t n_nodes, int64_t value_bytes) {
   const size_t e = static_cast<size_t>(n_edges > 0 ? n_edges : 1), n = static_cast<size_t>(n_nodes);
   const size_t b = static_cast<size_t>(blob_count(n_edges, value_bytes));
-  return round_up_256(n * 4) + round_up_256((n + 1) * 4) + round_up_256((n + b + 1) * 4) +
-         3 * round_up_256((b + 1) * 4) + round_up_256(e * 4) + round_up_256(e * 2) + round_up_256((e + 1) * 4) +
+  return round_up_256(kHeaderWords * 8) + round_up_256(n * 4) + round_up_256((n + 1) * 4) +
+         round_up_256((n + b + 1) * 4) + 3 * round_up_256((b + 1) * 4) + round_up_256(e * 4) + round_up_256(e * 2) + round_up_256((e + 1) * 4) +
          round_up_256(e * 4) + round_up_256((n + 1) * 4);
 }
 
@@ -876,11 +884,27 @@ __global__ __launch_bounds__(256) void plan_record_slots_kernel(const int64_t* _
 
 // ---- the two passes of a planned call ----
 
+// v clamped to [low, high].
+__device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t low, int32_t high) {
+  return v < low ? low : (v > high ? high : v);
+}
+
+struct BlobView;
+template <typename T>
+__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes);
+
 struct BlobView {
+  const int64_t* header;
   const int32_t *perm, *piece_first, *piece_t, *blob_piece, *blob_rec, *blob_entry, *row_edge, *rec_entry,
       *pos_records, *pos_rec;
   const uint16_t* entry_row;
 };
+
+template <typename T>
+__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes) {
+  return plan.header[0] == kPlanMagic && plan.header[1] == n_edges && plan.header[2] == n_nodes &&
+         plan.header[3] == static_cast<int64_t>(sizeof(T));
+}
 
 template <typename T>
 __device__ __forceinline__ void store_record(T* __restrict__ out, const T (&acc)[12]) {
@@ -902,6 +926,7 @@ __device__ __forceinline__ void store_record(T* __restrict__ out, const T (&acc)
 // t0); lane l sums rows l, l + kPieceLanes, ... in order, then a fixed
 // butterfly adds the lanes.
 constexpr int kPieceLanes = 8;
+
 
 template <typename T, typename Bound>
 __device__ __forceinline__ void blob_pieces(const T* rows, int32_t count, int64_t t0, int32_t piece0, Bound bound,
@@ -964,9 +989,10 @@ __device__ __forceinline__ void blob_record(const T* rows, int32_t from, int32_t
 #pragma unroll
   for (int i = 0; i < 12; ++i) acc[i] = T(0);
   int32_t j = from;
+  const auto row = [&](int32_t k) { return rows + row_of(k) * 6; };
   for (; j + 2 <= to; j += 2) {  // two entries' reads in flight; the sums stay in entry order
-    const T* a = rows + row_of(j) * 6;
-    const T* b = rows + row_of(j + 1) * 6;
+    const T* a = row(j);
+    const T* b = row(j + 1);
     T ra[6], rb[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
@@ -976,7 +1002,7 @@ __device__ __forceinline__ void blob_record(const T* rows, int32_t from, int32_t
     sub_source(acc, ra);
     sub_source(acc, rb);
   }
-  if (j < to) sub_source(acc, rows + row_of(j) * 6);
+  if (j < to) sub_source(acc, row(j));
   store_record(out, acc);
 }
 
@@ -996,7 +1022,8 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
                                                                   const T* __restrict__ edge_vec, BlobView plan,
                                                                   double* __restrict__ dst_rec,
                                                                   T* __restrict__ src_rec, int64_t n_edges,
-                                                                  int64_t blobs) {
+                                                                  int64_t n_nodes, int64_t blobs, int32_t n_records,
+                                                                  int32_t n_pieces) {
   constexpr int64_t kRows = blob_rows_of<T>();
   constexpr int kRounds = static_cast<int>((kRows + kBlobThreads - 1) / kBlobThreads);
   __shared__ T rows[kRows * 6];
@@ -1005,13 +1032,18 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
   // each XCD takes a contiguous range of blobs (so of atom positions): pass 2 on
   // that XCD then reads the records its L2 received
   const int64_t blob = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
-  if (blob >= blobs) return;
+  if (blob >= blobs || !plan_matches<T>(plan, n_edges, n_nodes)) return;
   const int tid = static_cast<int>(threadIdx.x);
   const int64_t t0 = blob * kRows;
   const int64_t count = n_edges - t0 < kRows ? n_edges - t0 : kRows;
-  const int32_t entry0 = plan.blob_entry[blob], entry_count = plan.blob_entry[blob + 1] - entry0;
-  const int32_t piece0 = plan.blob_piece[blob], piece_count = plan.blob_piece[blob + 1] - piece0;
-  const int32_t rec0 = plan.blob_rec[blob], rec1 = plan.blob_rec[blob + 1];
+  // a plan's own extents are consistent; the caller's record and piece counts bound them
+  const int32_t edges = static_cast<int32_t>(n_edges);
+  const int32_t entry0 = clamp_i32(plan.blob_entry[blob], 0, edges);
+  const int32_t entry_count = clamp_i32(plan.blob_entry[blob + 1], entry0, edges) - entry0;
+  const int32_t piece0 = clamp_i32(plan.blob_piece[blob], 0, n_pieces);
+  const int32_t piece_count = clamp_i32(plan.blob_piece[blob + 1], piece0, n_pieces) - piece0;
+  const int32_t rec0 = clamp_i32(plan.blob_rec[blob], 0, n_records);
+  const int32_t rec1 = clamp_i32(plan.blob_rec[blob + 1], rec0, n_records);
   const bool staged_entries = entry_count <= kRows;
   const bool staged_pieces = piece_count < kBlobThreads;
 
@@ -1072,20 +1104,25 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
 template <typename T>
 __global__ __launch_bounds__(256) void force_records_kernel(BlobView plan, const double* __restrict__ dst_rec,
                                                             const T* __restrict__ src_rec, T* __restrict__ force,
-                                                            T* __restrict__ virial, int64_t n_nodes) {
+                                                            T* __restrict__ virial, int64_t n_edges, int64_t n_nodes,
+                                                            int32_t n_records, int32_t n_pieces) {
   const int64_t block = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
   const int64_t i = block * (256 / kRecordLanes) + threadIdx.x / kRecordLanes;
   if (i >= n_nodes) return;
   const int c = threadIdx.x & (kRecordLanes - 1);
+  if (!plan_matches<T>(plan, n_edges, n_nodes)) return;
   const int32_t atom = plan.perm[i];
-  const int32_t piece0 = plan.piece_first[i], piece1 = plan.piece_first[i + 1];
-  const int32_t rec0 = plan.pos_rec[i], rec1 = plan.pos_rec[i + 1];
+  const int32_t piece0 = clamp_i32(plan.piece_first[i], 0, n_pieces);
+  const int32_t piece1 = clamp_i32(plan.piece_first[i + 1], piece0, n_pieces);
+  const int32_t rec0 = clamp_i32(plan.pos_rec[i], 0, n_records);
+  const int32_t rec1 = clamp_i32(plan.pos_rec[i + 1], rec0, n_records);
   const int cc = c < 12 ? c : 0;
   double acc = 0.0;
   for (int32_t p = piece0; p < piece1; ++p) acc += c < 3 ? dst_rec[static_cast<int64_t>(p) * 3 + c] : 0.0;
   for (int32_t base = rec0; base < rec1; base += kRecordLanes) {
     const int32_t here = rec1 - base < kRecordLanes ? rec1 - base : kRecordLanes;
-    const int32_t mine = plan.pos_records[base + (c < here ? c : 0)];
+    const int32_t id = plan.pos_records[base + (c < here ? c : 0)];
+    const int32_t mine = static_cast<uint32_t>(id) < static_cast<uint32_t>(n_records) ? id : 0;
     T part[kRecordLanes];
 #pragma unroll
     for (int k = 0; k < kRecordLanes; ++k) {
@@ -1110,7 +1147,7 @@ int check_plan_shapes(int64_t n_edges, int64_t n_nodes, const char* what) {
 }
 
 BlobView view_of(const BlobPlan& p) {
-  return BlobView{p.perm,     p.piece_first, p.piece_t,  p.blob_piece, p.blob_rec, p.blob_entry,
+  return BlobView{p.header, p.perm, p.piece_first, p.piece_t,  p.blob_piece, p.blob_rec, p.blob_entry,
                   p.row_edge, p.rec_entry,   p.pos_records, p.pos_rec, p.entry_row};
 }
 
@@ -1146,11 +1183,13 @@ int run_planned(const T* grad_edge, const T* edge_vec, T* force, T* virial, int6
   const BlobView view = view_of(arrays);
   const int64_t blobs = blob_count(n_edges, sizeof(T));
   force_blob_kernel<T><<<launch_grid(blobs, kBlobThreads), kBlobThreads, 0, stream>>>(
-      grad_edge, edge_vec, view, dst_rec, src_rec, n_edges, blobs);
+      grad_edge, edge_vec, view, dst_rec, src_rec, n_edges, n_nodes, blobs, static_cast<int32_t>(n_records),
+      static_cast<int32_t>(n_pieces));
   if (int s = launched("force_blob_kernel")) return s;
   const int64_t groups = (n_nodes + (256 / kRecordLanes) - 1) / (256 / kRecordLanes);
-  force_records_kernel<T><<<launch_grid(groups, 256), 256, 0, stream>>>(view, dst_rec, src_rec, force, virial,
-                                                                          n_nodes);
+  force_records_kernel<T><<<launch_grid(groups, 256), 256, 0, stream>>>(
+      view, dst_rec, src_rec, force, virial, n_edges, n_nodes, static_cast<int32_t>(n_records),
+      static_cast<int32_t>(n_pieces));
   return launched("force_records_kernel");
 }
 
@@ -1167,6 +1206,8 @@ int build_plan(const int64_t* dst_offsets, const int64_t* src_offsets, const int
   const int64_t rows = blob_rows_of<T>();
   const int64_t blobs = blob_count(n_edges, sizeof(T));
   const unsigned int node_blocks = stride_blocks(n_nodes + 1), edge_blocks = stride_blocks(n_edges);
+  // the header names the graph only once the plan is complete
+  if (int s = zero_fill(plan.header, kHeaderWords * sizeof(int64_t), stream)) return s;
   // validity of both CSRs, and the breadth-first root
   fill_i32_kernel<<<1, 256, 0, stream>>>(w.flags, kMaxLevels + 8, 0);
   if (int s = launched("fill_i32_kernel")) return s;
@@ -1261,6 +1302,10 @@ int build_plan(const int64_t* dst_offsets, const int64_t* src_offsets, const int
   plan_record_slots_kernel<<<stride_blocks(records > n_nodes + 1 ? records : n_nodes + 1), 256, 0, stream>>>(
       w.order, w.key_offsets, plan.pos_records, plan.pos_rec, records, n_nodes);
   if (int s = launched("plan_record_slots_kernel")) return s;
+  const int64_t header[kHeaderWords] = {kPlanMagic, n_edges, n_nodes, static_cast<int64_t>(sizeof(T))};
+  if (int s = hip_status(hipMemcpyAsync(plan.header, header, sizeof(header), hipMemcpyHostToDevice, stream),
+                         "hipMemcpyAsync"))
+    return s;
   counts_out[0] = records;
   counts_out[1] = pieces;
   return hip_status(hipStreamSynchronize(stream), "hipStreamSynchronize");

@@ -252,7 +252,12 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
  * `stream` (it reads the record and piece counts back, returned in
  * counts[0] and counts[1]) and fails with DPA4K_EINVAL unless both offsets
  * arrays are CSRs of n_edges slots.  Slots of src_order out of [0, E) are
- * skipped, as in the direct kernels.  The calls write the caller's records
+ * skipped, as in the direct kernels.  A plan starts with a header naming
+ * the edge count, atom count and value size it was built for: the planned
+ * calls leave their outputs unwritten for a plan whose header differs (a
+ * plan of another graph of the same sizes gives wrong sums, never an access
+ * out of bounds), and they bound the plan's records and pieces by the given
+ * counts.  The calls write the caller's records
  * buffer (dpa4k_force_assembly_records_size bytes): calls sharing one must
  * not overlap.  value_bytes = 4 (float32) or 8 (float64); a plan serves the
  * dtype it was built for.  E < 2^31 - 1, N >= 1.  The plan needs

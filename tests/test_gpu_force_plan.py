@@ -195,7 +195,7 @@ def _decode_plan(plan: _C.ForcePlan):
     atoms, edges = plan.n_nodes, plan.n_edges
     blobs = -(-edges // ROWS[plan.value_bytes])
     e = max(edges, 1)
-    layout = [("perm", atoms, np.int32), ("piece_first", atoms + 1, np.int32),
+    layout = [("header", 4, np.int64), ("perm", atoms, np.int32), ("piece_first", atoms + 1, np.int32),
               ("piece_t", atoms + blobs + 1, np.int32), ("blob_piece", blobs + 1, np.int32),
               ("blob_rec", blobs + 1, np.int32), ("blob_entry", blobs + 1, np.int32), ("row_edge", e, np.int32),
               ("entry_row", e, np.uint16), ("rec_entry", e + 1, np.int32), ("pos_records", e, np.int32),
@@ -213,6 +213,8 @@ def _check_plan_layout(plan, case):
     expected = _plan_restated(case, plan.value_bytes)
     got = _decode_plan(plan)
     assert plan.n_records == expected["records"] and plan.n_pieces == expected["pieces"]
+    magic = int.from_bytes(b"DPA4FPLN", "little")  # the header names what the plan was built for
+    np.testing.assert_array_equal(got["header"], [magic, plan.n_edges, plan.n_nodes, plan.value_bytes])
     lengths = {"piece_t": expected["pieces"] + 1, "rec_entry": expected["records"] + 1,
                "pos_records": expected["records"], "entry_row": expected["rec_entry"][-1]}
     for name in ("perm", "piece_first", "piece_t", "blob_piece", "blob_rec", "blob_entry", "row_edge", "entry_row",
