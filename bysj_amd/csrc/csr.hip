@@ -257,6 +257,18 @@ __device__ __forceinline__ int tile_elements(int64_t tile_base, int64_t limit) {
 // kFlagUnsorted (some in-range key followed by a smaller one, the element
 // after the tile included); `first_of_wave` is LDS scratch of
 // (kItems + 1) * kGroupWaves words.
+// Lane l receives lane l - 1's value (wave_shr:1; lane 0 keeps `fill`) or
+// lane l + 1's (wave_shl:1; lane 63 keeps `fill`): a DPP move on the VALU,
+// where __shfl_up/__shfl_down would each take an LDS round trip.
+__device__ __forceinline__ uint32_t from_lane_below(uint32_t value, uint32_t fill) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(fill), static_cast<int>(value), 0x138, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t from_lane_above(uint32_t value, uint32_t fill) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(fill), static_cast<int>(value), 0x130, 0xf, 0xf, false));
+}
+
 template <bool kCheck>
 __device__ __forceinline__ void load_keys64(const int64_t* keys, int64_t tile_base, int64_t limit, uint64_t n_nodes,
                                             TileKeys& tile, int32_t& flags, uint32_t* first_of_wave,
@@ -299,8 +311,8 @@ __device__ __forceinline__ void load_keys64(const int64_t* keys, int64_t tile_ba
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kItems; ++r) {
-      uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(tile.key[r]), 1, 64));
-      uint32_t next_ok = static_cast<uint32_t>(__shfl_down(static_cast<int>((tile.ok >> r) & 1u), 1, 64));
+      uint32_t next = from_lane_above(tile.key[r], 0u);
+      uint32_t next_ok = from_lane_above((tile.ok >> r) & 1u, 0u);
       if (lane == 63) {
         const int slot = wave + 1 < kGroupWaves ? r * kGroupWaves + wave + 1 : (r + 1) * kGroupWaves;
         next = first_of_wave[slot];
@@ -360,8 +372,8 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(const int64_t* __r
   for (int r = 0; r < kItems; ++r) {
     const bool valid = ((tile.ok >> r) & 1u) != 0u;
     const uint32_t digit = (tile.key[r] >> shift) & digit_mask;
-    const uint32_t previous = static_cast<uint32_t>(__shfl_up(static_cast<int>(digit), 1, 64));
-    const bool previous_valid = __shfl_up(valid ? 1 : 0, 1, 64) != 0;
+    const uint32_t previous = from_lane_below(digit, 0u);  // lane 0 is a head whatever it holds
+    const bool previous_valid = from_lane_below(valid ? 1u : 0u, 0u) != 0u;
     const bool head = valid && (lane == 0 || !previous_valid || previous != digit);
     // a run ends at the next head or invalid element
     const uint64_t stops = __ballot(head || !valid);
