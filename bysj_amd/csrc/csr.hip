@@ -90,17 +90,28 @@ __device__ __forceinline__ uint32_t load_u32(BufferView view, uint32_t offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(view, static_cast<int>(offset), 0, 0);
 }
 
+// A DPP move of `value` (control kCtrl, rows kRowMask); lanes whose source
+// lies outside their row, and rows outside the mask, read 0.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t value) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(value), kCtrl, kRowMask, 0xf, true));
+}
+
 // Exclusive scan of one value per thread over the workgroup; `total` gets
 // the sum.  Every thread must call it.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_t* wave_totals, uint32_t& total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  // inclusive scan of the wave on the VALU: row_shr 1, 2, 4, 8 scan each row
+  // of 16 lanes; row_bcast:15 adds lane 15's total to row 1 (and lane 47's
+  // to row 3), row_bcast:31 adds lane 31's to rows 2 and 3
   uint32_t inclusive = value;
-#pragma unroll
-  for (int offset = 1; offset < 64; offset <<= 1) {
-    const uint32_t other = __shfl_up(inclusive, offset, 64);
-    if (lane >= offset) inclusive += other;
-  }
+  inclusive += dpp_or_zero<0x111, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x112, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x114, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x118, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x142, 0xa>(inclusive);
+  inclusive += dpp_or_zero<0x143, 0xc>(inclusive);
   if (lane == 63) wave_totals[wave] = inclusive;
   __syncthreads();
   uint32_t before = 0, sum = 0;
