@@ -533,10 +533,12 @@ def edge_stream_job(n_edges: int, steps: int, warmup: int, graph: bool, label=No
     terms = [(1.0, x, None), (1.0, a, s), (1.0, b, None)]
 
     def chain(_):
+        # nothing is returned, so a captured step's [E, 10, 64] temporary goes back to the
+        # graph's pool for the next step (kept outputs would hold one per step)
         t = a * s
         t += x
         t += b
-        return torch.nn.functional.silu(t)
+        torch.nn.functional.silu(t, inplace=True)
 
     with torch.no_grad():
         ms = time_steps(lambda _: _C.edge_stream_combine(terms, shape, "silu", None, None, out), 1, steps, warmup,
