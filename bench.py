@@ -914,11 +914,12 @@ def _marked_steps(dispatches, labels: list[str]) -> dict:
 
 
 def _bench_json(path: str) -> dict:
+    """The full bench line of a log: the ``detail`` line when the run printed one, else its last JSON line."""
     with open(path) as handle:
-        rows = [row for row in handle if row.startswith("{")]
+        rows = [json.loads(row) for row in handle if row.startswith("{")]
     if not rows:
         raise SystemExit(f"no bench JSON line in {path}")
-    return json.loads(rows[-1])
+    return next((row for row in rows if row.get("detail")), rows[-1])
 
 
 def traffic_summary(fetch_csv: str, write_csv: str, bench_log: str, out_dir: Path | None = None) -> int:
@@ -984,6 +985,75 @@ def traffic_summary(fetch_csv: str, write_csv: str, bench_log: str, out_dir: Pat
     (out / "traffic.md").write_text("\n".join(text))
     print(f"wrote {len(table)} lines to {out / 'traffic.json'} and traffic.md")
     return 0
+
+
+# ---------------------------------------------------------------------------
+# the final line
+# ---------------------------------------------------------------------------
+
+# one row per `ops` entry of the final line; the detail line carries every field
+OPS_FIELDS = ("value", "unit", "us_per_step", "frac", "traffic_over_algorithmic", "share_of_same_bytes_copy",
+              "achieved_GBps")
+REFERENCE_FIELDS = ("eager_ms", "kernel_ms", "torch_gpu_ms", "dcu_ms", "dcu_torch_ms")
+FINAL_LINE_LIMIT = 8000  # bytes: the driver keeps the last ~8.5 KB of the output
+
+
+def _sig(value, digits: int = 4):
+    """``value`` rounded to ``digits`` significant digits (None and strings unchanged)."""
+    if not isinstance(value, (int, float)) or value == 0:
+        return value
+    return float(f"{value:.{digits}g}")
+
+
+def compact_line(line: dict) -> dict:
+    """The final JSON line: the headline's keys in full, every op as one row of OPS_FIELDS.
+
+    The full line (every field of every op, the reference's latency shapes with their sources,
+    the notes) is printed just before it with ``"detail": true``.
+    """
+    out = {key: value for key, value in line.items()
+           if key not in ("ops", "reference_shapes", "config5_dpa4_end_to_end", "cpu_baseline", "stream_ceilings",
+                          "traffic_marks")}
+    if "stream_ceilings" in line:
+        out["stream_ceilings"] = {k: v for k, v in line["stream_ceilings"].items() if k != "note"}
+    if "cpu_baseline" in line:
+        out["cpu_baseline"] = dict(line["cpu_baseline"])
+    ops = line.get("ops", {})
+    if ops:
+        out["ops_fields"] = list(OPS_FIELDS)
+        rows, cpu = {}, {}
+        for key, op in ops.items():
+            roof = op["roofline"]
+            traffic = roof.get("traffic")
+            ratio = round(traffic / roof["algorithmic_bytes"], 3) if traffic and roof["algorithmic_bytes"] else None
+            rows[key] = [_sig(op["value"]), op["unit"], round(op["ms_per_step"] * 1e3, 2), roof["frac"], ratio,
+                         op.get("share_of_same_bytes_copy"), round(roof["achieved"])]
+            if "cpu_baseline" in op:
+                c = op["cpu_baseline"]
+                cpu[key] = [_sig(c["value"]), c["unit"], c["cores"]]
+        out["ops"] = rows
+        if cpu:
+            out["ops_cpu_baseline_fields"] = ["value", "unit", "cores"]
+            out["ops_cpu_baseline"] = cpu
+    shapes = line.get("reference_shapes")
+    if shapes:
+        def ms(entry: dict, field: str):
+            if field in entry:
+                return entry[field]
+            micro = {"eager_ms": "eager_median_us", "kernel_ms": "kernel_us"}.get(field)  # the RMSNorm rows
+            return round(entry[micro] / 1e3, 5) if micro in entry else None
+
+        out["reference_shapes_fields"] = list(REFERENCE_FIELDS)
+        out["reference_shapes"] = {key: [ms(entry, field) for field in REFERENCE_FIELDS]
+                                   for key, entry in shapes.items() if isinstance(entry, dict)}
+    if "config5_dpa4_end_to_end" in line:
+        c5 = line["config5_dpa4_end_to_end"]
+        out["config5_dpa4_end_to_end"] = {"status": c5["status"], "unit": c5["unit"], "value": c5["value"]}
+    text = json.dumps(out)
+    if len(text) > FINAL_LINE_LIMIT:  # never expected: drop the secondary tables before the ops rows
+        for key in ("reference_shapes", "reference_shapes_fields", "ops_cpu_baseline", "ops_cpu_baseline_fields"):
+            out.pop(key, None)
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -1254,7 +1324,9 @@ def main() -> int:
         for name, result in extras.items():
             if name in ops:
                 ops[name]["cpu_baseline"] = result
-    print(json.dumps(line), flush=True)
+    # the full line first, then the compact one the driver keeps (it stores the last ~8.5 KB of output)
+    print(json.dumps({"detail": True, **line}), flush=True)
+    print(json.dumps(compact_line(line)), flush=True)
     return 0
 
 

@@ -324,11 +324,14 @@ int morton_bits(int64_t n_nodes) {
   return bits;
 }
 
-// A plan starts with a header naming what it was built for; the planned
-// kernels do nothing with a plan whose header does not match their call
-// (every index inside a plan is consistent with its own graph size).
+// A plan starts with a header naming what it was built for.  A planned call
+// whose graph sizes, value size or record and piece counts differ from the
+// header reads nothing else of the plan: it writes NaN into every output and
+// DPA4K_FORCE_PLAN_MISMATCH into the caller's status word (every index inside
+// a plan is consistent with its own graph size, so a plan of another graph of
+// the same sizes gives wrong sums, never an access out of bounds).
 constexpr int64_t kPlanMagic = 0x4e4c5046'34415044LL;  // "DPA4FPLN"
-constexpr int kHeaderWords = 4;                         // magic, n_edges, n_nodes, value_bytes
+constexpr int kHeaderWords = 6;  // magic, n_edges, n_nodes, value_bytes, n_records, n_pieces
 
 struct BlobPlan {
   int64_t* header;        // [kHeaderWords]
@@ -891,7 +894,8 @@ __device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t low, int32_t hig
 
 struct BlobView;
 template <typename T>
-__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes);
+__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes,
+                                             int32_t n_records, int32_t n_pieces);
 
 struct BlobView {
   const int64_t* header;
@@ -901,9 +905,11 @@ struct BlobView {
 };
 
 template <typename T>
-__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes) {
+__device__ __forceinline__ bool plan_matches(const BlobView& plan, int64_t n_edges, int64_t n_nodes,
+                                             int32_t n_records, int32_t n_pieces) {
   return plan.header[0] == kPlanMagic && plan.header[1] == n_edges && plan.header[2] == n_nodes &&
-         plan.header[3] == static_cast<int64_t>(sizeof(T));
+         plan.header[3] == static_cast<int64_t>(sizeof(T)) && plan.header[4] == n_records &&
+         plan.header[5] == n_pieces;
 }
 
 template <typename T>
@@ -1032,7 +1038,7 @@ __global__ __launch_bounds__(kBlobThreads) void force_blob_kernel(const T* __res
   // each XCD takes a contiguous range of blobs (so of atom positions): pass 2 on
   // that XCD then reads the records its L2 received
   const int64_t blob = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
-  if (blob >= blobs || !plan_matches<T>(plan, n_edges, n_nodes)) return;
+  if (blob >= blobs || !plan_matches<T>(plan, n_edges, n_nodes, n_records, n_pieces)) return;
   const int tid = static_cast<int>(threadIdx.x);
   const int64_t t0 = blob * kRows;
   const int64_t count = n_edges - t0 < kRows ? n_edges - t0 : kRows;
@@ -1105,12 +1111,23 @@ template <typename T>
 __global__ __launch_bounds__(256) void force_records_kernel(BlobView plan, const double* __restrict__ dst_rec,
                                                             const T* __restrict__ src_rec, T* __restrict__ force,
                                                             T* __restrict__ virial, int64_t n_edges, int64_t n_nodes,
-                                                            int32_t n_records, int32_t n_pieces) {
+                                                            int32_t n_records, int32_t n_pieces,
+                                                            int32_t* __restrict__ status) {
   const int64_t block = static_cast<int64_t>(blockIdx.y) * gridDim.x + xcd_block(blockIdx.x, gridDim.x);
   const int64_t i = block * (256 / kRecordLanes) + threadIdx.x / kRecordLanes;
+  const bool match = plan_matches<T>(plan, n_edges, n_nodes, n_records, n_pieces);
+  if (status != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    *status = match ? 0 : DPA4K_FORCE_PLAN_MISMATCH;
   if (i >= n_nodes) return;
   const int c = threadIdx.x & (kRecordLanes - 1);
-  if (!plan_matches<T>(plan, n_edges, n_nodes)) return;
+  if (!match) {  // nothing of the plan is read: atom i of this position's slot gets NaN
+    const T nan = __builtin_nan("");
+    if (c < 3)
+      force[i * 3 + c] = nan;
+    else if (c < 12)
+      virial[i * 9 + (c - 3)] = nan;
+    return;
+  }
   const int32_t atom = plan.perm[i];
   const int32_t piece0 = clamp_i32(plan.piece_first[i], 0, n_pieces);
   const int32_t piece1 = clamp_i32(plan.piece_first[i + 1], piece0, n_pieces);
@@ -1154,7 +1171,7 @@ BlobView view_of(const BlobPlan& p) {
 template <typename T>
 int run_planned(const T* grad_edge, const T* edge_vec, T* force, T* virial, int64_t n_edges, int64_t n_nodes,
                 const void* plan, size_t plan_bytes, void* records, size_t records_bytes, int64_t n_records,
-                int64_t n_pieces, dpa4k_stream_t stream_handle) {
+                int64_t n_pieces, int32_t* status, dpa4k_stream_t stream_handle) {
   clear_error();
   if (int s = check_plan_shapes(n_edges, n_nodes, "planned force assembly")) return s;
   if (force == nullptr || virial == nullptr || plan == nullptr || records == nullptr ||
@@ -1174,6 +1191,8 @@ int run_planned(const T* grad_edge, const T* edge_vec, T* force, T* virial, int6
     return fail(DPA4K_EINVAL, "planned force assembly: plan too small");
   hipStream_t stream = as_stream(stream_handle);
   if (n_edges == 0) {
+    if (status != nullptr)
+      if (int s = zero_fill(status, sizeof(int32_t), stream)) return s;
     if (int s = zero_fill(force, static_cast<size_t>(n_nodes) * 3 * sizeof(T), stream)) return s;
     return zero_fill(virial, static_cast<size_t>(n_nodes) * 9 * sizeof(T), stream);
   }
@@ -1189,7 +1208,7 @@ int run_planned(const T* grad_edge, const T* edge_vec, T* force, T* virial, int6
   const int64_t groups = (n_nodes + (256 / kRecordLanes) - 1) / (256 / kRecordLanes);
   force_records_kernel<T><<<launch_grid(groups, 256), 256, 0, stream>>>(
       view, dst_rec, src_rec, force, virial, n_edges, n_nodes, static_cast<int32_t>(n_records),
-      static_cast<int32_t>(n_pieces));
+      static_cast<int32_t>(n_pieces), status);
   return launched("force_records_kernel");
 }
 
@@ -1302,7 +1321,8 @@ int build_plan(const int64_t* dst_offsets, const int64_t* src_offsets, const int
   plan_record_slots_kernel<<<stride_blocks(records > n_nodes + 1 ? records : n_nodes + 1), 256, 0, stream>>>(
       w.order, w.key_offsets, plan.pos_records, plan.pos_rec, records, n_nodes);
   if (int s = launched("plan_record_slots_kernel")) return s;
-  const int64_t header[kHeaderWords] = {kPlanMagic, n_edges, n_nodes, static_cast<int64_t>(sizeof(T))};
+  const int64_t header[kHeaderWords] = {kPlanMagic, n_edges, n_nodes, static_cast<int64_t>(sizeof(T)), records,
+                                        pieces};
   if (int s = hip_status(hipMemcpyAsync(plan.header, header, sizeof(header), hipMemcpyHostToDevice, stream),
                          "hipMemcpyAsync"))
     return s;
@@ -1386,15 +1406,17 @@ extern "C" int dpa4k_force_assembly_plan(const int64_t* dst_offsets, const int64
 extern "C" int dpa4k_force_assembly_f32_planned(const float* grad_edge, const float* edge_vec, float* force,
                                                 float* virial, int64_t n_edges, int64_t n_nodes, const void* plan,
                                                 size_t plan_bytes, void* records, size_t records_bytes,
-                                                int64_t n_records, int64_t n_pieces, dpa4k_stream_t stream) {
+                                                int64_t n_records, int64_t n_pieces, int32_t* status,
+                                                dpa4k_stream_t stream) {
   return dpa4k::run_planned<float>(grad_edge, edge_vec, force, virial, n_edges, n_nodes, plan, plan_bytes, records,
-                                   records_bytes, n_records, n_pieces, stream);
+                                   records_bytes, n_records, n_pieces, status, stream);
 }
 
 extern "C" int dpa4k_force_assembly_f64_planned(const double* grad_edge, const double* edge_vec, double* force,
                                                 double* virial, int64_t n_edges, int64_t n_nodes, const void* plan,
                                                 size_t plan_bytes, void* records, size_t records_bytes,
-                                                int64_t n_records, int64_t n_pieces, dpa4k_stream_t stream) {
+                                                int64_t n_records, int64_t n_pieces, int32_t* status,
+                                                dpa4k_stream_t stream) {
   return dpa4k::run_planned<double>(grad_edge, edge_vec, force, virial, n_edges, n_nodes, plan, plan_bytes, records,
-                                    records_bytes, n_records, n_pieces, stream);
+                                    records_bytes, n_records, n_pieces, status, stream);
 }

@@ -22,6 +22,7 @@ inputs; ``segment_offsets``, ``group_by_key``, ``gie_group`` and the
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -277,10 +278,34 @@ def _null_checks(tensor, nodes, channels, what):
     _check(tensor.numel() == nodes * channels, f"{what} must have shape (n_nodes, channels)")
 
 
-def _offsets_fingerprint(offsets: torch.Tensor):
-    """Storage address, size and version counter of ``offsets`` (no counter for an inference tensor)."""
-    version = None if offsets.is_inference() else offsets._version
-    return (offsets.data_ptr(), offsets.numel(), version)
+class _TensorStamp:
+    """Which tensor a plan was built from: the object itself (weakly held), its storage, size and version.
+
+    A plan describes the values of its graph tensors when it was built.
+    :meth:`matches` holds for that same object only, unchanged since: not
+    for a copy, and not for a new tensor that the caching allocator placed
+    at a freed tensor's address (the weak reference of a freed tensor is
+    dead), nor after an in-place write (the version counter moves; an
+    inference tensor has none, and is trusted while it lives).
+    """
+
+    __slots__ = ("ref", "stamp")
+
+    def __init__(self, tensor: torch.Tensor):
+        self.ref = weakref.ref(tensor)
+        self.stamp = self._stamp_of(tensor)
+
+    @staticmethod
+    def _stamp_of(tensor: torch.Tensor):
+        version = None if tensor.is_inference() else tensor._version
+        return (tensor.data_ptr(), tensor.numel(), version)
+
+    def matches(self, tensor: torch.Tensor) -> bool:
+        return self.ref() is tensor and self.stamp == self._stamp_of(tensor)
+
+
+def _offsets_fingerprint(offsets: torch.Tensor) -> _TensorStamp:
+    return _TensorStamp(offsets)
 
 
 class SoftmaxPlan:
@@ -288,8 +313,9 @@ class SoftmaxPlan:
 
     ``fingerprint`` identifies the ``offsets`` tensor the plan was built from:
     a plan only lists that CSR's long segments, and the kernels would leave
-    any other long segment unwritten, so a plan is refused for offsets with
-    another storage, size or version (an in-place write).
+    any other long segment unwritten, so a plan is refused for any other
+    tensor (a copy, or a new tensor at a freed one's address) and after an
+    in-place write (:class:`_TensorStamp`).
     """
 
     __slots__ = ("words", "n_long", "capacity", "n_edges", "channels", "fingerprint")
@@ -322,7 +348,7 @@ def _plan_args(plan, offsets, edges, channels):
         return None
     _check(isinstance(plan, SoftmaxPlan) and plan.words.device == offsets.device
            and plan.n_edges == edges and plan.channels == channels
-           and plan.fingerprint == _offsets_fingerprint(offsets),
+           and plan.fingerprint is not None and plan.fingerprint.matches(offsets),
            "segment softmax plan was built for another graph, device or channel count")
     return plan
 
@@ -400,7 +426,8 @@ class ForcePlan:
     sums and per-record source sums), so calls that share a plan must not
     overlap (one stream at a time).  ``fingerprint`` identifies the offsets
     and ``src_order`` tensors the plan describes; a plan is refused for any
-    other (another storage, size or in-place version).
+    other tensor, even one at a freed tensor's address, and after an
+    in-place write (:class:`_TensorStamp`).
     """
 
     __slots__ = ("plan", "records", "n_edges", "n_nodes", "value_bytes", "n_records", "n_pieces", "fingerprint")
@@ -412,8 +439,12 @@ class ForcePlan:
         self.n_records, self.n_pieces, self.fingerprint = n_records, n_pieces, fingerprint
 
 
-def _force_fingerprint(dst_offsets, src_offsets, src_order):
-    return tuple(_offsets_fingerprint(t) for t in (dst_offsets, src_offsets, src_order))
+def _force_fingerprint(dst_offsets, src_offsets, src_order) -> tuple:
+    return tuple(_TensorStamp(t) for t in (dst_offsets, src_offsets, src_order))
+
+
+def _force_plan_matches(plan, dst_offsets, src_offsets, src_order) -> bool:
+    return all(stamp.matches(t) for stamp, t in zip(plan.fingerprint, (dst_offsets, src_offsets, src_order)))
 
 
 def force_assembly_plan(dst_offsets, src_offsets, src_order, edge_vec=None, *, value_bytes: int = 4) -> ForcePlan:
@@ -481,13 +512,13 @@ def force_assembly(grad_edge, edge_vec, dst_offsets, src_offsets, src_order, *, 
     if plan is not None:
         _check(isinstance(plan, ForcePlan) and plan.n_edges == edges and plan.n_nodes == nodes
                and plan.plan.device == grad_edge.device and plan.value_bytes == grad_edge.element_size()
-               and plan.fingerprint == _force_fingerprint(dst_offsets, src_offsets, src_order),
+               and _force_plan_matches(plan, dst_offsets, src_offsets, src_order),
                "force assembly plan was built for another graph, device or dtype")
         entry = _LIB.dpa4k_force_assembly_f32_planned if single else _LIB.dpa4k_force_assembly_f64_planned
         with _on(grad_edge.device) as stream:
             status = entry(_ptr(grad_edge), _ptr(edge_vec), force.data_ptr(), virial.data_ptr(), edges, nodes,
                            plan.plan.data_ptr(), plan.plan.numel(), plan.records.data_ptr(), plan.records.numel(),
-                           plan.n_records, plan.n_pieces, stream)
+                           plan.n_records, plan.n_pieces, None, stream)
         _lib.check(status)
         return force, virial
     entry = _LIB.dpa4k_force_assembly_f32 if single else _LIB.dpa4k_force_assembly_f64

@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libdpa4k.so"
 
 OK, EINVAL, EHIP, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -63,8 +63,8 @@ PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "dpa4k_force_assembly_records_size": (_SZ, [_I64, _I64, _I64]),
     "dpa4k_force_assembly_plan": (
         _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P, _SZ, ctypes.POINTER(ctypes.c_int64), _P]),
-    "dpa4k_force_assembly_f32_planned": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _SZ, _P, _SZ, _I64, _I64, _P]),
-    "dpa4k_force_assembly_f64_planned": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _SZ, _P, _SZ, _I64, _I64, _P]),
+    "dpa4k_force_assembly_f32_planned": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _SZ, _P, _SZ, _I64, _I64, _P, _P]),
+    "dpa4k_force_assembly_f64_planned": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _SZ, _P, _SZ, _I64, _I64, _P, _P]),
     "dpa4k_gie_group_workspace_size": (_SZ, [_I64, _I64]),
     "dpa4k_gie_group": (
         _INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, ctypes.POINTER(ctypes.c_int32), _P, _SZ, _P]),

@@ -41,23 +41,37 @@ def _seam_name(name: Any) -> str:
 def _normalize_fused(fused: Any) -> dict[str, bool] | None:
     """The per-seam switches of a ``fused`` argument, or None to install nothing.
 
-    ``True`` selects the default seams; a name, or a collection of names,
-    selects those; a mapping switches the seams it names.  Unknown names
-    raise ``ValueError``, other argument types ``TypeError``.
+    Any false value (``None``, ``False``, ``0``, ``""``, an empty collection)
+    installs nothing.  ``True`` selects the default seams; a name, or a
+    collection of names, selects those (the result names only them); a
+    mapping gives every default seam a switch, off unless the mapping turns
+    it on, plus any other seam it names.  Unknown names raise
+    ``ValueError``, other argument types ``TypeError``.
+    :func:`_patch_switches` turns a selection into the switch of every seam.
     """
-    if fused is None or fused is False:
+    if not fused:
         return None
     if fused is True:
         return {name: True for name, default in _SEAM_TABLE.items() if default}
     if isinstance(fused, Mapping):
-        selection = {_seam_name(name): bool(value) for name, value in fused.items()}
-    elif isinstance(fused, str):
-        selection = {_seam_name(fused): True}
-    elif isinstance(fused, Iterable):
-        selection = {_seam_name(name): True for name in fused}
-    else:
-        raise TypeError("fused must be a bool, a seam name, a collection of seam names or a mapping")
-    return selection or None
+        named = {_seam_name(name): bool(value) for name, value in fused.items()}
+        selection = {name: named.pop(name, False) for name, default in _SEAM_TABLE.items() if default}
+        selection.update(named)
+        return selection
+    if isinstance(fused, str):
+        return {_seam_name(fused): True}
+    if isinstance(fused, Iterable):
+        return {_seam_name(name): True for name in fused} or None
+    raise TypeError("fused must be a bool, a seam name, a collection of seam names or a mapping")
+
+
+def _patch_switches(selection: Mapping[str, bool]) -> dict[str, bool]:
+    """``deepmd_patch``'s keyword for every seam: on only where ``selection`` turns it on.
+
+    ``deepmd_patch`` switches the reference's two seams on by default, so a
+    selection of one seam must switch the others off explicitly.
+    """
+    return {name: bool(selection.get(name, False)) for name in SEAMS}
 
 
 def _create_deep_pot(model_file: str, **kwargs: Any) -> Any:
@@ -106,7 +120,8 @@ class DPA4Model:
         self.fused_ops: dict[str, Any] = {}
         if self.fused_seams:
             seams = _seam_module()
-            self.fused_ops = dict(seams.status(seams.deepmd_patch(self._deep_pot, **self.fused_seams)))
+            self.fused_ops = dict(seams.status(seams.deepmd_patch(self._deep_pot,
+                                                                  **_patch_switches(self.fused_seams))))
 
     def eval(self, coords: Any, cells: Any, atom_types: Any, *, atomic: bool = False, fparam: Any = None,
              aparam: Any = None, **kwargs: Any) -> Any:

@@ -170,6 +170,65 @@ class _CsrView:
         return len(self._entries)
 
 
+class _ForceView:
+    """What the force seam derives from DeepMD's two edge groupings, per ``(dst_order, src_order)`` pair (LRU).
+
+    ``force_assembly`` takes the values in destination order and names each
+    source slot's edge by its destination slot: ``slot_order[q] =
+    rank[src_order[q]]``, with ``rank`` the inverse of ``dst_order``.  Built
+    once per pair of tensor objects (one host synchronisation, to learn
+    whether ``dst_order`` is the identity, in which case the values need no
+    gather) and kept while both objects live unchanged, so that later calls
+    hand the same ``slot_order`` object to the operator, whose blob plan is
+    cached per that object.  Inference tensors keep no version counter:
+    nothing is kept for them.
+    """
+
+    def __init__(self, capacity: int = _CSR_CAPACITY):
+        self.capacity = capacity
+        self._entries: dict[tuple, tuple] = {}  # key -> (dst ref, src ref, stamps, slot_order, identity)
+
+    @staticmethod
+    def _stamp(tensor: torch.Tensor):
+        if tensor.is_inference():
+            return None
+        return (tensor.data_ptr(), tensor.numel(), tensor._version, str(tensor.device))
+
+    @staticmethod
+    def _derive(dst_order: torch.Tensor, src_order: torch.Tensor) -> tuple[torch.Tensor, bool]:
+        edges = dst_order.numel()
+        slots = torch.arange(edges, device=dst_order.device, dtype=dst_order.dtype)
+        rank = torch.empty_like(dst_order)
+        rank[dst_order] = slots
+        identity = bool(torch.equal(dst_order, slots))
+        return rank.index_select(0, src_order).contiguous(), identity
+
+    def _forget(self, key: tuple) -> None:
+        entry = self._entries.get(key)
+        if entry is not None and (entry[0]() is None or entry[1]() is None):
+            del self._entries[key]
+
+    def get(self, dst_order: torch.Tensor, src_order: torch.Tensor) -> tuple[torch.Tensor, bool]:
+        stamps = (self._stamp(dst_order), self._stamp(src_order))
+        if stamps[0] is None or stamps[1] is None:
+            return self._derive(dst_order, src_order)
+        key = (id(dst_order), id(src_order))
+        entry = self._entries.pop(key, None)
+        if entry is not None and entry[0]() is dst_order and entry[1]() is src_order and entry[2] == stamps:
+            self._entries[key] = entry            # most recently used last
+            return entry[3], entry[4]
+        slot_order, identity = self._derive(dst_order, src_order)
+        forget = lambda _, key=key: self._forget(key)  # noqa: E731
+        self._entries[key] = (weakref.ref(dst_order, forget), weakref.ref(src_order, forget), stamps, slot_order,
+                              identity)
+        while len(self._entries) > self.capacity:
+            self._entries.pop(next(iter(self._entries)))
+        return slot_order, identity
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+
 # ---------------------------------------------------------------------------
 # finding the seams
 # ---------------------------------------------------------------------------
@@ -281,6 +340,7 @@ class _Installation:
     def __init__(self, ops: Any, stats: FusedStats):
         self.ops, self.stats = ops, stats
         self.csr = _CsrView()
+        self.force_views = _ForceView()
         self.rebindings: list[_Rebinding] = []
         self.warned = False
 
@@ -388,13 +448,16 @@ class _Installation:
             self.fallback("force")
             return stock(*args)
         try:
-            # rank[e] = the slot of edge e in the destination grouping
-            rank = torch.empty_like(dst_order)
-            rank[dst_order] = torch.arange(dst_order.numel(), device=dst_order.device)
-            grouped_g = g.index_select(0, dst_order).contiguous()
-            grouped_v = edge_vec.detach().index_select(0, dst_order).contiguous()
+            # the source slots named by their destination slots (kept per grouping pair, so the
+            # operator's blob plan, cached per that tensor, is built once per neighbour graph)
+            slot_order, identity = self.force_views.get(dst_order, src_order)
+            if identity:
+                grouped_g, grouped_v = g, edge_vec.detach()
+            else:
+                grouped_g = g.index_select(0, dst_order)
+                grouped_v = edge_vec.detach().index_select(0, dst_order)
             force, virial = self.ops.force_assembly(grouped_g, grouped_v, None, None, dst_row_ptr, src_row_ptr,
-                                                    rank.index_select(0, src_order).contiguous())
+                                                    slot_order)
         except Exception as error:  # noqa: BLE001 -- a seam must never break inference
             self.fallback("force", error)
             return stock(*args)

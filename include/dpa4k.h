@@ -59,7 +59,7 @@ const char* dpa4k_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int dpa4k_abi_version(void);
-#define DPA4K_ABI_VERSION 9
+#define DPA4K_ABI_VERSION 10
 
 /* ------------------------------------------------------------------------
  * CSR construction
@@ -253,11 +253,17 @@ int dpa4k_force_assembly_f64(const double* grad_edge, const double* edge_vec,
  * counts[0] and counts[1]) and fails with DPA4K_EINVAL unless both offsets
  * arrays are CSRs of n_edges slots.  Slots of src_order out of [0, E) are
  * skipped, as in the direct kernels.  A plan starts with a header naming
- * the edge count, atom count and value size it was built for: the planned
- * calls leave their outputs unwritten for a plan whose header differs (a
- * plan of another graph of the same sizes gives wrong sums, never an access
- * out of bounds), and they bound the plan's records and pieces by the given
- * counts.  The calls write the caller's records
+ * the edge count, atom count, value size and the record and piece counts
+ * it was built with.  A planned call checks it on the device: for a plan
+ * whose header differs from the call (another graph's size, dtype or
+ * counts, or a build that did not finish), it reads nothing else of the
+ * plan, writes NaN into every element of force and virial and sets
+ * `*status` (a device int32, may be NULL) to DPA4K_FORCE_PLAN_MISMATCH;
+ * otherwise it sets `*status` to 0.  The call itself returns DPA4K_OK in
+ * both cases (it never synchronises): read `status` before trusting the
+ * outputs.  A plan of another graph with identical sizes and counts gives
+ * wrong sums, never an access out of bounds; the plan's own indices are
+ * bounded by the given counts.  The calls write the caller's records
  * buffer (dpa4k_force_assembly_records_size bytes): calls sharing one must
  * not overlap.  value_bytes = 4 (float32) or 8 (float64); a plan serves the
  * dtype it was built for.  E < 2^31 - 1, N >= 1.  The plan needs
@@ -283,14 +289,17 @@ int dpa4k_force_assembly_f32_planned(const float* grad_edge,
                                      int64_t n_nodes, const void* plan,
                                      size_t plan_bytes, void* records,
                                      size_t records_bytes, int64_t n_records,
-                                     int64_t n_pieces, dpa4k_stream_t stream);
+                                     int64_t n_pieces, int32_t* status,
+                                     dpa4k_stream_t stream);
 int dpa4k_force_assembly_f64_planned(const double* grad_edge,
                                      const double* edge_vec, double* force,
                                      double* virial, int64_t n_edges,
                                      int64_t n_nodes, const void* plan,
                                      size_t plan_bytes, void* records,
                                      size_t records_bytes, int64_t n_records,
-                                     int64_t n_pieces, dpa4k_stream_t stream);
+                                     int64_t n_pieces, int32_t* status,
+                                     dpa4k_stream_t stream);
+#define DPA4K_FORCE_PLAN_MISMATCH 4
 
 /* ------------------------------------------------------------------------
  * Edge-stream elementwise chain

@@ -166,3 +166,31 @@ def test_softmax_plan_is_refused_for_other_offsets():
         frozen = torch.tensor([0, 3, 9, 10], dtype=torch.int64)
     frozen_plan = _C.SoftmaxPlan(plan.words, 0, 96, 10, 8, _C._offsets_fingerprint(frozen))
     assert _C._plan_args(frozen_plan, frozen, 10, 8) is frozen_plan
+
+
+def test_plans_are_refused_for_a_new_tensor_at_a_freed_tensors_address():
+    """A plan holds its graph tensors weakly: a same-size graph allocated where a freed one was is refused."""
+    import gc
+
+    import torch
+
+    from bysj_amd.kernels import _C
+
+    offsets = torch.tensor([0, 3, 9, 10], dtype=torch.int64)
+    plan = _C.SoftmaxPlan(torch.zeros(4, dtype=torch.int32), 0, 96, 10, 8, _C._offsets_fingerprint(offsets))
+    stamp = plan.fingerprint.stamp
+    del offsets
+    gc.collect()
+    reused = torch.tensor([0, 1, 2, 10], dtype=torch.int64)
+    # whether or not the allocator hands back the same address, a stamp of the same
+    # address, size and version held by a dead reference must not match
+    plan.fingerprint.stamp = _C._TensorStamp._stamp_of(reused)
+    assert plan.fingerprint.ref() is None and stamp[1:] == plan.fingerprint.stamp[1:]
+    with pytest.raises(RuntimeError, match="another graph"):
+        _C._plan_args(plan, reused, 10, 8)
+    graph = [torch.tensor([0, 2, 5], dtype=torch.int64), torch.tensor([0, 4, 5], dtype=torch.int64),
+             torch.arange(5, dtype=torch.int64)]
+    stamps = _C._force_fingerprint(*graph)
+    holder = _C.ForcePlan(torch.zeros(1), torch.zeros(1), 5, 2, 4, 1, 1, stamps)
+    assert _C._force_plan_matches(holder, *graph)
+    assert not _C._force_plan_matches(holder, graph[0], graph[1], graph[2].clone())

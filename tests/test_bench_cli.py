@@ -115,3 +115,63 @@ def test_traffic_summary_refuses_passes_that_launched_different_kernels(tmp_path
     fetch, write, log = _traffic_case(tmp_path, write_steps=other)
     with pytest.raises(SystemExit, match="different kernels"):
         bench.traffic_summary(str(fetch), str(write), str(log), out_dir=tmp_path)
+
+
+# ---------------------------------------------------------------------------
+# the final line: every op row inside what the driver keeps
+# ---------------------------------------------------------------------------
+
+def _full_line(n_ops: int) -> dict:
+    roof = {"bound": "hbm", "achieved": 5656.2, "peak": 8000.0, "unit": "GB/s", "frac": 0.707, "traffic": 5_600_000_000,
+            "algorithmic_bytes": 5_503_000_000}
+    op = {"op": "segment_sum_fwd", "value": 10771234567.8, "unit": "edges/s", "ms_per_step": 0.97308, "input_sets": 3,
+          "roofline": roof, "edges": 10485760, "nodes": 262144, "channels": 128, "same_bytes_copy_us": 1041.9,
+          "share_of_same_bytes_copy": 1.0707,
+          "cpu_baseline": {"value": 2.7e7, "unit": "edges/s", "cores": 16, "sample": "x" * 120, "ms_per_call": 213.4}}
+    shapes = {f"shape_{i}": {"eager_ms": 0.0235, "kernel_ms": 0.0232, "torch_gpu_ms": 0.4899, "dcu_ms": 0.49,
+                             "dcu_torch_ms": 4.42, "source": "docs/task2-hip-fusion-plan.md:229"} for i in range(6)}
+    shapes["rmsnorm_1x128"] = {"eager_median_us": 9.9, "eager_p95_us": 10.2, "kernel_us": 1.9, "dcu_ms": None,
+                               "source": "tests/csrc/latency/test_rmsnorm_latency.py"}
+    shapes["note"] = "same inputs every call" * 5
+    return {"metric": "segment-op edges/s + % HBM roofline (segment_softmax forward, config 2)", "value": 5.7e10,
+            "unit": "edges/s", "n_gpus": 1, "steps": 20, "warmup": 5, "ms_per_step": 0.01516,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "segment_softmax_fwd_config2"}, "roofline": dict(roof),
+            "stream_ceilings": {"read_GBps": 6038.8, "note": "n" * 200},
+            "ops": {f"op_with_a_long_name_{i:02d}": dict(op) for i in range(n_ops)}, "reference_shapes": shapes,
+            "config5_dpa4_end_to_end": {"status": "unavailable", "unit": "atom-steps/s", "value": None,
+                                        "reason": "r" * 200},
+            "cpu_baseline": {"value": 6.4e7, "unit": "edges/s", "cores": 16, "kind": "port", "sample": "s" * 150}}
+
+
+def test_final_line_keeps_every_op_within_the_drivers_tail():
+    import json
+
+    import bench
+
+    line = _full_line(40)  # more ops than the default run prints (31)
+    assert len(json.dumps(line)) > 2 * bench.FINAL_LINE_LIMIT
+    final = bench.compact_line(line)
+    text = json.dumps(final)
+    assert len(text) < bench.FINAL_LINE_LIMIT
+    assert set(final["ops"]) == set(line["ops"])
+    row = dict(zip(final["ops_fields"], final["ops"]["op_with_a_long_name_07"]))
+    assert row["frac"] == 0.707 and row["unit"] == "edges/s" and row["us_per_step"] == 973.08
+    assert row["traffic_over_algorithmic"] == round(5_600_000_000 / 5_503_000_000, 3)
+    assert row["share_of_same_bytes_copy"] == 1.0707 and row["achieved_GBps"] == 5656
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "roofline", "cpu_baseline"):
+        assert final[key] == line[key]
+    shapes = dict(zip(final["reference_shapes_fields"], final["reference_shapes"]["rmsnorm_1x128"]))
+    assert shapes["eager_ms"] == 0.0099 and shapes["kernel_ms"] == 0.0019
+    assert final["config5_dpa4_end_to_end"]["status"] == "unavailable"
+
+
+def test_traffic_summary_reads_the_detail_line(tmp_path):
+    import json
+
+    import bench
+
+    detail = {"detail": True, "config": {"workload": "w"}, "roofline": {"algorithmic_bytes": 7}, "ops": {}}
+    log = tmp_path / "bench.log"
+    log.write_text(json.dumps(detail) + "\n" + json.dumps({"ops": {"x": [1, 2]}}) + "\n")
+    assert bench._bench_json(str(log)) == detail

@@ -195,7 +195,7 @@ def _decode_plan(plan: _C.ForcePlan):
     atoms, edges = plan.n_nodes, plan.n_edges
     blobs = -(-edges // ROWS[plan.value_bytes])
     e = max(edges, 1)
-    layout = [("header", 4, np.int64), ("perm", atoms, np.int32), ("piece_first", atoms + 1, np.int32),
+    layout = [("header", 6, np.int64), ("perm", atoms, np.int32), ("piece_first", atoms + 1, np.int32),
               ("piece_t", atoms + blobs + 1, np.int32), ("blob_piece", blobs + 1, np.int32),
               ("blob_rec", blobs + 1, np.int32), ("blob_entry", blobs + 1, np.int32), ("row_edge", e, np.int32),
               ("entry_row", e, np.uint16), ("rec_entry", e + 1, np.int32), ("pos_records", e, np.int32),
@@ -214,7 +214,8 @@ def _check_plan_layout(plan, case):
     got = _decode_plan(plan)
     assert plan.n_records == expected["records"] and plan.n_pieces == expected["pieces"]
     magic = int.from_bytes(b"DPA4FPLN", "little")  # the header names what the plan was built for
-    np.testing.assert_array_equal(got["header"], [magic, plan.n_edges, plan.n_nodes, plan.value_bytes])
+    np.testing.assert_array_equal(got["header"], [magic, plan.n_edges, plan.n_nodes, plan.value_bytes,
+                                                  plan.n_records, plan.n_pieces])
     lengths = {"piece_t": expected["pieces"] + 1, "rec_entry": expected["records"] + 1,
                "pos_records": expected["records"], "entry_row": expected["rec_entry"][-1]}
     for name in ("perm", "piece_first", "piece_t", "blob_piece", "blob_rec", "blob_entry", "row_edge", "entry_row",
@@ -386,3 +387,38 @@ def test_operator_plans_compact_graphs_only():
     after = segment_ops._FORCE_PLANS._entries[(id(d["src_order"]), torch.float32)][2]
     assert after is not None and after is not before
     segment_ops._FORCE_PLANS.clear()
+
+
+def test_planned_call_reports_a_plan_that_does_not_match_it():
+    """Through the C ABI: a plan whose header differs from the call (record count, or a buffer that no build
+    finished) yields NaN in every output and DPA4K_FORCE_PLAN_MISMATCH in the status word; a matching call
+    clears the word."""
+    from bysj_amd.kernels import _lib
+
+    announce("force plan mismatch through the C ABI")
+    library = _lib.load()
+    d = _on_device(_random_graph(300, 9000, 47))
+    g, v = d["grad_edge"].float(), d["edge_vec"].float()
+    plan = _plan(d, torch.float32)
+    status = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    force = torch.empty((300, 3), device=DEV)
+    virial = torch.empty((300, 9), device=DEV)
+
+    def call(plan_buffer, n_records):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = library.dpa4k_force_assembly_f32_planned(
+            g.data_ptr(), v.data_ptr(), force.data_ptr(), virial.data_ptr(), 9000, 300, plan_buffer.data_ptr(),
+            plan_buffer.numel(), plan.records.data_ptr(), plan.records.numel(), n_records, plan.n_pieces,
+            status.data_ptr(), stream)
+        assert rc == _lib.OK, library.dpa4k_last_error()
+        torch.cuda.synchronize()
+        return int(status.item())
+
+    assert call(plan.plan, plan.n_records - 1) == 4  # DPA4K_FORCE_PLAN_MISMATCH
+    assert torch.isnan(force).all() and torch.isnan(virial).all()
+    assert call(torch.zeros_like(plan.plan), plan.n_records) == 4  # no build finished in this buffer
+    assert torch.isnan(force).all() and torch.isnan(virial).all()
+    assert call(plan.plan, plan.n_records) == 0
+    direct = _run(d, torch.float32)
+    assert_close_scaled(force, direct[0], what="matching call: force")
+    assert_close_scaled(virial, direct[1], what="matching call: virial")

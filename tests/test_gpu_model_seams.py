@@ -129,3 +129,57 @@ def test_force_seam_on_gfx950_matches_the_stock_chain(clean, dtype):
         else:
             assert_close_scaled(got, exact, what=f"{label} vs fp64 truth")
             assert_close_scaled(got, theirs, what=f"{label} vs the stock chain")
+
+
+def test_force_seam_builds_the_blob_plan_once_per_graph(clean, monkeypatch):
+    """A water graph above the plan threshold, in a shuffled natural edge order (DeepMD's extended lists): two
+    seam calls with fresh per-edge gradients build one blob plan, run the planned kernels both times, and
+    match the stock chain."""
+    from bysj_amd import workloads
+    from bysj_amd.kernels import _C
+    from bysj_amd.kernels import segment as segment_ops
+    from seam_fakes import edge_force_virial_call, force_namespace
+
+    graph = workloads.water_graph(2048, seed=4)
+    n_edges = graph.n_edges
+    assert n_edges >= segment_ops._ForcePlanCache.MIN_EDGES
+    announce("force seam plan reuse", 2048, n_edges)
+    shuffle = torch.randperm(n_edges, generator=torch.Generator().manual_seed(5))
+    dst = torch.from_numpy(graph.dst)[shuffle].to(DEV)
+    src = torch.from_numpy(graph.src)[shuffle].to(DEV)
+    vec = torch.from_numpy(graph.edge_vec)[shuffle].float().contiguous().to(DEV)
+    builds, planned = [], []
+    build = _C.force_assembly_plan
+    run = _C.force_assembly
+
+    def counting_build(*args, **kwargs):
+        builds.append(args[2])
+        return build(*args, **kwargs)
+
+    def recording_run(*args, plan=None):
+        planned.append(plan is not None)
+        return run(*args, plan=plan)
+
+    monkeypatch.setattr(_C, "force_assembly_plan", counting_build)
+    monkeypatch.setattr(_C, "force_assembly", recording_run)
+    segment_ops._FORCE_PLANS.clear()
+    space = force_namespace()
+    stats = fused_deepmd.deepmd_patch(FakeModel([]), softmax=False, envelope=False, force=True,
+                                      force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    gen = torch.Generator().manual_seed(6)
+    g0 = torch.randn(n_edges, 3, generator=gen).to(DEV)
+    args = list(edge_force_virial_call(g0, vec, dst, src, 2048))
+    results = []
+    for step in range(2):
+        args[0] = torch.randn(n_edges, 3, generator=gen).to(DEV) if step else g0  # new gradients each step
+        results.append((tuple(args), space.edge_force_virial(*args)))
+    assert stats.force_hits == 2 and stats.force_fallbacks == 0, stats
+    assert len(builds) == 1, f"one blob plan per graph, got {len(builds)} builds"
+    assert planned == [True, True], "both calls run the planned kernels"
+    fused_deepmd.uninstall()
+    for call_args, (force, atom_virial, frame_virial, _) in results:
+        stock = space.edge_force_virial(*call_args)
+        for label, got, theirs in zip(("force", "atom virial", "frame virial"), (force, atom_virial, frame_virial),
+                                      stock):
+            assert_close_scaled(got, theirs, what=f"{label} vs the stock chain")
+    segment_ops._FORCE_PLANS.clear()

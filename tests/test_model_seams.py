@@ -355,7 +355,7 @@ def test_facade_installs_the_seams_and_uninstalls_once():
             mock.patch.object(fused_deepmd, "status", return_value=report), \
             mock.patch.object(fused_deepmd, "uninstall") as uninstall:
         model = DPA4Model("water.pt", fused=True)
-        patch.assert_called_once_with(pot, softmax=True, envelope=True)
+        patch.assert_called_once_with(pot, softmax=True, envelope=True, force=False)
         assert model.fused_ops == report and model.fused_seams == {"softmax": True, "envelope": True}
         assert "fused_ops={'softmax_hits': 0" in repr(model)
         model.close()
@@ -365,6 +365,30 @@ def test_facade_installs_the_seams_and_uninstalls_once():
         with DPA4Model("water.pt", fused=("softmax",)) as scoped:
             assert isinstance(scoped, DPA4Model)
     assert pot.closed
+
+
+@pytest.mark.parametrize("fused, switches", [
+    (("force",), {"softmax": False, "envelope": False, "force": True}),
+    ("envelope", {"softmax": False, "envelope": True, "force": False}),
+    ({"softmax": True}, {"softmax": True, "envelope": False, "force": False}),
+    ({"envelope": False, "force": True}, {"softmax": False, "envelope": False, "force": True}),
+])
+def test_facade_switches_off_every_seam_it_does_not_select(fused, switches):
+    """deepmd_patch turns the reference's two seams on by default: a partial selection passes every switch."""
+    with mock.patch.object(dpa4, "_create_deep_pot", return_value=_FakeDeepPot()), \
+            mock.patch.object(fused_deepmd, "deepmd_patch") as patch, \
+            mock.patch.object(fused_deepmd, "status", return_value={"x": 1}):
+        DPA4Model("water.pt", fused=fused)
+    assert patch.call_args.kwargs == switches
+
+
+def test_any_false_switch_installs_nothing():
+    for off in (False, None, (), 0, "", [], {}, np.bool_(False)):
+        assert _normalize_fused(off) is None, off
+    with mock.patch.object(dpa4, "_create_deep_pot", return_value=_FakeDeepPot()), \
+            mock.patch.object(fused_deepmd, "deepmd_patch") as patch:
+        DPA4Model("water.pt", fused=0)
+    patch.assert_not_called()
 
 
 def test_facade_rejects_bad_switches_before_loading():
@@ -462,3 +486,40 @@ def test_force_seam_is_opt_in_and_reports_missing_homes(any_device):
                                           force=True, force_namespaces=[])
     assert not stats.bound_force and "edge_force_virial is not importable here" in buffer.getvalue()
     fused_deepmd.uninstall()
+
+
+def test_force_seam_derives_its_slot_order_once_per_grouping_pair(any_device):
+    """The same (dst_order, src_order) objects give the operator the same slot_order object (so its plan cache
+    hits); an in-place write to either grouping or another pair derives it again; an identity dst_order makes
+    the seam pass the values without a gather."""
+    g, vec, dst, src, n_ext = _force_case(n_ext=9, n_edges=60, seed=8)
+    seen = []
+
+    class Recording(OracleOps):
+        def force_assembly(self, grad_edge, edge_vec, src, dst, dst_offsets, src_offsets=None, src_order=None):
+            seen.append((grad_edge, src_order))
+            return super().force_assembly(grad_edge, edge_vec, src, dst, dst_offsets, src_offsets, src_order)
+
+    space = force_namespace()
+    fused_deepmd.deepmd_patch(FakeModel([]), ops=Recording(), softmax=False, envelope=False, force=True,
+                              force_namespaces=[(space, "edge_force_virial")], verbose=False)
+    args = edge_force_virial_call(g, vec, dst, src, n_ext)
+    first = space.edge_force_virial(*args)
+    second = space.edge_force_virial(*args)
+    assert seen[0][1] is seen[1][1], "the slot order is derived once per grouping pair"
+    torch.testing.assert_close(first[0], second[0], rtol=0, atol=0)
+    args[6].add_(0)  # an in-place write to src_order: derived again
+    space.edge_force_virial(*args)
+    assert seen[2][1] is not seen[1][1]
+    torch.testing.assert_close(seen[2][1], seen[1][1], rtol=0, atol=0)
+    # destination-sorted natural order: dst_order is the identity and the values go in as they are
+    order = torch.argsort(dst, stable=True)
+    sorted_args = list(edge_force_virial_call(g[order].contiguous(), vec[order].contiguous(), dst[order], src[order],
+                                              n_ext))
+    sorted_args[4] = torch.arange(60)  # a stable grouping of a sorted list (the quoted argsort may swap ties)
+    result = space.edge_force_virial(*sorted_args)
+    assert seen[-1][0] is sorted_args[0]
+    fused_deepmd.uninstall()
+    expected = space.edge_force_virial(*sorted_args)
+    torch.testing.assert_close(result[0], expected[0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(result[1], expected[1], rtol=1e-5, atol=1e-5)
