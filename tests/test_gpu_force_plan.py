@@ -7,7 +7,8 @@ order.  The two paths therefore agree within rounding, and the planned one
 is reproducible run to run.  Its layout is checked exactly against a NumPy
 restatement of the plan's definition: positions along the breadth-first tree
 (float32 arithmetic, as the kernels do it), Morton cells, blobs of
-2816 / 1408 concatenated rows, pieces, entries and records.
+2816 / 1408 concatenated rows, pieces, entries (source slots in the spatial
+order of their atoms) and records.
 """
 from __future__ import annotations
 
@@ -164,9 +165,10 @@ def _plan_restated(case, value_bytes, hint=True):
     row_edge = np.empty(edges, dtype=np.int64)
     row_edge[tpos] = np.arange(edges)
 
-    slots = np.nonzero(valid)[0]
-    slot_blob = tpos[order[slots]] // rows
-    sorted_slots = slots[np.argsort(slot_blob, kind="stable")]
+    # entries: the source slots listed position by position, sorted stably by the blob of their edge
+    listed = np.concatenate([np.arange(src_off[a], src_off[a + 1]) for a in perm] + [np.zeros(0, np.int64)])
+    listed = listed[valid[listed]]
+    sorted_slots = listed[np.argsort(tpos[order[listed]] // rows, kind="stable")]
     entry_blob = tpos[order[sorted_slots]] // rows
     entry_row = tpos[order[sorted_slots]] - entry_blob * rows
     entry_atom = slot_atom[sorted_slots]
