@@ -140,8 +140,32 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
 // element the arithmetic is gie_forward_kernel's (edges in CSR order, product
 // rounded, then added, normalised after the sum): the same output bit for
 // bit.  Needs C % 4 == 0, 1 <= R <= 64, S <= 64, S * C / 4 <= 64 * PPL, and
-// at most MAXR rows per slot.
-template <int PPL, int MAXR, bool kOrdered>
+// at most MAXR rows per slot.  With kRowBcast (C / 4 a multiple of 16, so a
+// group is whole 16-lane rows of the wave), lane k of each row loads the
+// zonal value of its group's k-th row instead, and a DPP row broadcast
+// (row_newbcast) hands it to the row: a VALU move in place of the
+// ds_bpermute, which goes through the LDS pipeline.
+// Lane k of each 16-lane row of the wave, to every lane of that row (DPP row_newbcast:k).
+template <int K>
+__device__ __forceinline__ float row_broadcast_of(float value) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(value), 0x150 + K, 0xf, 0xf, false));
+}
+
+// k < 8, a constant once the caller's loop is unrolled (the switch folds away).
+__device__ __forceinline__ float row_broadcast(float value, int k) {
+  switch (k) {
+    case 0: return row_broadcast_of<0>(value);
+    case 1: return row_broadcast_of<1>(value);
+    case 2: return row_broadcast_of<2>(value);
+    case 3: return row_broadcast_of<3>(value);
+    case 4: return row_broadcast_of<4>(value);
+    case 5: return row_broadcast_of<5>(value);
+    case 6: return row_broadcast_of<6>(value);
+    default: return row_broadcast_of<7>(value);
+  }
+}
+
+template <int PPL, int MAXR, bool kRowBcast, bool kOrdered>
 __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
     const float* __restrict__ zonal, const float* __restrict__ radial,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ order,
@@ -215,7 +239,21 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][k].v[i] = 0.0f;
 
-  const int64_t zonal_row = lane < rows ? lane : rows - 1;
+  // the zonal row this lane loads: its own index (ds_bpermute), or the (lane mod 16)-th row of
+  // each pair's group (row broadcast)
+  int64_t zonal_row[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    if constexpr (kRowBcast) {
+      const int k = lane & 15;
+      int row = row_of[j][0];
+#pragma unroll
+      for (int kk = 1; kk < MAXR; ++kk) row = k == kk && kk < count[j] ? row_of[j][kk] : row;
+      zonal_row[j] = row;
+    } else {
+      zonal_row[j] = lane < rows ? lane : rows - 1;
+    }
+  }
   int64_t begin, end;
   segment_bounds(offsets, node, n_edges, begin, end);
   for (int64_t slot = begin; slot < end; slot += U) {
@@ -227,11 +265,13 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
       use[u] = e >= 0;
       edge[u] = e >= 0 ? e : begin;  // a valid edge to load from when this one is skipped
     }
-    float zq[U];
+    constexpr int ZQ = kRowBcast ? PPL : 1;
+    float zq[U][ZQ];
     fvec<4> x[U][PPL];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      zq[u] = zonal[edge[u] * n_rows + zonal_row];
+#pragma unroll
+      for (int j = 0; j < ZQ; ++j) zq[u][j] = zonal[edge[u] * n_rows + zonal_row[j]];
 #pragma unroll
       for (int j = 0; j < PPL; ++j) x[u][j] = load_vec<4>(radial + edge[u] * edge_stride + radial_col[j]);
     }
@@ -243,7 +283,11 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
         if (k >= group_rows) break;  // wave-uniform
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-          const float z = __int_as_float(__builtin_amdgcn_ds_bpermute(row_of[j][k] << 2, __float_as_int(zq[u])));
+          float z;
+          if constexpr (kRowBcast)
+            z = row_broadcast(zq[u][j], k);
+          else
+            z = __int_as_float(__builtin_amdgcn_ds_bpermute(row_of[j][k] << 2, __float_as_int(zq[u][0])));
           if (k < count[j])
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[j][k].v[i] = acc[j][k].v[i] + z * x[u][j].v[i];
@@ -633,6 +677,167 @@ __global__ __launch_bounds__(kBlock) void gie_backward_shared_kernel(
   }
 }
 
+// Shared radial slots, backward, with S slots known at compile time: RC =
+// C / 8 lanes serve one edge (lane c of the group owns channels [8 c, 8 c +
+// 8) of every slot: S * 8 radial values) and EW = 64 / RC edges are handled
+// side by side, every lane busy.  The node's upstream rows g[r + 1, :] sit in
+// LDS (each wave its own node's), and the wave walks the rows slot by slot,
+// in ascending order within a slot, with no masked iterations:
+//   dot                   = sum_c g[r, c] radial[e, s(r), c]   (8 FMAs, RC-lane butterfly)
+//   grad_zonal[e, r]      = inv * dot                          (kept by lane r mod RC)
+//   grad_radial[e, s, c] += g[r, c] * (zonal[e, r] * inv)
+//   grad_inv             += zonal[e, r] * dot                  (lane r mod RC)
+// zonal[e, r] is loaded by lane r mod RC of the edge's group and reaches
+// the others through ds_bpermute.  Each radial element is read and each
+// gradient written once.  The dot products and grad_radial are
+// gie_backward_shared_kernel's to the bit (same channel split, butterfly and
+// row order); grad_inv adds the same terms over another lane partition.
+// Needs C = 8 RC, n_rows <= ZR * RC and n_rows * C <= kEdgeLaneRowFloats.
+constexpr int kEdgeLaneRowFloats = 4096;  // upstream floats staged per wave (16 KB)
+
+template <int RC, int S, int ZR, bool kOrdered>
+__global__ __launch_bounds__(kBlock) void gie_backward_edge_lanes_kernel(
+    const float* __restrict__ grad_output, const float* __restrict__ zonal,
+    const float* __restrict__ radial, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ order, const int64_t* __restrict__ radial_slot,
+    const float* __restrict__ inv, float* __restrict__ grad_zonal, float* __restrict__ grad_radial,
+    float* __restrict__ grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+    int64_t channels) {
+  constexpr int V = 8;
+  constexpr int EW = 64 / RC;        // edges per wave step
+  constexpr int UU = 2;              // wave steps whose loads go out together
+  extern __shared__ float staged[];  // [kWaves][rows * C]
+  const int wave = threadIdx.x >> 6;
+  const int64_t node = block_index() * kWaves + wave;
+  const bool live = node < n_nodes;
+  const int lane = threadIdx.x & 63;
+  const int u = lane / RC, c = lane % RC;
+  const int rows = static_cast<int>(n_rows);
+  const int64_t edge_stride = S * channels;
+  float* g_rows = staged + wave * rows * channels;
+  const float scale = live ? inv[node] : 0.0f;
+
+  // the node's upstream rows 1..R into this wave's LDS
+  if (live) {
+    const float* src = grad_output + (node * (n_rows + 1) + 1) * channels;
+    for (int64_t q = lane; q < rows * channels / 4; q += 64) store_vec<4>(g_rows + 4 * q, load_vec<4>(src + 4 * q));
+  }
+  __syncthreads();
+  if (!live) return;
+
+  // the rows in slot order: lane k holds the k-th row of the slot-major list; first[s] bounds slot s
+  int slot_of_row = lane < rows ? static_cast<int>(radial_slot[lane]) : -1;
+  slot_of_row = static_cast<uint64_t>(slot_of_row) < static_cast<uint64_t>(S) ? slot_of_row : -1;
+  int listed = 0, first[S + 1];
+  first[0] = 0;
+#pragma unroll
+  for (int t = 0; t < S; ++t) {
+    const uint64_t mine = __ballot(slot_of_row == t);
+    const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mine >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mine), 0u));
+    // lane r (a row of slot t) becomes entry first[t] + before of the list
+    if (slot_of_row == t) listed = first[t] + before;
+    first[t + 1] = first[t] + __builtin_popcountll(mine);
+  }
+  int row_list = 0;  // lane k: the row at list position k
+  {
+    // scatter: row r goes to lane listed(r); a ds_permute writes each lane's value to the lane it names
+    const int target = slot_of_row >= 0 ? listed : 63;
+    row_list = __builtin_amdgcn_ds_permute(target << 2, lane);
+  }
+
+  float inv_partial = 0.0f;
+  int64_t begin, end;
+  segment_bounds(offsets, node, n_edges, begin, end);
+  for (int64_t base = begin; base < end; base += UU * EW) {
+    int64_t e[UU];
+    float x[UU][S][V], zq[UU][ZR];
+#pragma unroll
+    for (int uu = 0; uu < UU; ++uu) {
+      const int64_t at = base + uu * EW + u;
+      e[uu] = at < end ? edge_of<kOrdered>(order, at, n_edges) : -1;
+      const int64_t edge = e[uu] >= 0 ? e[uu] : begin;  // a valid edge to load from
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const fvec<4> part = load_vec<4>(radial + edge * edge_stride + t * channels + c * V + 4 * q);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[uu][t][4 * q + i] = part.v[i];
+        }
+#pragma unroll
+      for (int j = 0; j < ZR; ++j) {
+        const int r = j * RC + c;
+        zq[uu][j] = r < rows ? zonal[edge * n_rows + r] : 0.0f;
+      }
+    }
+    float out[UU][S][V], dz[UU][ZR];
+#pragma unroll
+    for (int uu = 0; uu < UU; ++uu) {
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int i = 0; i < V; ++i) out[uu][t][i] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < ZR; ++j) dz[uu][j] = 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      for (int k = first[t]; k < first[t + 1]; ++k) {  // uniform: the rows of slot t, ascending
+        const int r = __builtin_amdgcn_readlane(row_list, k);
+        const int holder = r % RC, j = r / RC;
+        const bool mine = c == holder;
+        const fvec<4> g0 = load_vec<4>(g_rows + r * channels + c * V);
+        const fvec<4> g1 = load_vec<4>(g_rows + r * channels + c * V + 4);
+        const float g[V] = {g0.v[0], g0.v[1], g0.v[2], g0.v[3], g1.v[0], g1.v[1], g1.v[2], g1.v[3]};
+#pragma unroll
+        for (int uu = 0; uu < UU; ++uu) {  // the row's upstream values serve every edge step in flight
+          float zr = zq[uu][0];
+#pragma unroll
+          for (int jj = 1; jj < ZR; ++jj) zr = j == jj ? zq[uu][jj] : zr;
+          const float z = __int_as_float(
+              __builtin_amdgcn_ds_bpermute((u * RC + holder) << 2, __float_as_int(zr)));
+          float dot = 0.0f;
+#pragma unroll
+          for (int i = 0; i < V; ++i) dot = __builtin_fmaf(g[i], x[uu][t][i], dot);
+          dot = group_sum<RC>(dot);
+#pragma unroll
+          for (int jj = 0; jj < ZR; ++jj) dz[uu][jj] = mine && j == jj ? dot * scale : dz[uu][jj];
+          inv_partial = mine && e[uu] >= 0 ? __builtin_fmaf(z, dot, inv_partial) : inv_partial;
+          const float weight = z * scale;
+#pragma unroll
+          for (int i = 0; i < V; ++i) out[uu][t][i] = __builtin_fmaf(g[i], weight, out[uu][t][i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int uu = 0; uu < UU; ++uu) {
+      if (e[uu] >= 0) {
+        if (grad_radial != nullptr)
+#pragma unroll
+          for (int t = 0; t < S; ++t)
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+              fvec<4> part;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) part.v[i] = out[uu][t][4 * q + i];
+              store_vec_stream<4>(grad_radial + e[uu] * edge_stride + t * channels + c * V + 4 * q, part);
+            }
+        if (grad_zonal != nullptr)
+#pragma unroll
+          for (int j = 0; j < ZR; ++j) {
+            const int r = j * RC + c;
+            if (r < rows) grad_zonal[e[uu] * n_rows + r] = dz[uu][j];  // 0 for a row whose slot is out of range
+          }
+      }
+    }
+  }
+  if (grad_inv != nullptr) {
+    const float total = group_sum<64>(inv_partial);
+    if (lane == 0) grad_inv[node] = total;
+  }
+}
+
 // General slot map: one wave per block.  Read chunks q = r * wc + c over
 // rows x window chunks, write chunks t = s * wc + c over slots x window
 // chunks.  LDS holds, per edge, the dot partials and the products
@@ -866,13 +1071,22 @@ int launch_forward_shared(int ppl, int maxr, const float* zonal, const float* ra
                           int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
                           int64_t channels, hipStream_t stream) {
   const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
-#define DPA4K_GIE_FWD_SHARED(P, M)                                                                  \
-  gie_forward_shared_kernel<P, M, kOrdered><<<grid, kBlock, 0, stream>>>(                           \
+#define DPA4K_GIE_FWD_SHARED(P, M, B)                                                               \
+  gie_forward_shared_kernel<P, M, B, kOrdered><<<grid, kBlock, 0, stream>>>(                        \
       zonal, radial, offsets, order, radial_slot, inv, out, n_edges, n_nodes, n_rows, n_radial, channels)
+  const bool bcast = (channels / 4) % 16 == 0;  // groups of whole 16-lane rows
   if (ppl == 1) {
-    if (maxr == 4) DPA4K_GIE_FWD_SHARED(1, 4); else DPA4K_GIE_FWD_SHARED(1, 8);
+    if (bcast) {
+      if (maxr == 4) DPA4K_GIE_FWD_SHARED(1, 4, true); else DPA4K_GIE_FWD_SHARED(1, 8, true);
+    } else {
+      if (maxr == 4) DPA4K_GIE_FWD_SHARED(1, 4, false); else DPA4K_GIE_FWD_SHARED(1, 8, false);
+    }
   } else {
-    if (maxr == 4) DPA4K_GIE_FWD_SHARED(2, 4); else DPA4K_GIE_FWD_SHARED(2, 8);
+    if (bcast) {
+      if (maxr == 4) DPA4K_GIE_FWD_SHARED(2, 4, true); else DPA4K_GIE_FWD_SHARED(2, 8, true);
+    } else {
+      if (maxr == 4) DPA4K_GIE_FWD_SHARED(2, 4, false); else DPA4K_GIE_FWD_SHARED(2, 8, false);
+    }
   }
 #undef DPA4K_GIE_FWD_SHARED
   return launched("gie_forward_shared_kernel");
@@ -912,6 +1126,35 @@ int dispatch_backward_shared(int64_t rc, int maxr, const float* grad_output, con
     default: DPA4K_GIE_RC_SHARED(16);
   }
 #undef DPA4K_GIE_RC_SHARED
+}
+
+template <bool kOrdered>
+int dispatch_edge_lanes(const float* grad_output, const float* zonal, const float* radial, const int64_t* offsets,
+                        const int64_t* order, const int64_t* radial_slot, const float* inv, float* grad_zonal,
+                        float* grad_radial, float* grad_inv, int64_t n_edges, int64_t n_nodes, int64_t n_rows,
+                        int64_t n_radial, int64_t channels, hipStream_t stream) {
+  const dim3 grid = launch_grid((n_nodes + kWaves - 1) / kWaves, kBlock);
+  const size_t lds = sizeof(float) * kWaves * static_cast<size_t>(n_rows * channels);
+  const int rc = static_cast<int>(channels / 8);
+  const int zr = n_rows <= 2 * rc ? 2 : 4;
+#define DPA4K_GIE_EDGE_LANES(RC, S, ZR)                                                                 \
+  gie_backward_edge_lanes_kernel<RC, S, ZR, kOrdered><<<grid, kBlock, lds, stream>>>(                  \
+      grad_output, zonal, radial, offsets, order, radial_slot, inv, grad_zonal, grad_radial, grad_inv, \
+      n_edges, n_nodes, n_rows, channels)
+#define DPA4K_GIE_EDGE_LANES_S(RC, ZR)            \
+  switch (n_radial) {                             \
+    case 2: DPA4K_GIE_EDGE_LANES(RC, 2, ZR); break; \
+    case 3: DPA4K_GIE_EDGE_LANES(RC, 3, ZR); break; \
+    default: DPA4K_GIE_EDGE_LANES(RC, 4, ZR); break; \
+  }
+  if (rc == 8) {
+    if (zr == 2) { DPA4K_GIE_EDGE_LANES_S(8, 2) } else { DPA4K_GIE_EDGE_LANES_S(8, 4) }
+  } else {
+    if (zr == 2) { DPA4K_GIE_EDGE_LANES_S(16, 2) } else { DPA4K_GIE_EDGE_LANES_S(16, 4) }
+  }
+#undef DPA4K_GIE_EDGE_LANES_S
+#undef DPA4K_GIE_EDGE_LANES
+  return launched("gie_backward_edge_lanes_kernel");
 }
 
 int check_shapes(int64_t n_edges, int64_t n_nodes, int64_t n_rows, int64_t n_radial,
@@ -1038,6 +1281,16 @@ extern "C" int dpa4k_gie_zonal_scatter_backward_csr(
                                              grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes,
                                              n_rows, n_radial, channels, stream);
   }
+  // Shared slots, a few of them: one lane group per edge, every lane busy.
+  if (vec4 && !(slot_info & kSlotsDistinct) && (channels == 64 || channels == 128) && n_radial >= 2 &&
+      n_radial <= 4 && n_rows <= 4 * (channels / 8) && n_rows * channels <= kEdgeLaneRowFloats)
+    return order != nullptr
+               ? dispatch_edge_lanes<true>(grad_output, zonal, radial, offsets, order, radial_slot, inv_sqrt_deg,
+                                           grad_zonal, grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows,
+                                           n_radial, channels, stream)
+               : dispatch_edge_lanes<false>(grad_output, zonal, radial, offsets, order, radial_slot, inv_sqrt_deg,
+                                            grad_zonal, grad_radial, grad_inv_sqrt_deg, n_edges, n_nodes, n_rows,
+                                            n_radial, channels, stream);
   // Shared slots with at most 8 rows per slot: registers only, 8 channels per lane.
   const int most = slot_rows(slot_info);
   const int64_t rc = channels / 8;

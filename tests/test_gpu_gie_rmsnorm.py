@@ -312,6 +312,9 @@ _SHARED_LAYOUTS = [
     (_DEEPMD_SLOTS, 3, 8),         # one lane per slot, 21 edges per wave step (backward)
     (_DEEPMD_SLOTS, 3, 20),        # channels % 8 != 0: forward shared, backward general
     (_DEEPMD_SLOTS, 3, 6),         # channels % 4 != 0: scalar kernels
+    ([0] * 3 + [1] * 5 + [2] * 7 + [3] * 9, 4, 64),  # lmax = 4: 24 rows, 9 on one slot; backward edge lanes
+    ([2, 0, 1, 2, 0, 1, 1, 2, 0, 2], 3, 64),         # rows of a slot interleaved with the others' (backward order)
+    ([1, 1, 0, 1, 1, 0, 1], 2, 128),                 # 16 lanes per edge, 4 edges per wave step
 ]
 
 
