@@ -56,6 +56,9 @@ def parse_args():
     parser.add_argument("--traffic-marks", action="store_true",
                         help="eager launches with marker kernels around every step and a 256 MiB calibration "
                              "copy, for two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)")
+    parser.add_argument("--trace-summary", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_LOG"),
+                        help="write profiles/all_ops_kernel_stats.md from a rocprofv3 kernel trace of the default "
+                             "bench (TRACE_COMMAND), then exit")
     parser.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "BENCH_LOG"),
                         help="write profiles/traffic.json and traffic.md from the two passes' counter CSVs and "
                              "the FETCH pass's bench output, then exit")
@@ -987,6 +990,66 @@ def traffic_summary(fetch_csv: str, write_csv: str, bench_log: str, out_dir: Pat
     return 0
 
 
+TRACE_COMMAND = ("timeout -k 10 600 rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_ops -o run "
+                 "-- python3 -u bench.py --no-cpu-baseline --steps 20 --warmup 5 > gpurun_out/prof_ops.log 2>&1")
+TRACE_SUMMARY_COMMAND = ("python3 bench.py --trace-summary gpurun_out/prof_ops/run_kernel_stats.csv "
+                         "gpurun_out/prof_ops/run_kernel_trace.csv gpurun_out/prof_ops.log")
+
+
+def trace_summary(stats_csv: str, trace_csv: str, bench_log: str, out_dir: Path | None = None) -> int:
+    """Write profiles/all_ops_kernel_stats.md from a rocprofv3 kernel trace of the default bench.
+
+    Library kernels from the stats file (averaged over every shape the bench runs them at), the
+    same trace by kernel and grid (median of a line's launches), and the bench's own per-step times
+    of the same process beside them.
+    """
+    import csv
+    import statistics
+    from collections import defaultdict
+
+    def short(name: str) -> str:
+        return _kernel_short(name)
+
+    rows = ["# Kernel durations of every bench line (rocprofv3 kernel trace)", "",
+            "Commands (repository root, one MI355X):", "", "```", TRACE_COMMAND, TRACE_SUMMARY_COMMAND, "```", "",
+            "Library kernels (`dpa4k::`) from `run_kernel_stats.csv`, averaged over every shape the bench runs for "
+            "that kernel template (the calibration `stream_*` kernels measure the same-bytes copies and the stream "
+            "ceilings):", "", "| Kernel | Calls | Average ns | Min ns | Max ns | % of GPU time |",
+            "| --- | --- | --- | --- | --- | --- |"]
+    with open(stats_csv, newline="") as handle:
+        for r in csv.DictReader(handle):
+            name = short(r["Name"])
+            if name.startswith("dpa4k::"):
+                rows.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']):.0f} | {float(r['MinNs']):.0f} | "
+                            f"{float(r['MaxNs']):.0f} | {float(r['Percentage']):.2f} |")
+    groups = defaultdict(list)
+    with open(trace_csv, newline="") as handle:
+        for r in csv.DictReader(handle):
+            name = short(r["Kernel_Name"])
+            if not name.startswith("dpa4k::"):
+                continue
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            groups[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    rows += ["", "The same trace by kernel and grid (launches of at least 20, i.e. a line's warm-up and timed steps; "
+             "median of the launches):", "", "| Kernel | Grid (work-items) | Launches | Median µs | Mean µs |",
+             "| --- | --- | --- | --- | --- |"]
+    for (name, grid), times in sorted(groups.items()):
+        if len(times) >= 20:
+            rows.append(f"| `{name}` | {grid:,} | {len(times)} | {statistics.median(times):.1f} | "
+                        f"{statistics.mean(times):.1f} |")
+    line = _bench_json(bench_log)
+    rows += ["", "Bench `ms_per_step` of the same process (graph replay, HIP events), for comparison:", "",
+             "| Bench line | µs per step | frac |", "| --- | --- | --- |",
+             f"| {line['config']['workload']} (headline) | {line['ms_per_step'] * 1000:.2f} | "
+             f"{line['roofline']['frac']} |"]
+    for key, op in line.get("ops", {}).items():
+        rows.append(f"| {key} | {op['ms_per_step'] * 1000:.2f} | {op['roofline']['frac']} |")
+    out = (out_dir or ROOT / "profiles") / "all_ops_kernel_stats.md"
+    out.write_text("\n".join(rows) + "\n")
+    print(f"wrote {out}")
+    return 0
+
+
 # ---------------------------------------------------------------------------
 # the final line
 # ---------------------------------------------------------------------------
@@ -1064,6 +1127,8 @@ def main() -> int:
     args = parse_args()
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
+    if args.trace_summary:
+        return trace_summary(*args.trace_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the operators would shard by contiguous destination-node ranges, one range per GPU, "

@@ -175,3 +175,35 @@ def test_traffic_summary_reads_the_detail_line(tmp_path):
     log = tmp_path / "bench.log"
     log.write_text(json.dumps(detail) + "\n" + json.dumps({"ops": {"x": [1, 2]}}) + "\n")
     assert bench._bench_json(str(log)) == detail
+
+
+def test_trace_summary_lists_library_kernels_and_the_bench_lines(tmp_path):
+    import csv
+    import json
+
+    import bench
+
+    stats, trace, log = tmp_path / "stats.csv", tmp_path / "trace.csv", tmp_path / "bench.log"
+    with open(stats, "w", newline="") as handle:
+        writer = csv.writer(handle)
+        writer.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"])
+        writer.writerow([_SOFTMAX, 24, 340000, 14166.7, 50.0, 14000, 14500, 10])
+        writer.writerow([_FILL, 3, 300, 100, 1.0, 90, 110, 1])
+    with open(trace, "w", newline="") as handle:
+        writer = csv.writer(handle)
+        writer.writerow(["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+                         "End_Timestamp"])
+        for i in range(24):
+            writer.writerow([_SOFTMAX, 16384, 1, 1, 1000 * i, 1000 * i + 14000 + i])
+    detail = {"detail": True, "config": {"workload": "segment_softmax_fwd_config2"}, "ms_per_step": 0.01514,
+              "roofline": {"frac": 0.49}, "ops": {"segment_sum_config1": {"ms_per_step": 0.0111,
+                                                                          "roofline": {"frac": 0.24}}}}
+    log.write_text(json.dumps(detail) + "\n" + json.dumps({"ops": {}}) + "\n")
+    assert bench.trace_summary(str(stats), str(trace), str(log), out_dir=tmp_path) == 0
+    text = (tmp_path / "all_ops_kernel_stats.md").read_text()
+    assert "| `dpa4k::softmax_forward_kernel<4, 1, true, false, true>` | 24 | 14167 |" in text
+    assert "FillFunctor" not in text  # torch kernels are not listed
+    assert "| `dpa4k::softmax_forward_kernel<4, 1, true, false, true>` | 16,384 | 24 | 14.0 |" in text
+    assert "| segment_softmax_fwd_config2 (headline) | 15.14 | 0.49 |" in text
+    assert "| segment_sum_config1 | 11.10 | 0.24 |" in text
+    assert bench.TRACE_COMMAND in text

@@ -424,3 +424,28 @@ def test_planned_call_reports_a_plan_that_does_not_match_it():
     direct = _run(d, torch.float32)
     assert_close_scaled(force, direct[0], what="matching call: force")
     assert_close_scaled(virial, direct[1], what="matching call: virial")
+
+
+def test_planned_float32_records_stay_within_their_stated_bound():
+    """Records sum their few terms in float32 (fused products); against the fp64 truth every output component
+    stays within L * 2^-24 * (the atom's sum of absolute terms) plus the final rounding, L the longest record."""
+    case = _water(4096, 8, False)
+    announce("force plan float32 record bound")
+    d = _on_device(case)
+    plan = _plan(d, torch.float32)
+    longest = int(np.diff(_decode_plan(plan)["rec_entry"][:plan.n_records + 1]).max())
+    force, virial = _run(d, torch.float32, plan)
+    g = case["grad_edge"].float().double()
+    v = case["edge_vec"].float().double()
+    atoms = case["dst_offsets"].numel() - 1
+    t_force, t_virial = (torch.from_numpy(t) for t in loops.force_assembly_loop(g, v, case["src"], case["dst"], atoms))
+    # the sum of absolute terms per output component: |g| on both sides, |g_r v_c| on the source side
+    a_force = torch.zeros(atoms, 3, dtype=torch.float64).index_add_(0, case["dst"], g.abs())
+    a_force.index_add_(0, case["src"], g.abs())
+    a_virial = torch.zeros(atoms, 9, dtype=torch.float64).index_add_(
+        0, case["src"], (g.abs().unsqueeze(2) * v.abs().unsqueeze(1)).reshape(-1, 9))
+    unit = 2.0 ** -24
+    for label, got, truth, absolute in (("force", force, t_force, a_force), ("virial", virial, t_virial, a_virial)):
+        error = (got.double().cpu() - truth).abs()
+        bound = (longest + 2) * unit * absolute + unit * truth.abs()
+        assert bool((error <= bound).all()), f"{label}: worst excess {float((error - bound).max()):.3e}"
