@@ -56,6 +56,12 @@ def parse_args():
     parser.add_argument("--traffic-marks", action="store_true",
                         help="eager launches with marker kernels around every step and a 256 MiB calibration "
                              "copy, for two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)")
+    parser.add_argument("--only-force", choices=("f32", "f64"),
+                        help="run only force_assembly on config 4 (random numbering) in this dtype, for a counter "
+                             "profile of its kernels (FORCE_COUNTER_COMMANDS), and print one JSON line")
+    parser.add_argument("--counter-table", nargs="+", metavar="COUNTER_CSV",
+                        help="print, per kernel, the median per dispatch of every counter in rocprofv3 --pmc "
+                             "counter CSVs (one pass each) as a Markdown table, then exit")
     parser.add_argument("--trace-summary", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_LOG"),
                         help="write profiles/all_ops_kernel_stats.md from a rocprofv3 kernel trace of the default "
                              "bench (TRACE_COMMAND), then exit")
@@ -990,6 +996,39 @@ def traffic_summary(fetch_csv: str, write_csv: str, bench_log: str, out_dir: Pat
     return 0
 
 
+FORCE_COUNTERS = (
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VMEM_RD "
+    "SQ_INSTS_VMEM_WR GRBM_GUI_ACTIVE",
+    "TCC_REQ_sum TCC_HIT_sum TCC_MISS_sum TCP_TCC_READ_REQ_sum TCP_TCC_READ_REQ_LATENCY_sum "
+    "TCP_PENDING_STALL_CYCLES_sum TA_BUSY_avr GRBM_GUI_ACTIVE",
+    "FETCH_SIZE",
+    "WRITE_SIZE",
+)
+FORCE_COUNTER_COMMAND = ("timeout -s KILL 300 rocprofv3 --pmc {counters} --kernel-include-regex force_ "
+                         "--output-format csv -d gpurun_out/pmc_force_{tag}_{dtype} -o run -- python3 bench.py "
+                         "--only-force {dtype} --eager --steps 40 --warmup 4")
+
+
+def counter_table(paths: list[str]) -> str:
+    """Per kernel, the median per dispatch of every counter of one or more rocprofv3 --pmc CSVs."""
+    import csv
+    import statistics
+    from collections import defaultdict
+
+    values = defaultdict(lambda: defaultdict(list))
+    for path in paths:
+        with open(path, newline="") as handle:
+            for row in csv.DictReader(handle):
+                values[_kernel_short(row["Kernel_Name"])][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    names = sorted({counter for kernel in values.values() for counter in kernel})
+    lines = ["| Kernel | Dispatches | " + " | ".join(names) + " |", "| --- | --- | " + " | ".join("---" for _ in names) + " |"]
+    for kernel, counters in sorted(values.items()):
+        dispatches = max(len(v) for v in counters.values())
+        cells = [f"{statistics.median(counters[n]):,.0f}" if n in counters else "" for n in names]
+        lines.append(f"| `{kernel}` | {dispatches} | " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
 TRACE_COMMAND = ("timeout -k 10 600 rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_ops -o run "
                  "-- python3 -u bench.py --no-cpu-baseline --steps 20 --warmup 5 > gpurun_out/prof_ops.log 2>&1")
 TRACE_SUMMARY_COMMAND = ("python3 bench.py --trace-summary gpurun_out/prof_ops/run_kernel_stats.csv "
@@ -1129,6 +1168,9 @@ def main() -> int:
         return traffic_summary(*args.traffic_summary)
     if args.trace_summary:
         return trace_summary(*args.trace_summary)
+    if args.counter_table:
+        print(counter_table(args.counter_table))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the operators would shard by contiguous destination-node ranges, one range per GPU, "
@@ -1146,6 +1188,13 @@ def main() -> int:
         print("libdpa4k.so is not usable on this device (build it with __graft_entry__.build())", file=sys.stderr)
         return 1
     graph = not (args.eager or args.traffic_marks)
+    if args.only_force:
+        job, _, _ = force_job(65536, args.steps, args.warmup, graph, args.only_force,
+                              label=f"force_assembly_config4_{args.only_force}")
+        print(json.dumps({"op": f"force_assembly_config4_{args.only_force}", "steps": args.steps,
+                          "ms_per_step": round(job["ms_per_step"], 5), "edges": job["edges"],
+                          "roofline": roofline(job["bytes"], job["ms_per_step"])}), flush=True)
+        return 0
     global MARKS
     if args.traffic_marks:
         from bysj_amd.kernels import _lib
