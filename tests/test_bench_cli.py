@@ -207,3 +207,18 @@ def test_trace_summary_lists_library_kernels_and_the_bench_lines(tmp_path):
     assert "| segment_softmax_fwd_config2 (headline) | 15.14 | 0.49 |" in text
     assert "| segment_sum_config1 | 11.10 | 0.24 |" in text
     assert bench.TRACE_COMMAND in text
+
+
+def test_counter_table_gives_each_kernels_median_per_counter(tmp_path):
+    import bench
+
+    first, second = tmp_path / "a.csv", tmp_path / "b.csv"
+    _write_counters(first, "SQ_WAVES", [(_SOFTMAX, 64, 10.0), (_SOFTMAX, 64, 30.0), (_SOFTMAX, 64, 20.0),
+                                        (_FILL, 10, 5.0)])
+    _write_counters(second, "GRBM_GUI_ACTIVE", [(_SOFTMAX, 64, 1000.0), (_SOFTMAX, 64, 3000.0)])
+    table = bench.counter_table([str(first), str(second)])
+    lines = table.splitlines()
+    assert lines[0] == "| Kernel | Dispatches | GRBM_GUI_ACTIVE | SQ_WAVES |"
+    assert "| `dpa4k::softmax_forward_kernel<4, 1, true, false, true>` | 3 | 2,000 | 20 |" in lines
+    assert any(line.startswith("| `at::native::vectorized_elementwise_kernel") and line.endswith("|  | 5 |")
+               for line in lines)
