@@ -941,6 +941,488 @@ __global__ __launch_bounds__(kThreads, 2) void finish_private_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// grouped two-level path: tile-local grouping, then bucket gathers
+// ---------------------------------------------------------------------------
+//
+// For packed 32-bit elements, fine digits of at most 6 bits and at most
+// kMaxRunTiles tiles the two-level sort takes two launches instead of four:
+//
+//   group   one workgroup per tile: the range and sortedness checks, then the
+//           tile's in-range elements grouped stably by the coarse digit and
+//           written back over the tile's own span of the packed buffer (one
+//           contiguous write), with the tile's row of bucket starts (16 bits
+//           each; entry `buckets` is the tile's in-range count) and its flags.
+//           No count pass and no scan over the tiles: nothing in a tile's
+//           output depends on another tile.
+//   gather  one workgroup per bucket: its run in every tile (two row
+//           entries), scanned over the tiles, places the runs one after the
+//           other; the bucket's elements, gathered chunk by chunk in tile
+//           order (consecutive lanes read consecutive elements of a run), are
+//           ranked by the fine digit and their edge indices placed in `order`.
+//           Every workgroup ORs the tiles' flags, so the sorted case takes the
+//           boundary path without a host round trip, and workgroup 0 writes
+//           the status word.
+//
+// The group ranks with wave_match_ranks (the lanes of equal coarse digits
+// found through LDS words instead of one ballot per digit bit), the gather
+// with wave_ballot_ranks (six ballots for the fine digit).
+
+constexpr int kMaxRunTiles = 1024;                    // tiles one gather holds (edges up to 2^23)
+constexpr int kRunTilesPerThread = kMaxRunTiles / kThreads;
+constexpr int kFineMatchBits = 6;                     // fine digits a gather ranks
+constexpr int kFineDigits = 1 << kFineMatchBits;
+
+// The same ranks as wave_split_ranks, with the lanes of equal digits found
+// through LDS instead of one ballot per digit bit.  Every lane first clears
+// the mask word its lane id names; each active lane then ORs its bit into the
+// word of its group and reads the word back: the lanes of its group.  Digits
+// of at most 6 bits name the word themselves.  A wider digit first names a
+// leader: every active lane writes its lane id into the byte of its digit
+// (one of the writes remains) and reads the byte back, so the lanes of one
+// digit, and only they, read the same lane id.  A wave's LDS operations take
+// effect in program order; the signal fences (compiler barriers, no
+// instruction) keep the compiler from reordering them or forwarding the
+// written byte to the read.  `leader` is the wave's [1 << kBits] bytes (unused
+// for kBits <= 6), `masks` its 65 words, `counter` its [digit] array, advanced
+// as in wave_split_ranks; the ranks of inactive lanes are unspecified.  Only
+// rounds [0, rounds) are ranked.  Every lane of the wave must call it.
+template <int kBits, int kRounds, typename DigitOf>
+__device__ __forceinline__ void wave_match_ranks(DigitOf digit, uint32_t valid, uint32_t* counter,
+                                                 uint8_t* leader, uint64_t* masks, uint32_t (&rank)[kRounds],
+                                                 int rounds = kRounds) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    if (r >= rounds) continue;  // wave-uniform: the rounds the wave's span holds
+    const bool active = ((valid >> r) & 1u) != 0u;
+    const uint32_t d = digit(r);
+    masks[lane] = 0ull;
+    uint32_t group = d;
+    if constexpr (kBits > kFineMatchBits) {
+      // inactive lanes write too: a byte one of them keeps names only that lane's digit
+      leader[d] = static_cast<uint8_t>(lane);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      group = leader[d];
+    }
+    group = active ? group : 64u;  // inactive lanes OR into word 64, which no active lane reads
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    atomicOr(reinterpret_cast<unsigned long long*>(masks + group), static_cast<unsigned long long>(1ull << lane));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint64_t same = masks[group];
+    const uint32_t below = lanes_below(same);
+    const uint32_t size = static_cast<uint32_t>(__popcll(same));
+    // digits are masked, so every lane's read is in range; the leader's store
+    // follows the wave's read in LDS order
+    const uint32_t before = counter[d];
+    if (active && below == 0u) counter[d] = before + size;
+    rank[r] = before + below;
+    asm volatile("" : "+v"(rank[r]));  // summed here, not held as two registers to the end
+  }
+}
+
+// The same ranks as wave_split_ranks with one ballot per digit bit, arranged
+// so that no LDS round trip stalls a round: every lane reads its digit's
+// counter first, the ballots run while the read is in flight, and the
+// group's leader then adds the group's size to the counter without waiting
+// for the old value (a wave's LDS operations take effect in program order, so
+// the next round's reads see the addition).  Only rounds [0, rounds) are
+// ranked; ranks of inactive lanes are unspecified.  Every lane of the wave
+// must call it.
+template <int kBits, int kRounds, typename DigitOf>
+__device__ __forceinline__ void wave_ballot_ranks(DigitOf digit, uint32_t valid, uint32_t* counter,
+                                                  uint32_t (&rank)[kRounds], int rounds = kRounds) {
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    if (r >= rounds) continue;  // wave-uniform: the rounds the wave's span holds
+    const bool active = ((valid >> r) & 1u) != 0u;
+    const uint32_t d = digit(r);
+    const uint32_t before = counter[d];
+    const uint64_t same = lanes_with_digit<kBits>(d, active);
+    const uint32_t below = lanes_below(same);
+    if (active && below == 0u) atomicAdd(&counter[d], static_cast<uint32_t>(__popcll(same)));
+    rank[r] = before + below;
+    asm volatile("" : "+v"(rank[r]));  // summed here, not held as two registers to the end
+  }
+}
+
+// Lane l receives lane l + 1's value and lane 63 lane 0's (DPP wave_rol:1).
+__device__ __forceinline__ uint32_t rotate_from_lane_above(uint32_t value) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(value), 0x134, 0xf, 0xf, false));
+}
+
+// Exclusive running maximum over the workgroup of one value per thread (0 for
+// thread 0).  Every thread must call it.
+__device__ __forceinline__ uint32_t block_exclusive_max(uint32_t value, uint32_t* wave_totals) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t inclusive = value;
+  inclusive = max(inclusive, dpp_or_zero<0x111, 0xf>(inclusive));
+  inclusive = max(inclusive, dpp_or_zero<0x112, 0xf>(inclusive));
+  inclusive = max(inclusive, dpp_or_zero<0x114, 0xf>(inclusive));
+  inclusive = max(inclusive, dpp_or_zero<0x118, 0xf>(inclusive));
+  inclusive = max(inclusive, dpp_or_zero<0x142, 0xa>(inclusive));
+  inclusive = max(inclusive, dpp_or_zero<0x143, 0xc>(inclusive));
+  if (lane == 63) wave_totals[wave] = inclusive;
+  __syncthreads();
+  uint32_t before = 0u;
+#pragma unroll
+  for (int w = 0; w < kGroupWaves; ++w) before = w < wave ? max(before, wave_totals[w]) : before;
+  __syncthreads();
+  return max(before, from_lane_below(inclusive, 0u));
+}
+
+// One tile: checks, stable grouping by the coarse digit (key >> fine_bits),
+// the grouped packed elements over packed[tile_base, tile_base + in-range
+// count), the row rows[tile][0, buckets] of bucket starts and the in-range
+// count, and tile_flags[tile].  Wave w takes the tile's elements
+// [w S, (w + 1) S) (S = kScatterSpan), 64 consecutive ones a round.
+__global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* __restrict__ keys, int64_t n,
+                                                                 uint64_t n_nodes, int fine_bits, int buckets,
+                                                                 uint32_t* __restrict__ packed,
+                                                                 uint16_t* __restrict__ rows, int64_t row_stride,
+                                                                 uint32_t* __restrict__ tile_flags) {
+  // the wave counters, then (once every place is known) the grouped tile
+  __shared__ __align__(16) uint32_t sorted[kTile];
+  uint32_t* wave_count = sorted;
+  // the match tables while the waves rank, then the bucket starts
+  struct MatchTables {
+    uint8_t leader[kGroupWaves][kMaxBuckets];
+    uint64_t masks[kGroupWaves][64 + 1];
+  };
+  __shared__ union {
+    MatchTables match;
+    uint32_t tile_start[kMaxBuckets];
+  } tables;
+  __shared__ uint32_t wave_totals[kGroupWaves];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const unsigned int tile = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t tile_base = static_cast<int64_t>(tile) * kTile;
+  const int64_t rest = n - tile_base;
+  const int n_tile = static_cast<int>(rest > kTile ? kTile : rest);
+  const int extent = static_cast<int>(rest > kTile + 1 ? kTile + 1 : rest);  // one element past the tile
+  const uint32_t digit_mask = static_cast<uint32_t>(kMaxBuckets - 1);
+  const uint32_t fine_mask = (1u << fine_bits) - 1u;
+  for (int i = t; i < kGroupWaves * kMaxBuckets; i += kThreads) wave_count[i] = 0u;
+
+  const BufferView view = buffer_view(keys + tile_base, static_cast<int64_t>(extent) * 8);
+  const int first = wave * kScatterSpan + lane;  // the lane's element of round 0
+  int64_t raw[kScatterRounds];
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r) raw[r] = load_i64(view, static_cast<uint32_t>(first + 64 * r) * 8u);
+  // the element after the wave's span: the next wave's first, or the one after the tile
+  const int after_q = (wave + 1) * kScatterSpan;
+  const int64_t after = load_i64(view, static_cast<uint32_t>(after_q) * 8u);
+  uint32_t key[kScatterRounds];
+  uint32_t ok = 0u;  // bit r: the round-r element exists and is in range
+  int32_t flags = 0;
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r) {
+    const bool valid = first + 64 * r < n_tile;
+    const bool in = valid && static_cast<uint64_t>(raw[r]) < n_nodes;
+    key[r] = static_cast<uint32_t>(raw[r]);
+    ok |= in ? (1u << r) : 0u;
+    if (valid && !in) flags |= kFlagOutOfRange;
+  }
+  // element q against q + 1 (both in range): the next lane of the round, lane
+  // 0 of the next round for lane 63, and `after` past the wave's last round.
+  // A wave rotation (lane l reads lane l + 1, lane 63 reads lane 0) of round
+  // r + 1 holds lane 63's successor.
+  const uint32_t after_ok = after_q < extent && static_cast<uint64_t>(after) < n_nodes ? 1u : 0u;
+  const uint32_t ok_above = rotate_from_lane_above(ok);
+  uint32_t key_above = rotate_from_lane_above(key[0]);
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r) {
+    uint32_t next = key_above;
+    uint32_t next_ok = (ok_above >> r) & 1u;
+    if (r + 1 < kScatterRounds) {
+      key_above = rotate_from_lane_above(key[r + 1 < kScatterRounds ? r + 1 : r]);
+      if (lane == 63) {
+        next = key_above;
+        next_ok = (ok_above >> (r + 1)) & 1u;
+      }
+    } else if (lane == 63) {
+      next = static_cast<uint32_t>(after);
+      next_ok = after_ok;
+    }
+    if (((ok >> r) & 1u) && next_ok && next < key[r]) flags |= kFlagUnsorted;
+  }
+  asm volatile("" : "+v"(flags));  // the checks finish here, before the ranking
+  __syncthreads();  // the wave counters are zero
+
+  // (empty asm: the compiler rebuilds per-round conditions and digits from these
+  // registers where they are used instead of holding them across the phases)
+  asm volatile("" : "+v"(ok));
+  const auto digit = [&](int r) { return (key[r] >> fine_bits) & digit_mask; };
+  uint32_t rank[kScatterRounds];
+  uint32_t* counter = wave_count + wave * kMaxBuckets;
+  wave_match_ranks<kDigitBits, kScatterRounds>(digit, ok, counter, tables.match.leader[wave],
+                                               tables.match.masks[wave], rank);
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r) asm volatile("" : "+v"(key[r]));
+  asm volatile("" : "+v"(ok));
+  __syncthreads();
+  wave_prefix(wave_count, kMaxBuckets, buckets, tables.tile_start);
+  __syncthreads();
+  const uint32_t in_tile = lds_exclusive_scan(tables.tile_start, buckets, 0u, wave_totals);
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r)
+    rank[r] += ((ok >> r) & 1u) ? tables.tile_start[digit(r)] + counter[digit(r)] : 0u;
+  const int32_t found = (__syncthreads_or(flags & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
+                        (__syncthreads_or(flags & kFlagUnsorted) ? kFlagUnsorted : 0);
+  // (the barriers above: every counter is read before the grouped tile overwrites them)
+#pragma unroll
+  for (int r = 0; r < kScatterRounds; ++r)
+    if ((ok >> r) & 1u)
+      sorted[rank[r]] = (static_cast<uint32_t>(tile_base + first + 64 * r) << fine_bits) | (key[r] & fine_mask);
+  uint16_t* row = rows + static_cast<int64_t>(tile) * row_stride;
+  for (int b = t; b < buckets; b += kThreads) row[b] = static_cast<uint16_t>(tables.tile_start[b]);
+  if (t == 0) {
+    row[buckets] = static_cast<uint16_t>(in_tile);
+    tile_flags[tile] = static_cast<uint32_t>(found);
+  }
+  __syncthreads();
+  // the grouped tile, four elements a thread and store while they lie inside the tile
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  uint32_t* out = packed + tile_base;
+  for (int p = 4 * t; p < static_cast<int>(in_tile); p += 4 * kThreads) {
+    if (p + 4 <= n_tile) {
+      *reinterpret_cast<u32x4*>(out + p) = *reinterpret_cast<const u32x4*>(sorted + p);
+    } else {
+      for (int i = p; i < static_cast<int>(in_tile); ++i) out[i] = sorted[i];
+    }
+  }
+}
+
+// One bucket: see the section comment.  A run's elements sit at packed[delta
+// + position in the bucket], with delta = (tile * kTile + the run's start in
+// the tile) - (the run's first position in the bucket); delta never decreases
+// from one tile to the next (a run ends inside its tile), so a running maximum
+// over the run starts, each marked with delta + 1, gives every position of the
+// chunk its source.  Buckets of more than one chunk count their fine digits in
+// a gather pass of their own first.
+__global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
+    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ rows, int64_t row_stride,
+    const uint32_t* __restrict__ tile_flags, int tiles, int buckets, int fine_bits,
+    const int64_t* __restrict__ keys, int64_t n_edges, int64_t n_nodes, int64_t* __restrict__ order,
+    int64_t* __restrict__ offsets, int32_t* __restrict__ status, int or_status) {
+  constexpr int kRounds = kLocalChunk / kGroupWaves / 64;  // rounds of the longest span
+  constexpr int kMarks = kLocalChunk / kThreads;  // positions a thread scans
+  constexpr size_t kRegion = kLocalChunk * sizeof(uint32_t) > sizeof(GapList) ? kLocalChunk * sizeof(uint32_t)
+                                                                                 : sizeof(GapList);
+  // the chunk's marks while it is gathered, then the sorted chunk; the gap list on the sorted path
+  __shared__ __align__(16) unsigned char region[kRegion];
+  // per wave and fine digit: the counters while the wave ranks, then the
+  // digit's first place in the chunk for the wave's elements
+  __shared__ uint32_t wave_base[kGroupWaves * kFineDigits];
+  __shared__ uint32_t fine_base[kFineDigits];
+  __shared__ uint32_t chunk_start[kFineDigits];
+  __shared__ uint32_t target_shift[kFineDigits];
+  __shared__ uint32_t wave_totals[kGroupWaves];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+
+  // buckets dealt to XCDs in contiguous ranges: neighbouring buckets read the same lines of runs and rows
+  const bool has_bucket = static_cast<int>(blockIdx.x) < buckets;
+  const int b = has_bucket ? static_cast<int>(xcd_block(blockIdx.x, static_cast<unsigned int>(buckets))) : 0;
+  const int fines = 1 << fine_bits;
+  const uint32_t fine_mask = static_cast<uint32_t>(fines - 1);
+
+  // the bucket's run in each of this thread's tiles (consecutive tiles),
+  // loaded while the tiles' flags are reduced
+  const int per = (tiles + kThreads - 1) / kThreads;
+  const int first_tile = t * per;
+  uint32_t run_first[kRunTilesPerThread], run_length[kRunTilesPerThread];
+  uint32_t sum_start = 0u, sum_length = 0u;
+#pragma unroll
+  for (int i = 0; i < kRunTilesPerThread; ++i) {
+    const int tile = first_tile + i;
+    run_first[i] = 0u;
+    run_length[i] = 0u;
+    if (has_bucket && i < per && tile < tiles) {
+      const uint16_t* row = rows + static_cast<int64_t>(tile) * row_stride;
+      run_first[i] = row[b];
+      run_length[i] = static_cast<uint32_t>(row[b + 1]) - run_first[i];
+    }
+    sum_start += run_first[i];
+    sum_length += run_length[i];
+  }
+  // the tiles' flags
+  uint32_t local = 0u;
+  for (int i = t; i < tiles; i += kThreads) local |= tile_flags[i];
+  const int32_t found = (__syncthreads_or(local & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
+                        (__syncthreads_or(local & kFlagUnsorted) ? kFlagUnsorted : 0);
+  if (blockIdx.x == 0 && t == 0) {
+    if (or_status)
+      atomicOr(status, found);
+    else
+      *status = found;
+  }
+  if (!(found & kFlagUnsorted)) {
+    boundary_offsets(keys, n_edges, n_nodes, offsets, order, blockIdx.x, gridDim.x,
+                     *reinterpret_cast<GapList*>(region));
+    return;
+  }
+  if (!has_bucket) return;
+  uint32_t count = 0u, bucket_start = 0u;
+  uint32_t placed = block_exclusive_scan(sum_length, wave_totals, count);
+  block_exclusive_scan(sum_start, wave_totals, bucket_start);
+  uint32_t run_delta[kRunTilesPerThread];
+#pragma unroll
+  for (int i = 0; i < kRunTilesPerThread; ++i) {
+    run_delta[i] = static_cast<uint32_t>(first_tile + i) * kTile + run_first[i] - placed;
+    run_first[i] = placed;  // from here: the run's first position in the bucket
+    placed += run_length[i];
+  }
+  for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] = 0u;
+  for (int f = t; f < kFineDigits; f += kThreads) fine_base[f] = 0u;
+
+  const BufferView packed_view = buffer_view(packed, n_edges * 4);
+  uint32_t* mark = reinterpret_cast<uint32_t*>(region);
+  // The chunk's elements in equal spans of whole rounds, one span a wave in
+  // order: value[r] of element j = wave * span + 64 r + lane for r < rounds
+  // (bit r of the result: j < in_chunk; zero elsewhere).
+  const auto span_rounds = [](int in_chunk) {
+    return (in_chunk + kGroupWaves * 64 - 1) / (kGroupWaves * 64);
+  };
+  const auto gather = [&](uint32_t c0, int in_chunk, uint32_t (&value)[kRounds]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const int rounds = span_rounds(in_chunk);
+    // (empty asm: per-round indices are rebuilt in every chunk, not hoisted out
+    // of the chunk loop and held in registers)
+    int first = wave * 64 * rounds + lane;
+    asm volatile("" : "+v"(first));
+    u32x4* mark4 = reinterpret_cast<u32x4*>(mark);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < kMarks / 4; ++k) mark4[t * (kMarks / 4) + k] = zero;
+    __syncthreads();
+    // the first position of every run that meets the chunk gets delta + 1
+#pragma unroll
+    for (int i = 0; i < kRunTilesPerThread; ++i) {
+      const uint32_t rs = run_first[i], re = run_first[i] + run_length[i];
+      if (run_length[i] > 0u && re > c0 && rs < c0 + static_cast<uint32_t>(in_chunk))
+        mark[(rs > c0 ? rs : c0) - c0] = run_delta[i] + 1u;
+    }
+    __syncthreads();
+    // running maximum over the chunk
+    uint32_t m[kMarks];
+#pragma unroll
+    for (int k = 0; k < kMarks / 4; ++k) {
+      const u32x4 four = mark4[t * (kMarks / 4) + k];
+      m[4 * k] = four.x;
+      m[4 * k + 1] = four.y;
+      m[4 * k + 2] = four.z;
+      m[4 * k + 3] = four.w;
+    }
+    uint32_t running = 0u;
+#pragma unroll
+    for (int k = 0; k < kMarks; ++k) running = max(running, m[k]);
+    running = block_exclusive_max(running, wave_totals);
+#pragma unroll
+    for (int k = 0; k < kMarks; ++k) m[k] = running = max(running, m[k]);
+#pragma unroll
+    for (int k = 0; k < kMarks / 4; ++k) {
+      const u32x4 four = {m[4 * k], m[4 * k + 1], m[4 * k + 2], m[4 * k + 3]};
+      mark4[t * (kMarks / 4) + k] = four;
+    }
+    __syncthreads();
+    uint32_t valid = 0u;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      value[r] = 0u;
+      if (r >= rounds) continue;
+      const int j = first + 64 * r;
+      // every position carries a mark (position 0 lies in a run); past the chunk the view reads zero
+      const uint32_t source = mark[j] - 1u + c0 + static_cast<uint32_t>(j);
+      const bool inside = j < in_chunk;
+      valid |= inside ? (1u << r) : 0u;
+      value[r] = load_u32(packed_view, inside ? source * 4u : kNoRow);
+    }
+    return valid;
+  };
+  const auto write_offsets = [&]() {
+    for (int f = t; f < fines; f += kThreads) {
+      const int64_t key = (static_cast<int64_t>(b) << fine_bits) + f;
+      if (key < n_nodes) offsets[key] = fine_base[f];
+    }
+    if (b == buckets - 1 && t == 0) offsets[n_nodes] = static_cast<int64_t>(bucket_start) + count;
+  };
+  const bool one_chunk = count <= static_cast<uint32_t>(kLocalChunk);
+
+  if (!one_chunk) {
+    // the bucket's fine-digit histogram -> offsets of its keys
+    for (uint32_t c0 = 0u; c0 < count; c0 += kLocalChunk) {
+      const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kLocalChunk) ? count - c0 : kLocalChunk);
+      uint32_t value[kRounds];
+      const uint32_t valid = gather(c0, in_chunk, value);
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r)
+        if ((valid >> r) & 1u) atomicAdd(&fine_base[value[r] & fine_mask], 1u);
+      __syncthreads();  // the marks are read before the next chunk clears them
+    }
+    lds_exclusive_scan(fine_base, fines, bucket_start, wave_totals);
+    write_offsets();
+    if (order == nullptr) return;
+  }
+
+  // an empty bucket takes one (empty) round too: it still writes its keys' offsets
+  for (uint32_t c0 = 0u; c0 < count || c0 == 0u; c0 += kLocalChunk) {
+    const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kLocalChunk) ? count - c0 : kLocalChunk);
+    uint32_t value[kRounds], rank[kRounds];
+    const uint32_t valid = gather(c0, in_chunk, value);
+    const auto fine = [&](int r) { return value[r] & fine_mask; };
+    uint32_t* counter = wave_base + wave * kFineDigits;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) rank[r] = 0u;
+    wave_ballot_ranks<kFineMatchBits, kRounds>(fine, valid, counter, rank, span_rounds(in_chunk));
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) asm volatile("" : "+v"(value[r]));
+    __syncthreads();
+    wave_prefix(wave_base, kFineDigits, fines, chunk_start);
+    __syncthreads();
+    lds_exclusive_scan(chunk_start, fines, 0u, wave_totals);
+    // each wave's first place of every digit: the digit's start in the chunk plus the earlier waves' elements
+    for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] += chunk_start[i % kFineDigits];
+    if (one_chunk) {
+      // the chunk is the bucket: its digit counts are the histogram
+      for (int f = t; f < fines; f += kThreads) fine_base[f] = bucket_start + chunk_start[f];
+      __syncthreads();
+      write_offsets();
+      if (order == nullptr) return;
+    }
+    for (int f = t; f < fines; f += kThreads) target_shift[f] = fine_base[f] - chunk_start[f];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) rank[r] += ((valid >> r) & 1u) ? counter[fine(r)] : 0u;
+    __syncthreads();  // the marks are read before the sorted chunk overwrites them
+    uint32_t* sorted = mark;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r)
+      if ((valid >> r) & 1u) sorted[rank[r]] = value[r];
+    __syncthreads();
+    const uint32_t end = bucket_start + count;
+    for (int p = t; p < in_chunk; p += kThreads) {
+      const uint32_t e = sorted[p];
+      const uint32_t target = target_shift[e & fine_mask] + static_cast<uint32_t>(p);
+      // unreachable outside the bucket: its fine digits were counted from the same elements
+      if (target >= bucket_start && target < end) order[target] = static_cast<int64_t>(e >> fine_bits);
+    }
+    __syncthreads();
+    // the next chunk's elements of digit f follow this chunk's; the wave counters restart
+    for (int f = t; f < fines; f += kThreads) {
+      const uint32_t next = f + 1 < fines ? chunk_start[f + 1] : static_cast<uint32_t>(in_chunk);
+      fine_base[f] += next - chunk_start[f];
+    }
+    for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] = 0u;
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void widen_kernel(const uint32_t* __restrict__ index, int64_t n,
                                                          const uint32_t* count_limit, int64_t* __restrict__ order,
                                                          const int32_t* __restrict__ status, int gate) {
@@ -997,6 +1479,7 @@ struct Plan {
   int buckets = 1;
   bool wide = false;      // packed as uint64 (index << fine_bits does not fit 32 bits)
   bool narrow_elements = false;  // the scatter's LDS elements fit 32 bits (keys of at most 19 bits)
+  bool grouped = false;  // the two-launch form: tile grouping, then bucket gathers
   // LSD path
   int passes = 0;
   int digit_bits = 0;
@@ -1011,6 +1494,7 @@ struct Plan {
       buckets = static_cast<int>((nodes + (int64_t(1) << fine_bits) - 1) >> fine_bits);
       wide = edges > 0 && ((static_cast<uint64_t>(edges) - 1) << fine_bits) > 0xffffffffull;
       narrow_elements = bits <= 19;
+      grouped = !wide && fine_bits <= kFineMatchBits && tiles <= kMaxRunTiles;
     } else {
       passes = (bits + kDigitBits - 1) / kDigitBits;
       digit_bits = (bits + passes - 1) / passes;
@@ -1031,6 +1515,7 @@ struct Scratch {
   uint32_t* counts = nullptr;     // [buckets of the pass][tiles]
   uint32_t* bucket_total = nullptr;
   uint32_t* bucket_start = nullptr;
+  uint32_t* tile_flags = nullptr;  // grouped path: per tile
   void* packed = nullptr;         // two-level path
   uint32_t* keys[2] = {nullptr, nullptr};   // LSD ping-pong
   uint32_t* index[2] = {nullptr, nullptr};
@@ -1040,7 +1525,7 @@ size_t scratch_bytes(const Plan& plan) {
   const size_t edges = static_cast<size_t>(plan.n_edges > 0 ? plan.n_edges : 1);
   const size_t tiles = static_cast<size_t>(plan.tiles > 0 ? plan.tiles : 1);
   size_t bytes = 256 + 256 + round_up_256(tiles * kMaxBuckets * 4) + round_up_256(kMaxBuckets * 4) +
-                 round_up_256((kMaxBuckets + 1) * 4);
+                 round_up_256((kMaxBuckets + 1) * 4) + round_up_256(kMaxRunTiles * 4);
   if (plan.two_level)
     bytes += round_up_256(edges * (plan.wide ? 8 : 4));
   else
@@ -1058,16 +1543,18 @@ bool carve(void* workspace, size_t bytes, const Plan& plan, Scratch& out) {
   out.counts = carver.take<uint32_t>(tiles * kMaxBuckets);
   out.bucket_total = carver.take<uint32_t>(kMaxBuckets);
   out.bucket_start = carver.take<uint32_t>(kMaxBuckets + 1);
+  out.tile_flags = carver.take<uint32_t>(kMaxRunTiles);
   if (plan.two_level) {
     out.packed = carver.take<char>(edges * (plan.wide ? 8 : 4));
-    return out.flags && out.valid_count && out.counts && out.bucket_total && out.bucket_start && out.packed;
+    return out.flags && out.valid_count && out.counts && out.bucket_total && out.bucket_start && out.tile_flags &&
+           out.packed;
   }
   for (int k = 0; k < 2; ++k) {
     out.keys[k] = carver.take<uint32_t>(edges);
     out.index[k] = carver.take<uint32_t>(edges);
   }
-  return out.flags && out.valid_count && out.counts && out.bucket_total && out.bucket_start && out.keys[0] &&
-         out.keys[1] && out.index[0] && out.index[1];
+  return out.flags && out.valid_count && out.counts && out.bucket_total && out.bucket_start && out.tile_flags &&
+         out.keys[0] && out.keys[1] && out.index[0] && out.index[1];
 }
 
 int check_sizes(int64_t n_edges, int64_t n_nodes, const char* what) {
@@ -1084,8 +1571,11 @@ int check_sizes(int64_t n_edges, int64_t n_nodes, const char* what) {
 int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64_t* order, int32_t* status,
                   const int64_t* radial_slot, int64_t n_rows, int64_t n_radial, const Scratch& s,
                   hipStream_t stream) {
-  clear_word_kernel<<<1, 64, 0, stream>>>(status);
-  if (int code = launched("clear_word_kernel")) return code;
+  // the grouped path's gather writes the status word itself (ORs into it after the slot checks)
+  if (!plan.grouped || n_rows > 0 || plan.n_edges == 0) {
+    clear_word_kernel<<<1, 64, 0, stream>>>(status);
+    if (int code = launched("clear_word_kernel")) return code;
+  }
   if (n_rows > 0) {
     slot_check_kernel<<<1, 64, 0, stream>>>(radial_slot, n_rows, n_radial, status);
     if (int code = launched("slot_check_kernel")) return code;
@@ -1100,6 +1590,22 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
   };
   // sorted keys: the finish launch's boundary path (its grid also strides over the keys)
   const int64_t boundary_blocks = std::min<int64_t>((plan.n_edges + kThreads) / kThreads, 2048);
+  if (plan.grouped) {
+    const int64_t row_stride = plan.buckets + 1;
+    uint16_t* rows = reinterpret_cast<uint16_t*>(s.counts);
+    uint32_t* packed = static_cast<uint32_t*>(s.packed);
+    tile_group_kernel<<<tiles, kThreads, 0, stream>>>(keys, plan.n_edges, nodes, plan.fine_bits, plan.buckets, packed,
+                                                      rows, row_stride, s.tile_flags);
+    if (int code = launched("tile_group_kernel")) return code;
+    // one workgroup per bucket; at least 512 for the boundary path of sorted keys
+    const unsigned int blocks =
+        static_cast<unsigned int>(std::max<int64_t>(plan.buckets, std::min<int64_t>(boundary_blocks, 512)));
+    bucket_gather_kernel<<<blocks, kThreads, 0, stream>>>(packed, rows, row_stride, s.tile_flags,
+                                                          static_cast<int>(plan.tiles), plan.buckets, plan.fine_bits,
+                                                          keys, plan.n_edges, plan.n_nodes, order, offsets, status,
+                                                          n_rows > 0 ? 1 : 0);
+    return launched("bucket_gather_kernel");
+  }
   if (plan.two_level) {
     const int shift = plan.fine_bits, bits = plan.bucket_bits, buckets = plan.buckets;
     tile_count_kernel<false, true><<<tiles, kThreads, 0, stream>>>(keys, nullptr, plan.n_edges, nullptr, nodes, shift,
