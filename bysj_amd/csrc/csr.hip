@@ -97,8 +97,9 @@ __device__ __forceinline__ uint32_t dpp_or_zero(uint32_t value) {
   return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(value), kCtrl, kRowMask, 0xf, true));
 }
 
-// Exclusive scan of one value per thread over the workgroup; `total` gets
-// the sum.  Every thread must call it.
+// Exclusive scan of one value per thread over a workgroup of kT threads;
+// `total` gets the sum.  Every thread must call it.
+template <int kT = kThreads>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_t* wave_totals, uint32_t& total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -116,7 +117,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_
   __syncthreads();
   uint32_t before = 0, sum = 0;
 #pragma unroll
-  for (int w = 0; w < kGroupWaves; ++w) {
+  for (int w = 0; w < kT / 64; ++w) {
     const uint32_t part = wave_totals[w];
     before += w < wave ? part : 0u;
     sum += part;
@@ -126,17 +127,18 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_
   return before + inclusive - value;
 }
 
-// In-place exclusive scan of values[0, n) in LDS (plus `base`); returns the
-// total.  Every thread must call it.
+// In-place exclusive scan of values[0, n) in LDS (plus `base`) by a
+// workgroup of kT threads; returns the total.  Every thread must call it.
+template <int kT = kThreads>
 __device__ __forceinline__ uint32_t lds_exclusive_scan(uint32_t* values, int n, uint32_t base,
                                                        uint32_t* wave_totals) {
-  const int per = (n + kThreads - 1) / kThreads;
+  const int per = (n + kT - 1) / kT;
   const int first = threadIdx.x * per;
   uint32_t sum = 0;
   for (int i = 0; i < per; ++i)
     if (first + i < n) sum += values[first + i];
   uint32_t total = 0;
-  uint32_t running = base + block_exclusive_scan(sum, wave_totals, total);
+  uint32_t running = base + block_exclusive_scan<kT>(sum, wave_totals, total);
   for (int i = 0; i < per; ++i)
     if (first + i < n) {
       const uint32_t value = values[first + i];
@@ -227,13 +229,15 @@ __device__ __forceinline__ void wave_split_ranks(DigitOf digit, uint32_t valid, 
   }
 }
 
-// In place over digits [0, digits): the per-wave counts become the counts of
-// the earlier waves, and `total[d]` gets the digit's count over all waves.
+// In place over digits [0, digits): the per-wave counts of a workgroup of kT
+// threads become the counts of the earlier waves, and `total[d]` gets the
+// digit's count over all waves.
+template <int kT = kThreads>
 __device__ __forceinline__ void wave_prefix(uint32_t* wave_count, int stride, int digits, uint32_t* total) {
-  for (int d = threadIdx.x; d < digits; d += kThreads) {
+  for (int d = threadIdx.x; d < digits; d += kT) {
     uint32_t running = 0u;
 #pragma unroll
-    for (int w = 0; w < kGroupWaves; ++w) {
+    for (int w = 0; w < kT / 64; ++w) {
       const uint32_t count = wave_count[w * stride + d];
       wave_count[w * stride + d] = running;
       running += count;
@@ -599,19 +603,21 @@ __global__ __launch_bounds__(kThreads, 4) void tile_scatter_kernel(
 // longer ones (sparse keys) are listed in LDS and filled by the whole
 // workgroup.  With `identity`, also identity[e] = e.  Workgroups `block` of
 // `blocks` stride over the list.
-struct GapList {
-  int64_t low[kThreads];
-  int64_t high[kThreads];
-  int64_t edge[kThreads];
+template <int kT>
+struct GapListOf {
+  int64_t low[kT];
+  int64_t high[kT];
+  int64_t edge[kT];
   int count;
 };
+using GapList = GapListOf<kThreads>;
 
-template <typename K>
+template <typename K, int kT = kThreads>
 __device__ __forceinline__ void boundary_offsets(const K* __restrict__ keys, int64_t limit, int64_t n_nodes,
                                                  int64_t* __restrict__ offsets, int64_t* __restrict__ identity,
-                                                 int64_t block, int64_t blocks, GapList& gaps) {
-  const int64_t stride = blocks * kThreads;
-  for (int64_t first = block * kThreads; first <= limit; first += stride) {
+                                                 int64_t block, int64_t blocks, GapListOf<kT>& gaps) {
+  const int64_t stride = blocks * kT;
+  for (int64_t first = block * kT; first <= limit; first += stride) {
     if (threadIdx.x == 0) gaps.count = 0;
     __syncthreads();
     const int64_t e = first + threadIdx.x;
@@ -633,7 +639,7 @@ __device__ __forceinline__ void boundary_offsets(const K* __restrict__ keys, int
     __syncthreads();
     const int listed = gaps.count;
     for (int g = 0; g < listed; ++g)
-      for (int64_t k = gaps.low[g] + threadIdx.x; k <= gaps.high[g]; k += kThreads) offsets[k] = gaps.edge[g];
+      for (int64_t k = gaps.low[g] + threadIdx.x; k <= gaps.high[g]; k += kT) offsets[k] = gaps.edge[g];
     __syncthreads();
   }
 }
@@ -972,6 +978,13 @@ constexpr int kMaxRunTiles = 1024;                    // tiles one gather holds 
 constexpr int kRunTilesPerThread = kMaxRunTiles / kThreads;
 constexpr int kFineMatchBits = 6;                     // fine digits a gather ranks
 constexpr int kFineDigits = 1 << kFineMatchBits;
+// A gather's workgroup and the elements it ranks at once: 6144 at eight waves
+// per SIMD (four gathers per CU, so 1024 buckets run in one round) when the
+// buckets average at most 95% of that, else 8192 at six (three per CU).  A
+// bucket longer than its chunk takes the multi-chunk path: slower, not wrong.
+constexpr int kGatherThreads = 512;
+constexpr int kGatherSmallChunk = 6144;
+constexpr int kGatherLargeChunk = 8192;
 
 // The same ranks as wave_split_ranks, with the lanes of equal digits found
 // through LDS instead of one ballot per digit bit.  Every lane first clears
@@ -1052,8 +1065,9 @@ __device__ __forceinline__ uint32_t rotate_from_lane_above(uint32_t value) {
       __builtin_amdgcn_update_dpp(0, static_cast<int>(value), 0x134, 0xf, 0xf, false));
 }
 
-// Exclusive running maximum over the workgroup of one value per thread (0 for
-// thread 0).  Every thread must call it.
+// Exclusive running maximum over a workgroup of kT threads of one value per
+// thread (0 for thread 0).  Every thread must call it.
+template <int kT = kThreads>
 __device__ __forceinline__ uint32_t block_exclusive_max(uint32_t value, uint32_t* wave_totals) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -1068,7 +1082,7 @@ __device__ __forceinline__ uint32_t block_exclusive_max(uint32_t value, uint32_t
   __syncthreads();
   uint32_t before = 0u;
 #pragma unroll
-  for (int w = 0; w < kGroupWaves; ++w) before = w < wave ? max(before, wave_totals[w]) : before;
+  for (int w = 0; w < kT / 64; ++w) before = w < wave ? max(before, wave_totals[w]) : before;
   __syncthreads();
   return max(before, from_lane_below(inclusive, 0u));
 }
@@ -1204,27 +1218,33 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
 // over the run starts, each marked with delta + 1, gives every position of the
 // chunk its source.  Buckets of more than one chunk count their fine digits in
 // a gather pass of their own first.
-__global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
+template <int kGT, int kChunk, int kMinWaves>
+__global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
     const uint32_t* __restrict__ packed, const uint16_t* __restrict__ rows, int64_t row_stride,
     const uint32_t* __restrict__ tile_flags, int tiles, int buckets, int fine_bits,
     const int64_t* __restrict__ keys, int64_t n_edges, int64_t n_nodes, int64_t* __restrict__ order,
     int64_t* __restrict__ offsets, int32_t* __restrict__ status, int or_status) {
-  constexpr int kRounds = kLocalChunk / kGroupWaves / 64;  // rounds of the longest span
-  constexpr int kMarks = kLocalChunk / kThreads;  // positions a thread scans
-  constexpr size_t kRegion = kLocalChunk * sizeof(uint32_t) > sizeof(GapList) ? kLocalChunk * sizeof(uint32_t)
-                                                                                 : sizeof(GapList);
+  constexpr int kGW = kGT / 64;                            // waves of the workgroup
+  constexpr int kRounds = kChunk / kGW / 64;          // rounds of the longest span
+  constexpr int kMarks = kChunk / kGT;                // positions a thread scans
+  constexpr int kRunsPerThread = kMaxRunTiles / kGT;
+  using Gaps = GapListOf<kGT>;
+  constexpr size_t kRegion = kChunk * sizeof(uint32_t) > sizeof(Gaps) ? kChunk * sizeof(uint32_t)
+                                                                              : sizeof(Gaps);
   // the chunk's marks while it is gathered, then the sorted chunk; the gap list on the sorted path
   __shared__ __align__(16) unsigned char region[kRegion];
   // per wave and fine digit: the counters while the wave ranks, then the
   // digit's first place in the chunk for the wave's elements
-  __shared__ uint32_t wave_base[kGroupWaves * kFineDigits];
+  __shared__ uint32_t wave_base[kGW * kFineDigits];
   __shared__ uint32_t fine_base[kFineDigits];
   __shared__ uint32_t chunk_start[kFineDigits];
   __shared__ uint32_t target_shift[kFineDigits];
-  __shared__ uint32_t wave_totals[kGroupWaves];
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = t >> 6;
+  __shared__ uint32_t wave_totals[kGW];
+  // (not const: the chunk loop rebuilds them, so that nothing derived from the
+  // thread index is hoisted out of the loop and held in registers across it)
+  int t = threadIdx.x;
+  int lane = t & 63;
+  int wave = t >> 6;
 
   // buckets dealt to XCDs in contiguous ranges: neighbouring buckets read the same lines of runs and rows
   const bool has_bucket = static_cast<int>(blockIdx.x) < buckets;
@@ -1234,12 +1254,12 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
 
   // the bucket's run in each of this thread's tiles (consecutive tiles),
   // loaded while the tiles' flags are reduced
-  const int per = (tiles + kThreads - 1) / kThreads;
+  const int per = (tiles + kGT - 1) / kGT;
   const int first_tile = t * per;
-  uint32_t run_first[kRunTilesPerThread], run_length[kRunTilesPerThread];
+  uint32_t run_first[kRunsPerThread], run_length[kRunsPerThread];
   uint32_t sum_start = 0u, sum_length = 0u;
 #pragma unroll
-  for (int i = 0; i < kRunTilesPerThread; ++i) {
+  for (int i = 0; i < kRunsPerThread; ++i) {
     const int tile = first_tile + i;
     run_first[i] = 0u;
     run_length[i] = 0u;
@@ -1253,7 +1273,7 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
   }
   // the tiles' flags
   uint32_t local = 0u;
-  for (int i = t; i < tiles; i += kThreads) local |= tile_flags[i];
+  for (int i = t; i < tiles; i += kGT) local |= tile_flags[i];
   const int32_t found = (__syncthreads_or(local & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
                         (__syncthreads_or(local & kFlagUnsorted) ? kFlagUnsorted : 0);
   if (blockIdx.x == 0 && t == 0) {
@@ -1263,23 +1283,23 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
       *status = found;
   }
   if (!(found & kFlagUnsorted)) {
-    boundary_offsets(keys, n_edges, n_nodes, offsets, order, blockIdx.x, gridDim.x,
-                     *reinterpret_cast<GapList*>(region));
+    boundary_offsets<int64_t, kGT>(keys, n_edges, n_nodes, offsets, order, blockIdx.x, gridDim.x,
+                                   *reinterpret_cast<Gaps*>(region));
     return;
   }
   if (!has_bucket) return;
   uint32_t count = 0u, bucket_start = 0u;
-  uint32_t placed = block_exclusive_scan(sum_length, wave_totals, count);
-  block_exclusive_scan(sum_start, wave_totals, bucket_start);
-  uint32_t run_delta[kRunTilesPerThread];
+  uint32_t placed = block_exclusive_scan<kGT>(sum_length, wave_totals, count);
+  block_exclusive_scan<kGT>(sum_start, wave_totals, bucket_start);
+  uint32_t run_delta[kRunsPerThread];
 #pragma unroll
-  for (int i = 0; i < kRunTilesPerThread; ++i) {
+  for (int i = 0; i < kRunsPerThread; ++i) {
     run_delta[i] = static_cast<uint32_t>(first_tile + i) * kTile + run_first[i] - placed;
     run_first[i] = placed;  // from here: the run's first position in the bucket
     placed += run_length[i];
   }
-  for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] = 0u;
-  for (int f = t; f < kFineDigits; f += kThreads) fine_base[f] = 0u;
+  for (int i = t; i < kGW * kFineDigits; i += kGT) wave_base[i] = 0u;
+  for (int f = t; f < kFineDigits; f += kGT) fine_base[f] = 0u;
 
   const BufferView packed_view = buffer_view(packed, n_edges * 4);
   uint32_t* mark = reinterpret_cast<uint32_t*>(region);
@@ -1287,15 +1307,12 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
   // order: value[r] of element j = wave * span + 64 r + lane for r < rounds
   // (bit r of the result: j < in_chunk; zero elsewhere).
   const auto span_rounds = [](int in_chunk) {
-    return (in_chunk + kGroupWaves * 64 - 1) / (kGroupWaves * 64);
+    return (in_chunk + kGW * 64 - 1) / (kGW * 64);
   };
   const auto gather = [&](uint32_t c0, int in_chunk, uint32_t (&value)[kRounds]) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const int rounds = span_rounds(in_chunk);
-    // (empty asm: per-round indices are rebuilt in every chunk, not hoisted out
-    // of the chunk loop and held in registers)
-    int first = wave * 64 * rounds + lane;
-    asm volatile("" : "+v"(first));
+    const int first = wave * 64 * rounds + lane;
     u32x4* mark4 = reinterpret_cast<u32x4*>(mark);
     const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -1303,7 +1320,7 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
     __syncthreads();
     // the first position of every run that meets the chunk gets delta + 1
 #pragma unroll
-    for (int i = 0; i < kRunTilesPerThread; ++i) {
+    for (int i = 0; i < kRunsPerThread; ++i) {
       const uint32_t rs = run_first[i], re = run_first[i] + run_length[i];
       if (run_length[i] > 0u && re > c0 && rs < c0 + static_cast<uint32_t>(in_chunk))
         mark[(rs > c0 ? rs : c0) - c0] = run_delta[i] + 1u;
@@ -1322,7 +1339,7 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
     uint32_t running = 0u;
 #pragma unroll
     for (int k = 0; k < kMarks; ++k) running = max(running, m[k]);
-    running = block_exclusive_max(running, wave_totals);
+    running = block_exclusive_max<kGT>(running, wave_totals);
 #pragma unroll
     for (int k = 0; k < kMarks; ++k) m[k] = running = max(running, m[k]);
 #pragma unroll
@@ -1346,18 +1363,18 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
     return valid;
   };
   const auto write_offsets = [&]() {
-    for (int f = t; f < fines; f += kThreads) {
+    for (int f = t; f < fines; f += kGT) {
       const int64_t key = (static_cast<int64_t>(b) << fine_bits) + f;
       if (key < n_nodes) offsets[key] = fine_base[f];
     }
     if (b == buckets - 1 && t == 0) offsets[n_nodes] = static_cast<int64_t>(bucket_start) + count;
   };
-  const bool one_chunk = count <= static_cast<uint32_t>(kLocalChunk);
+  const bool one_chunk = count <= static_cast<uint32_t>(kChunk);
 
   if (!one_chunk) {
     // the bucket's fine-digit histogram -> offsets of its keys
-    for (uint32_t c0 = 0u; c0 < count; c0 += kLocalChunk) {
-      const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kLocalChunk) ? count - c0 : kLocalChunk);
+    for (uint32_t c0 = 0u; c0 < count; c0 += kChunk) {
+      const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kChunk) ? count - c0 : kChunk);
       uint32_t value[kRounds];
       const uint32_t valid = gather(c0, in_chunk, value);
 #pragma unroll
@@ -1365,14 +1382,17 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
         if ((valid >> r) & 1u) atomicAdd(&fine_base[value[r] & fine_mask], 1u);
       __syncthreads();  // the marks are read before the next chunk clears them
     }
-    lds_exclusive_scan(fine_base, fines, bucket_start, wave_totals);
+    lds_exclusive_scan<kGT>(fine_base, fines, bucket_start, wave_totals);
     write_offsets();
     if (order == nullptr) return;
   }
 
   // an empty bucket takes one (empty) round too: it still writes its keys' offsets
-  for (uint32_t c0 = 0u; c0 < count || c0 == 0u; c0 += kLocalChunk) {
-    const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kLocalChunk) ? count - c0 : kLocalChunk);
+  for (uint32_t c0 = 0u; c0 < count || c0 == 0u; c0 += kChunk) {
+    asm volatile("" : "+v"(t));
+    lane = t & 63;
+    wave = t >> 6;
+    const int in_chunk = static_cast<int>(count - c0 < static_cast<uint32_t>(kChunk) ? count - c0 : kChunk);
     uint32_t value[kRounds], rank[kRounds];
     const uint32_t valid = gather(c0, in_chunk, value);
     const auto fine = [&](int r) { return value[r] & fine_mask; };
@@ -1383,19 +1403,19 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) asm volatile("" : "+v"(value[r]));
     __syncthreads();
-    wave_prefix(wave_base, kFineDigits, fines, chunk_start);
+    wave_prefix<kGT>(wave_base, kFineDigits, fines, chunk_start);
     __syncthreads();
-    lds_exclusive_scan(chunk_start, fines, 0u, wave_totals);
+    lds_exclusive_scan<kGT>(chunk_start, fines, 0u, wave_totals);
     // each wave's first place of every digit: the digit's start in the chunk plus the earlier waves' elements
-    for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] += chunk_start[i % kFineDigits];
+    for (int i = t; i < kGW * kFineDigits; i += kGT) wave_base[i] += chunk_start[i % kFineDigits];
     if (one_chunk) {
       // the chunk is the bucket: its digit counts are the histogram
-      for (int f = t; f < fines; f += kThreads) fine_base[f] = bucket_start + chunk_start[f];
+      for (int f = t; f < fines; f += kGT) fine_base[f] = bucket_start + chunk_start[f];
       __syncthreads();
       write_offsets();
       if (order == nullptr) return;
     }
-    for (int f = t; f < fines; f += kThreads) target_shift[f] = fine_base[f] - chunk_start[f];
+    for (int f = t; f < fines; f += kGT) target_shift[f] = fine_base[f] - chunk_start[f];
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) rank[r] += ((valid >> r) & 1u) ? counter[fine(r)] : 0u;
@@ -1406,7 +1426,7 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
       if ((valid >> r) & 1u) sorted[rank[r]] = value[r];
     __syncthreads();
     const uint32_t end = bucket_start + count;
-    for (int p = t; p < in_chunk; p += kThreads) {
+    for (int p = t; p < in_chunk; p += kGT) {
       const uint32_t e = sorted[p];
       const uint32_t target = target_shift[e & fine_mask] + static_cast<uint32_t>(p);
       // unreachable outside the bucket: its fine digits were counted from the same elements
@@ -1414,11 +1434,11 @@ __global__ __launch_bounds__(kThreads, 6) void bucket_gather_kernel(
     }
     __syncthreads();
     // the next chunk's elements of digit f follow this chunk's; the wave counters restart
-    for (int f = t; f < fines; f += kThreads) {
+    for (int f = t; f < fines; f += kGT) {
       const uint32_t next = f + 1 < fines ? chunk_start[f + 1] : static_cast<uint32_t>(in_chunk);
       fine_base[f] += next - chunk_start[f];
     }
-    for (int i = t; i < kGroupWaves * kFineDigits; i += kThreads) wave_base[i] = 0u;
+    for (int i = t; i < kGW * kFineDigits; i += kGT) wave_base[i] = 0u;
     __syncthreads();
   }
 }
@@ -1600,11 +1620,16 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
     // one workgroup per bucket; at least 512 for the boundary path of sorted keys
     const unsigned int blocks =
         static_cast<unsigned int>(std::max<int64_t>(plan.buckets, std::min<int64_t>(boundary_blocks, 512)));
-    bucket_gather_kernel<<<blocks, kThreads, 0, stream>>>(packed, rows, row_stride, s.tile_flags,
-                                                          static_cast<int>(plan.tiles), plan.buckets, plan.fine_bits,
-                                                          keys, plan.n_edges, plan.n_nodes, order, offsets, status,
-                                                          n_rows > 0 ? 1 : 0);
-    return launched("bucket_gather_kernel");
+    const auto gather = [&](auto kernel) {
+      kernel<<<blocks, kGatherThreads, 0, stream>>>(packed, rows, row_stride, s.tile_flags,
+                                                     static_cast<int>(plan.tiles), plan.buckets, plan.fine_bits, keys,
+                                                     plan.n_edges, plan.n_nodes, order, offsets, status,
+                                                     n_rows > 0 ? 1 : 0);
+      return launched("bucket_gather_kernel");
+    };
+    if (plan.n_edges * 20 <= static_cast<int64_t>(plan.buckets) * kGatherSmallChunk * 19)
+      return gather(bucket_gather_kernel<kGatherThreads, kGatherSmallChunk, 8>);
+    return gather(bucket_gather_kernel<kGatherThreads, kGatherLargeChunk, 6>);
   }
   if (plan.two_level) {
     const int shift = plan.fine_bits, bits = plan.bucket_bits, buckets = plan.buckets;

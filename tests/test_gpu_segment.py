@@ -105,6 +105,17 @@ def test_counting_sort_skewed_and_sparse_keys():
     _check_grouping_against_numpy(np.array([0, 9_999_999], dtype=np.int64), 10_000_000, "two keys, ends")
 
 
+@pytest.mark.parametrize("edges,nodes", [(700_000, 128), (800_000, 128), (6_300_000, 2**16)])
+def test_counting_sort_bucket_chunks(edges, nodes):
+    """Buckets that average just under and just over 95% of the gather's 6144-element chunk (the two
+    chunk sizes of the grouped path), and config-4-sized buckets past it, with one bucket pushed over
+    the chunk so that it takes the multi-chunk path beside ones that do not."""
+    announce("counting sort: bucket chunks", edges, nodes)
+    keys = workloads.rng(edges % 997 + nodes).integers(0, nodes, size=edges).astype(np.int64)
+    keys[: edges // 64] = 5
+    _check_grouping_against_numpy(keys, nodes, f"chunks E={edges} N={nodes}")
+
+
 def test_group_by_key_async_status_and_capture():
     """The asynchronous build reports the status bits on the device, allocates nothing when given its
     buffers, and replays from a HIP graph with the same result as the synchronous call."""
