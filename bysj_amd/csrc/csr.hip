@@ -90,6 +90,14 @@ __device__ __forceinline__ uint32_t load_u32(BufferView view, uint32_t offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(view, static_cast<int>(offset), 0, 0);
 }
 
+// Loads of data read once (cache policy nt: streamed rather than kept in L2).
+constexpr int kStreamed = 2;
+__device__ __forceinline__ int64_t load_i64_streamed(BufferView view, uint32_t offset) {
+  const u32x2 raw = __builtin_amdgcn_raw_buffer_load_b64(view, static_cast<int>(offset), 0, kStreamed);
+  return __builtin_bit_cast(int64_t, raw);
+}
+
+
 // A DPP move of `value` (control kCtrl, rows kRowMask); lanes whose source
 // lies outside their row, and rows outside the mask, read 0.
 template <int kCtrl, int kRowMask>
@@ -957,8 +965,9 @@ __global__ __launch_bounds__(kThreads, 2) void finish_private_kernel(
 //   group   one workgroup per tile: the range and sortedness checks, then the
 //           tile's in-range elements grouped stably by the coarse digit and
 //           written back over the tile's own span of the packed buffer (one
-//           contiguous write), with the tile's row of bucket starts (16 bits
-//           each; entry `buckets` is the tile's in-range count) and its flags.
+//           contiguous write), with the tile's row of the buckets' runs (the
+//           run's first and end position in the tile, 16 bits each, in one
+//           word, so that a gather reads one word per tile) and its flags.
 //           No count pass and no scan over the tiles: nothing in a tile's
 //           output depends on another tile.
 //   gather  one workgroup per bucket: its run in every tile (two row
@@ -1089,13 +1098,13 @@ __device__ __forceinline__ uint32_t block_exclusive_max(uint32_t value, uint32_t
 
 // One tile: checks, stable grouping by the coarse digit (key >> fine_bits),
 // the grouped packed elements over packed[tile_base, tile_base + in-range
-// count), the row rows[tile][0, buckets] of bucket starts and the in-range
-// count, and tile_flags[tile].  Wave w takes the tile's elements
+// count), the row rows[tile][0, buckets) of the buckets' runs in the tile
+// (first | end << 16), and tile_flags[tile].  Wave w takes the tile's elements
 // [w S, (w + 1) S) (S = kScatterSpan), 64 consecutive ones a round.
 __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* __restrict__ keys, int64_t n,
                                                                  uint64_t n_nodes, int fine_bits, int buckets,
                                                                  uint32_t* __restrict__ packed,
-                                                                 uint16_t* __restrict__ rows, int64_t row_stride,
+                                                                 uint32_t* __restrict__ rows, int64_t row_stride,
                                                                  uint32_t* __restrict__ tile_flags) {
   // the wave counters, then (once every place is known) the grouped tile
   __shared__ __align__(16) uint32_t sorted[kTile];
@@ -1120,13 +1129,15 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   const int extent = static_cast<int>(rest > kTile + 1 ? kTile + 1 : rest);  // one element past the tile
   const uint32_t digit_mask = static_cast<uint32_t>(kMaxBuckets - 1);
   const uint32_t fine_mask = (1u << fine_bits) - 1u;
-  for (int i = t; i < kGroupWaves * kMaxBuckets; i += kThreads) wave_count[i] = 0u;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (int i = t; i < kGroupWaves * kMaxBuckets / 4; i += kThreads) reinterpret_cast<u32x4*>(wave_count)[i] = zero;
 
   const BufferView view = buffer_view(keys + tile_base, static_cast<int64_t>(extent) * 8);
   const int first = wave * kScatterSpan + lane;  // the lane's element of round 0
   int64_t raw[kScatterRounds];
 #pragma unroll
-  for (int r = 0; r < kScatterRounds; ++r) raw[r] = load_i64(view, static_cast<uint32_t>(first + 64 * r) * 8u);
+  for (int r = 0; r < kScatterRounds; ++r) raw[r] = load_i64_streamed(view, static_cast<uint32_t>(first + 64 * r) * 8u);
   // the element after the wave's span: the next wave's first, or the one after the tile
   const int after_q = (wave + 1) * kScatterSpan;
   const int64_t after = load_i64(view, static_cast<uint32_t>(after_q) * 8u);
@@ -1182,9 +1193,15 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   wave_prefix(wave_count, kMaxBuckets, buckets, tables.tile_start);
   __syncthreads();
   const uint32_t in_tile = lds_exclusive_scan(tables.tile_start, buckets, 0u, wave_totals);
+  // every wave counter += its digit's start in the tile: one read per element below
+  // (digits past `buckets` hold no element; their sums are never read)
+  for (int i = t; i < kGroupWaves * kMaxBuckets / 4; i += kThreads) {
+    u32x4* four = reinterpret_cast<u32x4*>(wave_count) + i;
+    *four += reinterpret_cast<const u32x4*>(tables.tile_start)[i % (kMaxBuckets / 4)];
+  }
+  __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kScatterRounds; ++r)
-    rank[r] += ((ok >> r) & 1u) ? tables.tile_start[digit(r)] + counter[digit(r)] : 0u;
+  for (int r = 0; r < kScatterRounds; ++r) rank[r] += ((ok >> r) & 1u) ? counter[digit(r)] : 0u;
   const int32_t found = (__syncthreads_or(flags & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
                         (__syncthreads_or(flags & kFlagUnsorted) ? kFlagUnsorted : 0);
   // (the barriers above: every counter is read before the grouped tile overwrites them)
@@ -1192,15 +1209,13 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   for (int r = 0; r < kScatterRounds; ++r)
     if ((ok >> r) & 1u)
       sorted[rank[r]] = (static_cast<uint32_t>(tile_base + first + 64 * r) << fine_bits) | (key[r] & fine_mask);
-  uint16_t* row = rows + static_cast<int64_t>(tile) * row_stride;
-  for (int b = t; b < buckets; b += kThreads) row[b] = static_cast<uint16_t>(tables.tile_start[b]);
-  if (t == 0) {
-    row[buckets] = static_cast<uint16_t>(in_tile);
-    tile_flags[tile] = static_cast<uint32_t>(found);
-  }
+  uint32_t* row = rows + static_cast<int64_t>(tile) * row_stride;
+  for (int b = t; b < buckets; b += kThreads)
+    row[b] = tables.tile_start[b] | ((b + 1 < buckets ? tables.tile_start[b + 1] : in_tile) << 16);
+  if (t == 0) tile_flags[tile] = static_cast<uint32_t>(found);
   __syncthreads();
   // the grouped tile, four elements a thread and store while they lie inside the tile
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  // (cached stores: the gathers read them next, from the Infinity Cache)
   uint32_t* out = packed + tile_base;
   for (int p = 4 * t; p < static_cast<int>(in_tile); p += 4 * kThreads) {
     if (p + 4 <= n_tile) {
@@ -1220,7 +1235,7 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
 // a gather pass of their own first.
 template <int kGT, int kChunk, int kMinWaves>
 __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
-    const uint32_t* __restrict__ packed, const uint16_t* __restrict__ rows, int64_t row_stride,
+    const uint32_t* __restrict__ packed, const uint32_t* __restrict__ rows, int64_t row_stride,
     const uint32_t* __restrict__ tile_flags, int tiles, int buckets, int fine_bits,
     const int64_t* __restrict__ keys, int64_t n_edges, int64_t n_nodes, int64_t* __restrict__ order,
     int64_t* __restrict__ offsets, int32_t* __restrict__ status, int or_status) {
@@ -1264,9 +1279,9 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
     run_first[i] = 0u;
     run_length[i] = 0u;
     if (has_bucket && i < per && tile < tiles) {
-      const uint16_t* row = rows + static_cast<int64_t>(tile) * row_stride;
-      run_first[i] = row[b];
-      run_length[i] = static_cast<uint32_t>(row[b + 1]) - run_first[i];
+      const uint32_t run = rows[static_cast<int64_t>(tile) * row_stride + b];  // first | end << 16
+      run_first[i] = run & 0xffffu;
+      run_length[i] = (run >> 16) - run_first[i];
     }
     sum_start += run_first[i];
     sum_length += run_length[i];
@@ -1358,6 +1373,7 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
       const uint32_t source = mark[j] - 1u + c0 + static_cast<uint32_t>(j);
       const bool inside = j < in_chunk;
       valid |= inside ? (1u << r) : 0u;
+      // (cached: the neighbouring buckets gathered beside this one read the same lines)
       value[r] = load_u32(packed_view, inside ? source * 4u : kNoRow);
     }
     return valid;
@@ -1430,7 +1446,9 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
       const uint32_t e = sorted[p];
       const uint32_t target = target_shift[e & fine_mask] + static_cast<uint32_t>(p);
       // unreachable outside the bucket: its fine digits were counted from the same elements
-      if (target >= bucket_start && target < end) order[target] = static_cast<int64_t>(e >> fine_bits);
+      // (non-temporal: the order is not read again by this build, so it streams past L2)
+      if (target >= bucket_start && target < end)
+        __builtin_nontemporal_store(static_cast<int64_t>(e >> fine_bits), order + target);
     }
     __syncthreads();
     // the next chunk's elements of digit f follow this chunk's; the wave counters restart
@@ -1611,8 +1629,8 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
   // sorted keys: the finish launch's boundary path (its grid also strides over the keys)
   const int64_t boundary_blocks = std::min<int64_t>((plan.n_edges + kThreads) / kThreads, 2048);
   if (plan.grouped) {
-    const int64_t row_stride = plan.buckets + 1;
-    uint16_t* rows = reinterpret_cast<uint16_t*>(s.counts);
+    const int64_t row_stride = plan.buckets;
+    uint32_t* rows = s.counts;
     uint32_t* packed = static_cast<uint32_t*>(s.packed);
     tile_group_kernel<<<tiles, kThreads, 0, stream>>>(keys, plan.n_edges, nodes, plan.fine_bits, plan.buckets, packed,
                                                       rows, row_stride, s.tile_flags);
