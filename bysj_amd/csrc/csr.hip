@@ -199,6 +199,23 @@ __device__ __forceinline__ uint64_t lanes_with_digit(uint32_t digit, bool active
   return active ? same : 0ull;
 }
 
+// The same mask for an active lane, without clearing it for inactive ones:
+// `active_lanes` is the ballot of the active lanes.
+template <int kBits>
+__device__ __forceinline__ uint64_t lanes_with_digit_unmasked(uint32_t digit, uint64_t active_lanes) {
+  constexpr uint32_t kOrOfXor = 0xF6;  // v_bitop3 table of a | (b ^ c)
+  constexpr int kNotEqual = 33;        // the integer predicate "ne" of the compare builtin
+  uint32_t differ_lo = 0u, differ_hi = 0u;
+#pragma unroll
+  for (int i = 0; i < kBits; ++i) {
+    const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int>(digit), i, 1));
+    const uint64_t with = __builtin_amdgcn_uicmp(m, 0u, kNotEqual);
+    differ_lo = __builtin_amdgcn_bitop3_b32(differ_lo, static_cast<uint32_t>(with), m, kOrOfXor);
+    differ_hi = __builtin_amdgcn_bitop3_b32(differ_hi, static_cast<uint32_t>(with >> 32), m, kOrOfXor);
+  }
+  return ~((static_cast<uint64_t>(differ_hi) << 32) | differ_lo) & active_lanes;
+}
+
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
@@ -1019,6 +1036,8 @@ __device__ __forceinline__ void wave_match_ranks(DigitOf digit, uint32_t valid, 
     if (r >= rounds) continue;  // wave-uniform: the rounds the wave's span holds
     const bool active = ((valid >> r) & 1u) != 0u;
     const uint32_t d = digit(r);
+    // read first: it follows the previous round's addition in LDS order
+    const uint32_t before = counter[d];
     masks[lane] = 0ull;
     uint32_t group = d;
     if constexpr (kBits > kFineMatchBits) {
@@ -1033,13 +1052,10 @@ __device__ __forceinline__ void wave_match_ranks(DigitOf digit, uint32_t valid, 
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const uint64_t same = masks[group];
     const uint32_t below = lanes_below(same);
-    const uint32_t size = static_cast<uint32_t>(__popcll(same));
-    // digits are masked, so every lane's read is in range; the leader's store
-    // follows the wave's read in LDS order
-    const uint32_t before = counter[d];
-    if (active && below == 0u) counter[d] = before + size;
     rank[r] = before + below;
-    asm volatile("" : "+v"(rank[r]));  // summed here, not held as two registers to the end
+    asm volatile("" : "+v"(rank[r]));  // summed before the addition is issued, which then needs no wait
+    // digits are masked, so every lane's read above was in range
+    if (active && below == 0u) atomicAdd(&counter[d], static_cast<uint32_t>(__popcll(same)));
   }
 }
 
@@ -1060,11 +1076,12 @@ __device__ __forceinline__ void wave_ballot_ranks(DigitOf digit, uint32_t valid,
     const bool active = ((valid >> r) & 1u) != 0u;
     const uint32_t d = digit(r);
     const uint32_t before = counter[d];
-    const uint64_t same = lanes_with_digit<kBits>(d, active);
+    // (an inactive lane's mask is garbage; only active lanes use theirs)
+    const uint64_t same = lanes_with_digit_unmasked<kBits>(d, __ballot(active));
     const uint32_t below = lanes_below(same);
-    if (active && below == 0u) atomicAdd(&counter[d], static_cast<uint32_t>(__popcll(same)));
     rank[r] = before + below;
-    asm volatile("" : "+v"(rank[r]));  // summed here, not held as two registers to the end
+    asm volatile("" : "+v"(rank[r]));  // summed before the addition is issued, which then needs no wait
+    if (active && below == 0u) atomicAdd(&counter[d], static_cast<uint32_t>(__popcll(same)));
   }
 }
 
@@ -1096,6 +1113,21 @@ __device__ __forceinline__ uint32_t block_exclusive_max(uint32_t value, uint32_t
   return max(before, from_lane_below(inclusive, 0u));
 }
 
+// The wave's OR of the range and sortedness flags into wave_flags[wave]
+// (lane 0 writes); after a barrier, wave_or_read gives the workgroup's.
+__device__ __forceinline__ void wave_or_flags(int32_t flags, int32_t* wave_flags) {
+  const int32_t wave_flags_or = (__ballot(flags & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
+                                (__ballot(flags & kFlagUnsorted) ? kFlagUnsorted : 0);
+  if ((threadIdx.x & 63) == 0) wave_flags[threadIdx.x >> 6] = wave_flags_or;
+}
+template <int kT>
+__device__ __forceinline__ int32_t wave_or_read(const int32_t* wave_flags) {
+  int32_t all = 0;
+#pragma unroll
+  for (int w = 0; w < kT / 64; ++w) all |= wave_flags[w];
+  return all;
+}
+
 // One tile: checks, stable grouping by the coarse digit (key >> fine_bits),
 // the grouped packed elements over packed[tile_base, tile_base + in-range
 // count), the row rows[tile][0, buckets) of the buckets' runs in the tile
@@ -1119,6 +1151,7 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
     uint32_t tile_start[kMaxBuckets];
   } tables;
   __shared__ uint32_t wave_totals[kGroupWaves];
+  __shared__ int32_t wave_flags[kGroupWaves];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -1202,9 +1235,8 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kScatterRounds; ++r) rank[r] += ((ok >> r) & 1u) ? counter[digit(r)] : 0u;
-  const int32_t found = (__syncthreads_or(flags & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
-                        (__syncthreads_or(flags & kFlagUnsorted) ? kFlagUnsorted : 0);
-  // (the barriers above: every counter is read before the grouped tile overwrites them)
+  wave_or_flags(flags, wave_flags);
+  __syncthreads();  // every counter is read before the grouped tile overwrites them
 #pragma unroll
   for (int r = 0; r < kScatterRounds; ++r)
     if ((ok >> r) & 1u)
@@ -1212,7 +1244,7 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   uint32_t* row = rows + static_cast<int64_t>(tile) * row_stride;
   for (int b = t; b < buckets; b += kThreads)
     row[b] = tables.tile_start[b] | ((b + 1 < buckets ? tables.tile_start[b + 1] : in_tile) << 16);
-  if (t == 0) tile_flags[tile] = static_cast<uint32_t>(found);
+  if (t == 0) tile_flags[tile] = static_cast<uint32_t>(wave_or_read<kThreads>(wave_flags));
   __syncthreads();
   // the grouped tile, four elements a thread and store while they lie inside the tile
   // (cached stores: the gathers read them next, from the Infinity Cache)
@@ -1255,6 +1287,7 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
   __shared__ uint32_t chunk_start[kFineDigits];
   __shared__ uint32_t target_shift[kFineDigits];
   __shared__ uint32_t wave_totals[kGW];
+  __shared__ int32_t wave_flags[kGW];
   // (not const: the chunk loop rebuilds them, so that nothing derived from the
   // thread index is hoisted out of the loop and held in registers across it)
   int t = threadIdx.x;
@@ -1289,8 +1322,9 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
   // the tiles' flags
   uint32_t local = 0u;
   for (int i = t; i < tiles; i += kGT) local |= tile_flags[i];
-  const int32_t found = (__syncthreads_or(local & kFlagOutOfRange) ? kFlagOutOfRange : 0) |
-                        (__syncthreads_or(local & kFlagUnsorted) ? kFlagUnsorted : 0);
+  wave_or_flags(static_cast<int32_t>(local), wave_flags);
+  __syncthreads();
+  const int32_t found = wave_or_read<kGT>(wave_flags);
   if (blockIdx.x == 0 && t == 0) {
     if (or_status)
       atomicOr(status, found);
