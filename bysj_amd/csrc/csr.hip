@@ -135,6 +135,46 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t value, uint32_
   return before + inclusive - value;
 }
 
+// block_exclusive_scan of two values per thread at once (one pair of
+// barriers): returns the exclusive scan of `first`; `totals` gets both sums.
+// `wave_totals` holds 2 kT / 64 words.  Every thread must call it.
+template <int kT = kThreads>
+__device__ __forceinline__ uint32_t block_exclusive_scan2(uint32_t first, uint32_t second, uint32_t* wave_totals,
+                                                          uint32_t& first_total, uint32_t& second_total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t a = first, b = second;
+  a += dpp_or_zero<0x111, 0xf>(a);
+  b += dpp_or_zero<0x111, 0xf>(b);
+  a += dpp_or_zero<0x112, 0xf>(a);
+  b += dpp_or_zero<0x112, 0xf>(b);
+  a += dpp_or_zero<0x114, 0xf>(a);
+  b += dpp_or_zero<0x114, 0xf>(b);
+  a += dpp_or_zero<0x118, 0xf>(a);
+  b += dpp_or_zero<0x118, 0xf>(b);
+  a += dpp_or_zero<0x142, 0xa>(a);
+  b += dpp_or_zero<0x142, 0xa>(b);
+  a += dpp_or_zero<0x143, 0xc>(a);
+  b += dpp_or_zero<0x143, 0xc>(b);
+  if (lane == 63) {
+    wave_totals[2 * wave] = a;
+    wave_totals[2 * wave + 1] = b;
+  }
+  __syncthreads();
+  uint32_t before = 0, sum_a = 0, sum_b = 0;
+#pragma unroll
+  for (int w = 0; w < kT / 64; ++w) {
+    const uint32_t part = wave_totals[2 * w];
+    before += w < wave ? part : 0u;
+    sum_a += part;
+    sum_b += wave_totals[2 * w + 1];
+  }
+  __syncthreads();
+  first_total = sum_a;
+  second_total = sum_b;
+  return before + a - first;
+}
+
 // In-place exclusive scan of values[0, n) in LDS (plus `base`) by a
 // workgroup of kT threads; returns the total.  Every thread must call it.
 template <int kT = kThreads>
@@ -1141,14 +1181,13 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   // the wave counters, then (once every place is known) the grouped tile
   __shared__ __align__(16) uint32_t sorted[kTile];
   uint32_t* wave_count = sorted;
-  // the match tables while the waves rank, then the bucket starts
+  // the match tables while the waves rank
   struct MatchTables {
     uint8_t leader[kGroupWaves][kMaxBuckets];
     uint64_t masks[kGroupWaves][64 + 1];
   };
-  __shared__ union {
+  __shared__ struct {
     MatchTables match;
-    uint32_t tile_start[kMaxBuckets];
   } tables;
   __shared__ uint32_t wave_totals[kGroupWaves];
   __shared__ int32_t wave_flags[kGroupWaves];
@@ -1223,15 +1262,35 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   for (int r = 0; r < kScatterRounds; ++r) asm volatile("" : "+v"(key[r]));
   asm volatile("" : "+v"(ok));
   __syncthreads();
-  wave_prefix(wave_count, kMaxBuckets, buckets, tables.tile_start);
-  __syncthreads();
-  const uint32_t in_tile = lds_exclusive_scan(tables.tile_start, buckets, 0u, wave_totals);
-  // every wave counter += its digit's start in the tile: one read per element below
-  // (digits past `buckets` hold no element; their sums are never read)
-  for (int i = t; i < kGroupWaves * kMaxBuckets / 4; i += kThreads) {
-    u32x4* four = reinterpret_cast<u32x4*>(wave_count) + i;
-    *four += reinterpret_cast<const u32x4*>(tables.tile_start)[i % (kMaxBuckets / 4)];
+  // Thread t takes digits 2t and 2t + 1 (digits past `buckets` count nothing):
+  // their counts in every wave, scanned over the digits and then the waves,
+  // become in place the place of each wave's first element of the digit in
+  // the grouped tile, and the digits' runs go to the tile's row.
+  static_assert(kMaxBuckets == 2 * kThreads, "two digits a thread");
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  u32x2v* pairs = reinterpret_cast<u32x2v*>(wave_count);
+  u32x2v counts[kGroupWaves];
+  uint32_t total0 = 0u, total1 = 0u;
+#pragma unroll
+  for (int w = 0; w < kGroupWaves; ++w) {
+    counts[w] = pairs[w * (kMaxBuckets / 2) + t];
+    total0 += counts[w].x;
+    total1 += counts[w].y;
   }
+  uint32_t in_tile = 0u;
+  const uint32_t start0 = block_exclusive_scan(total0 + total1, wave_totals, in_tile);
+  const uint32_t start1 = start0 + total0;
+  uint32_t run0 = start0, run1 = start1;
+#pragma unroll
+  for (int w = 0; w < kGroupWaves; ++w) {
+    const u32x2v place = {run0, run1};
+    pairs[w * (kMaxBuckets / 2) + t] = place;
+    run0 += counts[w].x;
+    run1 += counts[w].y;
+  }
+  uint32_t* row = rows + static_cast<int64_t>(tile) * row_stride;
+  if (2 * t < buckets) row[2 * t] = start0 | (start1 << 16);
+  if (2 * t + 1 < buckets) row[2 * t + 1] = start1 | ((start1 + total1) << 16);
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kScatterRounds; ++r) rank[r] += ((ok >> r) & 1u) ? counter[digit(r)] : 0u;
@@ -1241,9 +1300,6 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   for (int r = 0; r < kScatterRounds; ++r)
     if ((ok >> r) & 1u)
       sorted[rank[r]] = (static_cast<uint32_t>(tile_base + first + 64 * r) << fine_bits) | (key[r] & fine_mask);
-  uint32_t* row = rows + static_cast<int64_t>(tile) * row_stride;
-  for (int b = t; b < buckets; b += kThreads)
-    row[b] = tables.tile_start[b] | ((b + 1 < buckets ? tables.tile_start[b + 1] : in_tile) << 16);
   if (t == 0) tile_flags[tile] = static_cast<uint32_t>(wave_or_read<kThreads>(wave_flags));
   __syncthreads();
   // the grouped tile, four elements a thread and store while they lie inside the tile
@@ -1286,7 +1342,7 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
   __shared__ uint32_t fine_base[kFineDigits];
   __shared__ uint32_t chunk_start[kFineDigits];
   __shared__ uint32_t target_shift[kFineDigits];
-  __shared__ uint32_t wave_totals[kGW];
+  __shared__ uint32_t wave_totals[2 * kGW];
   __shared__ int32_t wave_flags[kGW];
   // (not const: the chunk loop rebuilds them, so that nothing derived from the
   // thread index is hoisted out of the loop and held in registers across it)
@@ -1338,8 +1394,7 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
   }
   if (!has_bucket) return;
   uint32_t count = 0u, bucket_start = 0u;
-  uint32_t placed = block_exclusive_scan<kGT>(sum_length, wave_totals, count);
-  block_exclusive_scan<kGT>(sum_start, wave_totals, bucket_start);
+  uint32_t placed = block_exclusive_scan2<kGT>(sum_length, sum_start, wave_totals, count, bucket_start);
   uint32_t run_delta[kRunsPerThread];
 #pragma unroll
   for (int i = 0; i < kRunsPerThread; ++i) {
@@ -1484,6 +1539,7 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
       if (target >= bucket_start && target < end)
         __builtin_nontemporal_store(static_cast<int64_t>(e >> fine_bits), order + target);
     }
+    if (c0 + kChunk >= count) break;  // the last chunk: nothing follows it
     __syncthreads();
     // the next chunk's elements of digit f follow this chunk's; the wave counters restart
     for (int f = t; f < fines; f += kGT) {
