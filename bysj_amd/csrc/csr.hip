@@ -105,6 +105,20 @@ __device__ __forceinline__ uint32_t dpp_or_zero(uint32_t value) {
   return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(value), kCtrl, kRowMask, 0xf, true));
 }
 
+// Inclusive scan of one value per lane over the wave on the VALU: row_shr 1,
+// 2, 4, 8 scan each row of 16 lanes; row_bcast:15 adds lane 15's total to row
+// 1 (and lane 47's to row 3), row_bcast:31 adds lane 31's to rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t value) {
+  uint32_t inclusive = value;
+  inclusive += dpp_or_zero<0x111, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x112, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x114, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x118, 0xf>(inclusive);
+  inclusive += dpp_or_zero<0x142, 0xa>(inclusive);
+  inclusive += dpp_or_zero<0x143, 0xc>(inclusive);
+  return inclusive;
+}
+
 // Exclusive scan of one value per thread over a workgroup of kT threads;
 // `total` gets the sum.  Every thread must call it.
 template <int kT = kThreads>
@@ -1508,23 +1522,38 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) asm volatile("" : "+v"(value[r]));
     __syncthreads();
-    wave_prefix<kGT>(wave_base, kFineDigits, fines, chunk_start);
+    if (wave == 0) {
+      // lane f: fine digit f (digits past `fines` count nothing).  Its counts in
+      // every wave, scanned over the digits (within the wave) and then over the
+      // waves, become the place of each wave's first element of the digit.
+      static_assert(kFineDigits == 64, "one lane a fine digit");
+      uint32_t counts[kGW], total = 0u;
+#pragma unroll
+      for (int w = 0; w < kGW; ++w) {
+        counts[w] = wave_base[w * kFineDigits + lane];
+        total += counts[w];
+      }
+      const uint32_t start = wave_inclusive_scan(total) - total;
+      uint32_t running = start;
+#pragma unroll
+      for (int w = 0; w < kGW; ++w) {
+        wave_base[w * kFineDigits + lane] = running;
+        running += counts[w];
+      }
+      chunk_start[lane] = start;
+      // a bucket of one chunk: its digit counts are the histogram
+      const uint32_t base = one_chunk ? bucket_start + start : fine_base[lane];
+      fine_base[lane] = base;
+      target_shift[lane] = base - start;
+    }
     __syncthreads();
-    lds_exclusive_scan<kGT>(chunk_start, fines, 0u, wave_totals);
-    // each wave's first place of every digit: the digit's start in the chunk plus the earlier waves' elements
-    for (int i = t; i < kGW * kFineDigits; i += kGT) wave_base[i] += chunk_start[i % kFineDigits];
     if (one_chunk) {
-      // the chunk is the bucket: its digit counts are the histogram
-      for (int f = t; f < fines; f += kGT) fine_base[f] = bucket_start + chunk_start[f];
-      __syncthreads();
       write_offsets();
       if (order == nullptr) return;
     }
-    for (int f = t; f < fines; f += kGT) target_shift[f] = fine_base[f] - chunk_start[f];
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) rank[r] += ((valid >> r) & 1u) ? counter[fine(r)] : 0u;
-    __syncthreads();  // the marks are read before the sorted chunk overwrites them
+    // (the marks were all read before the ranking's barriers: the sorted chunk may overwrite them)
     uint32_t* sorted = mark;
 #pragma unroll
     for (int r = 0; r < kRounds; ++r)
