@@ -199,37 +199,41 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
   int row_of[PPL][MAXR];
   int count[PPL];
   int64_t radial_col[PPL], chunk_col[PPL];
+  // (a lambda: the edge loop's row-broadcast path rebuilds the rows after the loop)
+  const auto plan_pairs = [&](int who) {
 #pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int p = lane + 64 * j;
-    const int group = p / row_chunks;
-    const int c = p - group * row_chunks;
-    int slot = -1, part = 0, first = 0;
-    for (int t = 0; t < slots; ++t) {
-      const int groups = (__builtin_amdgcn_readlane(rows_of_lane_slot, t) + group_rows - 1) / group_rows;
-      if (group >= first && group < first + groups) {
-        slot = t;
-        part = group - first;
+    for (int j = 0; j < PPL; ++j) {
+      const int p = who + 64 * j;
+      const int group = p / row_chunks;
+      const int c = p - group * row_chunks;
+      int slot = -1, part = 0, first = 0;
+      for (int t = 0; t < slots; ++t) {
+        const int groups = (__builtin_amdgcn_readlane(rows_of_lane_slot, t) + group_rows - 1) / group_rows;
+        if (group >= first && group < first + groups) {
+          slot = t;
+          part = group - first;
+        }
+        first += groups;
       }
-      first += groups;
-    }
-    radial_col[j] = slot >= 0 ? static_cast<int64_t>(slot) * channels + c * 4 : 0;
-    chunk_col[j] = c * 4;
-    count[j] = 0;
+      radial_col[j] = slot >= 0 ? static_cast<int64_t>(slot) * channels + c * 4 : 0;
+      chunk_col[j] = c * 4;
+      count[j] = 0;
 #pragma unroll
-    for (int k = 0; k < MAXR; ++k) row_of[j][k] = 0;
-    int seen = 0;
-    for (int r = 0; r < rows; ++r) {
-      const bool reads = slot >= 0 && radial_slot[r] == slot;
-      const int k = seen - part * group_rows;
-      const bool mine = reads && k >= 0 && k < group_rows;
+      for (int k = 0; k < MAXR; ++k) row_of[j][k] = 0;
+      int seen = 0;
+      for (int r = 0; r < rows; ++r) {
+        const bool reads = slot >= 0 && radial_slot[r] == slot;
+        const int k = seen - part * group_rows;
+        const bool mine = reads && k >= 0 && k < group_rows;
 #pragma unroll
-      for (int kk = 0; kk < MAXR; ++kk)
-        if (mine && k == kk) row_of[j][kk] = r;
-      count[j] += mine ? 1 : 0;
-      seen += reads ? 1 : 0;
+        for (int kk = 0; kk < MAXR; ++kk)
+          if (mine && k == kk) row_of[j][kk] = r;
+        count[j] += mine ? 1 : 0;
+        seen += reads ? 1 : 0;
+      }
     }
-  }
+  };
+  plan_pairs(lane);
 
   fvec<4> acc[PPL][MAXR];
 #pragma unroll
@@ -296,6 +300,12 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
     }
   }
 
+  if constexpr (kRowBcast) {
+    // (the rows of each pair rebuilt here rather than held in registers through the edge loop)
+    int again = lane;
+    asm volatile("" : "+v"(again));
+    plan_pairs(again);
+  }
   const float scale = inv[node];
   float* node_out = out + node * (n_rows + 1) * channels;
 #pragma unroll
