@@ -3,7 +3,15 @@
 //
 // Restates python/kernels/segment.py:46-71 of the reference
 // (segment_offsets = [0] ++ cumsum(bincount(keys)), group_by_source = stable
-// argsort + offsets) as a bounded-key counting sort, written for wave64:
+// argsort + offsets) as a bounded-key counting sort, written for wave64.
+// Keys of up to 20 bits take two levels: a coarse digit (the key's high bits,
+// at most 1024 buckets) and a fine digit (its low bits).
+//
+// Packed 32-bit elements with fine digits of at most 6 bits and at most 1024
+// tiles (N <= 2^16 and E <= 2^23) take two launches: tile_group_kernel groups
+// each tile by the coarse digit in place and writes its row of runs, and
+// bucket_gather_kernel gathers each bucket's runs and ranks them by the fine
+// digit (the section "grouped two-level path" below).  Other shapes take four:
 //
 //   count     one pass over the int64 keys in tiles of 8192: the range and
 //             sortedness checks (the reference's dst.min()/dst.max() test),
