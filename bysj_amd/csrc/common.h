@@ -276,6 +276,22 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const fvec<N>& 
 // the same kernel (outputs of [E, C] size).
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Non-temporal load of rows read once, so that they do not displace lines
+// the kernel reads again (per-edge scales gathered through an order, the
+// order itself, offsets).
+template <int N>
+__device__ __forceinline__ fvec<N> load_vec_stream(const float* __restrict__ p) {
+  if constexpr (N == 4) {
+    const f32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return fvec<4>{{raw.x, raw.y, raw.z, raw.w}};
+  } else {
+    fvec<N> out;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out.v[i] = __builtin_nontemporal_load(p + i);
+    return out;
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void store_vec_stream(float* __restrict__ p, const fvec<N>& value) {
   if constexpr (N == 4) {

@@ -12,7 +12,11 @@
 // each element sequentially (product rounded, then added), normalising once
 // after the sum.  The node's [R, C] accumulator never leaves registers, the
 // output is written once, and the result equals the sequential fp32 chain
-// `gather -> mul -> index_add_ -> mul` bit for bit.
+// `gather -> mul -> index_add_ -> mul` bit for bit.  The forward kernels load
+// the radial rows non-temporally: each is read once, and keeping them out of
+// the caches' normal replacement made the [E, 16, 64] forward 5% (fused with
+// RMSNorm 8%) faster; the backward kernels keep ordinary loads, which were
+// equal or faster there.
 //
 // Backward is node-parallel as well.  It recomputes the unnormalised sum for
 // the inverse-degree gradient in the same pass that reads radial/zonal for
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
       for (int j = 0; j < CPL; ++j) {
         if (live[j] && (!kOrdered || edge[u] >= 0)) {
           z[u][j] = zonal[edge[u] * n_rows + zonal_col[j]];
-          x[u][j] = load_vec<V>(radial + edge[u] * edge_stride + radial_col[j]);
+          x[u][j] = load_vec_stream<V>(radial + edge[u] * edge_stride + radial_col[j]);
         } else {
           z[u][j] = 0.0f;
 #pragma unroll
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(kBlock) void gie_forward_kernel(
     for (int j = 0; j < CPL; ++j) {
       if (!live[j]) continue;
       const float zv = zonal[e * n_rows + zonal_col[j]];
-      const fvec<V> xv = load_vec<V>(radial + e * edge_stride + radial_col[j]);
+      const fvec<V> xv = load_vec_stream<V>(radial + e * edge_stride + radial_col[j]);
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + zv * xv.v[i];
     }
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(kBlock) void gie_forward_shared_kernel(
 #pragma unroll
       for (int j = 0; j < ZQ; ++j) zq[u][j] = zonal[edge[u] * n_rows + zonal_row[j]];
 #pragma unroll
-      for (int j = 0; j < PPL; ++j) x[u][j] = load_vec<4>(radial + edge[u] * edge_stride + radial_col[j]);
+      for (int j = 0; j < PPL; ++j) x[u][j] = load_vec_stream<4>(radial + edge[u] * edge_stride + radial_col[j]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -399,7 +403,7 @@ __global__ __launch_bounds__(kBlock) void gie_rmsnorm_forward_kernel(
       for (int j = 0; j < CPL; ++j) {
         if (live[j] && (!kOrdered || edge[u] >= 0)) {
           z[u][j] = zonal[edge[u] * n_rows + zonal_col[j]];
-          x[u][j] = load_vec<V>(radial + edge[u] * edge_stride + radial_col[j]);
+          x[u][j] = load_vec_stream<V>(radial + edge[u] * edge_stride + radial_col[j]);
         } else {
           z[u][j] = 0.0f;
 #pragma unroll
@@ -422,7 +426,7 @@ __global__ __launch_bounds__(kBlock) void gie_rmsnorm_forward_kernel(
     for (int j = 0; j < CPL; ++j) {
       if (!live[j]) continue;
       const float zv = zonal[e * n_rows + zonal_col[j]];
-      const fvec<V> xv = load_vec<V>(radial + e * edge_stride + radial_col[j]);
+      const fvec<V> xv = load_vec_stream<V>(radial + e * edge_stride + radial_col[j]);
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[j].v[i] = acc[j].v[i] + zv * xv.v[i];
     }

@@ -57,7 +57,9 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
     for (int i = 0; i < V; ++i) acc[j].v[i] = 0.0f;
 
   // U slots per round, all loads of a round issued before any add; the adds
-  // then run in slot order, so each element is a sequential sum.
+  // then run in slot order, so each element is a sequential sum.  Rows are
+  // read once and loaded non-temporally, which keeps the lines of the order
+  // and of the gathered edge scales cached for the neighbouring slots.
   for (int64_t slot = begin; slot < end; slot += U) {
     int64_t edge[U];
     float weight[U];
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum_forward_kernel(
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         if (live[j] && ok) {
-          x[u][j] = load_vec<V>(src + edge[u] * channels + column[j]);
+          x[u][j] = load_vec_stream<V>(src + edge[u] * channels + column[j]);
         } else {
 #pragma unroll
           for (int i = 0; i < V; ++i) x[u][j].v[i] = 0.0f;
