@@ -344,23 +344,30 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t value) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Cache policy of buffer loads and stores: 0 the default, kNonTemporal for
+// data read or written once.
+constexpr int kNonTemporal = 2;
+
+template <int kPolicy = 0>
 __device__ __forceinline__ float buffer_load_f32(BufferView view, uint32_t offset) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(view, static_cast<int>(offset), 0, 0));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_raw_buffer_load_b32(view, static_cast<int>(offset), 0, kPolicy));
 }
 
-template <int N>
+template <int N, int kPolicy = 0>
 __device__ __forceinline__ fvec<N> buffer_load_vec(BufferView view, uint32_t offset) {
   fvec<N> out;
   if constexpr (N == 4) {
     const f32x4 raw = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(offset),
-                                                                                        0, 0));
+                                                                                        0, kPolicy));
     out.v[0] = raw.x;
     out.v[1] = raw.y;
     out.v[2] = raw.z;
     out.v[3] = raw.w;
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) out.v[i] = buffer_load_f32(view, offset == kNoRow ? kNoRow : offset + 4u * i);
+    for (int i = 0; i < N; ++i)
+      out.v[i] = buffer_load_f32<kPolicy>(view, offset == kNoRow ? kNoRow : offset + 4u * i);
   }
   return out;
 }
@@ -368,7 +375,6 @@ __device__ __forceinline__ fvec<N> buffer_load_vec(BufferView view, uint32_t off
 // Non-temporal (cache policy nt) store of N floats; dropped at kNoRow.
 template <int N>
 __device__ __forceinline__ void buffer_store_vec_stream(BufferView view, uint32_t offset, const fvec<N>& value) {
-  constexpr int kNonTemporal = 2;
   if constexpr (N == 4) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const f32x4 raw = {value.v[0], value.v[1], value.v[2], value.v[3]};

@@ -136,7 +136,8 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_backward_kernel(
   }
 
   // Rows wave_id, wave_id + waves, ... two per round: both rows' loads are
-  // issued before either is reduced.
+  // issued before either is reduced.  The rows are read once and loaded
+  // non-temporally (config 3R: 261 -> 247 us).
   for (int64_t first = wave_id; first < rows; first += 2 * waves) {
     fvec<V> g[2][CPL], xv[2][CPL];
     float inv[2];
@@ -149,8 +150,8 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_backward_kernel(
       for (int j = 0; j < CPL; ++j) {
         const int64_t q = lane + 64 * j;
         if (ok && q < chunks) {
-          g[r][j] = load_vec<V>(grad + row * width + q * V);
-          xv[r][j] = load_vec<V>(x + row * width + q * V);
+          g[r][j] = load_vec_stream<V>(grad + row * width + q * V);
+          xv[r][j] = load_vec_stream<V>(x + row * width + q * V);
         } else {
 #pragma unroll
           for (int i = 0; i < V; ++i) g[r][j].v[i] = xv[r][j].v[i] = 0.0f;

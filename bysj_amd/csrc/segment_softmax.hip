@@ -352,9 +352,12 @@ __device__ __forceinline__ void forward_loads(const ForwardArgs& a, const Tiles<
   if constexpr (!kOrdered) {
     const BufferView logit = row_view(a.logit, t.base, a.n_edges, a.channels);
     const BufferView env = row_view(a.env, t.base, a.n_edges, 1);
+    // Logit rows are read once and loaded non-temporally (config 2: 14.3 ->
+    // 13.7 us, 2R: 138 -> 127 us); the envelope loads keep the default
+    // policy, which was faster for them.
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const fvec<V> x = buffer_load_vec<V>(logit, t.at(i));
+      const fvec<V> x = buffer_load_vec<V, kNonTemporal>(logit, t.at(i));
       envelope[i] = buffer_load_f32(env, t.scalar_at(i));
 #pragma unroll
       for (int v = 0; v < V; ++v) value[i][v] = x.v[v];
@@ -364,7 +367,7 @@ __device__ __forceinline__ void forward_loads(const ForwardArgs& a, const Tiles<
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int64_t e = t.e[i] >= 0 ? t.e[i] : 0;
-      const fvec<V> x = load_vec<V>(a.logit + e * a.channels + column);
+      const fvec<V> x = load_vec_stream<V>(a.logit + e * a.channels + column);
       const float env = a.env[e];
       envelope[i] = t.e[i] >= 0 ? env : 0.0f;
 #pragma unroll
@@ -720,13 +723,14 @@ __device__ __forceinline__ Tiles<R, STEP, kOrdered> backward_tiles(const Backwar
     const BufferView alpha = row_view(a.alpha, t.base, a.n_edges, a.channels);
     const BufferView grad = row_view(a.grad_alpha, t.base, a.n_edges, a.channels);
     const BufferView env = row_view(a.env, t.base, a.n_edges, 1);
-    // envelopes first: they are consumed last, after the row sums
+    // envelopes first: they are consumed last, after the row sums.  The rows
+    // are read once and loaded non-temporally (config 2R: 222 -> 200 us).
 #pragma unroll
     for (int i = 0; i < R; ++i) envelope[i] = buffer_load_f32(env, t.scalar_at(i));
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const fvec<V> xv = buffer_load_vec<V>(alpha, t.at(i));
-      const fvec<V> gv = buffer_load_vec<V>(grad, t.at(i));
+      const fvec<V> xv = buffer_load_vec<V, kNonTemporal>(alpha, t.at(i));
+      const fvec<V> gv = buffer_load_vec<V, kNonTemporal>(grad, t.at(i));
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         x[i][v] = xv.v[v];
@@ -741,8 +745,8 @@ __device__ __forceinline__ Tiles<R, STEP, kOrdered> backward_tiles(const Backwar
 #pragma unroll
       for (int i = 0; i < R; ++i) {
         const int64_t e = t.e[i] >= 0 ? t.e[i] : 0;
-        const fvec<V> xv = load_vec<V>(a.alpha + e * a.channels + column);
-        const fvec<V> gv = load_vec<V>(a.grad_alpha + e * a.channels + column);
+        const fvec<V> xv = load_vec_stream<V>(a.alpha + e * a.channels + column);
+        const fvec<V> gv = load_vec_stream<V>(a.grad_alpha + e * a.channels + column);
         const float env = a.env[e];
         const bool has = t.e[i] >= 0;
         envelope[i] = has ? env : 0.0f;
