@@ -640,7 +640,7 @@ def stream_ceilings(read_bytes: int, write_bytes: int, steps: int) -> dict:
     """Read-only and copy rates of plain streams on this part, and a copy of one operator's bytes.
 
     1 GiB read-only and copy passes (dpa4k_stream_calibrate: grid-stride, four 16-byte chunks per
-    thread per round), then a copy that reads `read_bytes` and writes `write_bytes`, rotated
+    thread per round, non-temporal loads and stores), then a copy that reads `read_bytes` and writes `write_bytes`, rotated
     through 1 GiB of distinct sources like the operator lines.  Same graph-replay timing.
     """
     import torch
