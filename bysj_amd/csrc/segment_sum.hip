@@ -263,8 +263,8 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
       const int item = t + k * kBlock;
       const int row = item / chunks;
       const int64_t e = item < items ? edge_of<kOrdered>(order, first + row, n_edges) : -1;
-      if (e >= 0) {
-        x[k] = load_vec<4>(src + e * channels + static_cast<int64_t>(item - row * chunks) * 4);
+      if (e >= 0) {  // rows are read once: non-temporal (config 1: 7.6 -> 7.25 us)
+        x[k] = load_vec_stream<4>(src + e * channels + static_cast<int64_t>(item - row * chunks) * 4);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[k].v[i] = 0.0f;
