@@ -504,10 +504,18 @@ bool small_grid(int64_t n_nodes, int group) { return n_nodes * group / 64 < 2048
 // from HBM than more, shorter ones at the same bytes in flight (config 1R,
 // C = 128: 954 us against 1022 us with 8 slots, at 2 waves per SIMD against
 // 4); rows named by `order` are scattered, and there the occupancy wins
-// (1184 us with 8 slots against 1594 us with 32).
+// (1184 us with 8 slots against 1594 us with 32; 4 slots, below, better still).
 template <int V, int CPL>
 constexpr int contiguous_unroll_for() {
   return CPL * V >= 8 ? unroll_for<V, CPL>(false) : 32;
+}
+
+// Rows gathered through an order, narrow rows: 4 slots a round (config 1R
+// with scales through a shuffled order: 1,117 us against 1,135 us with 8 and
+// 1,228 us with 16).
+template <int V, int CPL>
+constexpr int ordered_unroll_for() {
+  return CPL * V >= 8 ? unroll_for<V, CPL>(false) : 4;
 }
 
 template <int V, int G, int CPL>
@@ -522,8 +530,8 @@ int launch_forward(const float* src, const int64_t* offsets, const float* edge_s
     return launch_forward_u<V, G, CPL, contiguous_unroll_for<V, CPL>()>(src, offsets, edge_scale, node_scale,
                                                                         order, out, n_edges, n_nodes, channels,
                                                                         chunk_base, stream);
-  return launch_forward_u<V, G, CPL, unroll_for<V, CPL>(false)>(src, offsets, edge_scale, node_scale, order, out,
-                                                                n_edges, n_nodes, channels, chunk_base, stream);
+  return launch_forward_u<V, G, CPL, ordered_unroll_for<V, CPL>()>(src, offsets, edge_scale, node_scale, order, out,
+                                                                   n_edges, n_nodes, channels, chunk_base, stream);
 }
 
 template <int V, int G, int CPL, int U>
