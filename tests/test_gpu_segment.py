@@ -116,6 +116,15 @@ def test_counting_sort_bucket_chunks(edges, nodes):
     _check_grouping_against_numpy(keys, nodes, f"chunks E={edges} N={nodes}")
 
 
+@pytest.mark.parametrize("edges,nodes", [(8_388_609, 2**16), (9_000_000, 4096)])
+def test_counting_sort_past_the_grouped_tile_limit(edges, nodes):
+    """Keys that the grouped path would take (at most 6 fine bits) but in more tiles than it handles
+    (1,024 tiles of 8,192 keys): the four-launch build, one key past the limit and well past it."""
+    announce("counting sort: past the grouped tile limit", edges, nodes)
+    keys = workloads.rng(edges % 991 + nodes).integers(0, nodes, size=edges).astype(np.int64)
+    _check_grouping_against_numpy(keys, nodes, f"four-launch E={edges} N={nodes}")
+
+
 def test_group_by_key_async_status_and_capture():
     """The asynchronous build reports the status bits on the device, allocates nothing when given its
     buffers, and replays from a HIP graph with the same result as the synchronous call."""
