@@ -105,11 +105,12 @@ def test_counting_sort_skewed_and_sparse_keys():
     _check_grouping_against_numpy(np.array([0, 9_999_999], dtype=np.int64), 10_000_000, "two keys, ends")
 
 
-@pytest.mark.parametrize("edges,nodes", [(700_000, 128), (800_000, 128), (6_300_000, 2**16)])
+@pytest.mark.parametrize("edges,nodes", [(700_000, 128), (800_000, 128), (6_300_000, 2**16), (8_388_608, 2**16)])
 def test_counting_sort_bucket_chunks(edges, nodes):
     """Buckets that average just under and just over 95% of the gather's 6144-element chunk (the two
     chunk sizes of the grouped path), and config-4-sized buckets past it, with one bucket pushed over
-    the chunk so that it takes the multi-chunk path beside ones that do not."""
+    the chunk so that it takes the multi-chunk path beside ones that do not; the last case fills every
+    one of the grouped path's 1,024 tiles."""
     announce("counting sort: bucket chunks", edges, nodes)
     keys = workloads.rng(edges % 997 + nodes).integers(0, nodes, size=edges).astype(np.int64)
     keys[: edges // 64] = 5
