@@ -1216,7 +1216,9 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const unsigned int tile = xcd_block(blockIdx.x, gridDim.x);
+  // tiles in launch order, dealt round-robin over the XCDs: the key stream ran 1 us faster at config 4
+  // than with each XCD taking a contiguous range of tiles
+  const unsigned int tile = blockIdx.x;
   const int64_t tile_base = static_cast<int64_t>(tile) * kTile;
   const int64_t rest = n - tile_base;
   const int n_tile = static_cast<int>(rest > kTile ? kTile : rest);
