@@ -145,6 +145,10 @@ def time_steps(step, n_sets: int, steps: int, warmup: int, *, graph: bool = True
             for i in range(steps):
                 keep.append(step(i % n_sets))
         torch.cuda.synchronize()
+        # one untimed replay first: a graph's first launch also uploads it (about 7-10 us for the
+        # headline's 20-step graph, 0.3-0.5 us a step); the timed replay then runs the same K steps
+        hip_graph.replay()
+        torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         hip_graph.replay()
