@@ -7,8 +7,8 @@
 // Keys of up to 20 bits take two levels: a coarse digit (the key's high bits,
 // at most 1024 buckets) and a fine digit (its low bits).
 //
-// Packed 32-bit elements with fine digits of at most 6 bits and at most 1024
-// tiles (N <= 2^16 and E <= 2^23) take two launches: tile_group_kernel groups
+// Packed 32-bit elements with fine digits of at most 7 bits and at most 2048
+// tiles (N <= 2^17 and E <= 2^24) take two launches: tile_group_kernel groups
 // each tile by the coarse digit in place and writes its row of runs, and
 // bucket_gather_kernel gathers each bucket's runs and ranks them by the fine
 // digit (the section "grouped two-level path" below).  Other shapes take four:
@@ -1038,8 +1038,9 @@ __global__ __launch_bounds__(kThreads, 2) void finish_private_kernel(
 // grouped two-level path: tile-local grouping, then bucket gathers
 // ---------------------------------------------------------------------------
 //
-// For packed 32-bit elements, fine digits of at most 6 bits and at most
-// kMaxRunTiles tiles the two-level sort takes two launches instead of four:
+// For packed 32-bit elements, fine digits of at most kGroupedFineBits (7) bits
+// and at most kMaxRunTiles (2048) tiles the two-level sort takes two launches
+// instead of four:
 //
 //   group   one workgroup per tile: the range and sortedness checks, then the
 //           tile's in-range elements grouped stably by the coarse digit and
@@ -1060,12 +1061,15 @@ __global__ __launch_bounds__(kThreads, 2) void finish_private_kernel(
 //
 // The group ranks with wave_match_ranks (the lanes of equal coarse digits
 // found through LDS words instead of one ballot per digit bit), the gather
-// with wave_ballot_ranks (six ballots for the fine digit).
+// with wave_ballot_ranks (one ballot per fine digit bit).  The gather is
+// instantiated for 64 or 128 fine digits and 1024 or 2048 tiles; the wider
+// instances hold more per thread and spill a few registers, still well ahead
+// of the four launches (a config-4R source list, N = 131,072 and 11.9M
+// edges: 116 against 155 us).
 
-constexpr int kMaxRunTiles = 1024;                    // tiles one gather holds (edges up to 2^23)
-constexpr int kRunTilesPerThread = kMaxRunTiles / kThreads;
-constexpr int kFineMatchBits = 6;                     // fine digits a gather ranks
-constexpr int kFineDigits = 1 << kFineMatchBits;
+constexpr int kMaxRunTiles = 2048;                    // tiles a gather holds (edges up to 2^24)
+constexpr int kFineMatchBits = 6;                     // digits that name their own LDS mask word
+constexpr int kGroupedFineBits = 7;                   // fine digits a gather ranks (at most)
 // A gather's workgroup and the elements it ranks at once: 6144 at eight waves
 // per SIMD (four gathers per CU, so 1024 buckets run in one round) when the
 // buckets average at most 95% of that, else 8192 at six (three per CU).  A
@@ -1345,7 +1349,7 @@ __global__ __launch_bounds__(kThreads, 6) void tile_group_kernel(const int64_t* 
 // over the run starts, each marked with delta + 1, gives every position of the
 // chunk its source.  Buckets of more than one chunk count their fine digits in
 // a gather pass of their own first.
-template <int kGT, int kChunk, int kMinWaves>
+template <int kGT, int kChunk, int kMinWaves, int kFB, int kTiles>
 __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
     const uint32_t* __restrict__ packed, const uint32_t* __restrict__ rows, int64_t row_stride,
     const uint32_t* __restrict__ tile_flags, int tiles, int buckets, int fine_bits,
@@ -1354,7 +1358,9 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
   constexpr int kGW = kGT / 64;                            // waves of the workgroup
   constexpr int kRounds = kChunk / kGW / 64;          // rounds of the longest span
   constexpr int kMarks = kChunk / kGT;                // positions a thread scans
-  constexpr int kRunsPerThread = kMaxRunTiles / kGT;
+  constexpr int kRunsPerThread = kTiles / kGT;
+  constexpr int kFineDigits = 1 << kFB;               // fine digits of the instance (64 or 128)
+  static_assert(kFineDigits % 64 == 0 && kTiles <= kMaxRunTiles, "whole waves of digits; tiles held");
   using Gaps = GapListOf<kGT>;
   constexpr size_t kRegion = kChunk * sizeof(uint32_t) > sizeof(Gaps) ? kChunk * sizeof(uint32_t)
                                                                               : sizeof(Gaps);
@@ -1528,33 +1534,40 @@ __global__ __launch_bounds__(kGT, kMinWaves) void bucket_gather_kernel(
     uint32_t* counter = wave_base + wave * kFineDigits;
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) rank[r] = 0u;
-    wave_ballot_ranks<kFineMatchBits, kRounds>(fine, valid, counter, rank, span_rounds(in_chunk));
+    wave_ballot_ranks<kFB, kRounds>(fine, valid, counter, rank, span_rounds(in_chunk));
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) asm volatile("" : "+v"(value[r]));
     __syncthreads();
     if (wave == 0) {
-      // lane f: fine digit f (digits past `fines` count nothing).  Its counts in
-      // every wave, scanned over the digits (within the wave) and then over the
-      // waves, become the place of each wave's first element of the digit.
-      static_assert(kFineDigits == 64, "one lane a fine digit");
-      uint32_t counts[kGW], total = 0u;
+      // lane l: fine digits f = l + 64 h (digits past `fines` count nothing).
+      // Their counts in every wave, scanned over the digits (within the wave,
+      // then after the previous group of 64) and then over the waves, become
+      // the place of each wave's first element of the digit.
+      uint32_t carry = 0u;
 #pragma unroll
-      for (int w = 0; w < kGW; ++w) {
-        counts[w] = wave_base[w * kFineDigits + lane];
-        total += counts[w];
-      }
-      const uint32_t start = wave_inclusive_scan(total) - total;
-      uint32_t running = start;
+      for (int h = 0; h < kFineDigits / 64; ++h) {
+        const int f = 64 * h + lane;
+        uint32_t counts[kGW], total = 0u;
 #pragma unroll
-      for (int w = 0; w < kGW; ++w) {
-        wave_base[w * kFineDigits + lane] = running;
-        running += counts[w];
+        for (int w = 0; w < kGW; ++w) {
+          counts[w] = wave_base[w * kFineDigits + f];
+          total += counts[w];
+        }
+        const uint32_t inclusive = wave_inclusive_scan(total);
+        const uint32_t start = carry + inclusive - total;
+        carry += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inclusive), 63));
+        uint32_t running = start;
+#pragma unroll
+        for (int w = 0; w < kGW; ++w) {
+          wave_base[w * kFineDigits + f] = running;
+          running += counts[w];
+        }
+        chunk_start[f] = start;
+        // a bucket of one chunk: its digit counts are the histogram
+        const uint32_t base = one_chunk ? bucket_start + start : fine_base[f];
+        fine_base[f] = base;
+        target_shift[f] = base - start;
       }
-      chunk_start[lane] = start;
-      // a bucket of one chunk: its digit counts are the histogram
-      const uint32_t base = one_chunk ? bucket_start + start : fine_base[lane];
-      fine_base[lane] = base;
-      target_shift[lane] = base - start;
     }
     __syncthreads();
     if (one_chunk) {
@@ -1661,7 +1674,7 @@ struct Plan {
       buckets = static_cast<int>((nodes + (int64_t(1) << fine_bits) - 1) >> fine_bits);
       wide = edges > 0 && ((static_cast<uint64_t>(edges) - 1) << fine_bits) > 0xffffffffull;
       narrow_elements = bits <= 19;
-      grouped = !wide && fine_bits <= kFineMatchBits && tiles <= kMaxRunTiles;
+      grouped = !wide && fine_bits <= kGroupedFineBits && tiles <= kMaxRunTiles;
     } else {
       passes = (bits + kDigitBits - 1) / kDigitBits;
       digit_bits = (bits + passes - 1) / passes;
@@ -1774,9 +1787,19 @@ int enqueue_build(const int64_t* keys, const Plan& plan, int64_t* offsets, int64
                                                      n_rows > 0 ? 1 : 0);
       return launched("bucket_gather_kernel");
     };
-    if (plan.n_edges * 20 <= static_cast<int64_t>(plan.buckets) * kGatherSmallChunk * 19)
-      return gather(bucket_gather_kernel<kGatherThreads, kGatherSmallChunk, 8>);
-    return gather(bucket_gather_kernel<kGatherThreads, kGatherLargeChunk, 6>);
+    // instances by the fine digits (6 or 7 bits) and the tiles (1024 or 2048) they hold
+    const bool small = plan.n_edges * 20 <= static_cast<int64_t>(plan.buckets) * kGatherSmallChunk * 19;
+    const bool fine7 = plan.fine_bits > kFineMatchBits, tiles2k = plan.tiles > kMaxRunTiles / 2;
+#define DPA4K_GATHER(FB, TILES)                                                                    \
+  return small ? gather(bucket_gather_kernel<kGatherThreads, kGatherSmallChunk, 8, FB, TILES>)      \
+               : gather(bucket_gather_kernel<kGatherThreads, kGatherLargeChunk, 6, FB, TILES>)
+    if (fine7) {
+      if (tiles2k) DPA4K_GATHER(7, 2048);
+      DPA4K_GATHER(7, 1024);
+    }
+    if (tiles2k) DPA4K_GATHER(6, 2048);
+    DPA4K_GATHER(6, 1024);
+#undef DPA4K_GATHER
   }
   if (plan.two_level) {
     const int shift = plan.fine_bits, bits = plan.bucket_bits, buckets = plan.buckets;

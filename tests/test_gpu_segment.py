@@ -105,23 +105,25 @@ def test_counting_sort_skewed_and_sparse_keys():
     _check_grouping_against_numpy(np.array([0, 9_999_999], dtype=np.int64), 10_000_000, "two keys, ends")
 
 
-@pytest.mark.parametrize("edges,nodes", [(700_000, 128), (800_000, 128), (6_300_000, 2**16), (8_388_608, 2**16)])
+@pytest.mark.parametrize("edges,nodes", [(700_000, 128), (800_000, 128), (6_300_000, 2**16), (8_388_608, 2**16),
+                                         (9_000_000, 4096), (3_000_000, 2**17), (12_000_000, 2**17)])
 def test_counting_sort_bucket_chunks(edges, nodes):
     """Buckets that average just under and just over 95% of the gather's 6144-element chunk (the two
     chunk sizes of the grouped path), and config-4-sized buckets past it, with one bucket pushed over
-    the chunk so that it takes the multi-chunk path beside ones that do not; the last case fills every
-    one of the grouped path's 1,024 tiles."""
+    the chunk so that it takes the multi-chunk path beside ones that do not; then the gather's wider
+    instances: 1,024 tiles exactly, more than 1,024 tiles, 7-bit fine digits, and both at once with
+    every bucket longer than a chunk (a config-4R-sized list)."""
     announce("counting sort: bucket chunks", edges, nodes)
     keys = workloads.rng(edges % 997 + nodes).integers(0, nodes, size=edges).astype(np.int64)
     keys[: edges // 64] = 5
     _check_grouping_against_numpy(keys, nodes, f"chunks E={edges} N={nodes}")
 
 
-@pytest.mark.parametrize("edges,nodes", [(8_388_609, 2**16), (9_000_000, 4096)])
-def test_counting_sort_past_the_grouped_tile_limit(edges, nodes):
-    """Keys that the grouped path would take (at most 6 fine bits) but in more tiles than it handles
-    (1,024 tiles of 8,192 keys): the four-launch build, one key past the limit and well past it."""
-    announce("counting sort: past the grouped tile limit", edges, nodes)
+@pytest.mark.parametrize("edges,nodes", [(16_777_217, 2**16), (2_000_000, 2**18)])
+def test_counting_sort_past_the_grouped_limits(edges, nodes):
+    """Keys that the grouped path does not take: more tiles than it holds (2,048 tiles of 8,192 keys;
+    one key past the limit) and 8 fine bits.  The four-launch build."""
+    announce("counting sort: past the grouped limits", edges, nodes)
     keys = workloads.rng(edges % 991 + nodes).integers(0, nodes, size=edges).astype(np.int64)
     _check_grouping_against_numpy(keys, nodes, f"four-launch E={edges} N={nodes}")
 
