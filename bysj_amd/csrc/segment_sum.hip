@@ -308,7 +308,8 @@ __global__ __launch_bounds__(kBlock) void segment_sum_staged_kernel(
 // segment's rows round-robin, U rows per group per round with every load of
 // a round issued first.  grad_edge_scale is per edge; the groups' partial
 // grad_node_scale sums meet in LDS in group order.  Rows of at most 64 chunks.
-template <int G, int U, bool kOrdered>
+// kStreamRows loads the rows non-temporally (small grids, see the launcher).
+template <int G, int U, bool kOrdered, bool kStreamRows>
 __global__ __launch_bounds__(kBlock) void segment_sum_backward_wide_kernel(
     const float* __restrict__ grad_out, const float* __restrict__ src,
     const int64_t* __restrict__ offsets, const float* __restrict__ edge_scale,
@@ -356,7 +357,8 @@ __global__ __launch_bounds__(kBlock) void segment_sum_backward_wide_kernel(
     for (int u = 0; u < U; ++u) {
       weight[u] = has_edge_scale && edge[u] >= 0 ? edge_scale[edge[u]] : 1.0f;
       if (need_dot && live && edge[u] >= 0) {
-        x[u] = load_vec<4>(src + edge[u] * channels + column);
+        x[u] = kStreamRows ? load_vec_stream<4>(src + edge[u] * channels + column)
+                           : load_vec<4>(src + edge[u] * channels + column);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[u].v[i] = 0.0f;
@@ -417,14 +419,19 @@ int launch_wide_backward_g(const float* grad_out, const float* src, const int64_
                            int64_t n_nodes, int64_t channels, hipStream_t stream) {
   constexpr int U = 8;
   const dim3 grid = launch_grid(n_nodes, kBlock);
-  if (order != nullptr)
-    segment_sum_backward_wide_kernel<G, U, true><<<grid, kBlock, 0, stream>>>(
-        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
-        n_edges, n_nodes, channels);
-  else
-    segment_sum_backward_wide_kernel<G, U, false><<<grid, kBlock, 0, stream>>>(
-        grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale,
-        n_edges, n_nodes, channels);
+  // Non-temporal row loads pay on small grids (config 1: 11.4 -> 10.6-10.9 us) and not on large ones
+  // (config 1R: 1,846 -> 1,886-1,903 us), measured on one box.
+  const bool stream_rows = n_nodes < 4096;
+#define DPA4K_SUM_BWD_WIDE(ORD, NT)                                                                    \
+  segment_sum_backward_wide_kernel<G, U, ORD, NT><<<grid, kBlock, 0, stream>>>(                         \
+      grad_out, src, offsets, edge_scale, node_scale, order, grad_src, grad_edge_scale, grad_node_scale, \
+      n_edges, n_nodes, channels)
+  if (order != nullptr) {
+    if (stream_rows) DPA4K_SUM_BWD_WIDE(true, true); else DPA4K_SUM_BWD_WIDE(true, false);
+  } else {
+    if (stream_rows) DPA4K_SUM_BWD_WIDE(false, true); else DPA4K_SUM_BWD_WIDE(false, false);
+  }
+#undef DPA4K_SUM_BWD_WIDE
   return launched("segment_sum_backward_wide_kernel");
 }
 
