@@ -99,9 +99,8 @@ __device__ __forceinline__ uint32_t load_u32(BufferView view, uint32_t offset) {
 }
 
 // Loads of data read once (cache policy nt: streamed rather than kept in L2).
-constexpr int kStreamed = 2;
 __device__ __forceinline__ int64_t load_i64_streamed(BufferView view, uint32_t offset) {
-  const u32x2 raw = __builtin_amdgcn_raw_buffer_load_b64(view, static_cast<int>(offset), 0, kStreamed);
+  const u32x2 raw = __builtin_amdgcn_raw_buffer_load_b64(view, static_cast<int>(offset), 0, kNonTemporal);
   return __builtin_bit_cast(int64_t, raw);
 }
 
