@@ -481,21 +481,26 @@ __global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
   const int64_t edge_stride = n_radial * channels;
   const float scale = inv[node];
 
-  int64_t row[CPL], radial_col[CPL];
-  bool in_range[CPL];
-  fvec<V> g[CPL], h[CPL], pre[CPL];
+  // Per-lane 32-bit byte offsets into an edge's radial block and zonal row
+  // (kNoRow where the lane has no row), so the edge loop keeps no 64-bit
+  // addresses in registers.
+  uint32_t col_at[CPL], zon_at[CPL], out_at[CPL], gz_at[CPL];
+  fvec<V> g[CPL], pre[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int64_t q = lane + 64 * j;
     const int64_t s = q / RC;
     const int64_t c = q % RC;
-    in_range[j] = q < chunks;
+    const bool in_range = q < chunks;
     int64_t r = -1;
-    if (in_range[j])
+    if (in_range)
       for (int64_t k = 0; k < n_rows; ++k)
         if (radial_slot[k] == s) r = k;
-    row[j] = r;
-    radial_col[j] = s * channels + c * V;
+    const uint32_t col = static_cast<uint32_t>(s * channels + c * V) * 4u;
+    col_at[j] = r >= 0 ? col : kNoRow;
+    zon_at[j] = r >= 0 ? static_cast<uint32_t>(r) * 4u : kNoRow;
+    out_at[j] = in_range ? col : kNoRow;
+    gz_at[j] = in_range && r >= 0 && (lane % RC) == 0 ? static_cast<uint32_t>(r) * 4u : kNoRow;
     if (r >= 0) {
       g[j] = load_vec<V>(grad_output + (node * (n_rows + 1) + r + 1) * channels + c * V);
     } else {
@@ -503,30 +508,30 @@ __global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
       for (int i = 0; i < V; ++i) g[j].v[i] = 0.0f;
     }
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      h[j].v[i] = g[j].v[i] * scale;
-      pre[j].v[i] = 0.0f;
-    }
+    for (int i = 0; i < V; ++i) pre[j].v[i] = 0.0f;
   }
+  const int64_t radial_bytes = edge_stride * 4, zonal_bytes = n_rows * 4;
 
   int64_t begin, end;
   segment_bounds(offsets, node, n_edges, begin, end);
   for (int64_t slot = begin; slot < end; ++slot) {
-    const int64_t e = edge_of<kOrdered>(order, slot, n_edges);
+    const int64_t e = uniform_i64(edge_of<kOrdered>(order, slot, n_edges));
     if (kOrdered && e < 0) continue;
+    const BufferView rv = buffer_view(radial + e * edge_stride, radial_bytes);
+    const BufferView zv = buffer_view(zonal + e * n_rows, zonal_bytes);
     fvec<V> x[CPL];
     float z[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      if (row[j] >= 0) {
-        x[j] = load_vec<V>(radial + e * edge_stride + radial_col[j]);
-        z[j] = zonal[e * n_rows + row[j]];
-      } else {
-        z[j] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < V; ++i) x[j].v[i] = 0.0f;
-      }
+      x[j] = buffer_load_vec<V>(rv, col_at[j]);
+      z[j] = buffer_load_f32(zv, zon_at[j]);
     }
+    float sc = scale;
+    asm volatile("" : "+v"(sc));  // keeps g * scale inside the loop
+    const BufferView ov = grad_radial != nullptr ? buffer_view(grad_radial + e * edge_stride, radial_bytes)
+                                                 : buffer_view(radial, 0);
+    const BufferView gv = grad_zonal != nullptr ? buffer_view(grad_zonal + e * n_rows, zonal_bytes)
+                                                : buffer_view(radial, 0);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       float dot = 0.0f;
@@ -534,15 +539,13 @@ __global__ __launch_bounds__(kBlock) void gie_backward_distinct_kernel(
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         pre[j].v[i] = pre[j].v[i] + z[j] * x[j].v[i];
-        dot = dot + h[j].v[i] * x[j].v[i];
-        out.v[i] = h[j].v[i] * z[j];
+        const float h = g[j].v[i] * sc;
+        dot = dot + h * x[j].v[i];
+        out.v[i] = h * z[j];
       }
       dot = group_sum<RC>(dot);
-      if (in_range[j]) {
-        if (grad_radial != nullptr) store_vec_stream<V>(grad_radial + e * edge_stride + radial_col[j], out);
-        if (grad_zonal != nullptr && row[j] >= 0 && (lane % RC) == 0)
-          grad_zonal[e * n_rows + row[j]] = dot;
-      }
+      buffer_store_vec_stream<V>(ov, out_at[j], out);
+      buffer_store_f32(gv, gz_at[j], dot);
     }
   }
   if (grad_inv != nullptr) {
